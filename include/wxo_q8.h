@@ -1,0 +1,133 @@
+/*
+ * wxo_q8.h -- C ABI of the MI355X (gfx950) matvecQ8 path.
+ *
+ * A drop-in backend for web-xpu-ops' W8A32 GEMV and the quantize/packQ8 steps
+ * that produce its operands.  Plain C: no HIP, torch or C++ types cross this
+ * boundary, so a Node-API addon (gcc), ctypes or any other FFI binds it
+ * directly.  Entry points and the reference interface each one replaces:
+ *
+ *   wxo_matvec_q8             ops/matvec/reference.ts:117-131 (matvecQ8) and the
+ *                             WGSL dispatch it backs: ops/matvec/wgsl/q8.wgsl:26-35
+ *                             bindings {weight, scale, vector, output, {N,K}},
+ *                             called from llm/kernels.ts:195-211 (runMatVecQ8) and
+ *                             llm/engine-q8-resident.ts:1843-1845, :1869
+ *                             M > 1: M independent matvecQ8 calls on one weight
+ *   wxo_quantize              ops/quantize/reference.ts:13-38 (quantize)
+ *   wxo_pack_q8               ops/matvec/reference.ts:267-283 (packQ8)
+ *   wxo_pack_int8_rows        llm/weights-q8.ts:137-139 (packInt8Rows)
+ *   wxo_quantize_pack_q8      packQ8(quantize(w).output, N, K) + quantize(w).scales
+ *                             in one pass (the composition at ops/matvec/reference.ts:87-90)
+ *   wxo_*_host                the same ops on host arrays, synchronous: the TS op
+ *                             API's calling convention (typed arrays in, fresh
+ *                             typed arrays out)
+ *   wxo_malloc/free/memcpy/   device buffers for resident weights:
+ *   stream/event              harness/resident.ts:98-145 (createStorageBuffer,
+ *                             upload, batch, readback) and harness/wgsl.ts:37-52 (time)
+ *
+ * Data formats (identical to the reference's wire format):
+ *   weight  u32 [N, ceil(K/4)] row-major; code 4w+l of a row in bits 8l..8l+7
+ *           of word w (least-significant byte first), two's complement; pad
+ *           lanes past K are never read by wxo_matvec_q8 and written as 0 by
+ *           the pack entry points.
+ *   scale   f32 [N], applied once per row after the dot product.
+ *   vector  f32 [M, K] row-major (M = 1 for plain matvecQ8); output f32 [M, N].
+ *
+ * Errors: every entry point returns a wxo_status; nothing throws or aborts
+ * across the ABI.  On failure wxo_last_error() gives a message for the calling
+ * thread.  Unlike the reference (which reads `undefined` -> NaN on short
+ * inputs), sizes are validated: N*ceil(K/4), M*K etc. must fit in 2^40
+ * elements, M must be >= 1, and non-empty operands need non-NULL pointers.
+ *
+ * Streams: wxo_stream_t is a HIP stream (hipStream_t); NULL means the device's
+ * null stream.  Device entry points are asynchronous on that stream and
+ * allocate nothing; *_host entry points are synchronous and copy in and out.
+ */
+#ifndef WXO_Q8_H
+#define WXO_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WXO_ABI_VERSION 1
+
+typedef enum wxo_status {
+    WXO_OK = 0,
+    WXO_ERR_INVALID = 1,   /* bad argument: sizes, NULL pointers, overflow */
+    WXO_ERR_NO_DEVICE = 2, /* no gfx950 GPU visible, or HIP runtime unusable */
+    WXO_ERR_DEVICE = 3,    /* a HIP call failed (launch, copy, sync) */
+    WXO_ERR_OOM = 4        /* device allocation failed */
+} wxo_status;
+
+typedef struct wxo_stream_opaque* wxo_stream_t; /* hipStream_t */
+typedef struct wxo_event_opaque* wxo_event_t;   /* hipEvent_t */
+
+/* ---- library / device ---------------------------------------------------- */
+int wxo_abi_version(void);
+/* Message for the last failing call on this thread ("" if none). */
+const char* wxo_last_error(void);
+/* Initialises the HIP runtime on the current device and checks it is gfx950. */
+int wxo_init(void);
+/* One line: device name, arch, CU count, HBM size, library build, kernels. */
+const char* wxo_describe(void);
+int wxo_device_count(int* count);
+int wxo_set_device(int ordinal);
+
+/* ---- memory, streams, events ---------------------------------------------- */
+int wxo_malloc(void** ptr, size_t bytes);
+int wxo_free(void* ptr);
+int wxo_memcpy_htod(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
+int wxo_memcpy_dtoh(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
+int wxo_memcpy_dtod(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
+int wxo_synchronize(void);
+int wxo_stream_create(wxo_stream_t* stream);
+int wxo_stream_destroy(wxo_stream_t stream);
+int wxo_stream_synchronize(wxo_stream_t stream);
+int wxo_event_create(wxo_event_t* event);
+int wxo_event_destroy(wxo_event_t event);
+int wxo_event_record(wxo_event_t event, wxo_stream_t stream);
+int wxo_event_synchronize(wxo_event_t event);
+int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
+
+/* ---- ops on device pointers (asynchronous on `stream`) --------------------- */
+
+/* output[m*N + n] = (sum_{k<K} sext8(byte k of row n) * vector[m*K + k]) * scale[n]
+ * for m < M, n < N.  f32 accumulation; |y - y_ref| <= 1e-5 * sum_k|s q x| + 1e-7
+ * against the reference's f64 sum. */
+int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output,
+                  uint32_t N, uint32_t K, uint32_t M, wxo_stream_t stream);
+
+/* Per-row absmax quantization, bit-exact to ops/quantize/reference.ts:13-38:
+ * output int32 [N, D] codes in [-127, 127], scales f32 [N]. */
+int wxo_quantize(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales,
+                 wxo_stream_t stream);
+
+/* packQ8: int32 codes [N, K] -> u32 [N, ceil(K/4)], each code taken & 0xff. */
+int wxo_pack_q8(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed, wxo_stream_t stream);
+
+/* packInt8Rows: int8 codes [N, K] -> u32 [N, ceil(K/4)]. */
+int wxo_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed,
+                       wxo_stream_t stream);
+
+/* quantize + packQ8 in one pass: f32 [N, K] -> packed u32 [N, ceil(K/4)] and
+ * scales f32 [N]; bit-exact to packQ8(quantize(w).output, N, K). */
+int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* packed, float* scales,
+                         wxo_stream_t stream);
+
+/* ---- the same ops on host arrays (synchronous; copy in, run, copy out) ----- */
+int wxo_matvec_q8_host(const uint32_t* weight, const float* scale, const float* vector, float* output,
+                       uint32_t N, uint32_t K, uint32_t M);
+int wxo_quantize_host(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales);
+int wxo_pack_q8_host(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed);
+int wxo_pack_int8_rows_host(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed);
+int wxo_quantize_pack_q8_host(const float* input, uint32_t N, uint32_t K, uint32_t* packed,
+                              float* scales);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WXO_Q8_H */

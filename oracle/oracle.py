@@ -1,0 +1,149 @@
+"""numpy front end of the C oracle (oracle/q8_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as the
+checker, and by bench.py's cpu_baseline leg.  The product never imports it.
+
+Functions mirror the reference's TypeScript definitions:
+  quantize            ops/quantize/reference.ts:13-38
+  pack_q8             ops/matvec/reference.ts:267-283
+  pack_int8_rows      llm/weights-q8.ts:137-139
+  matvec_q8           ops/matvec/reference.ts:113-131
+  matvec_q8_batched   M x matvec_q8 (no reference function; defined that way)
+  absterm             sum_k |s*q*x| per row in f64 (tolerance base)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_q8.so")
+_lib = None
+
+
+def build() -> str:
+    """Compiles the oracle with its Makefile (gcc, seconds)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    p = ctypes.c_void_p
+    sz = ctypes.c_size_t
+    lib.q8o_js_round.argtypes = [ctypes.c_double]
+    lib.q8o_js_round.restype = ctypes.c_double
+    lib.q8o_quantize.argtypes = [p, sz, sz, p, p]
+    lib.q8o_pack_q8.argtypes = [p, sz, sz, p]
+    lib.q8o_pack_int8_rows.argtypes = [p, sz, sz, p]
+    lib.q8o_matvec_q8.argtypes = [p, p, p, sz, sz, p]
+    lib.q8o_matvec_q8_batched.argtypes = [p, p, p, sz, sz, sz, p]
+    lib.q8o_matvec_q8_absterm.argtypes = [p, p, p, sz, sz, p]
+    for name in ("q8o_quantize", "q8o_pack_q8", "q8o_pack_int8_rows", "q8o_matvec_q8",
+                 "q8o_matvec_q8_batched", "q8o_matvec_q8_absterm"):
+        getattr(lib, name).restype = None
+    _lib = lib
+    return lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def words_per_row(K: int) -> int:
+    return (K + 3) // 4
+
+
+def js_round(v: float) -> float:
+    return _load().q8o_js_round(float(v))
+
+
+def quantize(inp: np.ndarray, N: int, D: int) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(inp, dtype=np.float32).reshape(-1)
+    assert x.size >= N * D
+    out = np.empty(N * D, dtype=np.int32)
+    scales = np.empty(N, dtype=np.float32)
+    _load().q8o_quantize(_ptr(x), N, D, _ptr(out), _ptr(scales))
+    return out, scales
+
+
+def pack_q8(codes: np.ndarray, N: int, K: int) -> np.ndarray:
+    c = np.ascontiguousarray(codes, dtype=np.int32).reshape(-1)
+    assert c.size >= N * K
+    out = np.empty(N * words_per_row(K), dtype=np.uint32)
+    _load().q8o_pack_q8(_ptr(c), N, K, _ptr(out))
+    return out
+
+
+def pack_int8_rows(codes: np.ndarray, N: int, K: int) -> np.ndarray:
+    c = np.ascontiguousarray(codes, dtype=np.int8).reshape(-1)
+    assert c.size >= N * K
+    out = np.empty(N * words_per_row(K), dtype=np.uint32)
+    _load().q8o_pack_int8_rows(_ptr(c), N, K, _ptr(out))
+    return out
+
+
+def matvec_q8(weight: np.ndarray, scale: np.ndarray, vector: np.ndarray, N: int, K: int) -> np.ndarray:
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(vector, dtype=np.float32).reshape(-1)
+    assert w.size >= N * words_per_row(K) and s.size >= N and v.size >= K
+    out = np.empty(N, dtype=np.float32)
+    _load().q8o_matvec_q8(_ptr(w), _ptr(s), _ptr(v), N, K, _ptr(out))
+    return out
+
+
+def matvec_q8_batched(weight, scale, vectors, N: int, K: int, M: int) -> np.ndarray:
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(vectors, dtype=np.float32).reshape(-1)
+    assert w.size >= N * words_per_row(K) and s.size >= N and v.size >= M * K
+    out = np.empty(M * N, dtype=np.float32)
+    _load().q8o_matvec_q8_batched(_ptr(w), _ptr(s), _ptr(v), N, K, M, _ptr(out))
+    return out.reshape(M, N)
+
+
+def absterm(weight, scale, vector, N: int, K: int) -> np.ndarray:
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(vector, dtype=np.float32).reshape(-1)
+    out = np.empty(N, dtype=np.float64)
+    _load().q8o_matvec_q8_absterm(_ptr(w), _ptr(s), _ptr(v), N, K, _ptr(out))
+    return out
+
+
+# Output tolerance of the f32 kernels against the f64 reference, per row:
+# |y - y_ref| <= REL * sum_k |s*q*x| + ABS.
+REL = 1e-5
+ABS = 1e-7
+
+
+def check_matvec(got: np.ndarray, want: np.ndarray, bound: np.ndarray) -> tuple[bool, str]:
+    """Returns (ok, worst-offender report) in the shape of harness/agree.ts:27-46."""
+    got = np.asarray(got, dtype=np.float64).reshape(-1)
+    want = np.asarray(want, dtype=np.float64).reshape(-1)
+    bound = np.asarray(bound, dtype=np.float64).reshape(-1)
+    if got.shape != want.shape:
+        return False, f"length mismatch: got {got.size}, want {want.size}"
+    both_nan = np.isnan(got) & np.isnan(want)
+    same_inf = np.isinf(got) & np.isinf(want) & (np.sign(got) == np.sign(want))
+    with np.errstate(invalid="ignore"):
+        err = np.abs(got - want)
+        allowed = REL * bound + ABS
+        bad = ~(both_nan | same_inf | (err <= allowed))
+    if not bad.any():
+        return True, "ok"
+    idx = np.flatnonzero(bad)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        ratio = np.where(np.isfinite(err[idx]), err[idx] / allowed[idx], np.inf)
+    worst = idx[int(np.nanargmax(ratio))] if ratio.size else idx[0]
+    return False, (f"{idx.size} rows out of tolerance; worst row {worst}: got {got[worst]!r} "
+                   f"want {want[worst]!r} |err| {err[worst]:.3e} allowed {allowed[worst]:.3e}")

@@ -1,0 +1,147 @@
+/*
+ * q8_oracle.c -- CPU restatement of web-xpu-ops' matvecQ8 / quantize / packQ8.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the thing measured or
+ * shipped).  Build: oracle/Makefile, compiled with -O2 -ffp-contract=off so
+ * that no multiply-add is fused: the reference's arithmetic is separate f64
+ * multiplies and adds.
+ *
+ * The reference is TypeScript; its numbers are IEEE-754 binary64 and its
+ * typed-array stores define the narrowing:
+ *   Float32Array[i] = v   -> round-to-nearest-even binary32   (C: (float)v)
+ *   Int32Array[i]   = v   -> ToInt32(v); NaN -> 0, -0 -> 0     (to_int32 below)
+ *   Uint32Array[i]  = v   -> ToUint32(v)
+ */
+#include "q8_oracle.h"
+
+#include <math.h>
+
+/* Math.max / Math.min: NaN if either operand is NaN (ECMAScript 21.3.2.24/25). */
+static double js_max(double a, double b) {
+    if (isnan(a) || isnan(b)) return NAN;
+    if (a == 0.0 && b == 0.0) return signbit(a) ? b : a; /* +0 beats -0 */
+    return a > b ? a : b;
+}
+
+static double js_min(double a, double b) {
+    if (isnan(a) || isnan(b)) return NAN;
+    if (a == 0.0 && b == 0.0) return signbit(a) ? a : b; /* -0 beats +0 */
+    return a < b ? a : b;
+}
+
+/* Math.round (ECMAScript 21.3.2.28): the integral Number closest to v, ties
+ * toward +Infinity.  floor(v) + (v - floor(v) >= 0.5) has no second rounding:
+ * v - floor(v) is exact wherever the comparison can go either way (the band
+ * the reference's numpy twin documents at llm/tools/quant_common.py:11-22).
+ * v + 0.5 would round 0.49999999999999994 up to 1. */
+double q8o_js_round(double v) {
+    if (isnan(v) || isinf(v)) return v;
+    double f = floor(v);
+    return (v - f >= 0.5) ? f + 1.0 : f;
+}
+
+/* ToInt32 for the values quantize can produce: an integral double in
+ * [-127, 127] or NaN. */
+static int32_t to_int32(double v) {
+    if (isnan(v) || isinf(v)) return 0;
+    return (int32_t)v;
+}
+
+/* ops/quantize/reference.ts:13-38.  Per row: absmax in f64 over |x| with NaN
+ * propagating through Math.max (:27); scale = absmax === 0 ? 1 : absmax/127
+ * stored to Float32Array (:29); inverse = absmax === 0 ? 0 : 127/absmax in f64
+ * (:30); code = clamp(Math.round(x * inverse), -127, 127) stored to
+ * Int32Array (:33-34). */
+void q8o_quantize(const float* input, size_t N, size_t D, int32_t* output, float* scales) {
+    for (size_t row = 0; row < N; ++row) {
+        const float* x = input + row * D;
+        double absmax = 0.0;
+        for (size_t col = 0; col < D; ++col) absmax = js_max(absmax, fabs((double)x[col]));
+        scales[row] = absmax == 0.0 ? 1.0f : (float)(absmax / 127.0);
+        const double inverse = absmax == 0.0 ? 0.0 : 127.0 / absmax;
+        for (size_t col = 0; col < D; ++col) {
+            const double value = q8o_js_round((double)x[col] * inverse);
+            output[row * D + col] = to_int32(js_max(-127.0, js_min(127.0, value)));
+        }
+    }
+}
+
+/* ops/matvec/reference.ts:267-283.  wordsPerRow = ceil(K/4); lane `l` of
+ * word `w` carries (codes[row*K + 4w + l] & 0xff) << 8l; lanes past K stay 0
+ * (the `break` at :274); the word is stored through `>>> 0`. */
+void q8o_pack_q8(const int32_t* codes, size_t N, size_t K, uint32_t* packed) {
+    const size_t W = (K + 3) / 4;
+    for (size_t row = 0; row < N; ++row) {
+        for (size_t word = 0; word < W; ++word) {
+            uint32_t bits = 0;
+            for (size_t lane = 0; lane < 4; ++lane) {
+                const size_t col = word * 4 + lane;
+                if (col >= K) break;
+                bits |= ((uint32_t)codes[row * K + col] & 0xffu) << (8 * lane);
+            }
+            packed[row * W + word] = bits;
+        }
+    }
+}
+
+/* llm/weights-q8.ts:137-139: packQ8 applied to an Int8Array; `& 0xff` of an
+ * Int8Array element reads the same two's-complement byte. */
+void q8o_pack_int8_rows(const int8_t* codes, size_t N, size_t K, uint32_t* packed) {
+    const size_t W = (K + 3) / 4;
+    for (size_t row = 0; row < N; ++row) {
+        for (size_t word = 0; word < W; ++word) {
+            uint32_t bits = 0;
+            for (size_t lane = 0; lane < 4; ++lane) {
+                const size_t col = word * 4 + lane;
+                if (col >= K) break;
+                bits |= ((uint32_t)(uint8_t)codes[row * K + col]) << (8 * lane);
+            }
+            packed[row * W + word] = bits;
+        }
+    }
+}
+
+/* ops/matvec/reference.ts:113-115 (unpackI8: byte >= 128 ? byte - 256 : byte). */
+static int unpack_i8(uint32_t byte) { return byte >= 128 ? (int)byte - 256 : (int)byte; }
+
+/* ops/matvec/reference.ts:117-131.  Sum left to right in f64 over col < K only
+ * (pad lanes are never read), then one f64 multiply by the row's scale and
+ * one rounding to f32. */
+void q8o_matvec_q8(const uint32_t* weight, const float* scale, const float* vector,
+                   size_t N, size_t K, float* output) {
+    const size_t W = (K + 3) / 4;
+    for (size_t row = 0; row < N; ++row) {
+        const size_t rowOffset = row * W;
+        double sum = 0.0;
+        for (size_t col = 0; col < K; ++col) {
+            const uint32_t word = weight[rowOffset + (col >> 2)];
+            const uint32_t byte = (word >> ((col & 3) * 8)) & 0xffu;
+            sum += (double)unpack_i8(byte) * (double)vector[col];
+        }
+        output[row] = (float)(sum * (double)scale[row]);
+    }
+}
+
+/* M independent matvecQ8 calls: vectors [M, K], output [M, N]. */
+void q8o_matvec_q8_batched(const uint32_t* weight, const float* scale, const float* vectors,
+                           size_t N, size_t K, size_t M, float* output) {
+    for (size_t m = 0; m < M; ++m)
+        q8o_matvec_q8(weight, scale, vectors + m * K, N, K, output + m * N);
+}
+
+/* Per-row magnitude sum_k |s_n * q_nk * x_k| in f64: the scale of the f32
+ * rounding error any summation order can make, used as the tolerance base
+ * |y - y_ref| <= 1e-5 * bound + 1e-7. */
+void q8o_matvec_q8_absterm(const uint32_t* weight, const float* scale, const float* vector,
+                           size_t N, size_t K, double* bound) {
+    const size_t W = (K + 3) / 4;
+    for (size_t row = 0; row < N; ++row) {
+        double sum = 0.0;
+        for (size_t col = 0; col < K; ++col) {
+            const uint32_t word = weight[row * W + (col >> 2)];
+            const uint32_t byte = (word >> ((col & 3) * 8)) & 0xffu;
+            sum += fabs((double)unpack_i8(byte) * (double)vector[col]);
+        }
+        bound[row] = sum * fabs((double)scale[row]);
+    }
+}

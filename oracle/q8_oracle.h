@@ -1,0 +1,49 @@
+/*
+ * q8_oracle.h -- CPU restatement of web-xpu-ops' matvecQ8 path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP path is compared
+ * against, never part of the product: only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load it.
+ *
+ * Every function restates one reference function with the reference's own
+ * ECMAScript semantics (JS numbers are IEEE f64; Float32Array stores round
+ * to nearest-even; Int32Array stores truncate, NaN -> 0):
+ *
+ *   q8o_quantize          ops/quantize/reference.ts:13-38
+ *   q8o_pack_q8           ops/matvec/reference.ts:267-283
+ *   q8o_pack_int8_rows    llm/weights-q8.ts:137-139 (packQ8 over Int8Array)
+ *   q8o_matvec_q8         ops/matvec/reference.ts:113-131 (unpackI8 + matvecQ8)
+ *   q8o_matvec_q8_absterm sum_k |s_n * q_nk * x_k| in f64: the per-row bound
+ *                         the f32 kernels are judged against
+ *
+ * Batched matvecQ8 (M vectors) has no reference function; it is M
+ * independent matvecQ8 calls by definition, so the checker loops M times.
+ */
+#ifndef Q8_ORACLE_H
+#define Q8_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Math.round: nearest integer, ties toward +Infinity, no double rounding. */
+double q8o_js_round(double v);
+
+void q8o_quantize(const float* input, size_t N, size_t D, int32_t* output, float* scales);
+void q8o_pack_q8(const int32_t* codes, size_t N, size_t K, uint32_t* packed);
+void q8o_pack_int8_rows(const int8_t* codes, size_t N, size_t K, uint32_t* packed);
+void q8o_matvec_q8(const uint32_t* weight, const float* scale, const float* vector,
+                   size_t N, size_t K, float* output);
+void q8o_matvec_q8_batched(const uint32_t* weight, const float* scale, const float* vectors,
+                           size_t N, size_t K, size_t M, float* output);
+void q8o_matvec_q8_absterm(const uint32_t* weight, const float* scale, const float* vector,
+                           size_t N, size_t K, double* bound);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

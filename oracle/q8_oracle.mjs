@@ -1,0 +1,80 @@
+/**
+ * q8_oracle.mjs -- ECMAScript restatement of web-xpu-ops' matvecQ8 path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the Node-side tests and the
+ * single-core CPU baseline that bench.py times beside the GPU.  It is never
+ * imported by the product (web-xpu-ops_amd/).
+ *
+ * Written for this build from the reference's definitions; it runs on the
+ * same engine semantics the reference runs on (V8 f64 numbers, Math.round,
+ * Float32Array/Int32Array/Uint32Array stores), so it is the most literal
+ * restatement available without the reference's own toolchain.
+ *
+ *   quantize       ops/quantize/reference.ts:13-38
+ *   packQ8         ops/matvec/reference.ts:267-283
+ *   packInt8Rows   llm/weights-q8.ts:137-139
+ *   matvecQ8       ops/matvec/reference.ts:113-131
+ */
+
+/** ops/quantize/reference.ts:13-38 */
+export function quantize({ input, N, D }) {
+  const output = new Int32Array(N * D);
+  const scales = new Float32Array(N);
+  for (let row = 0; row < N; row += 1) {
+    const base = row * D;
+    let absmax = 0;
+    for (let col = 0; col < D; col += 1) absmax = Math.max(absmax, Math.abs(input[base + col]));
+    scales[row] = absmax === 0 ? 1 : absmax / 127;
+    const inverse = absmax === 0 ? 0 : 127 / absmax;
+    for (let col = 0; col < D; col += 1) {
+      const value = Math.round(input[base + col] * inverse);
+      output[base + col] = Math.max(-127, Math.min(127, value));
+    }
+  }
+  return { output, scales };
+}
+
+/** ops/matvec/reference.ts:267-283 (also accepts an Int8Array: llm/weights-q8.ts:137-139) */
+export function packQ8({ codes, N, K }) {
+  const wordsPerRow = Math.ceil(K / 4);
+  const packed = new Uint32Array(N * wordsPerRow);
+  for (let row = 0; row < N; row += 1) {
+    for (let word = 0; word < wordsPerRow; word += 1) {
+      let bits = 0;
+      for (let lane = 0; lane < 4 && word * 4 + lane < K; lane += 1) {
+        bits |= (codes[row * K + word * 4 + lane] & 0xff) << (lane * 8);
+      }
+      packed[row * wordsPerRow + word] = bits >>> 0;
+    }
+  }
+  return packed;
+}
+
+export function packInt8Rows(codes, N, K) {
+  return packQ8({ codes, N, K });
+}
+
+/** ops/matvec/reference.ts:113-131: f64 sum over col < K, scale once, one f32 rounding. */
+export function matvecQ8({ weight, scale, vector, N, K }) {
+  const wordsPerRow = Math.ceil(K / 4);
+  const output = new Float32Array(N);
+  for (let row = 0; row < N; row += 1) {
+    const rowOffset = row * wordsPerRow;
+    let sum = 0;
+    for (let col = 0; col < K; col += 1) {
+      const byte = (weight[rowOffset + (col >> 2)] >>> ((col & 3) * 8)) & 0xff;
+      sum += (byte >= 128 ? byte - 256 : byte) * vector[col];
+    }
+    output[row] = sum * scale[row];
+  }
+  return output;
+}
+
+/** M independent matvecQ8 calls over vectors [M, K]; output [M, N]. */
+export function matvecQ8Batched({ weight, scale, vectors, N, K, M }) {
+  const output = new Float32Array(M * N);
+  for (let m = 0; m < M; m += 1) {
+    output.set(matvecQ8({ weight, scale, vector: vectors.subarray(m * K, (m + 1) * K), N, K }), m * N);
+  }
+  return output;
+}

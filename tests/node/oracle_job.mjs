@@ -1,0 +1,43 @@
+// Runs one op of the ECMAScript oracle (oracle/q8_oracle.mjs) on arrays sent as
+// base64 in a JSON job on stdin; prints the outputs as base64 JSON on stdout.
+// Lets the Python tests hold the C oracle and the JS oracle to each other.
+import { quantize, packQ8, packInt8Rows, matvecQ8 } from "../../oracle/q8_oracle.mjs";
+
+const typed = { f32: Float32Array, i32: Int32Array, u32: Uint32Array, i8: Int8Array };
+function decode(spec) {
+  const buf = Buffer.from(spec.b64, "base64");
+  const T = typed[spec.dtype];
+  const copy = new Uint8Array(buf.length);
+  copy.set(buf);
+  return new T(copy.buffer, 0, buf.length / T.BYTES_PER_ELEMENT);
+}
+const encode = (arr) => Buffer.from(arr.buffer, arr.byteOffset, arr.byteLength).toString("base64");
+
+let text = "";
+process.stdin.setEncoding("utf8");
+process.stdin.on("data", (chunk) => { text += chunk; });
+process.stdin.on("end", () => {
+  const job = JSON.parse(text);
+  const a = {};
+  for (const [name, spec] of Object.entries(job.arrays || {})) a[name] = decode(spec);
+  let out;
+  switch (job.op) {
+    case "quantize": {
+      const r = quantize({ input: a.input, N: job.N, D: job.D });
+      out = { output: encode(r.output), scales: encode(r.scales) };
+      break;
+    }
+    case "packQ8":
+      out = { packed: encode(packQ8({ codes: a.codes, N: job.N, K: job.K })) };
+      break;
+    case "packInt8Rows":
+      out = { packed: encode(packInt8Rows(a.codes, job.N, job.K)) };
+      break;
+    case "matvecQ8":
+      out = { output: encode(matvecQ8({ weight: a.weight, scale: a.scale, vector: a.vector, N: job.N, K: job.K })) };
+      break;
+    default:
+      throw new Error(`unknown op ${job.op}`);
+  }
+  process.stdout.write(JSON.stringify(out));
+});

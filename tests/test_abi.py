@@ -1,0 +1,103 @@
+"""The C ABI library on a machine without a GPU: it loads, exports every
+symbol include/wxo_q8.h declares, validates arguments before touching a
+device, and fails loudly (no CPU fallback) when no gfx950 is visible.
+Also checks the built device code for packed-FP32 instructions."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import wxo_q8
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wxo_q8.h")
+CSRC = os.path.join(ROOT, "web-xpu-ops_amd", "csrc")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wxo_[a-z0-9_]+)\s*\(", text)))
+
+
+def have_gpu():
+    try:
+        return wxo_q8.device_count() > 0
+    except wxo_q8.WxoError:
+        return False
+
+
+def test_library_is_built():
+    assert os.path.exists(wxo_q8.LIB_PATH), "run __graft_entry__.build() first"
+
+
+def test_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert len(names) >= 25
+    lib = ctypes.CDLL(wxo_q8.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python binding covers exactly the declared surface
+    assert sorted(wxo_q8.SIGNATURES) == names
+
+
+def test_abi_version_and_describe():
+    assert wxo_q8.lib().wxo_abi_version() == 1
+    text = wxo_q8.describe()
+    assert text.startswith("wxo_q8 abi=1")
+    if not have_gpu():
+        assert "device=none" in text
+
+
+def test_validation_happens_before_device_access():
+    L = wxo_q8.lib()
+    # M = 0
+    assert L.wxo_matvec_q8(None, None, None, None, 4, 8, 0, None) == wxo_q8.WXO_ERR_INVALID
+    assert "M (vectors)" in L.wxo_last_error().decode()
+    # NULL operand with work to do
+    assert L.wxo_matvec_q8(None, None, None, None, 4, 8, 1, None) == wxo_q8.WXO_ERR_INVALID
+    assert "weight is NULL" in L.wxo_last_error().decode()
+    # size overflow (N * ceil(K/4) > 2^40)
+    big = 0xFFFFFFFF
+    assert L.wxo_matvec_q8(1, 1, 1, 1, big, big, 1, None) == wxo_q8.WXO_ERR_INVALID
+    assert L.wxo_quantize(None, 3, 5, None, None, None) == wxo_q8.WXO_ERR_INVALID
+    assert L.wxo_pack_q8(None, 3, 5, None, None) == wxo_q8.WXO_ERR_INVALID
+    assert L.wxo_pack_int8_rows(None, 3, 5, None, None) == wxo_q8.WXO_ERR_INVALID
+    assert L.wxo_quantize_pack_q8(None, 3, 5, None, None, None) == wxo_q8.WXO_ERR_INVALID
+    with pytest.raises(wxo_q8.WxoError, match="weight has 3 elements"):
+        wxo_q8.matvecQ8(weight=np.zeros(3, np.uint32), scale=np.ones(2, np.float32),
+                        vector=np.ones(8, np.float32), N=2, K=8)
+
+
+@pytest.mark.skipif(have_gpu(), reason="checks the no-GPU failure path")
+def test_no_gpu_fails_loudly():
+    with pytest.raises(wxo_q8.WxoError) as e:
+        wxo_q8.init()
+    assert e.value.status == wxo_q8.WXO_ERR_NO_DEVICE
+    assert "no CPU fallback" in str(e.value)
+    with pytest.raises(wxo_q8.WxoError):
+        wxo_q8.matvecQ8(weight=np.zeros(2, np.uint32), scale=np.ones(2, np.float32),
+                        vector=np.ones(4, np.float32), N=2, K=4)
+    with pytest.raises(wxo_q8.WxoError):
+        wxo_q8.quantize(input=np.ones(8, np.float32), N=2, D=4)
+
+
+def test_device_code_has_no_packed_fp32():
+    # Every HIP source compiled to gfx950 assembly: no v_pk_add/mul/fma_f32.
+    hipcc = "/opt/rocm/bin/hipcc"
+    with tempfile.TemporaryDirectory() as tmp:
+        for src in ("matvec_q8.hip", "quantize_q8.hip"):
+            out = os.path.join(tmp, src + ".s")
+            subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only", "-S",
+                            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                            "-I", os.path.join(ROOT, "include"), "-I", CSRC, os.path.join(CSRC, src), "-o", out],
+                           check=True, capture_output=True)
+            asm = open(out).read()
+            assert re.search(r"v_pk_(add|mul|fma)_f32", asm) is None, src
+            # no register spills in any kernel
+            spills = [int(v) for v in re.findall(r"\.vgpr_spill_count:\s+(\d+)", asm)]
+            assert spills and max(spills) == 0, src

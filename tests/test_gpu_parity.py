@@ -1,0 +1,366 @@
+"""Parity of the gfx950 path with the oracle, through the C ABI (wxo_q8 / ctypes).
+
+Bars (from the reference's definitions):
+  * quantize codes, scales and packed words: bit-exact;
+  * matvecQ8 outputs: |y - y_ref| <= 1e-5 * sum_k |s*q*x| + 1e-7 per row
+    (oracle.REL, oracle.ABS), y_ref the f64 reference sum.
+Shapes follow the reference's own tests (ops/matvec/q8.wgsl.test.ts:48-149,
+ops/quantize/wgsl.test.ts, ops/matvec/reference.test.ts) plus every BASELINE
+configuration at full size.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import wxo_q8
+import wxo_workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    wxo_q8.init()
+    print(wxo_q8.describe(), flush=True)
+
+
+def kat():
+    with open(os.path.join(GOLDEN, "kat.json")) as f:
+        return json.load(f)
+
+
+def assert_matvec(got, w, s, x, N, K):
+    want = oracle.matvec_q8(w, s, x, N, K)
+    bound = oracle.absterm(w, s, x, N, K)
+    ok, msg = oracle.check_matvec(got, want, bound)
+    assert ok, f"N={N} K={K}: {msg}"
+
+
+def assert_bits_equal(got, want, what):
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, what
+    if got.dtype.kind == "f":
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), f"{what}: NaN positions differ"
+        g, w = got[~nan].view(np.uint32), want[~nan].view(np.uint32)
+    else:
+        g, w = got, want
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[0]}: got {got.reshape(-1)[bad[0]]!r} want {want.reshape(-1)[bad[0]]!r}"
+
+
+def random_weights(rng, N, K, full_range=False):
+    W = (K + 3) // 4
+    if full_range:  # any byte, 0x80 (-128) included
+        return rng.integers(0, 2 ** 32, N * W, dtype=np.uint64).astype(np.uint32)
+    codes = rng.integers(-127, 128, N * K, dtype=np.int32)
+    return oracle.pack_q8(codes, N, K)
+
+
+# ---------------------------------------------------------------- matvecQ8
+
+@pytest.mark.parametrize("case", kat()["matvec_q8"], ids=lambda c: c["source"].split(" ")[0])
+def test_matvec_kat(case):
+    N, K = case["N"], case["K"]
+    w = oracle.pack_q8(np.array(case["codes"], np.int32), N, K)
+    if "pad_patch" in case:
+        w[case["pad_patch"]["word"]] |= np.uint32(int(case["pad_patch"]["or"], 16))
+    x = np.array(case["vector"], np.float32)
+    y = wxo_q8.matvecQ8(weight=w, scale=np.array(case["scale"], np.float32), vector=x[:K], N=N, K=K)
+    assert y.tolist() == case["want"]
+
+
+def code_wave(n, k, phase=0.0):
+    return np.round(np.sin(np.arange(n) * k + phase) * 100).astype(np.int32)
+
+
+def wave(n, k, phase=0.0):
+    return (np.sin(np.arange(n) * k + phase) * 1.5).astype(np.float32)
+
+
+def scale_wave(n):
+    return (0.02 * (np.arange(n) + 1) + 0.007).astype(np.float32)
+
+
+@pytest.mark.parametrize("N,K", [(1, 3), (1, 8), (5, 1024), (3, 1030), (7, 1027), (2, 2600)])
+def test_matvec_reference_shapes(N, K):
+    # ops/matvec/q8.wgsl.test.ts:48-71 inputs (codeWave / scaleWave / wave).
+    w = oracle.pack_q8(code_wave(N * K, 0.37), N, K)
+    s = scale_wave(N)
+    x = wave(K, 0.11, 0.8)
+    assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
+
+
+def test_matvec_reads_past_first_pass():
+    # ops/matvec/q8.wgsl.test.ts:73-106
+    N, K = 3, 1030
+    codes = np.zeros((N, K), np.int32)
+    x = np.zeros(K, np.float32)
+    x[1027], x[K - 1] = 2, -3
+    for r in range(N):
+        codes[r, 1027] = 1 + r
+        codes[r, K - 1] = 2 * (r + 1)
+    w = oracle.pack_q8(codes, N, K)
+    s = scale_wave(N)
+    y = wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K)
+    assert_matvec(y, w, s, x, N, K)
+    assert np.all(y != 0)
+
+
+def test_matvec_sentinel_padded_device_buffers():
+    # ops/matvec/q8.wgsl.test.ts:108-149: buffers longer than N*W words and K
+    # floats, slack filled with sentinels; over-reads would change the answer.
+    N, K = 4, 1023
+    W = (K + 3) // 4
+    codes = np.array([(i // K) % 5 + 1 for i in range(N * K)], np.int32)
+    packed = oracle.pack_q8(codes, N, K)
+    w = np.concatenate([packed, np.full(256, 0x7F7F7F7F, np.uint32)])
+    x = np.concatenate([np.ones(K, np.float32), np.full(256, 1000, np.float32)])
+    s = scale_wave(N)
+    bw, bs, bx = (wxo_q8.DeviceBuffer.from_array(a) for a in (w, s, x))
+    by = wxo_q8.DeviceBuffer(4 * (N + 64))
+    by.upload(np.full(N + 64, -7.0, np.float32))
+    wxo_q8.matvec_q8_device(bw, bs, bx, by, N, K)
+    out = by.download(np.float32, N + 64)
+    assert_matvec(out[:N], packed, s, x[:K], N, K)
+    assert np.all(out[N:] == -7.0), "wrote past the output"
+    for b in (bw, bs, bx, by):
+        b.free()
+    assert W == 256
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 63, 64, 65, 255, 1023, 1024, 1025, 2048, 3072, 4095, 4096, 4099,
+                               5632, 8192, 12288, 16384, 16385, 20000])
+@pytest.mark.parametrize("N", [1, 17, 33])
+def test_matvec_k_sweep(N, K):
+    rng = np.random.default_rng(N * 100003 + K)
+    w = random_weights(rng, N, K, full_range=(K % 2 == 1))
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
+
+
+@pytest.mark.parametrize("N", [2, 15, 16, 31, 32, 1000, 4097])
+def test_matvec_row_tails(N):
+    rng = np.random.default_rng(N)
+    K = 4096
+    w = random_weights(rng, N, K)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
+
+
+def test_matvec_degenerate():
+    # N = 0: nothing; K = 0: y = 0 * s (NaN for non-finite scale), as the reference.
+    assert wxo_q8.matvecQ8(weight=np.zeros(0, np.uint32), scale=np.zeros(0, np.float32),
+                           vector=np.ones(4, np.float32), N=0, K=4).size == 0
+    s = np.array([2.0, -3.0, np.inf, np.nan], np.float32)
+    y = wxo_q8.matvecQ8(weight=np.zeros(0, np.uint32), scale=s, vector=np.zeros(0, np.float32), N=4, K=0)
+    want = oracle.matvec_q8(np.zeros(0, np.uint32), s, np.zeros(0, np.float32), 4, 0)
+    assert_bits_equal(y, want, "K=0")
+
+
+def test_matvec_nonfinite_scale_and_vector():
+    rng = np.random.default_rng(5)
+    N, K = 8, 100
+    w = random_weights(rng, N, K)
+    s = rng.uniform(0.01, 0.02, N).astype(np.float32)
+    s[2] = np.inf
+    s[3] = np.nan
+    x = rng.standard_normal(K).astype(np.float32)
+    y = wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K)
+    assert_matvec(y, w, s, x, N, K)
+    assert np.isnan(y[3])
+
+
+def test_matvec_row_chunks_equal_whole():
+    # llm/engine-q8-resident.ts:1214-1230 / llm/kernels.ts:140-151: a caller may
+    # run a projection as row chunks on sub-buffers; each chunk must give the
+    # same rows as one whole call.
+    rng = np.random.default_rng(9)
+    N, K = 1000, 1030
+    W = (K + 3) // 4
+    w = random_weights(rng, N, K)
+    s = rng.uniform(0.01, 0.02, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    bw, bs, bx = (wxo_q8.DeviceBuffer.from_array(a) for a in (w, s, x))
+    whole = wxo_q8.DeviceBuffer(4 * N)
+    wxo_q8.matvec_q8_device(bw, bs, bx, whole, N, K)
+    parts = wxo_q8.DeviceBuffer(4 * N)
+    for start, count in ((0, 333), (333, 1), (334, 666)):
+        wxo_q8.matvec_q8_device(bw.ptr + 4 * W * start, bs.ptr + 4 * start, bx, parts.ptr + 4 * start, count, K)
+    a = whole.download(np.float32, N)
+    b = parts.download(np.float32, N)
+    assert_matvec(a, w, s, x, N, K)
+    assert_bits_equal(b, a, "chunked vs whole")
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_matvec_baseline_configs(cfg):
+    c = wl.make_config(cfg)
+    N, K = c["N"], c["K"]
+    codes, scales = oracle.quantize(c["w"], N, K)
+    w = oracle.pack_q8(codes, N, K)
+    y = wxo_q8.matvecQ8(weight=w, scale=scales, vector=c["x"], N=N, K=K)
+    assert_matvec(y, w, scales, c["x"], N, K)
+    if cfg == "cfg3":
+        # outlier rows: absmax set by the x50 element, which alone codes to +-127
+        cr = codes.reshape(N, K)
+        assert np.all(np.max(np.abs(cr[c["outliers"]]), axis=1) == 127)
+
+
+def test_matvec_decoder_layer():
+    mats, xh, xf = wl.make_decoder_layer()
+    for name, N, K, wf in mats:
+        codes, scales = oracle.quantize(wf, N, K)
+        w = oracle.pack_q8(codes, N, K)
+        x = xf if K == 5632 else xh
+        assert_matvec(wxo_q8.matvecQ8(weight=w, scale=scales, vector=x, N=N, K=K), w, scales, x, N, K)
+
+
+# ---------------------------------------------------------------- batched
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 13, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(37, 64), (100, 1024), (9, 1030), (70, 2048), (21, 4099), (5, 8200), (3, 20000)])
+def test_batched_equals_m_calls(M, N, K):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    w = random_weights(rng, N, K, full_range=(M % 2 == 1))
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
+def test_batched_lm_head(M):
+    c = wl.make_config("cfg5", M=M)
+    N, K = c["N"], c["K"]
+    codes, scales = oracle.quantize(c["w"], N, K)
+    w = oracle.pack_q8(codes, N, K)
+    xs = c["x"].reshape(M, K)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=scales, vectors=xs, N=N, K=K, M=M)
+    rows = np.arange(0, N, 97)  # oracle on a row sample; all M vectors
+    W = (K + 3) // 4
+    wsub = w.reshape(N, W)[rows].reshape(-1)
+    for m in range(M):
+        assert_matvec(ys[m][rows], wsub, scales[rows], xs[m], rows.size, K)
+    assert np.all(np.isfinite(ys))
+
+
+# ---------------------------------------------------------------- quantize / packQ8
+
+@pytest.mark.parametrize("case", kat()["quantize"], ids=lambda c: c["source"].split(" ")[0])
+def test_quantize_kat(case):
+    x = np.array(case["input"], np.float32)
+    codes, scales = wxo_q8.quantize(input=x, N=1, D=x.size)
+    assert codes.tolist() == case["codes"]
+    assert int(scales.view(np.uint32)[0]) == int(case["scale_bits"], 16)
+    packed, s2 = wxo_q8.quantizePackQ8(input=x, N=1, K=x.size)
+    assert_bits_equal(packed, oracle.pack_q8(np.array(case["codes"], np.int32), 1, x.size), "fused words")
+    assert_bits_equal(s2, scales, "fused scale")
+
+
+def test_quantize_reference_fixture():
+    from test_oracle import _tiny_q8_pairs
+    for name, N, K, w, want_codes, want_scales in _tiny_q8_pairs():
+        codes, scales = wxo_q8.quantize(input=w, N=N, D=K)
+        assert_bits_equal(codes, want_codes.astype(np.int32), name + " codes")
+        assert_bits_equal(scales, want_scales, name + " scales")
+        packed, s2 = wxo_q8.quantizePackQ8(input=w, N=N, K=K)
+        assert_bits_equal(packed, oracle.pack_int8_rows(want_codes, N, K), name + " packed")
+        assert_bits_equal(s2, want_scales, name + " fused scales")
+        assert_bits_equal(wxo_q8.packInt8Rows(want_codes, N, K), packed, name + " packInt8Rows")
+
+
+def edge_rows(rng, N, D):
+    from test_oracle import tie_heavy_rows
+    x = tie_heavy_rows(rng, N, D)
+    x[3] = 0.0
+    x[4] = -0.0
+    x[5, 7 % D] = np.nan
+    x[6, 9 % D] = np.inf
+    x[7] = 1e-42
+    x[8, 11 % D] = -np.inf
+    x[9, 0] = 1.3530999422073364
+    if D > 1:
+        x[9, 1] = 0.005327165126800537
+    x[10] = np.float32(3.4e38)
+    x[11, :] = np.float32(1e-45) * np.arange(D)
+    return x
+
+
+def test_quantize_exact_half_ties_after_rounded_product():
+    # x = -absmax/2 and +absmax/2: x * (127/absmax) rounds (in f64) to exactly
+    # -63.5 / +63.5 while the exact product is not a tie.  Math.round on the
+    # rounded product gives -63 and 64; a fused multiply-subtract that skips
+    # the product's rounding gets -64 / 63.  (Regression: hipcc contracted
+    # x * inverse - floor(...) into one v_fma_f64.)
+    rows = np.array([[2.1543185710906982, -1.0771592855453491],
+                     [2.5792481899261475, 1.2896240949630737],
+                     [1.9307280778884888, 0.9653640389442444]], np.float32)
+    codes, _ = wxo_q8.quantize(input=rows, N=3, D=2)
+    assert codes.tolist() == [127, -63, 127, 64, 127, 64]
+    assert oracle.quantize(rows, 3, 2)[0].tolist() == [127, -63, 127, 64, 127, 64]
+    packed, _ = wxo_q8.quantizePackQ8(input=rows, N=3, K=2)
+    assert packed.tolist() == [0x0000C17F, 0x0000407F, 0x0000407F]
+
+
+@pytest.mark.parametrize("D", [1, 3, 4, 5, 64, 300, 517, 1023, 2048, 4096, 4099, 5632, 6144, 9000, 20001])
+def test_quantize_edges_bit_exact(D):
+    rng = np.random.default_rng(D)
+    N = 24
+    x = edge_rows(rng, N, D)
+    want_codes, want_scales = oracle.quantize(x, N, D)
+    codes, scales = wxo_q8.quantize(input=x, N=N, D=D)
+    assert_bits_equal(codes, want_codes, f"codes D={D}")
+    assert_bits_equal(scales, want_scales, f"scales D={D}")
+    packed, s2 = wxo_q8.quantizePackQ8(input=x, N=N, K=D)
+    assert_bits_equal(packed, oracle.pack_q8(want_codes, N, D), f"packed D={D}")
+    assert_bits_equal(s2, want_scales, f"fused scales D={D}")
+
+
+def test_quantize_decoder_layer_bit_exact():
+    mats, _, _ = wl.make_decoder_layer()
+    for name, N, K, wf in mats:
+        want_codes, want_scales = oracle.quantize(wf, N, K)
+        packed, scales = wxo_q8.quantizePackQ8(input=wf, N=N, K=K)
+        assert_bits_equal(packed, oracle.pack_q8(want_codes, N, K), name + " packed")
+        assert_bits_equal(scales, want_scales, name + " scales")
+    name, N, K, wf = mats[-1]
+    codes, scales = wxo_q8.quantize(input=wf, N=N, D=K)
+    assert_bits_equal(codes, oracle.quantize(wf, N, K)[0], "wDown codes")
+
+
+@pytest.mark.parametrize("N,K", [(1, 1), (3, 4), (5, 7), (7, 1027), (64, 4099), (2, 2), (300, 64)])
+def test_pack_bit_exact(N, K):
+    rng = np.random.default_rng(N * 17 + K)
+    codes = rng.integers(-300, 300, N * K, dtype=np.int32)
+    assert_bits_equal(wxo_q8.packQ8(codes=codes, N=N, K=K), oracle.pack_q8(codes, N, K), "packQ8")
+    i8 = rng.integers(-128, 128, N * K).astype(np.int8)
+    assert_bits_equal(wxo_q8.packInt8Rows(i8, N, K), oracle.pack_int8_rows(i8, N, K), "packInt8Rows")
+
+
+@pytest.mark.parametrize("case", kat()["pack_q8"], ids=lambda c: c["source"].split(" ")[0])
+def test_pack_kat(case):
+    words = wxo_q8.packQ8(codes=np.array(case["codes"], np.int32), N=case["N"], K=case["K"])
+    assert [f"0x{w:08x}" for w in words.tolist()] == case["words"]
+
+
+def test_round_trip_full_size():
+    # quantize -> packQ8 -> matvecQ8 on the GPU equals the oracle pipeline
+    # (cfg2 shape): codes/scales bit-exact, outputs within tolerance.
+    c = wl.make_config("cfg2")
+    N, K = c["N"], c["K"]
+    packed, scales = wxo_q8.quantizePackQ8(input=c["w"], N=N, K=K)
+    codes, want_scales = oracle.quantize(c["w"], N, K)
+    assert_bits_equal(packed, oracle.pack_q8(codes, N, K), "cfg2 packed")
+    assert_bits_equal(scales, want_scales, "cfg2 scales")
+    y = wxo_q8.matvecQ8(weight=packed, scale=scales, vector=c["x"], N=N, K=K)
+    assert_matvec(y, packed, scales, c["x"], N, K)

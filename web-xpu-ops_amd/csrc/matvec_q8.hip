@@ -1,0 +1,378 @@
+// matvec_q8.hip -- W8A32 GEMV for gfx950: y[m, n] = (sum_k q[n, k] * x[m, k]) * s[n].
+//
+// Reference semantics: ops/matvec/reference.ts:113-131 (matvecQ8); the WGSL
+// kernel it replaces is ops/matvec/wgsl/q8.wgsl (one 256-lane workgroup per
+// row, scalar u32 loads, 8-level LDS tree).  This is a different design:
+//
+//  * A "chunk" is 256 consecutive packed words (1 KiB) of one row: exactly one
+//    wave-wide global_load_dwordx4 (64 lanes x 16 B).  Lane l of a wave always
+//    owns words [4l, 4l+4) of its chunks, i.e. the 16 codes k = 1024c + 16l ..
+//    +15, so the 16 vector values it needs are fetched once per wave and live
+//    in VGPRs for every row the wave visits: no LDS traffic for x in the loop.
+//  * A workgroup of WAVES waves splits each row's chunks round-robin between
+//    its waves (chunk c -> wave c % WAVES, slot c / WAVES), and walks blocks of
+//    R rows with R independent dwordx4 loads in flight per wave per chunk.
+//  * Unpack is one v_cvt_f32_i32_sdwa (sign-extended byte select) per code
+//    feeding one v_fmac_f32: 2 VALU ops per code, no MFMA (bandwidth-bound).
+//  * R row sums are reduced across the wave with DPP/permlane halving
+//    (~R+6 ops, no LDS), partials of the WAVES waves meet in a 2-slot LDS
+//    buffer (one barrier per block), and the scale is applied once per row.
+//  * Pad lanes past K: the vector registers for k >= K are zero, so whatever
+//    the pad bytes hold contributes q * 0 = 0; words past the row end and
+//    vector entries past K are never loaded.
+//
+// The small-M batched kernel reuses every loaded word for MT vectors: one
+// unpack per code, MT FMAs, with the MT vector slices in VGPRs.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.hpp"
+#include "wave_ops.hpp"
+
+namespace wxo {
+
+constexpr uint32_t kChunkWords = 256;   // one wave-wide dwordx4 load
+constexpr uint32_t kChunkCodes = 1024;
+
+__device__ __forceinline__ float fma_word(uint32_t w, float x0, float x1, float x2, float x3, float acc) {
+    acc = __builtin_fmaf((float)(int8_t)(w), x0, acc);
+    acc = __builtin_fmaf((float)(int8_t)(w >> 8), x1, acc);
+    acc = __builtin_fmaf((float)(int8_t)(w >> 16), x2, acc);
+    acc = __builtin_fmaf((float)((int32_t)w >> 24), x3, acc);
+    return acc;
+}
+
+// Lane `lane`'s 16 vector values of chunk c (k = 1024c + 16 lane .. +15),
+// through a buffer resource over the K floats: entries past K clamp to 0
+// without a branch.
+__device__ __forceinline__ void load_x16_rsrc(__amdgpu_buffer_rsrc_t xrs, uint32_t c, int lane, float (&xr)[16]) {
+    const int off = (int)((c * kChunkCodes + (uint32_t)lane * 16u) * 4u);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off + 16 * q, 0, 0);
+        xr[4 * q + 0] = __uint_as_float(v.x);
+        xr[4 * q + 1] = __uint_as_float(v.y);
+        xr[4 * q + 2] = __uint_as_float(v.z);
+        xr[4 * q + 3] = __uint_as_float(v.w);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M = 1.  One block of R rows per workgroup; WAVES waves split each row's
+// chunks (chunk c -> wave c % WAVES, slot c / WAVES).
+//
+// Every load is a raw-buffer dwordx4 whose resource spans exactly the data it
+// may touch (the block's rows; the K-float vector).  gfx950 clamps buffer
+// loads per dword against the resource size (offset = VGPR + SGPR part), so
+// rows past N, words past the matrix end and vector entries past K read as 0
+// with no branch: the only control flow left is wave-uniform.  That matters
+// for speed as much as for safety: a per-lane tail branch makes the compiler
+// join two load sequences of different length, and at the join it waits for
+// every outstanding load (vmcnt(0)), i.e. for the whole block, before the
+// first FMA.  Words past W inside a row's last chunk belong to the next row
+// (or clamp to 0); their vector entries are past K, hence 0, so they add
+// q * 0 = 0.
+//
+// Issue order: the vector slice first (its first touch per XCD misses L2 and
+// must not queue behind the weight flood), then all R weight loads of the
+// block, row offset r * 4W in an SGPR, non-temporal (streamed once).
+// CPW > 0: the vector slices of CPW chunk slots are loaded once into VGPRs.
+// CPW == 0: any K; one slot at a time with its vector slice.
+template <int WAVES, int CPW, int R>
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W) {
+    constexpr int SHIFT = 6 - ilog2(R);
+    constexpr int XS = CPW > 0 ? CPW : 1;
+    const int lane = (int)(threadIdx.x & 63u);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t C = (W + kChunkWords - 1) / kChunkWords;
+    const uint32_t row0 = blockIdx.x * (uint32_t)R;
+    const uint32_t rows = min((uint32_t)R, N - row0);  // >= 1
+    const uint32_t rowbytes = W * 4u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)row0 * W, rows * rowbytes);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, K * 4u);
+
+    float xr[XS][16];
+    if constexpr (CPW > 0) {
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) load_x16_rsrc(xrs, wave + (uint32_t)j * WAVES, lane, xr[j]);
+    }
+    // Keep the issue order as written: the scheduler would otherwise trickle
+    // the weight loads in between FMAs to save VGPRs, throttling the bytes in
+    // flight when the whole block should be requested at once.
+    __builtin_amdgcn_sched_barrier(0);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+    const int slots = CPW > 0 ? CPW : (int)((C + WAVES - 1) / WAVES);
+#pragma unroll
+    for (int j = 0; j < slots; ++j) {
+        const uint32_t c = wave + (uint32_t)j * WAVES;
+        if (CPW != 1 && c >= C) break;  // wave-uniform; with CPW == 1 every wave owns a chunk
+        const int voff = (int)(c * kChunkWords * 4u + (uint32_t)lane * 16u);
+        u32x4v v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = load_nt_b128(wrs, voff, (int)(r * rowbytes));
+        __builtin_amdgcn_sched_barrier(0);
+        float xl[16];
+        if constexpr (CPW > 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xl[i] = xr[j][i];
+        } else {
+            load_x16_rsrc(xrs, c, lane, xl);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float a = acc[r];
+            a = fma_word(v[r].x, xl[0], xl[1], xl[2], xl[3], a);
+            a = fma_word(v[r].y, xl[4], xl[5], xl[6], xl[7], a);
+            a = fma_word(v[r].z, xl[8], xl[9], xl[10], xl[11], a);
+            a = fma_word(v[r].w, xl[12], xl[13], xl[14], xl[15], a);
+            acc[r] = a;
+        }
+    }
+
+    wave_reduce_rows<R>(acc, lane);
+    const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
+    const uint32_t rr = (uint32_t)lane >> SHIFT;
+    if constexpr (WAVES == 1) {
+        if (leader && rr < rows) y[row0 + rr] = acc[0] * scale[row0 + rr];
+    } else {
+        __shared__ float part[WAVES][R];
+        if (leader) part[wave][rr] = acc[0];
+        __syncthreads();
+        if (threadIdx.x < rows) {
+            float s = part[0][threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) s += part[w][threadIdx.x];
+            y[row0 + threadIdx.x] = s * scale[row0 + threadIdx.x];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Small-M batched: MT vectors per pass.  Lane l owns 4 codes (one word) per
+// 64-word chunk; the MT x 4 vector values of each owned word sit in VGPRs.
+// Each wave takes chunks c = wave, wave + WAVES, ... (CPW of them).
+template <int WAVES, int CPW, int R, int MT>
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_mb_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M, uint32_t nblocks) {
+    constexpr uint32_t CW = 64;  // words per chunk: one dword per lane
+    constexpr int SHIFT = 6 - ilog2(R * MT);
+    static_assert(R * MT <= 64, "R * MT values per lane are reduced across the wave");
+    const int lane = (int)(threadIdx.x & 63u);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t C = (W + CW - 1) / CW;
+    const uint32_t m0 = blockIdx.y * (uint32_t)MT;
+
+    float xr[CPW][4][MT];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        const uint32_t c = wave + (uint32_t)j * WAVES;
+        const uint32_t k0 = (c * CW + (uint32_t)lane) * 4u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const uint32_t k = k0 + (uint32_t)e;
+                const uint32_t mm = m0 + (uint32_t)m;
+                xr[j][e][m] = (c < C && k < K && mm < M) ? x[(size_t)mm * K + k] : 0.0f;
+            }
+    }
+
+    __shared__ float part[2][WAVES][R * MT];
+    uint32_t it = 0;
+    for (uint32_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x, ++it) {
+        const uint32_t r0 = blk * (uint32_t)R;
+        float acc[R * MT];
+#pragma unroll
+        for (int i = 0; i < R * MT; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) {
+            const uint32_t c = wave + (uint32_t)j * WAVES;
+            if (c >= C) break;
+            const uint32_t w = c * CW + (uint32_t)lane;
+            uint32_t v[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t row = r0 + (uint32_t)r;
+                v[r] = (row < N && w < W) ? weight[(size_t)row * W + w] : 0u;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float q0 = (float)(int8_t)(v[r]);
+                const float q1 = (float)(int8_t)(v[r] >> 8);
+                const float q2 = (float)(int8_t)(v[r] >> 16);
+                const float q3 = (float)((int32_t)v[r] >> 24);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float a = acc[r * MT + m];
+                    a = __builtin_fmaf(q0, xr[j][0][m], a);
+                    a = __builtin_fmaf(q1, xr[j][1][m], a);
+                    a = __builtin_fmaf(q2, xr[j][2][m], a);
+                    a = __builtin_fmaf(q3, xr[j][3][m], a);
+                    acc[r * MT + m] = a;
+                }
+            }
+        }
+        wave_reduce_rows<R * MT>(acc, lane);
+        const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
+        const uint32_t idx = (uint32_t)lane >> SHIFT;  // = r * MT + m
+        if constexpr (WAVES == 1) {
+            const uint32_t row = r0 + idx / MT, mm = m0 + idx % MT;
+            if (leader && row < N && mm < M) y[(size_t)mm * N + row] = acc[0] * scale[row];
+        } else {
+            if (leader) part[it & 1][wave][idx] = acc[0];
+            __syncthreads();
+            if (threadIdx.x < (unsigned)(R * MT)) {
+                const uint32_t row = r0 + threadIdx.x / MT, mm = m0 + threadIdx.x % MT;
+                if (row < N && mm < M) {
+                    float s = part[it & 1][0][threadIdx.x];
+#pragma unroll
+                    for (int w2 = 1; w2 < WAVES; ++w2) s += part[it & 1][w2][threadIdx.x];
+                    y[(size_t)mm * N + row] = s * scale[row];
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side dispatch.
+
+namespace {
+
+uint32_t grid_for(uint32_t nblocks, uint32_t max_groups) {
+    if (nblocks <= max_groups) return nblocks;
+    // Equal block counts per workgroup: every workgroup runs the same number
+    // of iterations, so none is left streaming alone at the end.
+    const uint32_t iters = (nblocks + max_groups - 1) / max_groups;
+    return (nblocks + iters - 1) / iters;
+}
+
+template <int WAVES, int CPW, int R>
+hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** variant) {
+    const uint32_t nblocks = (a.N + R - 1) / R;
+    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R>), dim3(nblocks), dim3(WAVES * 64), 0, stream, a.weight,
+                       a.scale, a.vector, a.output, a.N, a.K, a.W);
+    if (variant) *variant = CPW > 0 ? "m1.xreg" : "m1.xstream";
+    return hipGetLastError();
+}
+
+// Rows per workgroup: the largest R whose grid still gives every CU at least
+// two workgroups (fewer, fatter blocks amortise the per-workgroup vector
+// fetch; too few leave CUs idle).
+template <int WAVES, int CPW, int RMAX>
+hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    const uint32_t want = 2u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    if constexpr (RMAX >= 16) {
+        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16>(a, stream, variant);
+    }
+    if constexpr (RMAX >= 8) {
+        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8>(a, stream, variant);
+    }
+    if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4>(a, stream, variant);
+    return launch_m1<WAVES, CPW, 2>(a, stream, variant);
+}
+
+template <int WAVES, int CPW, int R, int MT>
+hipError_t launch_mb(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    const uint32_t nblocks = (a.N + R - 1) / R;
+    const uint32_t mtiles = (a.M + MT - 1) / MT;
+    const uint32_t max_groups = (uint32_t)dev.cu_count * (uint32_t)(8 / WAVES > 0 ? 8 / WAVES : 1);
+    const uint32_t grid = grid_for(nblocks, max_groups);
+    hipLaunchKernelGGL((matvec_q8_mb_kernel<WAVES, CPW, R, MT>), dim3(grid, mtiles), dim3(WAVES * 64), 0,
+                       stream, a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, nblocks);
+    if (variant) *variant = "mb.xreg";
+    return hipGetLastError();
+}
+
+template <int MT, int CPW>
+hipError_t dispatch_mb(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    // 64-word chunks (one dword per lane), split over up to 4 waves x CPW slots.
+    constexpr int R = (64 / MT) < 16 ? 64 / MT : 16;
+    const uint32_t C = (a.W + 63) / 64;
+    if constexpr (CPW == 1) {
+        if (C <= 1) return launch_mb<1, 1, R, MT>(a, dev, stream, variant);
+        if (C <= 2) return launch_mb<2, 1, R, MT>(a, dev, stream, variant);
+        return launch_mb<4, 1, R, MT>(a, dev, stream, variant);
+    } else {
+        return launch_mb<4, CPW, R, MT>(a, dev, stream, variant);
+    }
+}
+
+// Vector-tile width for batched calls: the tile's vector slices take
+// 4 * MT * CPW VGPRs per lane, kept at <= 64 (MT * CPW <= 16).
+template <int CPW>
+hipError_t dispatch_mb_tile(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream,
+                            const char** variant) {
+    constexpr int MT_MAX = 16 / CPW;
+    if (a.M <= 2 || MT_MAX <= 2) return dispatch_mb<2, CPW>(a, dev, stream, variant);
+    if constexpr (MT_MAX >= 4) {
+        if (a.M <= 4 || MT_MAX <= 4) return dispatch_mb<4, CPW>(a, dev, stream, variant);
+    }
+    if constexpr (MT_MAX >= 8) {
+        if (a.M <= 8 || MT_MAX <= 8) return dispatch_mb<8, CPW>(a, dev, stream, variant);
+    }
+    if constexpr (MT_MAX >= 16) return dispatch_mb<16, CPW>(a, dev, stream, variant);
+    return hipErrorNotSupported;
+}
+
+}  // namespace
+
+hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream,
+                            const char** variant) {
+    if (a.N == 0 || a.M == 0) return hipSuccess;
+    if (a.K == 0) {
+        // No terms: y = 0 * s (NaN for a non-finite scale), as the reference.
+        return launch_fill_scaled_zero(a.scale, a.output, a.N, a.M, stream);
+    }
+    if (a.M == 1) {
+        const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
+        if (C == 1) return dispatch_m1_rows<1, 1, 16>(a, dev, stream, variant);
+        if (C == 2) return dispatch_m1_rows<2, 1, 16>(a, dev, stream, variant);
+        if (C == 3) return dispatch_m1_rows<3, 1, 16>(a, dev, stream, variant);
+        if (C == 4) return dispatch_m1_rows<4, 1, 16>(a, dev, stream, variant);
+        if (C <= 8) return dispatch_m1_rows<4, 2, 8>(a, dev, stream, variant);
+        if (C <= 16) return dispatch_m1_rows<4, 4, 4>(a, dev, stream, variant);
+        return dispatch_m1_rows<4, 0, 4>(a, dev, stream, variant);
+    }
+    // Batched: vectors in tiles of up to 16 (blockIdx.y), each tile reading
+    // the weight once; K up to 32 x 256 codes keeps the tile's vector slices
+    // in VGPRs, larger K falls back to M independent single-vector passes.
+    const uint32_t C = (a.W + 63) / 64;
+    if (C <= 4) return dispatch_mb_tile<1>(a, dev, stream, variant);
+    if (C <= 8) return dispatch_mb_tile<2>(a, dev, stream, variant);
+    if (C <= 16) return dispatch_mb_tile<4>(a, dev, stream, variant);
+    if (C <= 32) return dispatch_mb_tile<8>(a, dev, stream, variant);
+    for (uint32_t m = 0; m < a.M; ++m) {
+        MatvecArgs one = a;
+        one.vector = a.vector + (size_t)m * a.K;
+        one.output = a.output + (size_t)m * a.N;
+        one.M = 1;
+        hipError_t e = launch_matvec_q8(one, dev, stream, variant);
+        if (e != hipSuccess) return e;
+    }
+    if (variant) *variant = "mb.loop_m1";
+    return hipSuccess;
+}
+
+__global__ void fill_scaled_zero_kernel(const float* __restrict__ scale, float* __restrict__ y, uint32_t N,
+                                        uint32_t M) {
+    const size_t total = (size_t)N * M;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = 0.0f * scale[i % N];
+}
+
+hipError_t launch_fill_scaled_zero(const float* scale, float* y, uint32_t N, uint32_t M, hipStream_t stream) {
+    const size_t total = (size_t)N * M;
+    const uint32_t grid = (uint32_t)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+    hipLaunchKernelGGL(fill_scaled_zero_kernel, dim3(grid), dim3(256), 0, stream, scale, y, N, M);
+    return hipGetLastError();
+}
+
+}  // namespace wxo

@@ -1,0 +1,414 @@
+// wxo_api.hip -- the C ABI (include/wxo_q8.h) over the gfx950 kernels.
+//
+// Status codes instead of exceptions; a per-thread message for the last
+// failure; sizes validated before any launch (the reference reads `undefined`
+// -> NaN on short inputs, this layer refuses them).  Device entry points are
+// asynchronous on the caller's stream and allocate nothing.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "../../include/wxo_q8.h"
+#include "kernels.hpp"
+
+#ifndef WXO_BUILD_ID
+#define WXO_BUILD_ID "dev"
+#endif
+
+namespace {
+
+thread_local char g_error[512] = {0};
+
+int fail(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int ok() {
+    g_error[0] = '\0';
+    return WXO_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return fail(WXO_ERR_OOM, "%s: %s", what, hipGetErrorString(e));
+    if (e == hipErrorNoDevice || e == hipErrorInsufficientDriver)
+        return fail(WXO_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));
+    return fail(WXO_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+wxo::DeviceInfo g_dev[kMaxDevices];
+std::mutex g_dev_mu;
+char g_describe[1024] = {0};
+
+// Device info for the current HIP device, probed once per device.
+int current_device(const wxo::DeviceInfo** out) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail(WXO_ERR_NO_DEVICE, "no HIP device visible (hipGetDeviceCount: %s); the matvecQ8 path has no CPU "
+                                       "fallback", e != hipSuccess ? hipGetErrorString(e) : "0 devices");
+    int ordinal = 0;
+    if ((e = hipGetDevice(&ordinal)) != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (ordinal < 0 || ordinal >= kMaxDevices) return fail(WXO_ERR_NO_DEVICE, "device ordinal %d out of range", ordinal);
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    wxo::DeviceInfo& d = g_dev[ordinal];
+    if (d.ordinal != ordinal) {
+        hipDeviceProp_t prop;
+        if ((e = hipGetDeviceProperties(&prop, ordinal)) != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            return fail(WXO_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 (MI355X) only", ordinal,
+                        prop.gcnArchName);
+        d.cu_count = prop.multiProcessorCount;
+        d.hbm_bytes = prop.totalGlobalMem;
+        snprintf(d.name, sizeof d.name, "%s", prop.name);
+        snprintf(d.arch, sizeof d.arch, "%s", prop.gcnArchName);
+        d.ordinal = ordinal;
+    }
+    *out = &d;
+    return WXO_OK;
+}
+
+constexpr uint64_t kMaxElems = 1ull << 40;
+
+bool too_big(uint64_t a, uint64_t b) { return a != 0 && b > kMaxElems / a; }
+
+int check_ptr(const void* p, uint64_t elems, const char* name) {
+    if (elems > 0 && p == nullptr) return fail(WXO_ERR_INVALID, "%s is NULL but %llu elements are needed", name,
+                                               (unsigned long long)elems);
+    return WXO_OK;
+}
+
+#define WXO_TRY(expr)              \
+    do {                           \
+        int _s = (expr);           \
+        if (_s != WXO_OK) return _s; \
+    } while (0)
+
+int validate_matvec(const uint32_t* w, const float* s, const float* x, const float* y, uint32_t N, uint32_t K,
+                    uint32_t M) {
+    if (M == 0) return fail(WXO_ERR_INVALID, "M (vectors) must be >= 1, got 0");
+    // Kernels address a block of rows and the vector with 32-bit buffer offsets.
+    if (K >= (1u << 27)) return fail(WXO_ERR_INVALID, "K=%u exceeds the supported maximum 2^27 - 1", K);
+    const uint64_t W = ((uint64_t)K + 3) / 4;
+    if (too_big(N, W) || too_big(M, K) || too_big(M, N))
+        return fail(WXO_ERR_INVALID, "sizes N=%u K=%u M=%u exceed 2^40 elements", N, K, M);
+    WXO_TRY(check_ptr(w, (uint64_t)N * W, "weight"));
+    WXO_TRY(check_ptr(s, N, "scale"));
+    WXO_TRY(check_ptr(x, (uint64_t)M * K, "vector"));
+    WXO_TRY(check_ptr(y, (uint64_t)M * N, "output"));
+    return WXO_OK;
+}
+
+int validate_rows(const void* in, uint32_t N, uint32_t K, const char* in_name) {
+    if (too_big(N, K)) return fail(WXO_ERR_INVALID, "sizes N=%u K=%u exceed 2^40 elements", N, K);
+    return check_ptr(in, (uint64_t)N * K, in_name);
+}
+
+hipStream_t as_hip(wxo_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// RAII device buffer for the *_host entry points.
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t bytes) {
+        if (bytes == 0) return WXO_OK;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            p = nullptr;
+            return hip_fail(e, "hipMalloc");
+        }
+        return WXO_OK;
+    }
+    int upload(const void* src, size_t bytes) {
+        if (bytes == 0) return WXO_OK;
+        hipError_t e = hipMemcpy(p, src, bytes, hipMemcpyHostToDevice);
+        return e == hipSuccess ? WXO_OK : hip_fail(e, "hipMemcpy H2D");
+    }
+    int download(void* dst, size_t bytes) const {
+        if (bytes == 0) return WXO_OK;
+        hipError_t e = hipMemcpy(dst, p, bytes, hipMemcpyDeviceToHost);
+        return e == hipSuccess ? WXO_OK : hip_fail(e, "hipMemcpy D2H");
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int wxo_abi_version(void) { return WXO_ABI_VERSION; }
+
+const char* wxo_last_error(void) { return g_error; }
+
+int wxo_init(void) {
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    return ok();
+}
+
+const char* wxo_describe(void) {
+    const wxo::DeviceInfo* d = nullptr;
+    if (current_device(&d) != WXO_OK) {
+        snprintf(g_describe, sizeof g_describe, "wxo_q8 abi=%d build=%s device=none (%s)", WXO_ABI_VERSION,
+                 WXO_BUILD_ID, g_error);
+        return g_describe;
+    }
+    snprintf(g_describe, sizeof g_describe,
+             "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(xreg|"
+             "xstream),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,pack_int8_rows",
+             WXO_ABI_VERSION, WXO_BUILD_ID, d->ordinal, d->name, d->arch, d->cu_count,
+             (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0));
+    return g_describe;
+}
+
+int wxo_device_count(int* count) {
+    if (!count) return fail(WXO_ERR_INVALID, "count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        *count = 0;
+        if (e == hipErrorNoDevice) return ok();
+        return hip_fail(e, "hipGetDeviceCount");
+    }
+    *count = n;
+    return ok();
+}
+
+int wxo_set_device(int ordinal) {
+    hipError_t e = hipSetDevice(ordinal);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return wxo_init();
+}
+
+int wxo_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(WXO_ERR_INVALID, "ptr is NULL");
+    *ptr = nullptr;
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    if (bytes == 0) return ok();
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        return hip_fail(e, "hipMalloc");
+    }
+    return ok();
+}
+
+int wxo_free(void* ptr) {
+    if (!ptr) return ok();
+    hipError_t e = hipFree(ptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "hipFree");
+}
+
+static int copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, wxo_stream_t stream, const char* what) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(WXO_ERR_INVALID, "%s: NULL pointer", what);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, as_hip(stream));
+    if (e == hipSuccess && kind != hipMemcpyDeviceToDevice) e = hipStreamSynchronize(as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, what);
+}
+
+int wxo_memcpy_htod(void* dst, const void* src, size_t bytes, wxo_stream_t stream) {
+    return copy(dst, src, bytes, hipMemcpyHostToDevice, stream, "memcpy H2D");
+}
+int wxo_memcpy_dtoh(void* dst, const void* src, size_t bytes, wxo_stream_t stream) {
+    return copy(dst, src, bytes, hipMemcpyDeviceToHost, stream, "memcpy D2H");
+}
+int wxo_memcpy_dtod(void* dst, const void* src, size_t bytes, wxo_stream_t stream) {
+    return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream, "memcpy D2D");
+}
+
+int wxo_synchronize(void) {
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? ok() : hip_fail(e, "hipDeviceSynchronize");
+}
+
+int wxo_stream_create(wxo_stream_t* stream) {
+    if (!stream) return fail(WXO_ERR_INVALID, "stream is NULL");
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);  // default priority
+    if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+    *stream = reinterpret_cast<wxo_stream_t>(s);
+    return ok();
+}
+
+int wxo_stream_destroy(wxo_stream_t stream) {
+    if (!stream) return ok();
+    hipError_t e = hipStreamDestroy(as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipStreamDestroy");
+}
+
+int wxo_stream_synchronize(wxo_stream_t stream) {
+    hipError_t e = hipStreamSynchronize(as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipStreamSynchronize");
+}
+
+int wxo_event_create(wxo_event_t* event) {
+    if (!event) return fail(WXO_ERR_INVALID, "event is NULL");
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+    *event = reinterpret_cast<wxo_event_t>(ev);
+    return ok();
+}
+
+int wxo_event_destroy(wxo_event_t event) {
+    if (!event) return ok();
+    hipError_t e = hipEventDestroy(reinterpret_cast<hipEvent_t>(event));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipEventDestroy");
+}
+
+int wxo_event_record(wxo_event_t event, wxo_stream_t stream) {
+    hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipEventRecord");
+}
+
+int wxo_event_synchronize(wxo_event_t event) {
+    hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(event));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipEventSynchronize");
+}
+
+int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop) {
+    if (!ms) return fail(WXO_ERR_INVALID, "ms is NULL");
+    hipError_t e = hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipEventElapsedTime");
+}
+
+// ---- ops on device pointers ------------------------------------------------
+
+int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output, uint32_t N,
+                  uint32_t K, uint32_t M, wxo_stream_t stream) {
+    WXO_TRY(validate_matvec(weight, scale, vector, output, N, K, M));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    wxo::MatvecArgs a{weight, scale, vector, output, N, K, M, (uint32_t)(((uint64_t)K + 3) / 4)};
+    hipError_t e = wxo::launch_matvec_q8(a, *d, as_hip(stream), nullptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8 launch");
+}
+
+int wxo_quantize(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales, wxo_stream_t stream) {
+    WXO_TRY(validate_rows(input, N, D, "input"));
+    WXO_TRY(check_ptr(output, (uint64_t)N * D, "output"));
+    WXO_TRY(check_ptr(scales, N, "scales"));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_quantize_rows(input, N, D, output, nullptr, scales, *d, as_hip(stream), nullptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "quantize launch");
+}
+
+int wxo_pack_q8(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed, wxo_stream_t stream) {
+    WXO_TRY(validate_rows(codes, N, K, "codes"));
+    WXO_TRY(check_ptr(packed, (uint64_t)N * (((uint64_t)K + 3) / 4), "packed"));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_pack_q8(codes, N, K, packed, *d, as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "pack_q8 launch");
+}
+
+int wxo_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed, wxo_stream_t stream) {
+    WXO_TRY(validate_rows(codes, N, K, "codes"));
+    WXO_TRY(check_ptr(packed, (uint64_t)N * (((uint64_t)K + 3) / 4), "packed"));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_pack_int8_rows(codes, N, K, packed, *d, as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "pack_int8_rows launch");
+}
+
+int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* packed, float* scales,
+                         wxo_stream_t stream) {
+    WXO_TRY(validate_rows(input, N, K, "input"));
+    WXO_TRY(check_ptr(packed, (uint64_t)N * (((uint64_t)K + 3) / 4), "packed"));
+    WXO_TRY(check_ptr(scales, N, "scales"));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_quantize_rows(input, N, K, nullptr, packed, scales, *d, as_hip(stream), nullptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "quantize_pack_q8 launch");
+}
+
+// ---- host-array forms ----------------------------------------------------------
+
+int wxo_matvec_q8_host(const uint32_t* weight, const float* scale, const float* vector, float* output, uint32_t N,
+                       uint32_t K, uint32_t M) {
+    WXO_TRY(validate_matvec(weight, scale, vector, output, N, K, M));
+    const size_t W = ((size_t)K + 3) / 4;
+    DevBuf w, s, x, y;
+    WXO_TRY(w.alloc((size_t)N * W * 4));
+    WXO_TRY(s.alloc((size_t)N * 4));
+    WXO_TRY(x.alloc((size_t)M * K * 4));
+    WXO_TRY(y.alloc((size_t)M * N * 4));
+    WXO_TRY(w.upload(weight, (size_t)N * W * 4));
+    WXO_TRY(s.upload(scale, (size_t)N * 4));
+    WXO_TRY(x.upload(vector, (size_t)M * K * 4));
+    WXO_TRY(wxo_matvec_q8((const uint32_t*)w.p, (const float*)s.p, (const float*)x.p, (float*)y.p, N, K, M, nullptr));
+    return y.download(output, (size_t)M * N * 4) == WXO_OK ? ok() : WXO_ERR_DEVICE;
+}
+
+int wxo_quantize_host(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales) {
+    WXO_TRY(validate_rows(input, N, D, "input"));
+    WXO_TRY(check_ptr(output, (uint64_t)N * D, "output"));
+    WXO_TRY(check_ptr(scales, N, "scales"));
+    DevBuf in, out, sc;
+    WXO_TRY(in.alloc((size_t)N * D * 4));
+    WXO_TRY(out.alloc((size_t)N * D * 4));
+    WXO_TRY(sc.alloc((size_t)N * 4));
+    WXO_TRY(in.upload(input, (size_t)N * D * 4));
+    WXO_TRY(wxo_quantize((const float*)in.p, N, D, (int32_t*)out.p, (float*)sc.p, nullptr));
+    WXO_TRY(out.download(output, (size_t)N * D * 4));
+    WXO_TRY(sc.download(scales, (size_t)N * 4));
+    return ok();
+}
+
+int wxo_pack_q8_host(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed) {
+    WXO_TRY(validate_rows(codes, N, K, "codes"));
+    const size_t W = ((size_t)K + 3) / 4;
+    WXO_TRY(check_ptr(packed, (uint64_t)N * W, "packed"));
+    DevBuf c, p;
+    WXO_TRY(c.alloc((size_t)N * K * 4));
+    WXO_TRY(p.alloc((size_t)N * W * 4));
+    WXO_TRY(c.upload(codes, (size_t)N * K * 4));
+    WXO_TRY(wxo_pack_q8((const int32_t*)c.p, N, K, (uint32_t*)p.p, nullptr));
+    WXO_TRY(p.download(packed, (size_t)N * W * 4));
+    return ok();
+}
+
+int wxo_pack_int8_rows_host(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed) {
+    WXO_TRY(validate_rows(codes, N, K, "codes"));
+    const size_t W = ((size_t)K + 3) / 4;
+    WXO_TRY(check_ptr(packed, (uint64_t)N * W, "packed"));
+    DevBuf c, p;
+    WXO_TRY(c.alloc((size_t)N * K));
+    WXO_TRY(p.alloc((size_t)N * W * 4));
+    WXO_TRY(c.upload(codes, (size_t)N * K));
+    WXO_TRY(wxo_pack_int8_rows((const int8_t*)c.p, N, K, (uint32_t*)p.p, nullptr));
+    WXO_TRY(p.download(packed, (size_t)N * W * 4));
+    return ok();
+}
+
+int wxo_quantize_pack_q8_host(const float* input, uint32_t N, uint32_t K, uint32_t* packed, float* scales) {
+    WXO_TRY(validate_rows(input, N, K, "input"));
+    const size_t W = ((size_t)K + 3) / 4;
+    WXO_TRY(check_ptr(packed, (uint64_t)N * W, "packed"));
+    WXO_TRY(check_ptr(scales, N, "scales"));
+    DevBuf in, p, sc;
+    WXO_TRY(in.alloc((size_t)N * K * 4));
+    WXO_TRY(p.alloc((size_t)N * W * 4));
+    WXO_TRY(sc.alloc((size_t)N * 4));
+    WXO_TRY(in.upload(input, (size_t)N * K * 4));
+    WXO_TRY(wxo_quantize_pack_q8((const float*)in.p, N, K, (uint32_t*)p.p, (float*)sc.p, nullptr));
+    WXO_TRY(p.download(packed, (size_t)N * W * 4));
+    WXO_TRY(sc.download(scales, (size_t)N * 4));
+    return ok();
+}
+
+}  // extern "C"
