@@ -1,0 +1,203 @@
+// The TypeScript op API of this package (web-xpu-ops_amd/ops, llm, harness)
+// against the ECMAScript oracle (oracle/q8_oracle.mjs).  Input generators and
+// shapes are the reference's own: ops/matvec/q8.wgsl.test.ts:23-71,
+// ops/quantize/wgsl.test.ts:6-56, ops/matvec/reference.test.ts:14-95,
+// llm/weights-q8.test.ts:17-42.
+import { test, gpuTest, assert, kat, assertBitsEqual, assertMatvecAgrees } from "./harness.mjs";
+import * as matvec from "../../web-xpu-ops_amd/ops/matvec/index.js";
+import * as quantizeOps from "../../web-xpu-ops_amd/ops/quantize/index.js";
+import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
+import { runMatVecQ8 } from "../../web-xpu-ops_amd/llm/kernels.js";
+import { createResidentQ8Device } from "../../web-xpu-ops_amd/harness/resident.js";
+import { native, describe } from "../../web-xpu-ops_amd/native/index.js";
+import * as oracle from "../../oracle/q8_oracle.mjs";
+
+const F = "api.test.mjs";
+
+// ------------------------------------------------------------------ no GPU needed
+
+test(F, "exports the reference's op names", () => {
+  for (const name of ["matvecQ8", "packQ8", "matvecQ8Batched"]) assert.strictEqual(typeof matvec[name], "function", name);
+  for (const name of ["quantize", "quantizePackQ8"]) assert.strictEqual(typeof quantizeOps[name], "function", name);
+  assert.strictEqual(typeof packInt8Rows, "function");
+  assert.strictEqual(typeof runMatVecQ8, "function");
+});
+
+test(F, "the addon loads and exports its whole surface", () => {
+  const a = native();
+  for (const name of ["abiVersion", "describe", "deviceCount", "init", "synchronize", "matvecQ8", "quantize", "packQ8",
+    "packInt8Rows", "quantizePackQ8", "malloc", "free", "upload", "download", "copy", "matvecQ8Device",
+    "quantizeDevice", "packQ8Device", "packInt8RowsDevice", "quantizePackQ8Device"]) {
+    assert.strictEqual(typeof a[name], "function", name);
+  }
+  assert.strictEqual(a.abiVersion(), 1);
+  assert.ok(describe().startsWith("wxo_q8 abi=1"));
+});
+
+test(F, "argument types and lengths are checked before the device is touched", () => {
+  const w = new Uint32Array(2), s = new Float32Array(2), x = new Float32Array(4);
+  assert.throws(() => matvec.matvecQ8({ weight: new Int32Array(2), scale: s, vector: x, N: 2, K: 4 }), TypeError);
+  assert.throws(() => matvec.matvecQ8({ weight: w, scale: new Float64Array(2), vector: x, N: 2, K: 4 }), TypeError);
+  assert.throws(() => matvec.matvecQ8({ weight: new Uint32Array(1), scale: s, vector: x, N: 2, K: 4 }), RangeError);
+  assert.throws(() => matvec.matvecQ8({ weight: w, scale: s, vector: new Float32Array(3), N: 2, K: 4 }), RangeError);
+  assert.throws(() => matvec.matvecQ8({ weight: w, scale: s, vector: x, N: -1, K: 4 }), TypeError);
+  assert.throws(() => matvec.matvecQ8({ weight: w, scale: s, vector: x, N: 1.5, K: 4 }), TypeError);
+  assert.throws(() => quantizeOps.quantize({ input: new Float32Array(5), N: 2, D: 3 }), RangeError);
+  assert.throws(() => matvec.packQ8({ codes: new Uint8Array(4), N: 1, K: 4 }), TypeError);
+  assert.throws(() => packInt8Rows(new Int32Array(4), 1, 4), TypeError);
+});
+
+test(F, "without a gfx950 GPU every op fails loudly (no CPU fallback)", () => {
+  if (native().deviceCount() > 0) return;  // covered by the GPU suite there
+  assert.throws(() => matvec.matvecQ8({ weight: new Uint32Array(2), scale: new Float32Array(2), vector: new Float32Array(4), N: 2, K: 4 }),
+    (e) => e.status === 2 && /no ROCm|no HIP device|no CPU fallback/.test(e.message));
+  assert.throws(() => quantizeOps.quantize({ input: new Float32Array(4), N: 1, D: 4 }), (e) => e.status === 2);
+});
+
+// ------------------------------------------------------------------ GPU
+
+const codeWave = (n, k, phase = 0) => Int32Array.from({ length: n }, (_, i) => Math.round(Math.sin(i * k + phase) * 100));
+const wave = (n, k, phase = 0) => Float32Array.from({ length: n }, (_, i) => Math.sin(i * k + phase) * 1.5);
+const scaleWave = (n) => Float32Array.from({ length: n }, (_, i) => 0.02 * (i + 1) + 0.007);
+
+gpuTest(F, "matvecQ8 KATs (ops/matvec/reference.test.ts:56-95), object and positional forms", () => {
+  for (const c of kat.matvec_q8) {
+    const weight = oracle.packQ8({ codes: Int32Array.from(c.codes), N: c.N, K: c.K });
+    if (c.pad_patch) weight[c.pad_patch.word] |= parseInt(c.pad_patch.or, 16);
+    const scale = Float32Array.from(c.scale);
+    const vector = Float32Array.from(c.vector).subarray(0, c.K);
+    assert.deepStrictEqual(Array.from(matvec.matvecQ8({ weight, scale, vector, N: c.N, K: c.K })), c.want);
+    assert.deepStrictEqual(Array.from(matvec.matvecQ8(vector, weight, scale, c.N, c.K)), c.want);
+  }
+});
+
+gpuTest(F, "matvecQ8 agrees with the reference at the WGSL test's shapes (q8.wgsl.test.ts:48-71)", () => {
+  for (const [N, K] of [[1, 3], [1, 8], [5, 1024], [3, 1030], [7, 1027], [2, 2600]]) {
+    const codes = codeWave(N * K, 0.37);
+    const weight = matvec.packQ8({ codes, N, K });
+    assertBitsEqual(weight, oracle.packQ8({ codes, N, K }), `packQ8 N=${N} K=${K}`);
+    const scale = scaleWave(N);
+    const vector = wave(K, 0.11, 0.8);
+    const args = { weight, scale, vector, N, K };
+    assertMatvecAgrees(matvec.matvecQ8(args), oracle.matvecQ8(args), args, `N=${N} K=${K}`);
+  }
+});
+
+gpuTest(F, "matvecQ8 ignores words and vector entries past the row (q8.wgsl.test.ts:108-149)", () => {
+  const N = 4, K = 1023, W = Math.ceil(K / 4);
+  const codes = Int32Array.from({ length: N * K }, (_, i) => (Math.floor(i / K) % 5) + 1);
+  const packed = oracle.packQ8({ codes, N, K });
+  const weight = Uint32Array.from({ length: N * W + 256 }, (_, i) => (i < N * W ? packed[i] : 0x7f7f7f7f));
+  const vector = Float32Array.from({ length: K + 256 }, (_, i) => (i < K ? 1 : 1000));
+  const scale = scaleWave(N);
+  const want = oracle.matvecQ8({ weight: packed, scale, vector: vector.slice(0, K), N, K });
+  assertMatvecAgrees(matvec.matvecQ8({ weight, scale, vector, N, K }), want, { weight: packed, scale, vector, N, K }, "sentinel");
+});
+
+gpuTest(F, "matvecQ8Batched is M independent matvecQ8 calls", () => {
+  const N = 33, K = 1030, M = 5;
+  const weight = matvec.packQ8({ codes: codeWave(N * K, 0.29), N, K });
+  const scale = scaleWave(N);
+  const vectors = Float32Array.from({ length: M * K }, (_, i) => Math.cos(i * 0.013) * 2);
+  const ys = matvec.matvecQ8Batched({ weight, scale, vectors, N, K, M });
+  for (let m = 0; m < M; m += 1) {
+    const vector = vectors.subarray(m * K, (m + 1) * K);
+    assertMatvecAgrees(ys.subarray(m * N, (m + 1) * N), oracle.matvecQ8({ weight, scale, vector, N, K }),
+      { weight, scale, vector, N, K }, `m=${m}`);
+  }
+});
+
+gpuTest(F, "quantize is bit-exact at the WGSL test's shapes, scales included (ops/quantize/wgsl.test.ts:11-33)", () => {
+  const qwave = (n, k = 0.37) => Float32Array.from({ length: n }, (_, i) => Math.sin(i * k) * 2);
+  for (const [N, D] of [[1, 64], [2, 300]]) {
+    const input = qwave(N * D, 0.41);
+    const got = quantizeOps.quantize({ input, N, D });
+    const want = oracle.quantize({ input, N, D });
+    assertBitsEqual(got.output, want.output, `codes N=${N} D=${D}`);
+    assertBitsEqual(got.scales, want.scales, `scales N=${N} D=${D}`);
+  }
+  const zero = quantizeOps.quantize({ input: new Float32Array(16), N: 1, D: 16 });  // wgsl.test.ts:35-55
+  assertBitsEqual(zero.output, new Int32Array(16), "all-zero codes");
+  assert.strictEqual(zero.scales[0], 1);
+});
+
+gpuTest(F, "quantize KATs (llm/tools/quant_common.py:73-86 rows)", () => {
+  for (const c of kat.quantize) {
+    const input = Float32Array.from(c.input);
+    const got = quantizeOps.quantize({ input, N: 1, D: input.length });
+    assert.deepStrictEqual(Array.from(got.output), c.codes);
+    assert.strictEqual(new Uint32Array(got.scales.buffer)[0], parseInt(c.scale_bits, 16));
+  }
+});
+
+gpuTest(F, "packQ8 / packInt8Rows KATs and equivalence (reference.test.ts:14-53, weights-q8.test.ts:17-42)", () => {
+  for (const c of kat.pack_q8) {
+    const words = matvec.packQ8({ codes: Int32Array.from(c.codes), N: c.N, K: c.K });
+    assert.deepStrictEqual(Array.from(words, (w) => "0x" + w.toString(16).padStart(8, "0")), c.words);
+  }
+  for (const c of kat.pack_int8_rows) {
+    const a = packInt8Rows(Int8Array.from(c.codes), c.N, c.K);
+    const b = matvec.packQ8({ codes: Int32Array.from(c.codes), N: c.N, K: c.K });
+    assertBitsEqual(a, b, "packInt8Rows == packQ8");
+    assertBitsEqual(a, oracle.packQ8({ codes: Int32Array.from(c.codes), N: c.N, K: c.K }), "vs oracle");
+  }
+});
+
+gpuTest(F, "quantize + packQ8 compose as in the reference, and the fused form equals the composition", () => {
+  const N = 96, K = 1027;
+  const input = Float32Array.from({ length: N * K }, (_, i) => Math.sin(i * 0.7) * 0.02 * (1 + (i % 7)));
+  const q = quantizeOps.quantize({ input, N, D: K });
+  const composed = matvec.packQ8({ codes: q.output, N, K });
+  const fused = quantizeOps.quantizePackQ8({ input, N, K });
+  const want = oracle.quantize({ input, N, D: K });
+  assertBitsEqual(composed, oracle.packQ8({ codes: want.output, N, K }), "composed");
+  assertBitsEqual(fused.weight, composed, "fused weight");
+  assertBitsEqual(fused.scale, want.scales, "fused scale");
+  const vector = wave(K, 0.05);
+  const args = { weight: fused.weight, scale: fused.scale, vector, N, K };
+  assertMatvecAgrees(matvec.matvecQ8(args), oracle.matvecQ8(args), args, "pipeline");
+});
+
+gpuTest(F, "runMatVecQ8 keeps llm/kernels.ts's signature (M = rows)", async () => {
+  const N = 70000, K = 64;  // past WebGPU's 65,535-row dispatch limit, one call here
+  const weight = matvec.packQ8({ codes: codeWave(N * K, 0.31), N, K });
+  const scale = scaleWave(N);
+  const vector = wave(K, 0.2);
+  const got = await runMatVecQ8(null, { weight, scale, vector, M: N, K });
+  const args = { weight, scale, vector, N, K };
+  assertMatvecAgrees(got, oracle.matvecQ8(args), args, "runMatVecQ8");
+});
+
+gpuTest(F, "ResidentQ8Device: resident weights, one sync per batch, no allocation in the loop", async () => {
+  const dev = await createResidentQ8Device();
+  assert.ok(dev);
+  const N = 512, K = 2048, W = K / 4;
+  const input = Float32Array.from({ length: N * K }, (_, i) => Math.sin(i * 0.013) * 0.02);
+  const wf = dev.createStorageBuffer(N * K * 4);
+  const packed = dev.createStorageBuffer(N * W * 4);
+  const scales = dev.createStorageBuffer(N * 4);
+  const x = dev.createStorageBuffer(K * 4);
+  const y = dev.createStorageBuffer(N * 4);
+  const y2 = dev.createStorageBuffer(N * 4);
+  dev.upload(wf, 0, input);
+  await dev.batch([{ kind: "quantizePackQ8", input: wf, N, K, packed, scales }]);
+  const created = dev.stats.buffersCreated;
+  const want = oracle.quantize({ input, N, D: K });
+  const wantPacked = oracle.packQ8({ codes: want.output, N, K });
+  for (let step = 0; step < 3; step += 1) {
+    const vector = wave(K, 0.07 * (step + 1));
+    dev.upload(x, 0, vector);
+    const [out, out2, words] = await dev.batch(
+      [{ kind: "matvecQ8", weight: packed, scale: scales, vector: x, output: y, N, K },
+       { kind: "copy", src: y, srcOffset: 0, dst: y2, dstOffset: 0, size: N * 4 }],
+      [{ source: y, sourceOffset: 0, length: N, type: "f32" }, { source: y2, sourceOffset: 0, length: N, type: "f32" },
+       { source: packed, sourceOffset: 0, length: N * W, type: "u32" }]);
+    assertBitsEqual(words, wantPacked, "resident packed weight");
+    const args = { weight: wantPacked, scale: want.scales, vector, N, K };
+    assertMatvecAgrees(out, oracle.matvecQ8(args), args, `step ${step}`);
+    assertBitsEqual(out2, out, "copy");
+  }
+  assert.strictEqual(dev.stats.buffersCreated, created);
+  assert.strictEqual(dev.stats.submits, 4);
+  dev.destroy();
+});

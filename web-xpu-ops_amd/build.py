@@ -80,7 +80,7 @@ def build_addon(verbose: bool = False) -> str | None:
         return None
     cc = shutil.which("gcc") or "cc"
     tmp = ADDON + ".tmp"
-    _run([cc, "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Wextra", "-DNAPI_VERSION=8",
+    _run([cc, "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Wextra", "-DNAPI_VERSION=8", "-DNODE_GYP_MODULE_NAME=wxo_q8",
           "-I", NODE_INCLUDE, "-I", INCLUDE, os.path.join(NAPI, "wxo_napi.c"),
           "-o", tmp, "-L", LIB_DIR, "-lwxo_q8", "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(tmp, ADDON)

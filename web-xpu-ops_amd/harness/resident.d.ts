@@ -1,0 +1,22 @@
+export interface ResidentBuffer {
+  readonly ptr: bigint;
+  readonly size: number;
+}
+export type ResidentQ8Op =
+  | { kind: "matvecQ8"; weight: ResidentBuffer; scale: ResidentBuffer; vector: ResidentBuffer; output: ResidentBuffer; N: number; K: number; M?: number }
+  | { kind: "quantizePackQ8"; input: ResidentBuffer; N: number; K: number; packed: ResidentBuffer; scales: ResidentBuffer }
+  | { kind: "copy"; src: ResidentBuffer; srcOffset: number; dst: ResidentBuffer; dstOffset: number; size: number };
+export interface ResidentQ8Readback {
+  source: ResidentBuffer;
+  sourceOffset: number;
+  length: number;
+  type: "f32" | "i32" | "u32";
+}
+export declare class ResidentQ8Device {
+  readonly stats: { buffersCreated: number; submits: number };
+  createStorageBuffer(bytes: number): ResidentBuffer;
+  upload(buffer: ResidentBuffer, offset: number, data: ArrayBufferView): void;
+  batch(ops: ResidentQ8Op[], readback?: ResidentQ8Readback[]): Promise<(Float32Array | Int32Array | Uint32Array)[]>;
+  destroy(): void;
+}
+export declare function createResidentQ8Device(): Promise<ResidentQ8Device | null>;

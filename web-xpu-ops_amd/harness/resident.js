@@ -1,0 +1,107 @@
+// harness/resident: device-resident buffers and one-sync batches for a decode
+// engine, the MI355X counterpart of the reference's ResidentDevice
+// (harness/resident.ts:98-145, createResidentDevice :148, batch :231-382)
+// restricted to what the matvecQ8 path needs: storage buffers, uploads,
+// matvecQ8 / quantize+packQ8 ops and device copies recorded into one batch,
+// one synchronisation per batch, selective readback.
+//
+// Buffers are HBM allocations (hipMalloc) owned by the device object and freed
+// by destroy(); ops are enqueued in order on the device's stream as batch()
+// walks them, so nothing is allocated inside a decode loop's steady state
+// (`stats.buffersCreated` stays flat, as the reference's test checks).
+import { native } from "../native/index.js";
+
+const TYPED = { f32: Float32Array, i32: Int32Array, u32: Uint32Array };
+
+export class ResidentQ8Device {
+  constructor() {
+    this.addon = native();
+    this.addon.init();
+    this.stats = { buffersCreated: 0, submits: 0 };
+    this.buffers = new Set();
+  }
+
+  /** A device buffer of `bytes` bytes: `{ ptr: bigint, size: number }`. */
+  createStorageBuffer(bytes) {
+    const ptr = this.addon.malloc(bytes);
+    const buffer = { ptr, size: bytes };
+    this.buffers.add(buffer);
+    this.stats.buffersCreated += 1;
+    return buffer;
+  }
+
+  /** Host-to-device copy of `data` into `buffer` at byte `offset` (synchronous). */
+  upload(buffer, offset, data) {
+    if (offset < 0 || offset + data.byteLength > buffer.size) {
+      throw new RangeError(`upload of ${data.byteLength} B at ${offset} overflows a ${buffer.size} B buffer`);
+    }
+    this.addon.upload(buffer.ptr + BigInt(offset), data);
+  }
+
+  /**
+   * Enqueues every op in order, waits once, then reads back only `readback`.
+   * ops: { kind: "matvecQ8", weight, scale, vector, output, N, K, M? }
+   *      { kind: "quantizePackQ8", input, N, K, packed, scales }
+   *      { kind: "copy", src, srcOffset, dst, dstOffset, size }
+   * readback: { source, sourceOffset, length, type: "f32" | "i32" | "u32" }
+   */
+  async batch(ops, readback = []) {
+    const a = this.addon;
+    for (const op of ops) {
+      switch (op.kind) {
+        case "matvecQ8": {
+          const M = op.M === undefined ? 1 : op.M;
+          const W = Math.ceil(op.K / 4);
+          need(op.weight, op.N * W * 4, "weight");
+          need(op.scale, op.N * 4, "scale");
+          need(op.vector, M * op.K * 4, "vector");
+          need(op.output, M * op.N * 4, "output");
+          a.matvecQ8Device(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.output.ptr, op.N, op.K, M);
+          break;
+        }
+        case "quantizePackQ8": {
+          need(op.input, op.N * op.K * 4, "input");
+          need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
+          need(op.scales, op.N * 4, "scales");
+          a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
+          break;
+        }
+        case "copy": {
+          if (op.srcOffset + op.size > op.src.size || op.dstOffset + op.size > op.dst.size) {
+            throw new RangeError("copy range outside its buffers");
+          }
+          a.copy(op.dst.ptr + BigInt(op.dstOffset), op.src.ptr + BigInt(op.srcOffset), op.size);
+          break;
+        }
+        default:
+          throw new TypeError(`unknown resident op kind ${op.kind}`);
+      }
+    }
+    a.synchronize();
+    this.stats.submits += 1;
+    return readback.map((r) => {
+      const T = TYPED[r.type];
+      if (!T) throw new TypeError(`unknown readback type ${r.type}`);
+      if (r.sourceOffset + r.length * 4 > r.source.size) throw new RangeError("readback outside its buffer");
+      return a.download(r.source.ptr + BigInt(r.sourceOffset), new T(r.length));
+    });
+  }
+
+  /** Frees every buffer this device created. */
+  destroy() {
+    for (const b of this.buffers) this.addon.free(b.ptr);
+    this.buffers.clear();
+  }
+}
+
+function need(buffer, bytes, name) {
+  if (!buffer || typeof buffer.ptr !== "bigint") throw new TypeError(`${name} must be a resident buffer`);
+  if (bytes > buffer.size) throw new RangeError(`${name} buffer holds ${buffer.size} B, ${bytes} B needed`);
+}
+
+/** Resolves to null when no gfx950 device is visible (as harness/resident.ts:148 does without an adapter). */
+export async function createResidentQ8Device() {
+  const a = native();
+  if (a.deviceCount() === 0) return null;
+  return new ResidentQ8Device();
+}

@@ -1,0 +1,490 @@
+/*
+ * wxo_napi.c -- Node-API addon over the C ABI in include/wxo_q8.h.
+ *
+ * Plain C against node_api.h (N-API 8, Node >= 12.22), built by
+ * web-xpu-ops_amd/build.py into lib/wxo_q8.node with an $ORIGIN rpath to
+ * lib/libwxo_q8.so.  It is the binding the TypeScript op API
+ * (ops/matvec, ops/quantize, llm/weights-q8, harness/resident in this
+ * package) calls; the reference's own WebGPU binding sits at the same place
+ * (harness/wgsl.ts:77-99 createRunner; harness/resident.ts:148).
+ *
+ * Host-array functions take typed arrays and plain numbers, validate types
+ * and lengths before touching the device, and return fresh typed arrays:
+ *   matvecQ8(weight: Uint32Array, scale: Float32Array, vector: Float32Array,
+ *            N, K, M = 1) -> Float32Array [M*N]
+ *   quantize(input: Float32Array, N, D) -> { output: Int32Array, scales: Float32Array }
+ *   packQ8(codes: Int32Array, N, K) -> Uint32Array
+ *   packInt8Rows(codes: Int8Array, N, K) -> Uint32Array
+ *   quantizePackQ8(input: Float32Array, N, K) -> { weight: Uint32Array, scale: Float32Array }
+ * Device-resident functions take BigInt device addresses (from malloc):
+ *   malloc(bytes) -> bigint, free(ptr), upload(ptr, typedArray),
+ *   download(ptr, typedArray), copy(dst, src, bytes), synchronize(),
+ *   matvecQ8Device(w, s, x, y, N, K, M), quantizeDevice(in, N, D, out, scales),
+ *   packQ8Device(codes, N, K, packed), packInt8RowsDevice(codes, N, K, packed),
+ *   quantizePackQ8Device(in, N, K, packed, scales)
+ * Device functions are stream-ordered on the null stream; synchronize()
+ * (or any download) waits for them.
+ * Errors: a TypeError/RangeError for bad arguments, an Error carrying
+ * wxo_last_error() (and a numeric `status` property) for a failed call.
+ */
+#include <node_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "wxo_q8.h"
+
+#define CHECK_NAPI(env, call)                                              \
+    do {                                                                   \
+        if ((call) != napi_ok) {                                           \
+            napi_throw_error((env), "WXO_NAPI", "internal N-API failure"); \
+            return NULL;                                                   \
+        }                                                                  \
+    } while (0)
+
+static napi_value throw_status(napi_env env, int status, const char* what) {
+    char msg[768];
+    snprintf(msg, sizeof msg, "%s failed (wxo status %d): %s", what, status, wxo_last_error());
+    napi_value text, err, code;
+    napi_create_string_utf8(env, msg, NAPI_AUTO_LENGTH, &text);
+    napi_create_error(env, NULL, text, &err);
+    napi_create_int32(env, status, &code);
+    napi_set_named_property(env, err, "status", code);
+    napi_throw(env, err);
+    return NULL;
+}
+
+static int type_error(napi_env env, const char* fmt, const char* a) {
+    char msg[256];
+    snprintf(msg, sizeof msg, fmt, a);
+    napi_throw_type_error(env, NULL, msg);
+    return 0;
+}
+
+static int range_error(napi_env env, const char* msg) {
+    napi_throw_range_error(env, NULL, msg);
+    return 0;
+}
+
+static int get_args(napi_env env, napi_callback_info info, size_t want_min, size_t* argc, napi_value* argv) {
+    size_t n = *argc;
+    if (napi_get_cb_info(env, info, &n, argv, NULL, NULL) != napi_ok) return type_error(env, "%s", "bad call");
+    if (n < want_min) {
+        char msg[96];
+        snprintf(msg, sizeof msg, "expected at least %zu arguments, got %zu", want_min, n);
+        napi_throw_type_error(env, NULL, msg);
+        return 0;
+    }
+    *argc = n;
+    return 1;
+}
+
+/* A non-negative integer number below 2^32 (what the reference's u32 uniforms hold). */
+static int get_u32(napi_env env, napi_value v, uint32_t* out, const char* name) {
+    napi_valuetype t;
+    if (napi_typeof(env, v, &t) != napi_ok || t != napi_number) return type_error(env, "%s must be a number", name);
+    double d;
+    napi_get_value_double(env, v, &d);
+    if (!(d >= 0.0 && d <= 4294967295.0) || d != (double)(uint64_t)d)
+        return type_error(env, "%s must be an integer in [0, 2^32)", name);
+    *out = (uint32_t)d;
+    return 1;
+}
+
+static const char* typed_name(napi_typedarray_type t) {
+    switch (t) {
+        case napi_int8_array: return "Int8Array";
+        case napi_uint8_array: return "Uint8Array";
+        case napi_int32_array: return "Int32Array";
+        case napi_uint32_array: return "Uint32Array";
+        case napi_float32_array: return "Float32Array";
+        default: return "typed array";
+    }
+}
+
+static int get_typed(napi_env env, napi_value v, napi_typedarray_type want, void** data, size_t* length,
+                     const char* name) {
+    bool is_typed = false;
+    napi_is_typedarray(env, v, &is_typed);
+    if (!is_typed) {
+        char msg[160];
+        snprintf(msg, sizeof msg, "%s must be a %s", name, typed_name(want));
+        napi_throw_type_error(env, NULL, msg);
+        return 0;
+    }
+    napi_typedarray_type t;
+    napi_value ab;
+    size_t off;
+    if (napi_get_typedarray_info(env, v, &t, length, data, &ab, &off) != napi_ok) return type_error(env, "%s", name);
+    if (t != want) {
+        char msg[160];
+        snprintf(msg, sizeof msg, "%s must be a %s, got a %s", name, typed_name(want), typed_name(t));
+        napi_throw_type_error(env, NULL, msg);
+        return 0;
+    }
+    return 1;
+}
+
+static int need_len(napi_env env, size_t have, uint64_t need, const char* name) {
+    if ((uint64_t)have < need) {
+        char msg[200];
+        snprintf(msg, sizeof msg, "%s has %zu elements, %llu needed", name, have, (unsigned long long)need);
+        napi_throw_range_error(env, NULL, msg);
+        return 0;
+    }
+    return 1;
+}
+
+static napi_value new_typed(napi_env env, napi_typedarray_type type, size_t elem, size_t length, void** data) {
+    napi_value ab, arr;
+    if (napi_create_arraybuffer(env, length * elem, data, &ab) != napi_ok) return NULL;
+    if (napi_create_typedarray(env, type, length, ab, 0, &arr) != napi_ok) return NULL;
+    return arr;
+}
+
+static int get_ptr(napi_env env, napi_value v, uint64_t* out, const char* name) {
+    napi_valuetype t;
+    if (napi_typeof(env, v, &t) != napi_ok || t != napi_bigint) return type_error(env, "%s must be a bigint device address", name);
+    bool lossless = false;
+    napi_get_value_bigint_uint64(env, v, out, &lossless);
+    if (!lossless) return type_error(env, "%s is not a 64-bit device address", name);
+    return 1;
+}
+
+static uint64_t words_per_row(uint32_t K) { return ((uint64_t)K + 3) / 4; }
+
+/* ---------------------------------------------------------------- library */
+
+static napi_value js_abi_version(napi_env env, napi_callback_info info) {
+    (void)info;
+    napi_value r;
+    napi_create_int32(env, wxo_abi_version(), &r);
+    return r;
+}
+
+static napi_value js_describe(napi_env env, napi_callback_info info) {
+    (void)info;
+    napi_value r;
+    napi_create_string_utf8(env, wxo_describe(), NAPI_AUTO_LENGTH, &r);
+    return r;
+}
+
+static napi_value js_device_count(napi_env env, napi_callback_info info) {
+    (void)info;
+    int n = 0;
+    int st = wxo_device_count(&n);
+    if (st != WXO_OK) return throw_status(env, st, "deviceCount");
+    napi_value r;
+    napi_create_int32(env, n, &r);
+    return r;
+}
+
+static napi_value js_init(napi_env env, napi_callback_info info) {
+    (void)info;
+    int st = wxo_init();
+    if (st != WXO_OK) return throw_status(env, st, "init");
+    return NULL;
+}
+
+static napi_value js_synchronize(napi_env env, napi_callback_info info) {
+    (void)info;
+    int st = wxo_synchronize();
+    if (st != WXO_OK) return throw_status(env, st, "synchronize");
+    return NULL;
+}
+
+/* ---------------------------------------------------------------- host-array ops */
+
+static napi_value js_matvec_q8(napi_env env, napi_callback_info info) {
+    size_t argc = 6;
+    napi_value argv[6];
+    if (!get_args(env, info, 5, &argc, argv)) return NULL;
+    void *w, *s, *x;
+    size_t lw, ls, lx;
+    uint32_t N, K, M = 1;
+    if (!get_typed(env, argv[0], napi_uint32_array, &w, &lw, "weight") ||
+        !get_typed(env, argv[1], napi_float32_array, &s, &ls, "scale") ||
+        !get_typed(env, argv[2], napi_float32_array, &x, &lx, "vector") || !get_u32(env, argv[3], &N, "N") ||
+        !get_u32(env, argv[4], &K, "K"))
+        return NULL;
+    if (argc > 5) {
+        napi_valuetype t;
+        napi_typeof(env, argv[5], &t);
+        if (t != napi_undefined && !get_u32(env, argv[5], &M, "M")) return NULL;
+    }
+    if (M == 0) {
+        range_error(env, "M must be >= 1");
+        return NULL;
+    }
+    if (!need_len(env, lw, (uint64_t)N * words_per_row(K), "weight") || !need_len(env, ls, N, "scale") ||
+        !need_len(env, lx, (uint64_t)M * K, "vector"))
+        return NULL;
+    void* y;
+    napi_value out = new_typed(env, napi_float32_array, 4, (size_t)M * N, &y);
+    if (!out) return NULL;
+    int st = wxo_matvec_q8_host(w, s, x, y, N, K, M);
+    if (st != WXO_OK) return throw_status(env, st, "matvecQ8");
+    return out;
+}
+
+static napi_value js_quantize(napi_env env, napi_callback_info info) {
+    size_t argc = 3;
+    napi_value argv[3];
+    if (!get_args(env, info, 3, &argc, argv)) return NULL;
+    void* in;
+    size_t lin;
+    uint32_t N, D;
+    if (!get_typed(env, argv[0], napi_float32_array, &in, &lin, "input") || !get_u32(env, argv[1], &N, "N") ||
+        !get_u32(env, argv[2], &D, "D"))
+        return NULL;
+    if (!need_len(env, lin, (uint64_t)N * D, "input")) return NULL;
+    void *codes, *scales;
+    napi_value a = new_typed(env, napi_int32_array, 4, (size_t)N * D, &codes);
+    napi_value b = new_typed(env, napi_float32_array, 4, N, &scales);
+    if (!a || !b) return NULL;
+    int st = wxo_quantize_host(in, N, D, codes, scales);
+    if (st != WXO_OK) return throw_status(env, st, "quantize");
+    napi_value obj;
+    CHECK_NAPI(env, napi_create_object(env, &obj));
+    napi_set_named_property(env, obj, "output", a);
+    napi_set_named_property(env, obj, "scales", b);
+    return obj;
+}
+
+static napi_value pack_common(napi_env env, napi_callback_info info, int int8) {
+    size_t argc = 3;
+    napi_value argv[3];
+    if (!get_args(env, info, 3, &argc, argv)) return NULL;
+    void* codes;
+    size_t lc;
+    uint32_t N, K;
+    if (!get_typed(env, argv[0], int8 ? napi_int8_array : napi_int32_array, &codes, &lc, "codes") ||
+        !get_u32(env, argv[1], &N, "N") || !get_u32(env, argv[2], &K, "K"))
+        return NULL;
+    if (!need_len(env, lc, (uint64_t)N * K, "codes")) return NULL;
+    void* packed;
+    napi_value out = new_typed(env, napi_uint32_array, 4, (size_t)(N * words_per_row(K)), &packed);
+    if (!out) return NULL;
+    int st = int8 ? wxo_pack_int8_rows_host(codes, N, K, packed) : wxo_pack_q8_host(codes, N, K, packed);
+    if (st != WXO_OK) return throw_status(env, st, int8 ? "packInt8Rows" : "packQ8");
+    return out;
+}
+
+static napi_value js_pack_q8(napi_env env, napi_callback_info info) { return pack_common(env, info, 0); }
+static napi_value js_pack_int8_rows(napi_env env, napi_callback_info info) { return pack_common(env, info, 1); }
+
+static napi_value js_quantize_pack_q8(napi_env env, napi_callback_info info) {
+    size_t argc = 3;
+    napi_value argv[3];
+    if (!get_args(env, info, 3, &argc, argv)) return NULL;
+    void* in;
+    size_t lin;
+    uint32_t N, K;
+    if (!get_typed(env, argv[0], napi_float32_array, &in, &lin, "input") || !get_u32(env, argv[1], &N, "N") ||
+        !get_u32(env, argv[2], &K, "K"))
+        return NULL;
+    if (!need_len(env, lin, (uint64_t)N * K, "input")) return NULL;
+    void *packed, *scales;
+    napi_value a = new_typed(env, napi_uint32_array, 4, (size_t)(N * words_per_row(K)), &packed);
+    napi_value b = new_typed(env, napi_float32_array, 4, N, &scales);
+    if (!a || !b) return NULL;
+    int st = wxo_quantize_pack_q8_host(in, N, K, packed, scales);
+    if (st != WXO_OK) return throw_status(env, st, "quantizePackQ8");
+    napi_value obj;
+    CHECK_NAPI(env, napi_create_object(env, &obj));
+    napi_set_named_property(env, obj, "weight", a);
+    napi_set_named_property(env, obj, "scale", b);
+    return obj;
+}
+
+/* ---------------------------------------------------------------- device memory */
+
+static napi_value js_malloc(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    if (!get_args(env, info, 1, &argc, argv)) return NULL;
+    napi_valuetype t;
+    napi_typeof(env, argv[0], &t);
+    double d = -1;
+    if (t == napi_number) napi_get_value_double(env, argv[0], &d);
+    if (!(d >= 0 && d <= 9007199254740991.0) || d != (double)(uint64_t)d) {
+        napi_throw_type_error(env, NULL, "bytes must be a non-negative integer");
+        return NULL;
+    }
+    void* p = NULL;
+    int st = wxo_malloc(&p, (size_t)d);
+    if (st != WXO_OK) return throw_status(env, st, "malloc");
+    napi_value r;
+    napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)p, &r);
+    return r;
+}
+
+static napi_value js_free(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint64_t p;
+    if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &p, "ptr")) return NULL;
+    int st = wxo_free((void*)(uintptr_t)p);
+    if (st != WXO_OK) return throw_status(env, st, "free");
+    return NULL;
+}
+
+static int typed_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
+    bool is_typed = false;
+    napi_is_typedarray(env, v, &is_typed);
+    if (!is_typed) return type_error(env, "%s", "expected a typed array");
+    napi_typedarray_type t;
+    size_t len, off;
+    napi_value ab;
+    napi_get_typedarray_info(env, v, &t, &len, data, &ab, &off);
+    size_t elem = (t == napi_int8_array || t == napi_uint8_array || t == napi_uint8_clamped_array) ? 1
+                  : (t == napi_int16_array || t == napi_uint16_array)                                 ? 2
+                  : (t == napi_float64_array || t == napi_bigint64_array || t == napi_biguint64_array) ? 8
+                                                                                                      : 4;
+    *bytes = len * elem;
+    return 1;
+}
+
+/* upload(ptr, typedArray) / download(ptr, typedArray): whole typed array. */
+static napi_value js_upload(napi_env env, napi_callback_info info) {
+    size_t argc = 2;
+    napi_value argv[2];
+    uint64_t p;
+    void* data;
+    size_t bytes;
+    if (!get_args(env, info, 2, &argc, argv) || !get_ptr(env, argv[0], &p, "ptr") ||
+        !typed_bytes(env, argv[1], &data, &bytes))
+        return NULL;
+    int st = wxo_memcpy_htod((void*)(uintptr_t)p, data, bytes, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "upload");
+    return NULL;
+}
+
+static napi_value js_download(napi_env env, napi_callback_info info) {
+    size_t argc = 2;
+    napi_value argv[2];
+    uint64_t p;
+    void* data;
+    size_t bytes;
+    if (!get_args(env, info, 2, &argc, argv) || !get_ptr(env, argv[0], &p, "ptr") ||
+        !typed_bytes(env, argv[1], &data, &bytes))
+        return NULL;
+    int st = wxo_memcpy_dtoh(data, (const void*)(uintptr_t)p, bytes, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "download");
+    return argv[1];
+}
+
+static napi_value js_copy(napi_env env, napi_callback_info info) {
+    size_t argc = 3;
+    napi_value argv[3];
+    uint64_t dst, src;
+    if (!get_args(env, info, 3, &argc, argv) || !get_ptr(env, argv[0], &dst, "dst") ||
+        !get_ptr(env, argv[1], &src, "src"))
+        return NULL;
+    double d = -1;
+    napi_get_value_double(env, argv[2], &d);
+    if (!(d >= 0) || d != (double)(uint64_t)d) {
+        napi_throw_type_error(env, NULL, "bytes must be a non-negative integer");
+        return NULL;
+    }
+    int st = wxo_memcpy_dtod((void*)(uintptr_t)dst, (const void*)(uintptr_t)src, (size_t)d, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "copy");
+    return NULL;
+}
+
+/* ---------------------------------------------------------------- device-pointer ops */
+
+static napi_value js_matvec_q8_device(napi_env env, napi_callback_info info) {
+    size_t argc = 7;
+    napi_value argv[7];
+    uint64_t w, s, x, y;
+    uint32_t N, K, M = 1;
+    if (!get_args(env, info, 6, &argc, argv) || !get_ptr(env, argv[0], &w, "weight") ||
+        !get_ptr(env, argv[1], &s, "scale") || !get_ptr(env, argv[2], &x, "vector") ||
+        !get_ptr(env, argv[3], &y, "output") || !get_u32(env, argv[4], &N, "N") || !get_u32(env, argv[5], &K, "K"))
+        return NULL;
+    if (argc > 6 && !get_u32(env, argv[6], &M, "M")) return NULL;
+    int st = wxo_matvec_q8((const uint32_t*)(uintptr_t)w, (const float*)(uintptr_t)s, (const float*)(uintptr_t)x,
+                           (float*)(uintptr_t)y, N, K, M, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "matvecQ8Device");
+    return NULL;
+}
+
+static napi_value js_quantize_device(napi_env env, napi_callback_info info) {
+    size_t argc = 5;
+    napi_value argv[5];
+    uint64_t in, out, sc;
+    uint32_t N, D;
+    if (!get_args(env, info, 5, &argc, argv) || !get_ptr(env, argv[0], &in, "input") ||
+        !get_u32(env, argv[1], &N, "N") || !get_u32(env, argv[2], &D, "D") || !get_ptr(env, argv[3], &out, "output") ||
+        !get_ptr(env, argv[4], &sc, "scales"))
+        return NULL;
+    int st = wxo_quantize((const float*)(uintptr_t)in, N, D, (int32_t*)(uintptr_t)out, (float*)(uintptr_t)sc, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "quantizeDevice");
+    return NULL;
+}
+
+static napi_value pack_device_common(napi_env env, napi_callback_info info, int int8) {
+    size_t argc = 4;
+    napi_value argv[4];
+    uint64_t codes, packed;
+    uint32_t N, K;
+    if (!get_args(env, info, 4, &argc, argv) || !get_ptr(env, argv[0], &codes, "codes") ||
+        !get_u32(env, argv[1], &N, "N") || !get_u32(env, argv[2], &K, "K") || !get_ptr(env, argv[3], &packed, "packed"))
+        return NULL;
+    int st = int8 ? wxo_pack_int8_rows((const int8_t*)(uintptr_t)codes, N, K, (uint32_t*)(uintptr_t)packed, NULL)
+                  : wxo_pack_q8((const int32_t*)(uintptr_t)codes, N, K, (uint32_t*)(uintptr_t)packed, NULL);
+    if (st != WXO_OK) return throw_status(env, st, int8 ? "packInt8RowsDevice" : "packQ8Device");
+    return NULL;
+}
+
+static napi_value js_pack_q8_device(napi_env env, napi_callback_info info) { return pack_device_common(env, info, 0); }
+static napi_value js_pack_int8_rows_device(napi_env env, napi_callback_info info) {
+    return pack_device_common(env, info, 1);
+}
+
+static napi_value js_quantize_pack_q8_device(napi_env env, napi_callback_info info) {
+    size_t argc = 5;
+    napi_value argv[5];
+    uint64_t in, packed, sc;
+    uint32_t N, K;
+    if (!get_args(env, info, 5, &argc, argv) || !get_ptr(env, argv[0], &in, "input") ||
+        !get_u32(env, argv[1], &N, "N") || !get_u32(env, argv[2], &K, "K") ||
+        !get_ptr(env, argv[3], &packed, "packed") || !get_ptr(env, argv[4], &sc, "scales"))
+        return NULL;
+    int st = wxo_quantize_pack_q8((const float*)(uintptr_t)in, N, K, (uint32_t*)(uintptr_t)packed,
+                                  (float*)(uintptr_t)sc, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "quantizePackQ8Device");
+    return NULL;
+}
+
+/* ---------------------------------------------------------------- module */
+
+static napi_value init_module(napi_env env, napi_value exports) {
+    napi_property_descriptor props[] = {
+        {"abiVersion", NULL, js_abi_version, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"describe", NULL, js_describe, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"init", NULL, js_init, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8", NULL, js_matvec_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"quantize", NULL, js_quantize, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"packQ8", NULL, js_pack_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"packInt8Rows", NULL, js_pack_int8_rows, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"quantizePackQ8", NULL, js_quantize_pack_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"malloc", NULL, js_malloc, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"free", NULL, js_free, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"upload", NULL, js_upload, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"quantizeDevice", NULL, js_quantize_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"packQ8Device", NULL, js_pack_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"packInt8RowsDevice", NULL, js_pack_int8_rows_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"quantizePackQ8Device", NULL, js_quantize_pack_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+    };
+    if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;
+    return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, init_module)

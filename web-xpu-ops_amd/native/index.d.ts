@@ -1,0 +1,26 @@
+/** Raw Node-API addon surface (see web-xpu-ops_amd/napi/wxo_napi.c). */
+export interface WxoAddon {
+  abiVersion(): number;
+  describe(): string;
+  deviceCount(): number;
+  init(): void;
+  synchronize(): void;
+  matvecQ8(weight: Uint32Array, scale: Float32Array, vector: Float32Array, N: number, K: number, M?: number): Float32Array;
+  quantize(input: Float32Array, N: number, D: number): { output: Int32Array; scales: Float32Array };
+  packQ8(codes: Int32Array, N: number, K: number): Uint32Array;
+  packInt8Rows(codes: Int8Array, N: number, K: number): Uint32Array;
+  quantizePackQ8(input: Float32Array, N: number, K: number): { weight: Uint32Array; scale: Float32Array };
+  malloc(bytes: number): bigint;
+  free(ptr: bigint): void;
+  upload(ptr: bigint, data: ArrayBufferView): void;
+  download<T extends ArrayBufferView>(ptr: bigint, into: T): T;
+  copy(dst: bigint, src: bigint, bytes: number): void;
+  matvecQ8Device(weight: bigint, scale: bigint, vector: bigint, output: bigint, N: number, K: number, M?: number): void;
+  quantizeDevice(input: bigint, N: number, D: number, output: bigint, scales: bigint): void;
+  packQ8Device(codes: bigint, N: number, K: number, packed: bigint): void;
+  packInt8RowsDevice(codes: bigint, N: number, K: number, packed: bigint): void;
+  quantizePackQ8Device(input: bigint, N: number, K: number, packed: bigint, scales: bigint): void;
+}
+export declare const ADDON_PATH: string;
+export declare function native(): WxoAddon;
+export declare function describe(): string;
