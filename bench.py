@@ -42,6 +42,9 @@ import wxo_q8  # noqa: E402
 import wxo_workloads as wl  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+# MI355X FP32 vector peak is 157.3 TFLOP/s with packed (2-wide) FMA; this build
+# compiles with packed FP32 disabled, so one-wide FMA gives half of it.
+PEAK_FP32_FMA_TFLOPS = 157.3 / 2
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "matvec_q8_cfg2_traffic.txt")
 
 
@@ -87,6 +90,129 @@ def cpu_baseline(packed, scales, x, N, K, budget_s):
     }
 
 
+def time_loop(stream, launch, steps, warmup):
+    """Mean us per step over `steps` back-to-back steps (events on the stream)."""
+    for i in range(warmup):
+        launch(i)
+    stream.synchronize()
+    e0, e1 = wxo_q8.Event(), wxo_q8.Event()
+    e0.record(stream)
+    for i in range(steps):
+        launch(i)
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) * 1e3 / steps
+
+
+def run_suite(stream, steps, warmup):
+    """Every BASELINE configuration on one GPU: us/step, algorithmic GB/s and
+    the fraction of the bound that applies (HBM, or for the batched LM head
+    the non-packed FP32 VALU rate when that is lower)."""
+    L = wxo_q8.lib()
+    sp = stream.handle
+    results = []
+    rot_target = 600 * 1024 * 1024  # > 2x the 256 MB Infinity Cache
+
+    def check(st):
+        if st != 0:
+            raise wxo_q8.WxoError(st, L.wxo_last_error().decode())
+
+    def prepare(w_f32, N, K, copies):
+        W = (K + 3) // 4
+        src = wxo_q8.DeviceBuffer.from_array(w_f32, stream)
+        packed = wxo_q8.DeviceBuffer(N * W * 4 * copies)
+        scale = wxo_q8.DeviceBuffer(N * 4)
+        wxo_q8.quantize_pack_q8_device(src, N, K, packed, scale, stream)
+        for i in range(1, copies):
+            check(L.wxo_memcpy_dtod(packed.ptr + i * N * W * 4, packed.ptr, N * W * 4, sp))
+        stream.synchronize()
+        src.free()
+        return packed, scale
+
+    def matvec_case(name, N, K, M, w_f32, x):
+        W = (K + 3) // 4
+        nbytes = wl.matvec_bytes(N, K, M)
+        copies = max(1, -(-rot_target // (N * W * 4)))
+        packed, scale = prepare(w_f32, N, K, copies)
+        vec = wxo_q8.DeviceBuffer.from_array(x, stream)
+        out = wxo_q8.DeviceBuffer(N * M * 4)
+        ptrs = [packed.ptr + i * N * W * 4 for i in range(copies)]
+        us = time_loop(stream, lambda i: check(L.wxo_matvec_q8(ptrs[i % copies], scale.ptr, vec.ptr, out.ptr,
+                                                               N, K, M, sp)), steps, warmup)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        flops = 2.0 * N * K * M
+        tflops = flops / (us * 1e-6) / 1e12
+        hbm_us = nbytes / (PEAK_HBM_GBS * 1e9) * 1e6
+        valu_us = flops / (PEAK_FP32_FMA_TFLOPS * 1e12) * 1e6
+        bound = "hbm" if hbm_us >= valu_us else "valu_fp32"
+        results.append({"case": name, "N": N, "K": K, "M": M, "us": round(us, 3), "GB/s": round(gbs, 1),
+                        "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "TFLOP/s": round(tflops, 2),
+                        "bound": bound, "pct_of_bound": round(100 * max(hbm_us, valu_us) / us, 1),
+                        "weight_copies": copies})
+        log(f"suite {name}: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM  bound={bound}")
+        for b in (packed, scale, vec, out):
+            b.free()
+
+    c1 = wl.make_config("cfg1")
+    matvec_case("cfg1 matvecQ8", c1["N"], c1["K"], 1, c1["w"], c1["x"])
+    c3 = wl.make_config("cfg3")
+    matvec_case("cfg3 matvecQ8 ragged K=4099", c3["N"], c3["K"], 1, c3["w"], c3["x"])
+    c2 = wl.make_config("cfg2")
+    matvec_case("cfg2 matvecQ8", c2["N"], c2["K"], 1, c2["w"], c2["x"])
+    del c1, c2, c3
+
+    # cfg4: one decoder layer's 7 projections back to back on resident weights,
+    # rotating over enough layers' worth of weights to stream from HBM.
+    mats, xh, xf = wl.make_decoder_layer()
+    layer_bytes = sum(wl.matvec_bytes(N, K) for _, N, K, _ in mats)
+    layers = max(1, -(-rot_target // layer_bytes))
+    prepared = [prepare(wf, N, K, layers) for _, N, K, wf in mats]
+    vh = wxo_q8.DeviceBuffer.from_array(xh, stream)
+    vf = wxo_q8.DeviceBuffer.from_array(xf, stream)
+    outb = wxo_q8.DeviceBuffer(5632 * 4)
+
+    def layer_step(i):
+        li = i % layers
+        for (name, N, K, _), (packed, scale) in zip(mats, prepared):
+            W = (K + 3) // 4
+            check(L.wxo_matvec_q8(packed.ptr + li * N * W * 4, scale.ptr, (vf if K == 5632 else vh).ptr, outb.ptr,
+                                  N, K, 1, sp))
+    us = time_loop(stream, layer_step, max(1, steps // 7), max(1, warmup // 7))
+    gbs = layer_bytes / (us * 1e-6) / 1e9
+    results.append({"case": "cfg4 decoder layer: 7 matvecQ8 calls", "bytes": layer_bytes, "us": round(us, 3),
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
+    log(f"suite cfg4 layer: {us:.2f} us/layer  {gbs:.0f} GB/s")
+    for packed, scale in prepared:
+        packed.free()
+        scale.free()
+
+    # cfg4: quantize + packQ8 (fused) of the seven f32 matrices.
+    srcs = [(N, K, wxo_q8.DeviceBuffer.from_array(wf, stream)) for _, N, K, wf in mats]
+    outs = [(wxo_q8.DeviceBuffer(N * ((K + 3) // 4) * 4), wxo_q8.DeviceBuffer(N * 4)) for _, N, K, _ in mats]
+    qbytes = sum(wl.quantize_pack_bytes(N, K) for _, N, K, _ in mats)
+
+    def quant_step(i):
+        for (N, K, src), (packed, scale) in zip(srcs, outs):
+            wxo_q8.quantize_pack_q8_device(src, N, K, packed, scale, stream)
+    us = time_loop(stream, quant_step, max(1, steps // 20), 2)
+    gbs = qbytes / (us * 1e-6) / 1e9
+    results.append({"case": "cfg4 quantize+packQ8 (fused) of the 7 matrices", "bytes": qbytes, "us": round(us, 3),
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
+    log(f"suite cfg4 quantize+pack: {us:.2f} us  {gbs:.0f} GB/s")
+    for (_, _, src), (packed, scale) in zip(srcs, outs):
+        src.free()
+        packed.free()
+        scale.free()
+    del mats, srcs, outs
+
+    # cfg5: vocab head N=151936, K=1024, M in {1, 4, 8, 16}.
+    for M in (1, 4, 8, 16):
+        c5 = wl.make_config("cfg5", M=M)
+        matvec_case(f"cfg5 LM head M={M}", c5["N"], c5["K"], M, c5["w"], c5["x"])
+        del c5
+    return results
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +221,8 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=12, help="distinct weight copies rotated through (HBM, not MALL)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--suite", metavar="PATH", default=None,
+                    help="also measure every BASELINE configuration and write the table (JSON) to PATH")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="after timing, run this many device copies of the packed weight (counter calibration)")
     args = ap.parse_args()
@@ -177,6 +305,11 @@ def main() -> int:
         packed_host = packed0.download(np.uint32, N * W)
         scales_host = scale.download(np.float32, N)
         baseline = cpu_baseline(packed_host, scales_host, c["x"], N, K, args.cpu_budget)
+
+    if args.suite:
+        table = run_suite(stream, args.steps, args.warmup)
+        with open(args.suite, "w") as f:
+            json.dump(table, f, indent=1)
 
     line = {
         "metric": "matvecQ8 achieved HBM GB/s (% of 8 TB/s peak; us/call) at N=11008, K=4096",
