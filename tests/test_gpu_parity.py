@@ -238,6 +238,22 @@ def test_batched_equals_m_calls(M, N, K):
         assert_matvec(ys[m], w, s, xs[m], N, K)
 
 
+@pytest.mark.parametrize("M,K", [(2, 8200), (3, 8200), (2, 13000), (16, 1024), (6, 4096)])
+def test_batched_same_sign_long_k(M, K):
+    # No cancellation: every term is positive, so y equals sum |s q x| and the
+    # bar is relative to y itself; the largest K at which the tile's x parts
+    # still fit in LDS gives the longest matrix-core accumulation chain.
+    rng = np.random.default_rng(K + M)
+    N = 40
+    codes = rng.integers(64, 128, size=(N, K)).astype(np.int32)
+    w = oracle.pack_q8(codes.reshape(-1), N, K)
+    s = rng.uniform(0.5, 1.0, N).astype(np.float32)
+    xs = rng.uniform(1.0, 2.0, (M, K)).astype(np.float32)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
+
+
 @pytest.mark.parametrize("M", [1, 4, 8, 16])
 def test_batched_lm_head(M):
     c = wl.make_config("cfg5", M=M)
