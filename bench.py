@@ -45,6 +45,9 @@ PEAK_HBM_GBS = 8000.0
 # MI355X FP32 vector peak is 157.3 TFLOP/s with packed (2-wide) FMA; this build
 # compiles with packed FP32 disabled, so one-wide FMA gives half of it.
 PEAK_FP32_FMA_TFLOPS = 157.3 / 2
+# Dense bf16 matrix-core peak (the batched path splits x into three bf16 parts
+# and runs 16-wide vector tiles, so it issues 3 x 2 x N x K x 16 flops per tile).
+PEAK_BF16_MFMA_TFLOPS = 2500.0
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "matvec_q8_cfg2_traffic.txt")
 
 
@@ -106,8 +109,9 @@ def time_loop(stream, launch, steps, warmup):
 
 def run_suite(stream, steps, warmup):
     """Every BASELINE configuration on one GPU: us/step, algorithmic GB/s and
-    the fraction of the bound that applies (HBM, or for the batched LM head
-    the non-packed FP32 VALU rate when that is lower)."""
+    the fraction of the bound that applies (HBM, or the compute rate of the
+    path that runs when that is lower: one-wide FP32 FMA for one vector, bf16
+    matrix cores for batched vectors)."""
     L = wxo_q8.lib()
     sp = stream.handle
     results = []
@@ -143,8 +147,13 @@ def run_suite(stream, steps, warmup):
         flops = 2.0 * N * K * M
         tflops = flops / (us * 1e-6) / 1e12
         hbm_us = nbytes / (PEAK_HBM_GBS * 1e9) * 1e6
-        valu_us = flops / (PEAK_FP32_FMA_TFLOPS * 1e12) * 1e6
-        bound = "hbm" if hbm_us >= valu_us else "valu_fp32"
+        if M == 1:  # one FMA per code on the VALU
+            comp_us, comp_name = flops / (PEAK_FP32_FMA_TFLOPS * 1e12) * 1e6, "valu_fp32"
+        else:  # matrix cores: three bf16 products per code, 16 vectors per tile
+            mflops = 3.0 * 2.0 * N * K * 16 * (-(-M // 16))
+            comp_us, comp_name = mflops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6, "mfma_bf16"
+        valu_us = comp_us
+        bound = "hbm" if hbm_us >= comp_us else comp_name
         results.append({"case": name, "N": N, "K": K, "M": M, "us": round(us, 3), "GB/s": round(gbs, 1),
                         "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "TFLOP/s": round(tflops, 2),
                         "bound": bound, "pct_of_bound": round(100 * max(hbm_us, valu_us) / us, 1),

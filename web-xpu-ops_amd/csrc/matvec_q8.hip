@@ -250,29 +250,31 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_mb_kernel(
 // bits; a non-finite x keeps all of itself in h so Inf/NaN propagate as IEEE
 // products do).  Every product q * part is exact in f32; the matrix core sums
 // them in f32.  h-products accumulate in one register set and the (2^-8 and
-// 2^-16 smaller) m, l products in another, so the long chain of roundings
-// sits on the h sum alone.  The h sum is folded into an outer sum every
-// 1024 codes, so its chain is at most 32 accumulations (plus the matrix
-// core's own 32-term sum) and a fold per 1024 codes: about 80 roundings for
-// the largest K that fits, 5e-6 of sum_k |s q x|, inside the 1e-5 bar.
+// 2^-16 smaller) m, l products in another, so the chain of roundings sits on
+// the h sum alone.  The h sum is folded into an outer sum every 1024 codes,
+// so a chain is at most 32 accumulations plus the matrix core's own 32-term
+// sum and a fold per 1024 codes: under 80 roundings for the largest K that
+// fits, 5e-6 of sum_k |s q x|, inside the 1e-5 bar.
 //
 // VALU work is the code conversion only (one v_cvt_f32_i32_sdwa per code,
 // one perm per two codes): 1.5 ops per code whatever M is, against 1 + M on
 // the FMA path.  The x parts for the tile's vectors live in LDS
-// (3 x MC x Kpad bf16) and are read per 32-code block as one ds_read_b128 per
-// part per lane.
+// (3 x MC x Kp bf16, in B-operand order) and are read per 32-code block as one
+// ds_read_b128 per part per lane.
 //
 // Operand layout (probed on gfx950): A lane l holds A[l % 16][8 (l / 16) + e],
 // B lane l holds B[8 (l / 16) + e][l % 16], C lane l holds C[4 (l / 16) + v][l % 16].
-// A lane of group g = l / 16 loads 32 consecutive codes of row l % 16
-// (bytes 32g .. 32g+31 of each 128-code step, so a row's 128-byte line is
-// covered by the four groups); block b of the step uses codes 8b .. 8b+7 of
-// them, and B is read with the same k order.
+// Any permutation of k serves as long as A and B use the same one: a lane of
+// group g = l / 16 loads codes 64u + 16g .. 64u + 16g + 15 of row l % 16 for
+// u = 0..3 of each 256-code step, so one load instruction covers 64
+// contiguous bytes of each of the tile's 16 rows (the four groups side by
+// side); block (u, e) of the step uses codes 8e .. 8e+7 of load u, and B is
+// read with the same k order.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kMfmaLdsBytes = 160u * 1024u;  // gfx950: 160 KB of LDS per CU, all usable by one workgroup
+
 
 __device__ __forceinline__ uint32_t bf16_hi_pair(float a, float b) {
     // high halves of two f32 (exact bf16 of small integers), a in the low half
@@ -288,52 +290,63 @@ __device__ __forceinline__ bf16x8 codes_to_bf16(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
-// Each wave owns groups of T row tiles (16 T rows) and walks the whole K in
-// 128-code steps; (group, step) pairs are flattened into one software
-// pipeline with the next step's loads in flight while the current step
-// computes, so there is no barrier after the prologue.  The workgroup's four
-// waves share the x parts in LDS.
-template <int T>
+// Each workgroup takes a contiguous range of 16-row tiles (ranges differ by
+// at most one tile) and its four waves split that range evenly; a wave walks
+// its tiles T at a time over all of K in 256-code steps, the (tile group,
+// step) pairs forming one software pipeline with D - 1 pairs' loads in
+// flight ahead of the one computing.  No wave waits for another after the
+// prologue.  A finished tile's 16 x 16 block of sums goes through a
+// per-wave LDS slot so each lane stores 16 contiguous bytes of one vector's
+// output.
+constexpr uint32_t kTileSlotFloats = 16u * 17u;  // one 16 x 16 block, rows skewed by a float
+
+template <int T, int D>
 __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
-    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M, uint32_t Kpad) {
-    extern __shared__ uint16_t xparts[];  // [3][MC][Kpad + 8]
+    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M, uint32_t Kp) {
+    // x parts in B-operand order: [part][32-code block][lane group g][column]
+    // x 8 bf16, so the 64 lanes of one B read cover one contiguous run.
+    extern __shared__ __attribute__((aligned(16))) uint16_t xparts[];  // 3 x Kp x MC bf16, then the tile slots
     const uint32_t m0 = blockIdx.y * 16u;
     const uint32_t MC = min(16u, M - m0);
-    const uint32_t kstride = Kpad + 8u;  // bf16 elements per row (+16 B skews LDS banks)
 
-    const int lane = (int)(threadIdx.x & 63u);
-    const uint32_t j = (uint32_t)lane & 15u, g = (uint32_t)lane >> 4;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t jb = min(j, MC - 1u);  // B column (lanes past MC compute columns nobody stores)
+    float* slot = reinterpret_cast<float*>(xparts + 3u * MC * Kp) + wv * kTileSlotFloats;
     const uint32_t rowbytes = W * 4u;
     const uint32_t ntiles = (N + 15u) / 16u;
-    const uint32_t ngroups = (ntiles + T - 1) / T;
-    const uint32_t S = Kpad / 128u;  // steps per group
-    const uint32_t gw = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const uint32_t gstride = gridDim.x * 4u;
-    const uint32_t mygroups = gw < ngroups ? (ngroups - gw + gstride - 1) / gstride : 0u;
-    const uint32_t total = mygroups * S;  // this wave's (group, step) pairs
-    const int voff = (int)(j * rowbytes + g * 32u);
+    const uint32_t S = Kp / 256u;  // steps per tile group
+    // this workgroup's tiles, then this wave's quarter of them
+    const uint32_t b0 = (uint32_t)((uint64_t)blockIdx.x * ntiles / gridDim.x);
+    const uint32_t b1 = (uint32_t)((uint64_t)(blockIdx.x + 1u) * ntiles / gridDim.x);
+    const uint32_t t0 = b0 + (b1 - b0) * wv / 4u, t1 = b0 + (b1 - b0) * (wv + 1u) / 4u;
+    const uint32_t ngroups = (t1 - t0 + T - 1) / T;
+    const uint32_t total = ngroups * S;
+    const int voff = (int)(j * rowbytes + g * 16u);
+    const uint32_t r_lane = (lane & 3u) * 4u;  // epilogue: rows r_lane .. r_lane + 3 of column lane / 4
 
-    // Loads of pair i: group gw + (i / S) * gstride, step i % S.  Past the
-    // wave's last pair the resource is empty and the loads read 0 without
-    // touching memory, so the issue is unconditional (a conditional issue
-    // would make the compiler join load sequences of different length and
-    // wait for all of them).
-    // The group's scales ride with its last step's loads (an epilogue load
-    // would wait, in issue order, for the next step's prefetched weights).
-    auto issue = [&](uint32_t i, u32x4v (&a0)[T], u32x4v (&a1)[T], u32x4v (&sc)[T]) {
-        const uint32_t grp = gw + (i / S) * gstride, step = i % S;
-        const uint32_t row0 = grp * (uint32_t)T * 16u;
-        const uint32_t rows = i < total ? min((uint32_t)T * 16u, N - row0) : 0u;
-        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)(i < total ? row0 : 0u) * W, rows * rowbytes);
-        const __amdgpu_buffer_rsrc_t srs =
-            make_rsrc(scale + (i < total ? row0 : 0u), step == S - 1u ? rows * 4u : 0u);
+    // Loads of pair i: tile group i / S, step i % S.  Past the last pair the
+    // resource is empty and the loads read 0 without touching memory, so the
+    // issue is unconditional (a conditional issue would make the compiler
+    // join load sequences of different length and wait for all of them).
+    // Codes past K in a row belong to the next row (or read 0 past the
+    // group) and meet x parts that are 0.  The group's scales ride with its
+    // last step (an epilogue load would wait, in issue order, for the next
+    // step's prefetched weights).
+    auto issue = [&](uint32_t i, u32x4v (&d)[T][4], u32x4v (&sc)[T]) {
+        const uint32_t step = i % S;
+        const uint32_t tile0 = i < total ? t0 + (i / S) * T : 0u;
+        const uint32_t rows = i < total ? min((uint32_t)T * 16u, min(t1 * 16u, N) - tile0 * 16u) : 0u;
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)tile0 * 16u * W, rows * rowbytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + tile0 * 16u, step == S - 1u ? rows * 4u : 0u);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int so = (int)((uint32_t)t * 16u * rowbytes + step * 128u);
-            a0[t] = load_nt_b128(wrs, voff, so);
-            a1[t] = load_nt_b128(wrs, voff + 16, so);
-            sc[t] = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(((uint32_t)t * 16u + g * 4u) * 4u), 0, 0);
+            const int so = (int)((uint32_t)t * 16u * rowbytes + step * 256u);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) d[t][u] = load_nt_b128(wrs, voff + 64 * u, so);
+            sc[t] = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(((uint32_t)t * 16u + r_lane) * 4u), 0, 0);
         }
     };
 
@@ -341,28 +354,29 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
     // before the first weights: a wait for x then never has to wait for the
     // weight loads queued behind it (vmcnt retires in issue order).
     constexpr int XU = 16;
-    const uint32_t kq = Kpad / 4u;  // float4 groups per vector row
-    const uint32_t n4 = MC * kq;
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, M * K * 4u);
+    const uint32_t kq4 = Kp / 4u;  // float4 groups per staged vector row
+    const uint32_t n4 = MC * kq4;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x + (size_t)m0 * K, MC * K * 4u);
     u32x4v xv[XU];
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
         const uint32_t idx = threadIdx.x + (uint32_t)u * 256u;
-        const uint32_t m = idx / kq, k = (idx - m * kq) * 4u;
+        const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
         // past the staged range: an offset beyond the resource reads 0
-        const int off = idx < n4 ? (int)(((m0 + m) * K + k) * 4u) : (int)0x7ffffff0;
+        const int off = idx < n4 ? (int)((m * K + k) * 4u) : (int)0x7ffffff0;
         xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
     }
 
-    u32x4v a0[T], a1[T], b0[T], b1[T], as[T], bs[T];
-    issue(0u, a0, a1, as);
+    u32x4v buf[D][T][4], sbuf[D][T];
+#pragma unroll
+    for (int q = 0; q < D - 1; ++q) issue((uint32_t)q, buf[q], sbuf[q]);
 
     auto split_store = [&](uint32_t idx, u32x4v v) {
-        const uint32_t m = idx / kq, k = (idx - m * kq) * 4u;
+        const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
         uint16_t hh[4], mm[4], ll[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            // entries past K belong to the next vector (or clamp to 0): zero them
+            // entries past K belong to the next vector (or read 0): zero them
             const float xe = (k + (uint32_t)e < K) ? __uint_as_float(v[e]) : 0.0f;
             const uint32_t hb = __float_as_uint(xe) & 0xffff0000u;
             uint32_t mb = 0u, lb = 0u;
@@ -375,22 +389,25 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
             mm[e] = (uint16_t)(mb >> 16);
             ll[e] = (uint16_t)(lb >> 16);
         }
+        // code k sits in block (k / 256) * 8 + ((k / 64) % 4) * 2 + (k / 8) % 2,
+        // lane group (k / 16) % 4, element k % 8 (the order compute() reads)
+        const uint32_t blk = (k >> 8) * 8u + ((k >> 6) & 3u) * 2u + ((k >> 3) & 1u);
+        const uint32_t at = ((blk * 4u + ((k >> 4) & 3u)) * MC + m) * 8u + (k & 7u);
         typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<u16x4*>(&xparts[(0u * MC + m) * kstride + k]) = u16x4{hh[0], hh[1], hh[2], hh[3]};
-        *reinterpret_cast<u16x4*>(&xparts[(1u * MC + m) * kstride + k]) = u16x4{mm[0], mm[1], mm[2], mm[3]};
-        *reinterpret_cast<u16x4*>(&xparts[(2u * MC + m) * kstride + k]) = u16x4{ll[0], ll[1], ll[2], ll[3]};
+        *reinterpret_cast<u16x4*>(&xparts[at]) = u16x4{hh[0], hh[1], hh[2], hh[3]};
+        *reinterpret_cast<u16x4*>(&xparts[Kp * MC + at]) = u16x4{mm[0], mm[1], mm[2], mm[3]};
+        *reinterpret_cast<u16x4*>(&xparts[2u * Kp * MC + at]) = u16x4{ll[0], ll[1], ll[2], ll[3]};
     };
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
         const uint32_t idx = threadIdx.x + (uint32_t)u * 256u;
         if (idx < n4) split_store(idx, xv[u]);
     }
-    for (uint32_t idx = threadIdx.x + XU * 256u; idx < n4; idx += 256u) {  // only when MC * Kpad > 16384
-        const uint32_t m = idx / kq, k = (idx - m * kq) * 4u;
-        split_store(idx, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(((m0 + m) * K + k) * 4u), 0, 0));
+    for (uint32_t idx = threadIdx.x + XU * 256u; idx < n4; idx += 256u) {  // only when MC * Kp > 16384
+        const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
+        split_store(idx, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((m * K + k) * 4u), 0, 0));
     }
     __syncthreads();
-    const bool bcol = j < MC;
 
     f32x4 hi[T], lo[T], hs[T];
 #pragma unroll
@@ -399,63 +416,67 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
         lo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         hs[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    const uint16_t* xb = &xparts[(g * MC + jb) * 8u];
+    const uint32_t pstride = Kp * MC;
+    const uint32_t bstride = 32u * MC;  // bf16 elements per block
 
-    auto compute = [&](uint32_t i, const u32x4v (&c0)[T], const u32x4v (&c1)[T], const u32x4v (&sc)[T]) {
-        const uint32_t k0 = (i % S) * 128u;
+    auto compute = [&](uint32_t i, const u32x4v (&d)[T][4], const u32x4v (&sc)[T]) {
+        const uint32_t step = i % S;
+        const uint16_t* xs = xb + step * 8u * bstride;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const uint32_t kb = k0 + g * 32u + (uint32_t)b * 8u;
-            bf16x8 bh = {}, bm = {}, bl = {};
-            if (bcol) {
-                bh = *reinterpret_cast<const bf16x8*>(&xparts[(0u * MC + j) * kstride + kb]);
-                bm = *reinterpret_cast<const bf16x8*>(&xparts[(1u * MC + j) * kstride + kb]);
-                bl = *reinterpret_cast<const bf16x8*>(&xparts[(2u * MC + j) * kstride + kb]);
-            }
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const uint32_t w0 = b < 2 ? c0[t][2 * b] : c1[t][2 * b - 4];
-                const uint32_t w1 = b < 2 ? c0[t][2 * b + 1] : c1[t][2 * b - 3];
-                const bf16x8 av = codes_to_bf16(w0, w1);
-                hi[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh, hi[t], 0, 0, 0);
-                lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bm, lo[t], 0, 0, 0);
-                lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl, lo[t], 0, 0, 0);
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t kb = ((uint32_t)u * 2u + (uint32_t)e) * bstride;
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(xs + kb);
+                const bf16x8 bm = *reinterpret_cast<const bf16x8*>(xs + pstride + kb);
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(xs + 2u * pstride + kb);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const bf16x8 av = codes_to_bf16(d[t][u][2 * e], d[t][u][2 * e + 1]);
+                    hi[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh, hi[t], 0, 0, 0);
+                    lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bm, lo[t], 0, 0, 0);
+                    lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl, lo[t], 0, 0, 0);
+                }
             }
-        }
-        if ((i % S) % 8u == 7u) {  // wave-uniform: fold the h chain every 1024 codes
+        if (step % 4u == 3u) {  // wave-uniform: fold the h chain every 1024 codes
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 hs[t] += hi[t];
                 hi[t] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        if (i % S == S - 1u) {  // wave-uniform: the group is complete
-            const uint32_t grp = gw + (i / S) * gstride;
-            const uint32_t row0 = grp * (uint32_t)T * 16u;
-            const uint32_t rows = min((uint32_t)T * 16u, N - row0);
-            if (bcol) {
-#pragma unroll
-                for (int t = 0; t < T; ++t)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const uint32_t rr = (uint32_t)t * 16u + g * 4u + (uint32_t)v;
-                        if (rr < rows)
-                            y[(size_t)(m0 + j) * N + row0 + rr] = ((hs[t][v] + hi[t][v]) + lo[t][v]) * __uint_as_float(sc[t][v]);
-                    }
-            }
+        if (step == S - 1u) {  // wave-uniform: the tile group is complete
+            const uint32_t tile0 = t0 + (i / S) * T;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
+                // C lane (j, g) holds rows 4g .. 4g+3 of column j: transpose
+                // through the slot so a lane stores 4 rows of one column.
+                const f32x4 v = (hs[t] + hi[t]) + lo[t];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) slot[j * 17u + g * 4u + (uint32_t)q] = v[q];
                 hi[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                 lo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                 hs[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const uint32_t c = lane >> 2;
+                const uint32_t row0 = (tile0 + (uint32_t)t) * 16u;
+                if (c < MC && tile0 + (uint32_t)t < t1) {
+                    float* yo = y + (size_t)(m0 + c) * N + row0 + r_lane;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (row0 + r_lane + (uint32_t)q < N)
+                            yo[q] = slot[c * 17u + r_lane + (uint32_t)q] * __uint_as_float(sc[t][q]);
+                }
             }
         }
     };
 
-    for (uint32_t i = 0; i < total; i += 2u) {
-        issue(i + 1u, b0, b1, bs);
-        compute(i, a0, a1, as);
-        issue(i + 2u, a0, a1, as);
-        if (i + 1u < total) compute(i + 1u, b0, b1, bs);
+    for (uint32_t i = 0; i < total; i += (uint32_t)D) {
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            issue(i + (uint32_t)(q + D - 1), buf[(q + D - 1) % D], sbuf[(q + D - 1) % D]);
+            if (q == 0 || i + (uint32_t)q < total) compute(i + (uint32_t)q, buf[q], sbuf[q]);
+        }
     }
 }
 
@@ -559,19 +580,25 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
         if (C <= 16) return dispatch_m1_rows<4, 4, 4>(a, dev, stream, variant);
         return dispatch_m1_rows<4, 0, 4>(a, dev, stream, variant);
     }
-    // Batched on the matrix cores when the tile's x parts fit in LDS.
+    // Batched on the matrix cores when the tile's x parts fit in LDS.  Two
+    // tiles per step share each B read when the tile holds 12 or more
+    // vectors (wider B reads), one tile with a deeper pipeline otherwise.
     {
-        constexpr int T = 4;
-        const uint32_t Kpad = (a.K + 127u) / 128u * 128u;
+        const uint32_t Kp = (a.K + 255u) / 256u * 256u;
         const uint32_t MC = a.M < 16u ? a.M : 16u;
-        const uint64_t lds = 3ull * MC * (Kpad + 8u) * 2u;
+        const uint64_t lds = 3ull * MC * Kp * 2u + 4ull * kTileSlotFloats * 4u;
         if (lds <= kMfmaLdsBytes) {
-            const uint32_t ngroups = ((a.N + 15u) / 16u + T - 1) / T;
-            const uint32_t wgs_per_cu = (uint32_t)(160u * 1024u / lds);
-            const uint32_t cap = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256) * min(wgs_per_cu > 0 ? wgs_per_cu : 1u, 2u);
-            const uint32_t grid = min((ngroups + 3u) / 4u, cap);
-            hipLaunchKernelGGL((matvec_q8_mfma_kernel<T>), dim3(grid, (a.M + 15u) / 16u), dim3(256), (size_t)lds, stream,
-                               a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kpad);
+            const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+            const uint32_t ntiles = (a.N + 15u) / 16u;
+            const uint32_t wgs = (uint32_t)(kMfmaLdsBytes / lds) < 2u ? (uint32_t)(kMfmaLdsBytes / lds) : 2u;
+            const uint32_t grid = min((ntiles + 3u) / 4u, cus * wgs);
+            const dim3 g(grid, (a.M + 15u) / 16u);
+            if (MC >= 12u)
+                hipLaunchKernelGGL((matvec_q8_mfma_kernel<2, 2>), g, dim3(256), (size_t)lds, stream, a.weight, a.scale,
+                                   a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
+            else
+                hipLaunchKernelGGL((matvec_q8_mfma_kernel<1, 3>), g, dim3(256), (size_t)lds, stream, a.weight, a.scale,
+                                   a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
             if (variant) *variant = "mb.mfma";
             return hipGetLastError();
         }
