@@ -12,6 +12,12 @@
  *                             called from llm/kernels.ts:195-211 (runMatVecQ8) and
  *                             llm/engine-q8-resident.ts:1843-1845, :1869
  *                             M > 1: M independent matvecQ8 calls on one weight
+ *   wxo_matvec_q8_residual    ops/matvec/reference.ts:235-243 (matvecQ8Residual) and
+ *                             its WGSL form ops/matvec/wgsl/q8_residual.wgsl, used for
+ *                             o_proj / down_proj at llm/engine-q8-resident.ts:1857, :1866
+ *   wxo_matvec_q8_ffn         ops/matvec/reference.ts:196-207 (matvecQ8Ffn) and
+ *                             ops/matvec/wgsl/q8_ffn.wgsl, the gate/up projection at
+ *                             llm/engine-q8-resident.ts:1863
  *   wxo_quantize              ops/quantize/reference.ts:13-38 (quantize)
  *   wxo_pack_q8               ops/matvec/reference.ts:267-283 (packQ8)
  *   wxo_pack_int8_rows        llm/weights-q8.ts:137-139 (packInt8Rows)
@@ -100,6 +106,21 @@ int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
 int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output,
                   uint32_t N, uint32_t K, uint32_t M, wxo_stream_t stream);
 
+/* matvecQ8Residual: output[n] = residual[n] + (matvecQ8 row n), the sum rounded
+ * to f32 after the scaled dot product is (two roundings, as the reference).
+ * M = 1.  output may be the residual buffer itself. */
+int wxo_matvec_q8_residual(const uint32_t* weight, const float* scale, const float* vector,
+                           const float* residual, float* output, uint32_t N, uint32_t K,
+                           wxo_stream_t stream);
+
+/* matvecQ8Ffn: output[n] = silu(g[n]) * u[n] with g, u the matvecQ8 rows of the
+ * gate and up weights (same shape, same vector); silu(g) = g / (1 + e^-g)
+ * evaluated in f64 and rounded to f32, then one f32 product.  Both weights are
+ * streamed in one pass.  M = 1. */
+int wxo_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
+                      const float* scale_up, const float* vector, float* output, uint32_t N, uint32_t K,
+                      wxo_stream_t stream);
+
 /* Per-row absmax quantization, bit-exact to ops/quantize/reference.ts:13-38:
  * output int32 [N, D] codes in [-127, 127], scales f32 [N]. */
 int wxo_quantize(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales,
@@ -120,6 +141,10 @@ int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* p
 /* ---- the same ops on host arrays (synchronous; copy in, run, copy out) ----- */
 int wxo_matvec_q8_host(const uint32_t* weight, const float* scale, const float* vector, float* output,
                        uint32_t N, uint32_t K, uint32_t M);
+int wxo_matvec_q8_residual_host(const uint32_t* weight, const float* scale, const float* vector,
+                                const float* residual, float* output, uint32_t N, uint32_t K);
+int wxo_matvec_q8_ffn_host(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
+                           const float* scale_up, const float* vector, float* output, uint32_t N, uint32_t K);
 int wxo_quantize_host(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales);
 int wxo_pack_q8_host(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed);
 int wxo_pack_int8_rows_host(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed);

@@ -9,6 +9,9 @@ Functions mirror the reference's TypeScript definitions:
   pack_int8_rows      llm/weights-q8.ts:137-139
   matvec_q8           ops/matvec/reference.ts:113-131
   matvec_q8_batched   M x matvec_q8 (no reference function; defined that way)
+  matvec_q8_residual  ops/matvec/reference.ts:235-243 (matvecQ8Residual)
+  matvec_q8_ffn       ops/matvec/reference.ts:196-207 (matvecQ8Ffn)
+  silu                ops/activation/reference.ts:91-92
   absterm             sum_k |s*q*x| per row in f64 (tolerance base)
 """
 from __future__ import annotations
@@ -47,8 +50,13 @@ def _load():
     lib.q8o_matvec_q8.argtypes = [p, p, p, sz, sz, p]
     lib.q8o_matvec_q8_batched.argtypes = [p, p, p, sz, sz, sz, p]
     lib.q8o_matvec_q8_absterm.argtypes = [p, p, p, sz, sz, p]
+    lib.q8o_matvec_q8_residual.argtypes = [p, p, p, p, sz, sz, p]
+    lib.q8o_matvec_q8_ffn.argtypes = [p, p, p, p, p, sz, sz, p]
+    lib.q8o_silu.argtypes = [ctypes.c_float]
+    lib.q8o_silu.restype = ctypes.c_float
     for name in ("q8o_quantize", "q8o_pack_q8", "q8o_pack_int8_rows", "q8o_matvec_q8",
-                 "q8o_matvec_q8_batched", "q8o_matvec_q8_absterm"):
+                 "q8o_matvec_q8_batched", "q8o_matvec_q8_absterm", "q8o_matvec_q8_residual",
+                 "q8o_matvec_q8_ffn"):
         getattr(lib, name).restype = None
     _lib = lib
     return lib
@@ -111,6 +119,34 @@ def matvec_q8_batched(weight, scale, vectors, N: int, K: int, M: int) -> np.ndar
     return out.reshape(M, N)
 
 
+def matvec_q8_residual(weight, scale, vector, residual, N: int, K: int) -> np.ndarray:
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(vector, dtype=np.float32).reshape(-1)
+    r = np.ascontiguousarray(residual, dtype=np.float32).reshape(-1)
+    assert w.size >= N * words_per_row(K) and s.size >= N and v.size >= K and r.size >= N
+    out = np.empty(N, dtype=np.float32)
+    _load().q8o_matvec_q8_residual(_ptr(w), _ptr(s), _ptr(v), _ptr(r), N, K, _ptr(out))
+    return out
+
+
+def matvec_q8_ffn(weight_gate, scale_gate, weight_up, scale_up, vector, N: int, K: int) -> np.ndarray:
+    wg = np.ascontiguousarray(weight_gate, dtype=np.uint32).reshape(-1)
+    sg = np.ascontiguousarray(scale_gate, dtype=np.float32).reshape(-1)
+    wu = np.ascontiguousarray(weight_up, dtype=np.uint32).reshape(-1)
+    su = np.ascontiguousarray(scale_up, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(vector, dtype=np.float32).reshape(-1)
+    W = words_per_row(K)
+    assert wg.size >= N * W and wu.size >= N * W and sg.size >= N and su.size >= N and v.size >= K
+    out = np.empty(N, dtype=np.float32)
+    _load().q8o_matvec_q8_ffn(_ptr(wg), _ptr(sg), _ptr(wu), _ptr(su), _ptr(v), N, K, _ptr(out))
+    return out
+
+
+def silu(x: float) -> float:
+    return float(_load().q8o_silu(float(x)))
+
+
 def absterm(weight, scale, vector, N: int, K: int) -> np.ndarray:
     w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
     s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
@@ -147,3 +183,59 @@ def check_matvec(got: np.ndarray, want: np.ndarray, bound: np.ndarray) -> tuple[
     worst = idx[int(np.nanargmax(ratio))] if ratio.size else idx[0]
     return False, (f"{idx.size} rows out of tolerance; worst row {worst}: got {got[worst]!r} "
                    f"want {want[worst]!r} |err| {err[worst]:.3e} allowed {allowed[worst]:.3e}")
+
+
+def _ulp32(v: np.ndarray) -> np.ndarray:
+    """Spacing of f32 numbers at |v| (the size of one f32 rounding step)."""
+    a = np.abs(np.asarray(v, dtype=np.float64)).astype(np.float32)
+    return np.spacing(a).astype(np.float64)
+
+
+def _report(got, want, allowed, what: str) -> tuple[bool, str]:
+    got = np.asarray(got, dtype=np.float64).reshape(-1)
+    want = np.asarray(want, dtype=np.float64).reshape(-1)
+    if got.shape != want.shape:
+        return False, f"length mismatch: got {got.size}, want {want.size}"
+    both_nan = np.isnan(got) & np.isnan(want)
+    same_inf = np.isinf(got) & np.isinf(want) & (np.sign(got) == np.sign(want))
+    with np.errstate(invalid="ignore"):
+        err = np.abs(got - want)
+        bad = ~(both_nan | same_inf | (err <= allowed))
+    if not bad.any():
+        return True, "ok"
+    idx = np.flatnonzero(bad)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        ratio = np.where(np.isfinite(err[idx]), err[idx] / allowed[idx], np.inf)
+    worst = idx[int(np.nanargmax(ratio))] if ratio.size else idx[0]
+    return False, (f"{what}: {idx.size} rows out of tolerance; worst row {worst}: got {got[worst]!r} "
+                   f"want {want[worst]!r} |err| {err[worst]:.3e} allowed {allowed[worst]:.3e}")
+
+
+def check_residual(got, want, bound) -> tuple[bool, str]:
+    """matvecQ8Residual: the projection's bar (REL * sum|s q x| + ABS) carried
+    through the f32 residual add, plus one f32 rounding step of the output
+    (the add may round the other way when the projection differs)."""
+    bound = np.asarray(bound, dtype=np.float64).reshape(-1)
+    allowed = REL * bound + ABS + _ulp32(want)
+    return _report(got, want, allowed, "matvecQ8Residual")
+
+
+# max |silu'(x)| over the reals (attained near x = 2.40)
+SILU_SLOPE = 1.0999
+
+
+def check_ffn(got, gate, up, bound_gate, bound_up) -> tuple[bool, str]:
+    """matvecQ8Ffn against its oracle components (gate, up: the oracle's f32
+    matvecQ8 rows; bound_*: sum|s q x| per row).  Each projection may be off by
+    its bar e = REL * bound + ABS; through out = silu(g) * u that moves the
+    output by at most |silu'| e_g |u| + |silu(g)| e_u + |silu'| e_g e_u, plus
+    one f32 rounding step of silu(g) (times |u|) and one of the product."""
+    g = np.asarray(gate, dtype=np.float32).reshape(-1)
+    u = np.asarray(up, dtype=np.float32).reshape(-1).astype(np.float64)
+    eg = REL * np.asarray(bound_gate, dtype=np.float64).reshape(-1) + ABS
+    eu = REL * np.asarray(bound_up, dtype=np.float64).reshape(-1) + ABS
+    sg = np.array([silu(v) for v in g], dtype=np.float32)
+    want = (sg.astype(np.float64) * u).astype(np.float32)
+    allowed = (SILU_SLOPE * eg * np.abs(u) + np.abs(sg.astype(np.float64)) * eu + SILU_SLOPE * eg * eu
+               + _ulp32(sg) * np.abs(u) + _ulp32(want))
+    return _report(got, want, allowed, "matvecQ8Ffn")

@@ -15,6 +15,7 @@
 #include "q8_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 /* Math.max / Math.min: NaN if either operand is NaN (ECMAScript 21.3.2.24/25). */
 static double js_max(double a, double b) {
@@ -144,4 +145,34 @@ void q8o_matvec_q8_absterm(const uint32_t* weight, const float* scale, const flo
         }
         bound[row] = sum * fabs((double)scale[row]);
     }
+}
+
+/* ops/matvec/reference.ts:235-243 (matvecQ8Residual): projected = matvecQ8 row
+ * (a Float32Array value), then residual[row] + projected[row] in f64, stored
+ * to a Float32Array. */
+void q8o_matvec_q8_residual(const uint32_t* weight, const float* scale, const float* vector,
+                            const float* residual, size_t N, size_t K, float* output) {
+    q8o_matvec_q8(weight, scale, vector, N, K, output);
+    for (size_t row = 0; row < N; ++row)
+        output[row] = (float)((double)residual[row] + (double)output[row]);
+}
+
+/* ops/activation/reference.ts:91-92: silu(x) = x / (1 + Math.exp(-x)) in f64,
+ * stored to a Float32Array. */
+float q8o_silu(float x) {
+    const double xd = (double)x;
+    return (float)(xd / (1.0 + exp(-xd)));
+}
+
+/* ops/matvec/reference.ts:196-207 (matvecQ8Ffn): gate and up are matvecQ8 rows
+ * (Float32Array values), gated = silu(gate) (Float32Array), then
+ * gated[row] * up[row] in f64 stored to a Float32Array. */
+void q8o_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
+                       const float* scale_up, const float* vector, size_t N, size_t K, float* output) {
+    float* up = (float*)malloc((N ? N : 1) * sizeof(float));
+    q8o_matvec_q8(weight_gate, scale_gate, vector, N, K, output);
+    q8o_matvec_q8(weight_up, scale_up, vector, N, K, up);
+    for (size_t row = 0; row < N; ++row)
+        output[row] = (float)((double)q8o_silu(output[row]) * (double)up[row]);
+    free(up);
 }

@@ -13,6 +13,9 @@
  *   q8o_pack_q8           ops/matvec/reference.ts:267-283
  *   q8o_pack_int8_rows    llm/weights-q8.ts:137-139 (packQ8 over Int8Array)
  *   q8o_matvec_q8         ops/matvec/reference.ts:113-131 (unpackI8 + matvecQ8)
+ *   q8o_matvec_q8_residual ops/matvec/reference.ts:235-243 (matvecQ8Residual)
+ *   q8o_matvec_q8_ffn     ops/matvec/reference.ts:196-207 (matvecQ8Ffn), with
+ *   q8o_silu              ops/activation/reference.ts:91-92 (silu)
  *   q8o_matvec_q8_absterm sum_k |s_n * q_nk * x_k| in f64: the per-row bound
  *                         the f32 kernels are judged against
  *
@@ -39,6 +42,11 @@ void q8o_matvec_q8(const uint32_t* weight, const float* scale, const float* vect
                    size_t N, size_t K, float* output);
 void q8o_matvec_q8_batched(const uint32_t* weight, const float* scale, const float* vectors,
                            size_t N, size_t K, size_t M, float* output);
+void q8o_matvec_q8_residual(const uint32_t* weight, const float* scale, const float* vector,
+                            const float* residual, size_t N, size_t K, float* output);
+float q8o_silu(float x);
+void q8o_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
+                       const float* scale_up, const float* vector, size_t N, size_t K, float* output);
 void q8o_matvec_q8_absterm(const uint32_t* weight, const float* scale, const float* vector,
                            size_t N, size_t K, double* bound);
 

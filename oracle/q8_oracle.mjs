@@ -14,6 +14,8 @@
  *   packQ8         ops/matvec/reference.ts:267-283
  *   packInt8Rows   llm/weights-q8.ts:137-139
  *   matvecQ8       ops/matvec/reference.ts:113-131
+ *   matvecQ8Ffn    ops/matvec/reference.ts:196-207, silu from ops/activation/reference.ts:91-92
+ *   matvecQ8Residual ops/matvec/reference.ts:235-243
  */
 
 /** ops/quantize/reference.ts:13-38 */
@@ -76,5 +78,29 @@ export function matvecQ8Batched({ weight, scale, vectors, N, K, M }) {
   for (let m = 0; m < M; m += 1) {
     output.set(matvecQ8({ weight, scale, vector: vectors.subarray(m * K, (m + 1) * K), N, K }), m * N);
   }
+  return output;
+}
+
+/** ops/activation/reference.ts:91-92 (silu = x / (1 + e^-x), f64). */
+export function silu(x) {
+  return x / (1 + Math.exp(-x));
+}
+
+/** ops/matvec/reference.ts:196-207: silu(gate) stored to a Float32Array, times up, stored. */
+export function matvecQ8Ffn({ weightGate, scaleGate, weightUp, scaleUp, vector, N, K }) {
+  const gate = matvecQ8({ weight: weightGate, scale: scaleGate, vector, N, K });
+  const up = matvecQ8({ weight: weightUp, scale: scaleUp, vector, N, K });
+  const gated = new Float32Array(N);
+  for (let i = 0; i < N; i += 1) gated[i] = silu(gate[i]);
+  const output = new Float32Array(N);
+  for (let row = 0; row < N; row += 1) output[row] = gated[row] * up[row];
+  return output;
+}
+
+/** ops/matvec/reference.ts:235-243: residual + projected, stored to a Float32Array. */
+export function matvecQ8Residual({ weight, scale, vector, residual, N, K }) {
+  const projected = matvecQ8({ weight, scale, vector, N, K });
+  const output = new Float32Array(N);
+  for (let row = 0; row < N; row += 1) output[row] = residual[row] + projected[row];
   return output;
 }

@@ -1,7 +1,7 @@
 // Runs one op of the ECMAScript oracle (oracle/q8_oracle.mjs) on arrays sent as
 // base64 in a JSON job on stdin; prints the outputs as base64 JSON on stdout.
 // Lets the Python tests hold the C oracle and the JS oracle to each other.
-import { quantize, packQ8, packInt8Rows, matvecQ8 } from "../../oracle/q8_oracle.mjs";
+import { quantize, packQ8, packInt8Rows, matvecQ8, matvecQ8Ffn, matvecQ8Residual } from "../../oracle/q8_oracle.mjs";
 
 const typed = { f32: Float32Array, i32: Int32Array, u32: Uint32Array, i8: Int8Array };
 function decode(spec) {
@@ -35,6 +35,14 @@ process.stdin.on("end", () => {
       break;
     case "matvecQ8":
       out = { output: encode(matvecQ8({ weight: a.weight, scale: a.scale, vector: a.vector, N: job.N, K: job.K })) };
+      break;
+    case "matvecQ8Ffn":
+      out = { output: encode(matvecQ8Ffn({ weightGate: a.weightGate, scaleGate: a.scaleGate, weightUp: a.weightUp,
+                                           scaleUp: a.scaleUp, vector: a.vector, N: job.N, K: job.K })) };
+      break;
+    case "matvecQ8Residual":
+      out = { output: encode(matvecQ8Residual({ weight: a.weight, scale: a.scale, vector: a.vector,
+                                                residual: a.residual, N: job.N, K: job.K })) };
       break;
     default:
       throw new Error(`unknown op ${job.op}`);

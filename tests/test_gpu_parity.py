@@ -270,6 +270,130 @@ def test_batched_lm_head(M):
     assert np.all(np.isfinite(ys))
 
 
+# ---------------------------------------------------------------- fused decode forms
+
+def assert_ffn(got, wg, sg, wu, su, x, N, K):
+    g, u = oracle.matvec_q8(wg, sg, x, N, K), oracle.matvec_q8(wu, su, x, N, K)
+    ok, msg = oracle.check_ffn(got, g, u, oracle.absterm(wg, sg, x, N, K), oracle.absterm(wu, su, x, N, K))
+    assert ok, f"N={N} K={K}: {msg}"
+
+
+def assert_residual(got, w, s, x, r, N, K):
+    want = oracle.matvec_q8_residual(w, s, x, r, N, K)
+    ok, msg = oracle.check_residual(got, want, oracle.absterm(w, s, x, N, K))
+    assert ok, f"N={N} K={K}: {msg}"
+
+
+@pytest.mark.parametrize("case", kat()["matvec_q8_ffn"], ids=lambda c: c["source"].split(" ")[0])
+def test_ffn_kat(case):
+    N, K = case["N"], case["K"]
+    wg = oracle.pack_q8(np.array(case["gate_codes"], np.int32), N, K)
+    wu = oracle.pack_q8(np.array(case["up_codes"], np.int32), N, K)
+    y = wxo_q8.matvecQ8Ffn(weightGate=wg, scaleGate=np.array(case["scale_gate"], np.float32), weightUp=wu,
+                           scaleUp=np.array(case["scale_up"], np.float32), vector=np.array(case["vector"], np.float32),
+                           N=N, K=K)
+    assert np.all(np.abs(y.astype(np.float64) - np.array(case["want"])) < case["abs_tol"])
+
+
+@pytest.mark.parametrize("case", kat()["matvec_q8_residual"], ids=lambda c: c["source"].split(" ")[0])
+def test_residual_kat(case):
+    N, K = case["N"], case["K"]
+    w = oracle.pack_q8(np.array(case["codes"], np.int32), N, K)
+    y = wxo_q8.matvecQ8Residual(weight=w, scale=np.array(case["scale"], np.float32),
+                                vector=np.array(case["vector"], np.float32),
+                                residual=np.array(case["residual"], np.float32), N=N, K=K)
+    assert np.all(np.abs(y.astype(np.float64) - np.array(case["want"])) < case["abs_tol"])
+
+
+FUSED_SHAPES = [(1, 1), (1, 4), (3, 7), (37, 64), (100, 1024), (9, 1030), (70, 2048), (21, 4099), (513, 4096),
+                (5, 8200), (3, 20000), (2000, 300), (4097, 1000)]
+
+
+@pytest.mark.parametrize("N,K", FUSED_SHAPES)
+def test_ffn_matches_oracle(N, K):
+    rng = np.random.default_rng(N * 31 + K + 1)
+    wg, wu = random_weights(rng, N, K, full_range=True), random_weights(rng, N, K)
+    sg = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    su = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = (3 * rng.standard_normal(K)).astype(np.float32)
+    y = wxo_q8.matvecQ8Ffn(weightGate=wg, scaleGate=sg, weightUp=wu, scaleUp=su, vector=x, N=N, K=K)
+    assert_ffn(y, wg, sg, wu, su, x, N, K)
+
+
+@pytest.mark.parametrize("N,K", FUSED_SHAPES)
+def test_residual_matches_oracle(N, K):
+    rng = np.random.default_rng(N * 37 + K + 2)
+    w = random_weights(rng, N, K, full_range=(K % 2 == 1))
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    r = (10 * rng.standard_normal(N)).astype(np.float32)
+    y = wxo_q8.matvecQ8Residual(weight=w, scale=s, vector=x, residual=r, N=N, K=K)
+    assert_residual(y, w, s, x, r, N, K)
+
+
+def test_fused_decoder_layer():
+    # cfg4 shapes: gate/up [5632, 2048] through the fused FFN; wo [2048, 2048]
+    # and down [2048, 5632] through the fused residual add.
+    mats, xh, xf = wl.make_decoder_layer()
+    packed = {}
+    for name, N, K, wf in mats:
+        codes, scales = oracle.quantize(wf, N, K)
+        packed[name] = (oracle.pack_q8(codes, N, K), scales, N, K)
+    wg, sg, N, K = packed["wGate"]
+    wu, su, _, _ = packed["wUp"]
+    assert_ffn(wxo_q8.matvecQ8Ffn(weightGate=wg, scaleGate=sg, weightUp=wu, scaleUp=su, vector=xh, N=N, K=K),
+               wg, sg, wu, su, xh, N, K)
+    rng = np.random.default_rng(4)
+    for name, x in (("wo", xh), ("wDown", xf)):
+        w, s, N, K = packed[name]
+        r = rng.standard_normal(N).astype(np.float32)
+        assert_residual(wxo_q8.matvecQ8Residual(weight=w, scale=s, vector=x, residual=r, N=N, K=K), w, s, x, r, N, K)
+
+
+def test_residual_in_place_on_device():
+    # the resident engine adds into the residual stream: output == residual
+    rng = np.random.default_rng(5)
+    N, K = 2048, 2048
+    w = random_weights(rng, N, K)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    r = rng.standard_normal(N).astype(np.float32)
+    bw, bs, bx = (wxo_q8.DeviceBuffer.from_array(a) for a in (w, s, x))
+    br = wxo_q8.DeviceBuffer.from_array(r)
+    wxo_q8.matvec_q8_residual_device(bw, bs, bx, br, br, N, K)
+    wxo_q8.synchronize()
+    assert_residual(br.download(np.float32, N), w, s, x, r, N, K)
+    for b in (bw, bs, bx, br):
+        b.free()
+
+
+def test_fused_k_zero_and_nonfinite():
+    N = 5
+    w = np.zeros(0, np.uint32)
+    sg = np.array([1, 2, np.inf, 0.5, 3], np.float32)
+    su = np.array([1, 1, 1, np.nan, 2], np.float32)
+    r = np.array([1, -2, 3, 4, np.inf], np.float32)
+    y = wxo_q8.matvecQ8Ffn(weightGate=w, scaleGate=sg, weightUp=w, scaleUp=su, vector=np.zeros(0, np.float32), N=N, K=0)
+    want = oracle.matvec_q8_ffn(w, sg, w, su, np.zeros(0, np.float32), N, 0)
+    assert_bits_equal(y, want, "ffn K=0")
+    y = wxo_q8.matvecQ8Residual(weight=w, scale=sg, vector=np.zeros(0, np.float32), residual=r, N=N, K=0)
+    assert_bits_equal(y, oracle.matvec_q8_residual(w, sg, np.zeros(0, np.float32), r, N, 0), "residual K=0")
+    # non-finite vector entries and scales propagate as in the reference
+    rng = np.random.default_rng(6)
+    N, K = 40, 300
+    wg, wu = random_weights(rng, N, K), random_weights(rng, N, K)
+    sg = rng.uniform(0.01, 0.05, N).astype(np.float32)
+    su = rng.uniform(0.01, 0.05, N).astype(np.float32)
+    sg[3], su[4] = np.inf, np.nan
+    x = rng.standard_normal(K).astype(np.float32)
+    y = wxo_q8.matvecQ8Ffn(weightGate=wg, scaleGate=sg, weightUp=wu, scaleUp=su, vector=x, N=N, K=K)
+    assert_ffn(y, wg, sg, wu, su, x, N, K)
+    x[7] = np.inf
+    r = rng.standard_normal(N).astype(np.float32)
+    y = wxo_q8.matvecQ8Residual(weight=wg, scale=sg, vector=x, residual=r, N=N, K=K)
+    assert_residual(y, wg, sg, x, r, N, K)
+
+
 # ---------------------------------------------------------------- quantize / packQ8
 
 @pytest.mark.parametrize("case", kat()["quantize"], ids=lambda c: c["source"].split(" ")[0])

@@ -236,6 +236,84 @@ def test_batched_is_m_independent_calls():
         assert np.array_equal(ys[m], oracle.matvec_q8(w, s, xs[m], N, K))
 
 
+# ---------------------------------------------------------------- fused decode forms
+
+@pytest.mark.parametrize("case", kat()["matvec_q8_ffn"], ids=lambda c: c["source"].split(" ")[0])
+def test_matvec_q8_ffn_kat(case):
+    N, K = case["N"], case["K"]
+    wg = oracle.pack_q8(np.array(case["gate_codes"], np.int32), N, K)
+    wu = oracle.pack_q8(np.array(case["up_codes"], np.int32), N, K)
+    y = oracle.matvec_q8_ffn(wg, np.array(case["scale_gate"], np.float32), wu, np.array(case["scale_up"], np.float32),
+                             np.array(case["vector"], np.float32), N, K)
+    assert np.all(np.abs(y.astype(np.float64) - np.array(case["want"])) < case["abs_tol"])
+
+
+@pytest.mark.parametrize("case", kat()["matvec_q8_residual"], ids=lambda c: c["source"].split(" ")[0])
+def test_matvec_q8_residual_kat(case):
+    N, K = case["N"], case["K"]
+    w = oracle.pack_q8(np.array(case["codes"], np.int32), N, K)
+    y = oracle.matvec_q8_residual(w, np.array(case["scale"], np.float32), np.array(case["vector"], np.float32),
+                                  np.array(case["residual"], np.float32), N, K)
+    assert np.all(np.abs(y.astype(np.float64) - np.array(case["want"])) < case["abs_tol"])
+
+
+def test_silu_closed_forms():
+    # silu(0) = 0; silu is odd-symmetric around x/2: silu(x) - silu(-x) = x;
+    # silu(-x) -> -0 for x past the f64 exp overflow; silu(x) -> x for large x.
+    assert oracle.silu(0.0) == 0.0
+    for x in (0.5, 1.0, 2.5, 7.0, 30.0):
+        hi, lo = oracle.silu(x), oracle.silu(-x)
+        assert abs((float(hi) - float(lo)) - x) <= 4 * np.spacing(np.float32(x))
+    assert oracle.silu(-1000.0) == 0.0 and np.signbit(oracle.silu(-1000.0))
+    assert oracle.silu(100.0) == 100.0
+    assert np.isnan(oracle.silu(float("nan")))
+    # the f32 rounding of the f64 value: 4 / (1 + e^-4)
+    assert oracle.silu(4.0) == np.float32(4.0 / (1.0 + 0.01831563888873418))
+
+
+def test_fused_forms_reduce_to_matvec():
+    rng = np.random.default_rng(11)
+    N, K = 13, 1031
+    w = le_view_pack(rng.integers(-127, 128, N * K), N, K)
+    s = rng.uniform(0.01, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = oracle.matvec_q8(w, s, x, N, K)
+    # zero residual: exactly the projection
+    assert np.array_equal(oracle.matvec_q8_residual(w, s, x, np.zeros(N, np.float32), N, K), y)
+    # residual add is an f32-rounded sum of two f32 values
+    r = rng.standard_normal(N).astype(np.float32)
+    assert np.array_equal(oracle.matvec_q8_residual(w, s, x, r, N, K),
+                          (r.astype(np.float64) + y.astype(np.float64)).astype(np.float32))
+    # gate == up: silu(y) * y
+    f = oracle.matvec_q8_ffn(w, s, w, s, x, N, K)
+    sy = np.array([oracle.silu(v) for v in y], np.float32)
+    assert np.array_equal(f, (sy.astype(np.float64) * y.astype(np.float64)).astype(np.float32))
+
+
+def test_fused_checks_reject_plausible_mistakes():
+    # The tolerance checks the GPU is judged by must catch a gate/up swap, a
+    # dropped residual and a residual added before the scale.
+    rng = np.random.default_rng(12)
+    N, K = 64, 512
+    wg = le_view_pack(rng.integers(-127, 128, N * K), N, K)
+    wu = le_view_pack(rng.integers(-127, 128, N * K), N, K)
+    sg = rng.uniform(0.01, 0.05, N).astype(np.float32)
+    su = rng.uniform(0.01, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    g, u = oracle.matvec_q8(wg, sg, x, N, K), oracle.matvec_q8(wu, su, x, N, K)
+    bg, bu = oracle.absterm(wg, sg, x, N, K), oracle.absterm(wu, su, x, N, K)
+    good = oracle.matvec_q8_ffn(wg, sg, wu, su, x, N, K)
+    assert oracle.check_ffn(good, g, u, bg, bu)[0]
+    swapped = oracle.matvec_q8_ffn(wu, su, wg, sg, x, N, K)
+    assert not oracle.check_ffn(swapped, g, u, bg, bu)[0]
+    r = rng.standard_normal(N).astype(np.float32)
+    res = oracle.matvec_q8_residual(wg, sg, x, r, N, K)
+    assert oracle.check_residual(res, res, bg)[0]
+    assert not oracle.check_residual(g, res, bg)[0]
+    unscaled_first = ((oracle.matvec_q8(wg, np.ones(N, np.float32), x, N, K) + r) * sg).astype(np.float32)
+    assert not oracle.check_residual(unscaled_first, res, bg)[0]
+
+
 # ---------------------------------------------------------------- C vs ECMAScript
 
 NODE = shutil.which("node")
@@ -306,6 +384,26 @@ def test_c_oracle_matches_ecmascript_oracle():
     assert np.array_equal(np.isnan(js_y), np.isnan(c_y))
     ok = ~np.isnan(c_y)
     assert np.array_equal(js_y[ok].view(np.uint32), c_y[ok].view(np.uint32))
+
+    # fused forms: the same compositions (silu through V8's Math.exp and glibc's
+    # exp, which agree after the f32 rounding on these rows)
+    w2 = oracle.pack_q8(rng.integers(-127, 128, N * K, dtype=np.int32), N, K)
+    s2 = rng.uniform(0.01, 0.5, N).astype(np.float32)
+    vec = (4 * rng.standard_normal(K)).astype(np.float32)
+    res = rng.standard_normal(N).astype(np.float32)
+    js = run_js({"op": "matvecQ8Ffn", "N": N, "K": K,
+                 "arrays": {"weightGate": enc(w, "u32"), "scaleGate": enc(c_scales, "f32"),
+                            "weightUp": enc(w2, "u32"), "scaleUp": enc(s2, "f32"), "vector": enc(vec, "f32")}})
+    js_f = dec(js["output"], np.float32)
+    c_f = oracle.matvec_q8_ffn(w, c_scales, w2, s2, vec, N, K)
+    assert np.array_equal(np.isnan(js_f), np.isnan(c_f))
+    ok = ~np.isnan(c_f)
+    assert np.array_equal(js_f[ok].view(np.uint32), c_f[ok].view(np.uint32))
+    js = run_js({"op": "matvecQ8Residual", "N": N, "K": K,
+                 "arrays": {"weight": enc(w2, "u32"), "scale": enc(s2, "f32"), "vector": enc(vec, "f32"),
+                            "residual": enc(res, "f32")}})
+    assert np.array_equal(dec(js["output"], np.float32).view(np.uint32),
+                          oracle.matvec_q8_residual(w2, s2, vec, res, N, K).view(np.uint32))
 
 
 # ---------------------------------------------------------------- the checks have teeth

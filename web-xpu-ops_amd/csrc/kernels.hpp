@@ -23,11 +23,34 @@ struct MatvecArgs {
     float* output;
     uint32_t N, K, M;
     uint32_t W;  // ceil(K / 4) words per row
+    // fused forms (M = 1): the up projection of matvecQ8Ffn, the residual of
+    // matvecQ8Residual
+    const uint32_t* weight2 = nullptr;
+    const float* scale2 = nullptr;
+    const float* residual = nullptr;
 };
+
+// Kernel arguments of the single-vector kernel (all epilogues).
+struct M1Params {
+    const uint32_t* weight;  // gate for the FFN form
+    const float* scale;
+    const uint32_t* weight2;  // up (FFN only)
+    const float* scale2;
+    const float* x;
+    const float* residual;  // residual form only
+    float* y;
+    uint32_t N, K, W;
+};
+
+enum : int { kEpiPlain = 0, kEpiResidual = 1, kEpiFfn = 2 };
 
 // `variant` (optional) receives a static string naming the kernel chosen.
 hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream,
                             const char** variant);
+// matvecQ8Residual (epi = kEpiResidual) or matvecQ8Ffn (kEpiFfn), M = 1.
+hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo& dev, hipStream_t stream,
+                                  const char** variant);
+hipError_t launch_fused_zero(const MatvecArgs& a, int epi, hipStream_t stream);
 hipError_t launch_fill_scaled_zero(const float* scale, float* y, uint32_t N, uint32_t M, hipStream_t stream);
 
 // quantize (codes != nullptr) and/or packQ8 (packed != nullptr) of f32 rows.

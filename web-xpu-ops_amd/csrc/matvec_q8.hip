@@ -57,6 +57,20 @@ __device__ __forceinline__ void load_x16_rsrc(__amdgpu_buffer_rsrc_t xrs, uint32
     }
 }
 
+// silu(g) * u as the reference composes it: silu in f64 on the f32 gate,
+// x / (1 + e^-x), rounded to f32, then one f32 product.
+__device__ __forceinline__ float ffn_epilogue(float g, float u) {
+    const double gd = (double)g;
+    const float gated = (float)(gd / (1.0 + exp(-gd)));
+    return __fmul_rn(gated, u);
+}
+
+// residual + projected as the reference adds them: in f64, then one rounding
+// to f32.
+__device__ __forceinline__ float residual_epilogue(float r, float projected) {
+    return (float)((double)r + (double)projected);
+}
+
 // ---------------------------------------------------------------------------
 // M = 1.  One block of R rows per workgroup; WAVES waves split each row's
 // chunks (chunk c -> wave c % WAVES, slot c / WAVES).
@@ -78,20 +92,34 @@ __device__ __forceinline__ void load_x16_rsrc(__amdgpu_buffer_rsrc_t xrs, uint32
 // block, row offset r * 4W in an SGPR, non-temporal (streamed once).
 // CPW > 0: the vector slices of CPW chunk slots are loaded once into VGPRs.
 // CPW == 0: any K; one slot at a time with its vector slice.
-template <int WAVES, int CPW, int R>
-__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
-    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
-    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W) {
-    constexpr int SHIFT = 6 - ilog2(R);
+//
+// EPI selects what happens to a row's dot product d once it is complete:
+//   kEpiPlain     y = d * s
+//   kEpiResidual  y = residual + (d * s): d * s rounded to f32, the sum taken
+//                 in f64 and rounded once, as the reference's
+//                 fround(residual + fround(d * s)) (ops/matvec/reference.ts:235-243)
+//   kEpiFfn       two weights streamed side by side (gate rows, then up rows:
+//                 2R dot products per block); y = silu(g) * u with g = dg * sg,
+//                 u = du * su, silu evaluated in f64 and rounded to f32 as
+//                 ops/activation/reference.ts:91-92 does, then one f32 product
+//                 (ops/matvec/reference.ts:196-207)
+template <int WAVES, int CPW, int R, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(M1Params p) {
+    constexpr int NWT = EPI == kEpiFfn ? 2 : 1;  // weights streamed
+    constexpr int V = R * NWT;                     // dot products per block
+    constexpr int SHIFT = 6 - ilog2(V);
     constexpr int XS = CPW > 0 ? CPW : 1;
+    const uint32_t N = p.N, K = p.K, W = p.W;
     const int lane = (int)(threadIdx.x & 63u);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t C = (W + kChunkWords - 1) / kChunkWords;
     const uint32_t row0 = blockIdx.x * (uint32_t)R;
     const uint32_t rows = min((uint32_t)R, N - row0);  // >= 1
     const uint32_t rowbytes = W * 4u;
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)row0 * W, rows * rowbytes);
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, K * 4u);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.weight + (size_t)row0 * W, rows * rowbytes);
+    const __amdgpu_buffer_rsrc_t wrs2 =
+        NWT == 2 ? make_rsrc(p.weight2 + (size_t)row0 * W, rows * rowbytes) : wrs;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, K * 4u);
 
     float xr[XS][16];
     if constexpr (CPW > 0) {
@@ -103,9 +131,9 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
     // flight when the whole block should be requested at once.
     __builtin_amdgcn_sched_barrier(0);
 
-    float acc[R];
+    float acc[V];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < V; ++r) acc[r] = 0.0f;
 
     const int slots = CPW > 0 ? CPW : (int)((C + WAVES - 1) / WAVES);
 #pragma unroll
@@ -113,9 +141,13 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
         const uint32_t c = wave + (uint32_t)j * WAVES;
         if (CPW != 1 && c >= C) break;  // wave-uniform; with CPW == 1 every wave owns a chunk
         const int voff = (int)(c * kChunkWords * 4u + (uint32_t)lane * 16u);
-        u32x4v v[R];
+        u32x4v v[V];
 #pragma unroll
         for (int r = 0; r < R; ++r) v[r] = load_nt_b128(wrs, voff, (int)(r * rowbytes));
+        if constexpr (NWT == 2) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) v[R + r] = load_nt_b128(wrs2, voff, (int)(r * rowbytes));
+        }
         __builtin_amdgcn_sched_barrier(0);
         float xl[16];
         if constexpr (CPW > 0) {
@@ -125,7 +157,7 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
             load_x16_rsrc(xrs, c, lane, xl);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < V; ++r) {
             float a = acc[r];
             a = fma_word(v[r].x, xl[0], xl[1], xl[2], xl[3], a);
             a = fma_word(v[r].y, xl[4], xl[5], xl[6], xl[7], a);
@@ -135,20 +167,30 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
         }
     }
 
-    wave_reduce_rows<R>(acc, lane);
+    wave_reduce_rows<V>(acc, lane);
     const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
     const uint32_t rr = (uint32_t)lane >> SHIFT;
-    if constexpr (WAVES == 1) {
-        if (leader && rr < rows) y[row0 + rr] = acc[0] * scale[row0 + rr];
+    if constexpr (WAVES == 1 && EPI == kEpiPlain) {
+        if (leader && rr < rows) p.y[row0 + rr] = acc[0] * p.scale[row0 + rr];
     } else {
-        __shared__ float part[WAVES][R];
+        __shared__ float part[WAVES][V];
         if (leader) part[wave][rr] = acc[0];
         __syncthreads();
         if (threadIdx.x < rows) {
-            float s = part[0][threadIdx.x];
+            const uint32_t t = threadIdx.x, row = row0 + t;
+            float d = part[0][t];
 #pragma unroll
-            for (int w = 1; w < WAVES; ++w) s += part[w][threadIdx.x];
-            y[row0 + threadIdx.x] = s * scale[row0 + threadIdx.x];
+            for (int w = 1; w < WAVES; ++w) d += part[w][t];
+            if constexpr (EPI == kEpiPlain) {
+                p.y[row] = d * p.scale[row];
+            } else if constexpr (EPI == kEpiResidual) {
+                p.y[row] = residual_epilogue(p.residual[row], __fmul_rn(d, p.scale[row]));
+            } else {
+                float du = part[0][R + t];
+#pragma unroll
+                for (int w = 1; w < WAVES; ++w) du += part[w][R + t];
+                p.y[row] = ffn_epilogue(__fmul_rn(d, p.scale[row]), __fmul_rn(du, p.scale2[row]));
+            }
         }
     }
 }
@@ -493,29 +535,45 @@ uint32_t grid_for(uint32_t nblocks, uint32_t max_groups) {
     return (nblocks + iters - 1) / iters;
 }
 
-template <int WAVES, int CPW, int R>
+template <int WAVES, int CPW, int R, int EPI>
 hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
-    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R>), dim3(nblocks), dim3(WAVES * 64), 0, stream, a.weight,
-                       a.scale, a.vector, a.output, a.N, a.K, a.W);
+    const M1Params p{a.weight, a.scale, a.weight2, a.scale2, a.vector, a.residual, a.output, a.N, a.K, a.W};
+    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI>), dim3(nblocks), dim3(WAVES * 64), 0, stream, p);
     if (variant) *variant = CPW > 0 ? "m1.xreg" : "m1.xstream";
     return hipGetLastError();
 }
 
 // Rows per workgroup: the largest R whose grid still gives every CU at least
 // two workgroups (fewer, fatter blocks amortise the per-workgroup vector
-// fetch; too few leave CUs idle).
-template <int WAVES, int CPW, int RMAX>
+// fetch; too few leave CUs idle).  The fused FFN streams two weights, so it
+// takes half the rows per block for the same loads in flight.
+template <int WAVES, int CPW, int RMAX, int EPI>
 hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    constexpr int RM = EPI == kEpiFfn ? RMAX / 2 : RMAX;
     const uint32_t want = 2u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
-    if constexpr (RMAX >= 16) {
-        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16>(a, stream, variant);
+    if constexpr (RM >= 16) {
+        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16, EPI>(a, stream, variant);
     }
-    if constexpr (RMAX >= 8) {
-        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8>(a, stream, variant);
+    if constexpr (RM >= 8) {
+        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8, EPI>(a, stream, variant);
     }
-    if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4>(a, stream, variant);
-    return launch_m1<WAVES, CPW, 2>(a, stream, variant);
+    if constexpr (RM >= 4) {
+        if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4, EPI>(a, stream, variant);
+    }
+    return launch_m1<WAVES, CPW, 2, EPI>(a, stream, variant);
+}
+
+template <int EPI>
+hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
+    if (C == 1) return dispatch_m1_rows<1, 1, 16, EPI>(a, dev, stream, variant);
+    if (C == 2) return dispatch_m1_rows<2, 1, 16, EPI>(a, dev, stream, variant);
+    if (C == 3) return dispatch_m1_rows<3, 1, 16, EPI>(a, dev, stream, variant);
+    if (C == 4) return dispatch_m1_rows<4, 1, 16, EPI>(a, dev, stream, variant);
+    if (C <= 8) return dispatch_m1_rows<4, 2, 8, EPI>(a, dev, stream, variant);
+    if (C <= 16) return dispatch_m1_rows<4, 4, 4, EPI>(a, dev, stream, variant);
+    return dispatch_m1_rows<4, 0, 4, EPI>(a, dev, stream, variant);
 }
 
 template <int WAVES, int CPW, int R, int MT>
@@ -570,16 +628,7 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
         // No terms: y = 0 * s (NaN for a non-finite scale), as the reference.
         return launch_fill_scaled_zero(a.scale, a.output, a.N, a.M, stream);
     }
-    if (a.M == 1) {
-        const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
-        if (C == 1) return dispatch_m1_rows<1, 1, 16>(a, dev, stream, variant);
-        if (C == 2) return dispatch_m1_rows<2, 1, 16>(a, dev, stream, variant);
-        if (C == 3) return dispatch_m1_rows<3, 1, 16>(a, dev, stream, variant);
-        if (C == 4) return dispatch_m1_rows<4, 1, 16>(a, dev, stream, variant);
-        if (C <= 8) return dispatch_m1_rows<4, 2, 8>(a, dev, stream, variant);
-        if (C <= 16) return dispatch_m1_rows<4, 4, 4>(a, dev, stream, variant);
-        return dispatch_m1_rows<4, 0, 4>(a, dev, stream, variant);
-    }
+    if (a.M == 1) return dispatch_m1<kEpiPlain>(a, dev, stream, variant);
     // Batched on the matrix cores when the tile's x parts fit in LDS.  Two
     // tiles per step share each B read when the tile holds 12 or more
     // vectors (wider B reads), one tile with a deeper pipeline otherwise.
@@ -621,6 +670,32 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
     }
     if (variant) *variant = "mb.loop_m1";
     return hipSuccess;
+}
+
+hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo& dev, hipStream_t stream,
+                                  const char** variant) {
+    if (a.N == 0) return hipSuccess;
+    if (a.M != 1 || (epi != kEpiResidual && epi != kEpiFfn)) return hipErrorInvalidValue;
+    if (a.K == 0) return launch_fused_zero(a, epi, stream);
+    return epi == kEpiFfn ? dispatch_m1<kEpiFfn>(a, dev, stream, variant)
+                          : dispatch_m1<kEpiResidual>(a, dev, stream, variant);
+}
+
+// K = 0: every dot product is 0.
+__global__ void fused_zero_kernel(M1Params p, int epi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < p.N; i += gridDim.x * blockDim.x) {
+        if (epi == kEpiFfn)
+            p.y[i] = ffn_epilogue(0.0f * p.scale[i], 0.0f * p.scale2[i]);
+        else
+            p.y[i] = residual_epilogue(p.residual[i], 0.0f * p.scale[i]);
+    }
+}
+
+hipError_t launch_fused_zero(const MatvecArgs& a, int epi, hipStream_t stream) {
+    const M1Params p{a.weight, a.scale, a.weight2, a.scale2, a.vector, a.residual, a.output, a.N, a.K, a.W};
+    const uint32_t grid = (a.N + 255) / 256 < 4096 ? (a.N + 255) / 256 : 4096;
+    hipLaunchKernelGGL(fused_zero_kernel, dim3(grid), dim3(256), 0, stream, p, epi);
+    return hipGetLastError();
 }
 
 __global__ void fill_scaled_zero_kernel(const float* __restrict__ scale, float* __restrict__ y, uint32_t N,

@@ -163,8 +163,9 @@ const char* wxo_describe(void) {
         return g_describe;
     }
     snprintf(g_describe, sizeof g_describe,
-             "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(xreg|"
-             "xstream),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,pack_int8_rows",
+             "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(plain|"
+             "residual|ffn),matvec_q8_mfma(bf16x3),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,"
+             "pack_int8_rows",
              WXO_ABI_VERSION, WXO_BUILD_ID, d->ordinal, d->name, d->arch, d->cu_count,
              (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0));
     return g_describe;
@@ -297,6 +298,33 @@ int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vecto
     return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8 launch");
 }
 
+int wxo_matvec_q8_residual(const uint32_t* weight, const float* scale, const float* vector, const float* residual,
+                           float* output, uint32_t N, uint32_t K, wxo_stream_t stream) {
+    WXO_TRY(validate_matvec(weight, scale, vector, output, N, K, 1));
+    WXO_TRY(check_ptr(residual, N, "residual"));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    wxo::MatvecArgs a{weight, scale, vector, output, N, K, 1, (uint32_t)(((uint64_t)K + 3) / 4)};
+    a.residual = residual;
+    hipError_t e = wxo::launch_matvec_q8_fused(a, wxo::kEpiResidual, *d, as_hip(stream), nullptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8_residual launch");
+}
+
+int wxo_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
+                      const float* scale_up, const float* vector, float* output, uint32_t N, uint32_t K,
+                      wxo_stream_t stream) {
+    WXO_TRY(validate_matvec(weight_gate, scale_gate, vector, output, N, K, 1));
+    WXO_TRY(check_ptr(weight_up, (uint64_t)N * (((uint64_t)K + 3) / 4), "weight_up"));
+    WXO_TRY(check_ptr(scale_up, N, "scale_up"));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    wxo::MatvecArgs a{weight_gate, scale_gate, vector, output, N, K, 1, (uint32_t)(((uint64_t)K + 3) / 4)};
+    a.weight2 = weight_up;
+    a.scale2 = scale_up;
+    hipError_t e = wxo::launch_matvec_q8_fused(a, wxo::kEpiFfn, *d, as_hip(stream), nullptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8_ffn launch");
+}
+
 int wxo_quantize(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales, wxo_stream_t stream) {
     WXO_TRY(validate_rows(input, N, D, "input"));
     WXO_TRY(check_ptr(output, (uint64_t)N * D, "output"));
@@ -352,6 +380,51 @@ int wxo_matvec_q8_host(const uint32_t* weight, const float* scale, const float* 
     WXO_TRY(x.upload(vector, (size_t)M * K * 4));
     WXO_TRY(wxo_matvec_q8((const uint32_t*)w.p, (const float*)s.p, (const float*)x.p, (float*)y.p, N, K, M, nullptr));
     return y.download(output, (size_t)M * N * 4) == WXO_OK ? ok() : WXO_ERR_DEVICE;
+}
+
+int wxo_matvec_q8_residual_host(const uint32_t* weight, const float* scale, const float* vector, const float* residual,
+                                float* output, uint32_t N, uint32_t K) {
+    WXO_TRY(validate_matvec(weight, scale, vector, output, N, K, 1));
+    WXO_TRY(check_ptr(residual, N, "residual"));
+    const size_t W = ((size_t)K + 3) / 4;
+    DevBuf w, s, x, r, y;
+    WXO_TRY(w.alloc((size_t)N * W * 4));
+    WXO_TRY(s.alloc((size_t)N * 4));
+    WXO_TRY(x.alloc((size_t)K * 4));
+    WXO_TRY(r.alloc((size_t)N * 4));
+    WXO_TRY(y.alloc((size_t)N * 4));
+    WXO_TRY(w.upload(weight, (size_t)N * W * 4));
+    WXO_TRY(s.upload(scale, (size_t)N * 4));
+    WXO_TRY(x.upload(vector, (size_t)K * 4));
+    WXO_TRY(r.upload(residual, (size_t)N * 4));
+    WXO_TRY(wxo_matvec_q8_residual((const uint32_t*)w.p, (const float*)s.p, (const float*)x.p, (const float*)r.p,
+                                   (float*)y.p, N, K, nullptr));
+    WXO_TRY(y.download(output, (size_t)N * 4));
+    return ok();
+}
+
+int wxo_matvec_q8_ffn_host(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
+                           const float* scale_up, const float* vector, float* output, uint32_t N, uint32_t K) {
+    WXO_TRY(validate_matvec(weight_gate, scale_gate, vector, output, N, K, 1));
+    const size_t W = ((size_t)K + 3) / 4;
+    WXO_TRY(check_ptr(weight_up, (uint64_t)N * W, "weight_up"));
+    WXO_TRY(check_ptr(scale_up, N, "scale_up"));
+    DevBuf wg, sg, wu, su, x, y;
+    WXO_TRY(wg.alloc((size_t)N * W * 4));
+    WXO_TRY(sg.alloc((size_t)N * 4));
+    WXO_TRY(wu.alloc((size_t)N * W * 4));
+    WXO_TRY(su.alloc((size_t)N * 4));
+    WXO_TRY(x.alloc((size_t)K * 4));
+    WXO_TRY(y.alloc((size_t)N * 4));
+    WXO_TRY(wg.upload(weight_gate, (size_t)N * W * 4));
+    WXO_TRY(sg.upload(scale_gate, (size_t)N * 4));
+    WXO_TRY(wu.upload(weight_up, (size_t)N * W * 4));
+    WXO_TRY(su.upload(scale_up, (size_t)N * 4));
+    WXO_TRY(x.upload(vector, (size_t)K * 4));
+    WXO_TRY(wxo_matvec_q8_ffn((const uint32_t*)wg.p, (const float*)sg.p, (const uint32_t*)wu.p, (const float*)su.p,
+                              (const float*)x.p, (float*)y.p, N, K, nullptr));
+    WXO_TRY(y.download(output, (size_t)N * 4));
+    return ok();
 }
 
 int wxo_quantize_host(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales) {

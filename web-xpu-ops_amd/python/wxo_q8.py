@@ -58,11 +58,15 @@ SIGNATURES = {
     "wxo_event_synchronize": ([_P], _I),
     "wxo_event_elapsed_ms": ([ctypes.POINTER(ctypes.c_float), _P, _P], _I),
     "wxo_matvec_q8": ([_P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
+    "wxo_matvec_q8_residual": ([_P, _P, _P, _P, _P, _U32, _U32, _P], _I),
+    "wxo_matvec_q8_ffn": ([_P, _P, _P, _P, _P, _P, _U32, _U32, _P], _I),
     "wxo_quantize": ([_P, _U32, _U32, _P, _P, _P], _I),
     "wxo_pack_q8": ([_P, _U32, _U32, _P, _P], _I),
     "wxo_pack_int8_rows": ([_P, _U32, _U32, _P, _P], _I),
     "wxo_quantize_pack_q8": ([_P, _U32, _U32, _P, _P, _P], _I),
     "wxo_matvec_q8_host": ([_P, _P, _P, _P, _U32, _U32, _U32], _I),
+    "wxo_matvec_q8_residual_host": ([_P, _P, _P, _P, _P, _U32, _U32], _I),
+    "wxo_matvec_q8_ffn_host": ([_P, _P, _P, _P, _P, _P, _U32, _U32], _I),
     "wxo_quantize_host": ([_P, _U32, _U32, _P, _P], _I),
     "wxo_pack_q8_host": ([_P, _U32, _U32, _P], _I),
     "wxo_pack_int8_rows_host": ([_P, _U32, _U32, _P], _I),
@@ -223,6 +227,17 @@ def matvec_q8_device(weight, scale, vector, output, N: int, K: int, M: int = 1, 
                                _stream_ptr(stream)))
 
 
+def matvec_q8_residual_device(weight, scale, vector, residual, output, N: int, K: int, stream=None) -> None:
+    _check(lib().wxo_matvec_q8_residual(_addr(weight), _addr(scale), _addr(vector), _addr(residual),
+                                        _addr(output), N, K, _stream_ptr(stream)))
+
+
+def matvec_q8_ffn_device(weight_gate, scale_gate, weight_up, scale_up, vector, output, N: int, K: int,
+                         stream=None) -> None:
+    _check(lib().wxo_matvec_q8_ffn(_addr(weight_gate), _addr(scale_gate), _addr(weight_up), _addr(scale_up),
+                                   _addr(vector), _addr(output), N, K, _stream_ptr(stream)))
+
+
 def quantize_device(inp, N: int, D: int, output, scales, stream=None) -> None:
     _check(lib().wxo_quantize(_addr(inp), N, D, _addr(output), _addr(scales), _stream_ptr(stream)))
 
@@ -261,6 +276,32 @@ def matvecQ8Batched(*, weight, scale, vectors, N: int, K: int, M: int) -> np.nda
     out = np.empty(M * N, dtype=np.float32)
     _check(lib().wxo_matvec_q8_host(w.ctypes.data, s.ctypes.data, x.ctypes.data, out.ctypes.data, N, K, M))
     return out.reshape(M, N)
+
+
+def matvecQ8Residual(*, weight, scale, vector, residual, N: int, K: int) -> np.ndarray:
+    """ops/matvec/reference.ts:235 -- residual[n] + matvecQ8 row n, f32 [N]."""
+    w = _need(weight, np.uint32, N * words_per_row(K), "weight")
+    s = _need(scale, np.float32, N, "scale")
+    x = _need(vector, np.float32, K, "vector")
+    r = _need(residual, np.float32, N, "residual")
+    out = np.empty(N, dtype=np.float32)
+    _check(lib().wxo_matvec_q8_residual_host(w.ctypes.data, s.ctypes.data, x.ctypes.data, r.ctypes.data,
+                                             out.ctypes.data, N, K))
+    return out
+
+
+def matvecQ8Ffn(*, weightGate, scaleGate, weightUp, scaleUp, vector, N: int, K: int) -> np.ndarray:
+    """ops/matvec/reference.ts:196 -- silu(gate row n) * up row n, f32 [N]."""
+    W = words_per_row(K)
+    wg = _need(weightGate, np.uint32, N * W, "weightGate")
+    sg = _need(scaleGate, np.float32, N, "scaleGate")
+    wu = _need(weightUp, np.uint32, N * W, "weightUp")
+    su = _need(scaleUp, np.float32, N, "scaleUp")
+    x = _need(vector, np.float32, K, "vector")
+    out = np.empty(N, dtype=np.float32)
+    _check(lib().wxo_matvec_q8_ffn_host(wg.ctypes.data, sg.ctypes.data, wu.ctypes.data, su.ctypes.data,
+                                        x.ctypes.data, out.ctypes.data, N, K))
+    return out
 
 
 def quantize(*, input, N: int, D: int) -> tuple[np.ndarray, np.ndarray]:
