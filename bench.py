@@ -191,6 +191,40 @@ def run_suite(stream, steps, warmup):
     results.append({"case": "cfg4 decoder layer: 7 matvecQ8 calls", "bytes": layer_bytes, "us": round(us, 3),
                     "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
     log(f"suite cfg4 layer: {us:.2f} us/layer  {gbs:.0f} GB/s")
+
+    # The same layer as the resident engine runs its decode projections
+    # (llm/engine-q8-resident.ts:1843-1869): q/k/v plain, o_proj and down_proj
+    # as matvecQ8Residual into the residual stream, gate/up as one
+    # matvecQ8Ffn: 6 launches, and the 3 elementwise passes folded in.
+    by = {name: i for i, (name, _, _, _) in enumerate(mats)}
+    resid = wxo_q8.DeviceBuffer.from_array(np.zeros(2048, np.float32), stream)
+    hidden = wxo_q8.DeviceBuffer(5632 * 4)
+
+    def fused_step(i):
+        li = i % layers
+
+        def wp(name):
+            _, N, K, _ = mats[by[name]]
+            packed, scale = prepared[by[name]]
+            return packed.ptr + li * N * ((K + 3) // 4) * 4, scale.ptr
+
+        for name in ("wq", "wk", "wv"):
+            w, sc = wp(name)
+            check(L.wxo_matvec_q8(w, sc, vh.ptr, outb.ptr, 2048, 2048, 1, sp))
+        w, sc = wp("wo")
+        check(L.wxo_matvec_q8_residual(w, sc, vh.ptr, resid.ptr, resid.ptr, 2048, 2048, sp))
+        (wg, sg), (wu, su) = wp("wGate"), wp("wUp")
+        check(L.wxo_matvec_q8_ffn(wg, sg, wu, su, vh.ptr, hidden.ptr, 5632, 2048, sp))
+        w, sc = wp("wDown")
+        check(L.wxo_matvec_q8_residual(w, sc, vf.ptr, resid.ptr, resid.ptr, 2048, 5632, sp))
+    us = time_loop(stream, fused_step, max(1, steps // 7), max(1, warmup // 7))
+    gbs = layer_bytes / (us * 1e-6) / 1e9
+    results.append({"case": "cfg4 decoder layer as the resident engine runs it: 3 matvecQ8 + 2 matvecQ8Residual "
+                            "+ 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+                    "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
+    log(f"suite cfg4 layer fused: {us:.2f} us/layer  {gbs:.0f} GB/s")
+    resid.free()
+    hidden.free()
     for packed, scale in prepared:
         packed.free()
         scale.free()

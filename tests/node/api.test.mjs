@@ -3,7 +3,8 @@
 // shapes are the reference's own: ops/matvec/q8.wgsl.test.ts:23-71,
 // ops/quantize/wgsl.test.ts:6-56, ops/matvec/reference.test.ts:14-95,
 // llm/weights-q8.test.ts:17-42.
-import { test, gpuTest, assert, kat, assertBitsEqual, assertMatvecAgrees } from "./harness.mjs";
+import { test, gpuTest, assert, kat, assertBitsEqual, assertMatvecAgrees, assertResidualAgrees, assertFfnAgrees }
+  from "./harness.mjs";
 import * as matvec from "../../web-xpu-ops_amd/ops/matvec/index.js";
 import * as quantizeOps from "../../web-xpu-ops_amd/ops/quantize/index.js";
 import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
@@ -17,7 +18,9 @@ const F = "api.test.mjs";
 // ------------------------------------------------------------------ no GPU needed
 
 test(F, "exports the reference's op names", () => {
-  for (const name of ["matvecQ8", "packQ8", "matvecQ8Batched"]) assert.strictEqual(typeof matvec[name], "function", name);
+  for (const name of ["matvecQ8", "packQ8", "matvecQ8Batched", "matvecQ8Ffn", "matvecQ8Residual"]) {
+    assert.strictEqual(typeof matvec[name], "function", name);
+  }
   for (const name of ["quantize", "quantizePackQ8"]) assert.strictEqual(typeof quantizeOps[name], "function", name);
   assert.strictEqual(typeof packInt8Rows, "function");
   assert.strictEqual(typeof runMatVecQ8, "function");
@@ -25,9 +28,10 @@ test(F, "exports the reference's op names", () => {
 
 test(F, "the addon loads and exports its whole surface", () => {
   const a = native();
-  for (const name of ["abiVersion", "describe", "deviceCount", "init", "synchronize", "matvecQ8", "quantize", "packQ8",
-    "packInt8Rows", "quantizePackQ8", "malloc", "free", "upload", "download", "copy", "matvecQ8Device",
-    "quantizeDevice", "packQ8Device", "packInt8RowsDevice", "quantizePackQ8Device"]) {
+  for (const name of ["abiVersion", "describe", "deviceCount", "init", "synchronize", "matvecQ8", "matvecQ8Ffn",
+    "matvecQ8Residual", "quantize", "packQ8", "packInt8Rows", "quantizePackQ8", "malloc", "free", "upload", "download",
+    "copy", "matvecQ8Device", "matvecQ8FfnDevice", "matvecQ8ResidualDevice", "quantizeDevice", "packQ8Device",
+    "packInt8RowsDevice", "quantizePackQ8Device"]) {
     assert.strictEqual(typeof a[name], "function", name);
   }
   assert.strictEqual(a.abiVersion(), 1);
@@ -158,6 +162,39 @@ gpuTest(F, "quantize + packQ8 compose as in the reference, and the fused form eq
   assertMatvecAgrees(matvec.matvecQ8(args), oracle.matvecQ8(args), args, "pipeline");
 });
 
+gpuTest(F, "matvecQ8Ffn / matvecQ8Residual KATs (ops/matvec/reference.test.ts:112-193)", () => {
+  for (const c of kat.matvec_q8_ffn) {
+    const weightGate = oracle.packQ8({ codes: Int32Array.from(c.gate_codes), N: c.N, K: c.K });
+    const weightUp = oracle.packQ8({ codes: Int32Array.from(c.up_codes), N: c.N, K: c.K });
+    const got = matvec.matvecQ8Ffn({ weightGate, scaleGate: Float32Array.from(c.scale_gate), weightUp,
+      scaleUp: Float32Array.from(c.scale_up), vector: Float32Array.from(c.vector), N: c.N, K: c.K });
+    c.want.forEach((w, i) => assert.ok(Math.abs(got[i] - w) < c.abs_tol, `${c.source}: row ${i} ${got[i]} vs ${w}`));
+  }
+  for (const c of kat.matvec_q8_residual) {
+    const weight = oracle.packQ8({ codes: Int32Array.from(c.codes), N: c.N, K: c.K });
+    const got = matvec.matvecQ8Residual({ weight, scale: Float32Array.from(c.scale), vector: Float32Array.from(c.vector),
+      residual: Float32Array.from(c.residual), N: c.N, K: c.K });
+    c.want.forEach((w, i) => assert.ok(Math.abs(got[i] - w) < c.abs_tol, `${c.source}: row ${i} ${got[i]} vs ${w}`));
+  }
+});
+
+gpuTest(F, "matvecQ8Ffn / matvecQ8Residual agree with the reference's composition at decode-layer shapes", () => {
+  for (const [N, K] of [[5632, 2048], [7, 1027], [300, 5632]]) {
+    const weightGate = matvec.packQ8({ codes: codeWave(N * K, 0.37), N, K });
+    const weightUp = matvec.packQ8({ codes: codeWave(N * K, 0.53, 1.1), N, K });
+    const scaleGate = scaleWave(N), scaleUp = Float32Array.from(scaleWave(N), (v) => v * 0.5);
+    const vector = wave(K, 0.11, 0.8);
+    const got = matvec.matvecQ8Ffn({ weightGate, scaleGate, weightUp, scaleUp, vector, N, K });
+    const ag = { weight: weightGate, scale: scaleGate, vector, N, K };
+    const au = { weight: weightUp, scale: scaleUp, vector, N, K };
+    assertFfnAgrees(got, oracle.matvecQ8(ag), oracle.matvecQ8(au), oracle.silu, ag, au, `ffn N=${N} K=${K}`);
+    const residual = wave(N, 0.29, 0.3);
+    const res = matvec.matvecQ8Residual({ weight: weightGate, scale: scaleGate, vector, residual, N, K });
+    assertResidualAgrees(res, oracle.matvecQ8Residual({ weight: weightGate, scale: scaleGate, vector, residual, N, K }),
+      ag, `residual N=${N} K=${K}`);
+  }
+});
+
 gpuTest(F, "runMatVecQ8 keeps llm/kernels.ts's signature (M = rows)", async () => {
   const N = 70000, K = 64;  // past WebGPU's 65,535-row dispatch limit, one call here
   const weight = matvec.packQ8({ codes: codeWave(N * K, 0.31), N, K });
@@ -199,5 +236,27 @@ gpuTest(F, "ResidentQ8Device: resident weights, one sync per batch, no allocatio
   }
   assert.strictEqual(dev.stats.buffersCreated, created);
   assert.strictEqual(dev.stats.submits, 4);
+  dev.destroy();
+});
+
+gpuTest(F, "ResidentQ8Device: fused FFN and an in-place residual add in one batch", async () => {
+  const dev = await createResidentQ8Device();
+  const N = 1024, K = 2048, W = K / 4;
+  const hw = (k, p) => matvec.packQ8({ codes: codeWave(N * K, k, p), N, K });
+  const wg = hw(0.37, 0), wu = hw(0.41, 0.5), wo = hw(0.23, 1.0);
+  const sg = scaleWave(N), su = scaleWave(N), so = scaleWave(N);
+  const buf = (a) => { const b = dev.createStorageBuffer(a.byteLength); dev.upload(b, 0, a); return b; };
+  const [bwg, bwu, bwo, bsg, bsu, bso] = [wg, wu, wo, sg, su, so].map(buf);
+  const vector = wave(K, 0.09), resid0 = wave(N, 0.17);
+  const bx = buf(vector), bres = buf(resid0), bh = dev.createStorageBuffer(N * 4);
+  const [h, r] = await dev.batch(
+    [{ kind: "matvecQ8Ffn", weightGate: bwg, scaleGate: bsg, weightUp: bwu, scaleUp: bsu, vector: bx, output: bh, N, K },
+     { kind: "matvecQ8Residual", weight: bwo, scale: bso, vector: bx, residual: bres, output: bres, N, K }],
+    [{ source: bh, sourceOffset: 0, length: N, type: "f32" }, { source: bres, sourceOffset: 0, length: N, type: "f32" }]);
+  const ag = { weight: wg, scale: sg, vector, N, K }, au = { weight: wu, scale: su, vector, N, K };
+  assertFfnAgrees(h, oracle.matvecQ8(ag), oracle.matvecQ8(au), oracle.silu, ag, au, "resident ffn");
+  const ao = { weight: wo, scale: so, vector, N, K };
+  assertResidualAgrees(r, oracle.matvecQ8Residual({ ...ao, residual: resid0 }), ao, "resident residual in place");
+  assert.strictEqual(W * 4 * N, wg.byteLength);
   dev.destroy();
 });

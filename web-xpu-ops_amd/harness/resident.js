@@ -2,7 +2,8 @@
 // engine, the MI355X counterpart of the reference's ResidentDevice
 // (harness/resident.ts:98-145, createResidentDevice :148, batch :231-382)
 // restricted to what the matvecQ8 path needs: storage buffers, uploads,
-// matvecQ8 / quantize+packQ8 ops and device copies recorded into one batch,
+// matvecQ8 (plain, fused FFN, fused residual) / quantize+packQ8 ops and device
+// copies recorded into one batch,
 // one synchronisation per batch, selective readback.
 //
 // Buffers are HBM allocations (hipMalloc) owned by the device object and freed
@@ -41,6 +42,9 @@ export class ResidentQ8Device {
   /**
    * Enqueues every op in order, waits once, then reads back only `readback`.
    * ops: { kind: "matvecQ8", weight, scale, vector, output, N, K, M? }
+   *      { kind: "matvecQ8Ffn", weightGate, scaleGate, weightUp, scaleUp, vector, output, N, K }
+   *      { kind: "matvecQ8Residual", weight, scale, vector, residual, output, N, K }
+   *        (output may be the residual buffer: the residual stream updated in place)
    *      { kind: "quantizePackQ8", input, N, K, packed, scales }
    *      { kind: "copy", src, srcOffset, dst, dstOffset, size }
    * readback: { source, sourceOffset, length, type: "f32" | "i32" | "u32" }
@@ -57,6 +61,28 @@ export class ResidentQ8Device {
           need(op.vector, M * op.K * 4, "vector");
           need(op.output, M * op.N * 4, "output");
           a.matvecQ8Device(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.output.ptr, op.N, op.K, M);
+          break;
+        }
+        case "matvecQ8Ffn": {
+          const bytes = op.N * Math.ceil(op.K / 4) * 4;
+          need(op.weightGate, bytes, "weightGate");
+          need(op.scaleGate, op.N * 4, "scaleGate");
+          need(op.weightUp, bytes, "weightUp");
+          need(op.scaleUp, op.N * 4, "scaleUp");
+          need(op.vector, op.K * 4, "vector");
+          need(op.output, op.N * 4, "output");
+          a.matvecQ8FfnDevice(op.weightGate.ptr, op.scaleGate.ptr, op.weightUp.ptr, op.scaleUp.ptr, op.vector.ptr,
+                              op.output.ptr, op.N, op.K);
+          break;
+        }
+        case "matvecQ8Residual": {
+          need(op.weight, op.N * Math.ceil(op.K / 4) * 4, "weight");
+          need(op.scale, op.N * 4, "scale");
+          need(op.vector, op.K * 4, "vector");
+          need(op.residual, op.N * 4, "residual");
+          need(op.output, op.N * 4, "output");
+          a.matvecQ8ResidualDevice(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.residual.ptr, op.output.ptr, op.N,
+                                   op.K);
           break;
         }
         case "quantizePackQ8": {

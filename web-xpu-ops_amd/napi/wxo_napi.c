@@ -227,6 +227,58 @@ static napi_value js_matvec_q8(napi_env env, napi_callback_info info) {
     return out;
 }
 
+/* matvecQ8Residual(weight u32, scale f32, vector f32, residual f32, N, K) -> Float32Array[N] */
+static napi_value js_matvec_q8_residual(napi_env env, napi_callback_info info) {
+    size_t argc = 6;
+    napi_value argv[6];
+    if (!get_args(env, info, 6, &argc, argv)) return NULL;
+    void *w, *s, *x, *r;
+    size_t lw, ls, lx, lr;
+    uint32_t N, K;
+    if (!get_typed(env, argv[0], napi_uint32_array, &w, &lw, "weight") ||
+        !get_typed(env, argv[1], napi_float32_array, &s, &ls, "scale") ||
+        !get_typed(env, argv[2], napi_float32_array, &x, &lx, "vector") ||
+        !get_typed(env, argv[3], napi_float32_array, &r, &lr, "residual") || !get_u32(env, argv[4], &N, "N") ||
+        !get_u32(env, argv[5], &K, "K"))
+        return NULL;
+    if (!need_len(env, lw, (uint64_t)N * words_per_row(K), "weight") || !need_len(env, ls, N, "scale") ||
+        !need_len(env, lx, K, "vector") || !need_len(env, lr, N, "residual"))
+        return NULL;
+    void* y;
+    napi_value out = new_typed(env, napi_float32_array, 4, N, &y);
+    if (!out) return NULL;
+    int st = wxo_matvec_q8_residual_host(w, s, x, r, y, N, K);
+    if (st != WXO_OK) return throw_status(env, st, "matvecQ8Residual");
+    return out;
+}
+
+/* matvecQ8Ffn(weightGate u32, scaleGate f32, weightUp u32, scaleUp f32, vector f32, N, K) -> Float32Array[N] */
+static napi_value js_matvec_q8_ffn(napi_env env, napi_callback_info info) {
+    size_t argc = 7;
+    napi_value argv[7];
+    if (!get_args(env, info, 7, &argc, argv)) return NULL;
+    void *wg, *sg, *wu, *su, *x;
+    size_t lwg, lsg, lwu, lsu, lx;
+    uint32_t N, K;
+    if (!get_typed(env, argv[0], napi_uint32_array, &wg, &lwg, "weightGate") ||
+        !get_typed(env, argv[1], napi_float32_array, &sg, &lsg, "scaleGate") ||
+        !get_typed(env, argv[2], napi_uint32_array, &wu, &lwu, "weightUp") ||
+        !get_typed(env, argv[3], napi_float32_array, &su, &lsu, "scaleUp") ||
+        !get_typed(env, argv[4], napi_float32_array, &x, &lx, "vector") || !get_u32(env, argv[5], &N, "N") ||
+        !get_u32(env, argv[6], &K, "K"))
+        return NULL;
+    const uint64_t nw = (uint64_t)N * words_per_row(K);
+    if (!need_len(env, lwg, nw, "weightGate") || !need_len(env, lsg, N, "scaleGate") ||
+        !need_len(env, lwu, nw, "weightUp") || !need_len(env, lsu, N, "scaleUp") || !need_len(env, lx, K, "vector"))
+        return NULL;
+    void* y;
+    napi_value out = new_typed(env, napi_float32_array, 4, N, &y);
+    if (!out) return NULL;
+    int st = wxo_matvec_q8_ffn_host(wg, sg, wu, su, x, y, N, K);
+    if (st != WXO_OK) return throw_status(env, st, "matvecQ8Ffn");
+    return out;
+}
+
 static napi_value js_quantize(napi_env env, napi_callback_info info) {
     size_t argc = 3;
     napi_value argv[3];
@@ -410,6 +462,42 @@ static napi_value js_matvec_q8_device(napi_env env, napi_callback_info info) {
     return NULL;
 }
 
+/* matvecQ8ResidualDevice(weight, scale, vector, residual, output, N, K): device addresses */
+static napi_value js_matvec_q8_residual_device(napi_env env, napi_callback_info info) {
+    size_t argc = 7;
+    napi_value argv[7];
+    uint64_t w, s, x, r, y;
+    uint32_t N, K;
+    if (!get_args(env, info, 7, &argc, argv) || !get_ptr(env, argv[0], &w, "weight") ||
+        !get_ptr(env, argv[1], &s, "scale") || !get_ptr(env, argv[2], &x, "vector") ||
+        !get_ptr(env, argv[3], &r, "residual") || !get_ptr(env, argv[4], &y, "output") ||
+        !get_u32(env, argv[5], &N, "N") || !get_u32(env, argv[6], &K, "K"))
+        return NULL;
+    int st = wxo_matvec_q8_residual((const uint32_t*)(uintptr_t)w, (const float*)(uintptr_t)s,
+                                    (const float*)(uintptr_t)x, (const float*)(uintptr_t)r, (float*)(uintptr_t)y, N,
+                                    K, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "matvecQ8ResidualDevice");
+    return NULL;
+}
+
+/* matvecQ8FfnDevice(weightGate, scaleGate, weightUp, scaleUp, vector, output, N, K): device addresses */
+static napi_value js_matvec_q8_ffn_device(napi_env env, napi_callback_info info) {
+    size_t argc = 8;
+    napi_value argv[8];
+    uint64_t wg, sg, wu, su, x, y;
+    uint32_t N, K;
+    if (!get_args(env, info, 8, &argc, argv) || !get_ptr(env, argv[0], &wg, "weightGate") ||
+        !get_ptr(env, argv[1], &sg, "scaleGate") || !get_ptr(env, argv[2], &wu, "weightUp") ||
+        !get_ptr(env, argv[3], &su, "scaleUp") || !get_ptr(env, argv[4], &x, "vector") ||
+        !get_ptr(env, argv[5], &y, "output") || !get_u32(env, argv[6], &N, "N") || !get_u32(env, argv[7], &K, "K"))
+        return NULL;
+    int st = wxo_matvec_q8_ffn((const uint32_t*)(uintptr_t)wg, (const float*)(uintptr_t)sg,
+                               (const uint32_t*)(uintptr_t)wu, (const float*)(uintptr_t)su,
+                               (const float*)(uintptr_t)x, (float*)(uintptr_t)y, N, K, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "matvecQ8FfnDevice");
+    return NULL;
+}
+
 static napi_value js_quantize_device(napi_env env, napi_callback_info info) {
     size_t argc = 5;
     napi_value argv[5];
@@ -468,6 +556,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"init", NULL, js_init, NULL, NULL, NULL, napi_enumerable, NULL},
         {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8", NULL, js_matvec_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8Residual", NULL, js_matvec_q8_residual, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8Ffn", NULL, js_matvec_q8_ffn, NULL, NULL, NULL, napi_enumerable, NULL},
         {"quantize", NULL, js_quantize, NULL, NULL, NULL, napi_enumerable, NULL},
         {"packQ8", NULL, js_pack_q8, NULL, NULL, NULL, napi_enumerable, NULL},
         {"packInt8Rows", NULL, js_pack_int8_rows, NULL, NULL, NULL, napi_enumerable, NULL},
@@ -478,6 +568,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
         {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8ResidualDevice", NULL, js_matvec_q8_residual_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8FfnDevice", NULL, js_matvec_q8_ffn_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"quantizeDevice", NULL, js_quantize_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"packQ8Device", NULL, js_pack_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"packInt8RowsDevice", NULL, js_pack_int8_rows_device, NULL, NULL, NULL, napi_enumerable, NULL},

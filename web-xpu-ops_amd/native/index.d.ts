@@ -6,6 +6,8 @@ export interface WxoAddon {
   init(): void;
   synchronize(): void;
   matvecQ8(weight: Uint32Array, scale: Float32Array, vector: Float32Array, N: number, K: number, M?: number): Float32Array;
+  matvecQ8Residual(weight: Uint32Array, scale: Float32Array, vector: Float32Array, residual: Float32Array, N: number, K: number): Float32Array;
+  matvecQ8Ffn(weightGate: Uint32Array, scaleGate: Float32Array, weightUp: Uint32Array, scaleUp: Float32Array, vector: Float32Array, N: number, K: number): Float32Array;
   quantize(input: Float32Array, N: number, D: number): { output: Int32Array; scales: Float32Array };
   packQ8(codes: Int32Array, N: number, K: number): Uint32Array;
   packInt8Rows(codes: Int8Array, N: number, K: number): Uint32Array;
@@ -16,6 +18,8 @@ export interface WxoAddon {
   download<T extends ArrayBufferView>(ptr: bigint, into: T): T;
   copy(dst: bigint, src: bigint, bytes: number): void;
   matvecQ8Device(weight: bigint, scale: bigint, vector: bigint, output: bigint, N: number, K: number, M?: number): void;
+  matvecQ8ResidualDevice(weight: bigint, scale: bigint, vector: bigint, residual: bigint, output: bigint, N: number, K: number): void;
+  matvecQ8FfnDevice(weightGate: bigint, scaleGate: bigint, weightUp: bigint, scaleUp: bigint, vector: bigint, output: bigint, N: number, K: number): void;
   quantizeDevice(input: bigint, N: number, D: number, output: bigint, scales: bigint): void;
   packQ8Device(codes: bigint, N: number, K: number, packed: bigint): void;
   packInt8RowsDevice(codes: bigint, N: number, K: number, packed: bigint): void;

@@ -1,5 +1,6 @@
-// ops/matvec: matvecQ8 and packQ8 on the MI355X, with the reference's op API
-// (ops/matvec/reference.ts:99-131 matvecQ8, :267-283 packQ8, exported the same
+// ops/matvec: matvecQ8, its fused decode forms and packQ8 on the MI355X, with
+// the reference's op API (ops/matvec/reference.ts:99-131 matvecQ8, :196-207
+// matvecQ8Ffn, :235-243 matvecQ8Residual, :267-283 packQ8, exported the same
 // way as ops/matvec/index.ts:1-11).
 //
 // Same call shapes and data formats as the reference: the weight is
@@ -30,6 +31,23 @@ export function matvecQ8(first, weight, scale, N, K) {
  */
 export function matvecQ8Batched({ weight, scale, vectors, N, K, M }) {
   return native().matvecQ8(weight, scale, vectors, N, K, M);
+}
+
+/**
+ * `matvecQ8Ffn({ weightGate, scaleGate, weightUp, scaleUp, vector, N, K })` ->
+ * Float32Array [N]: silu(gate row) * up row (ops/matvec/reference.ts:196-207),
+ * both weights streamed in one pass.
+ */
+export function matvecQ8Ffn({ weightGate, scaleGate, weightUp, scaleUp, vector, N, K }) {
+  return native().matvecQ8Ffn(weightGate, scaleGate, weightUp, scaleUp, vector, N, K);
+}
+
+/**
+ * `matvecQ8Residual({ weight, scale, vector, residual, N, K })` ->
+ * Float32Array [N]: residual + matvecQ8 row (ops/matvec/reference.ts:235-243).
+ */
+export function matvecQ8Residual({ weight, scale, vector, residual, N, K }) {
+  return native().matvecQ8Residual(weight, scale, vector, residual, N, K);
 }
 
 /**
