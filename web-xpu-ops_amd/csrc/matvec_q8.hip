@@ -342,6 +342,37 @@ __device__ __forceinline__ bf16x8 codes_to_bf16(uint32_t w0, uint32_t w1) {
 // output.
 constexpr uint32_t kTileSlotFloats = 16u * 17u;  // one 16 x 16 block, rows skewed by a float
 
+// Splits the four vector entries k .. k+3 of column m (v; entries past K count
+// as 0) into bf16 parts h, m, l and stores them in B-operand order:
+// [part][32-code block][lane group][column] x 8 bf16.  Code k sits in block
+// (k / 256) * 8 + ((k / 64) % 4) * 2 + (k / 8) % 2, lane group (k / 16) % 4,
+// element k % 8: the order in which the matrix-core kernels read them.
+__device__ __forceinline__ void store_x_parts(uint16_t* xparts, uint32_t MC, uint32_t Kp, uint32_t K, uint32_t m,
+                                              uint32_t k, u32x4v v) {
+    uint16_t hh[4], mm[4], ll[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        // entries past K belong to the next vector (or read 0): zero them
+        const float xe = (k + (uint32_t)e < K) ? __uint_as_float(v[e]) : 0.0f;
+        const uint32_t hb = __float_as_uint(xe) & 0xffff0000u;
+        uint32_t mb = 0u, lb = 0u;
+        if (isfinite(xe)) {
+            const float r1 = xe - __uint_as_float(hb);  // exact
+            mb = __float_as_uint(r1) & 0xffff0000u;
+            lb = __float_as_uint(r1 - __uint_as_float(mb));  // exact, <= 8 significant bits
+        }
+        hh[e] = (uint16_t)(hb >> 16);
+        mm[e] = (uint16_t)(mb >> 16);
+        ll[e] = (uint16_t)(lb >> 16);
+    }
+    const uint32_t blk = (k >> 8) * 8u + ((k >> 6) & 3u) * 2u + ((k >> 3) & 1u);
+    const uint32_t at = ((blk * 4u + ((k >> 4) & 3u)) * MC + m) * 8u + (k & 7u);
+    typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<u16x4*>(&xparts[at]) = u16x4{hh[0], hh[1], hh[2], hh[3]};
+    *reinterpret_cast<u16x4*>(&xparts[Kp * MC + at]) = u16x4{mm[0], mm[1], mm[2], mm[3]};
+    *reinterpret_cast<u16x4*>(&xparts[2u * Kp * MC + at]) = u16x4{ll[0], ll[1], ll[2], ll[3]};
+}
+
 template <int T, int D>
 __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
@@ -415,30 +446,7 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
 
     auto split_store = [&](uint32_t idx, u32x4v v) {
         const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
-        uint16_t hh[4], mm[4], ll[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            // entries past K belong to the next vector (or read 0): zero them
-            const float xe = (k + (uint32_t)e < K) ? __uint_as_float(v[e]) : 0.0f;
-            const uint32_t hb = __float_as_uint(xe) & 0xffff0000u;
-            uint32_t mb = 0u, lb = 0u;
-            if (isfinite(xe)) {
-                const float r1 = xe - __uint_as_float(hb);  // exact
-                mb = __float_as_uint(r1) & 0xffff0000u;
-                lb = __float_as_uint(r1 - __uint_as_float(mb));  // exact, <= 8 significant bits
-            }
-            hh[e] = (uint16_t)(hb >> 16);
-            mm[e] = (uint16_t)(mb >> 16);
-            ll[e] = (uint16_t)(lb >> 16);
-        }
-        // code k sits in block (k / 256) * 8 + ((k / 64) % 4) * 2 + (k / 8) % 2,
-        // lane group (k / 16) % 4, element k % 8 (the order compute() reads)
-        const uint32_t blk = (k >> 8) * 8u + ((k >> 6) & 3u) * 2u + ((k >> 3) & 1u);
-        const uint32_t at = ((blk * 4u + ((k >> 4) & 3u)) * MC + m) * 8u + (k & 7u);
-        typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<u16x4*>(&xparts[at]) = u16x4{hh[0], hh[1], hh[2], hh[3]};
-        *reinterpret_cast<u16x4*>(&xparts[Kp * MC + at]) = u16x4{mm[0], mm[1], mm[2], mm[3]};
-        *reinterpret_cast<u16x4*>(&xparts[2u * Kp * MC + at]) = u16x4{ll[0], ll[1], ll[2], ll[3]};
+        store_x_parts(xparts, MC, Kp, K, m, k, v);
     };
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
@@ -518,6 +526,196 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
         for (int q = 0; q < D; ++q) {
             issue(i + (uint32_t)(q + D - 1), buf[(q + D - 1) % D], sbuf[(q + D - 1) % D]);
             if (q == 0 || i + (uint32_t)q < total) compute(i + (uint32_t)q, buf[q], sbuf[q]);
+        }
+    }
+}
+
+// The same kernel with the weight tiles fetched straight into LDS
+// (buffer_load_dwordx4 ... lds): one instruction moves 4 rows x 256 bytes,
+// whole 128-byte lines, where the register form can only fetch 64 bytes of
+// each of 16 rows.  Each wave owns D stages of T x 4 KiB.  Piece q (16 bytes)
+// of row j of a tile is stored at position q ^ j of that row, so the 16 lanes
+// that read one piece of 16 different rows hit 16 different bank groups.
+// Waits are explicit, since the compiler does not track these loads: every
+// LDS read of a stage completes (lgkmcnt(0)) before the stage is refilled,
+// and a stage is read only after its loads have landed (vmcnt, counting the
+// loads issued after it; vector stores count there too, which can only make
+// the wait longer).
+constexpr uint32_t kDmaTileBytes = 16u * 256u;
+
+template <int T, int D>
+__global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M, uint32_t Kp) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t xparts[];  // x parts, weight stages, tile slots
+    const uint32_t m0 = blockIdx.y * 16u;
+    const uint32_t MC = min(16u, M - m0);
+
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t jb = min(j, MC - 1u);
+    uint8_t* stages = reinterpret_cast<uint8_t*>(xparts + 3u * MC * Kp);
+    uint8_t* wst = stages + wv * ((uint32_t)D * T * kDmaTileBytes);
+    float* slot = reinterpret_cast<float*>(stages + 4u * D * T * kDmaTileBytes) + wv * kTileSlotFloats;
+    const uint32_t rowbytes = W * 4u;
+    const uint32_t ntiles = (N + 15u) / 16u;
+    const uint32_t S = Kp / 256u;
+    const uint32_t b0 = (uint32_t)((uint64_t)blockIdx.x * ntiles / gridDim.x);
+    const uint32_t b1 = (uint32_t)((uint64_t)(blockIdx.x + 1u) * ntiles / gridDim.x);
+    const uint32_t t0 = b0 + (b1 - b0) * wv / 4u, t1 = b0 + (b1 - b0) * (wv + 1u) / 4u;
+    const uint32_t ngroups = (t1 - t0 + T - 1) / T;
+    const uint32_t total = ngroups * S;
+    const uint32_t r_lane = (lane & 3u) * 4u;
+    // load instruction ii of a tile: lane -> row 4 ii + lane / 16, stored at
+    // position lane % 16, which holds piece (lane % 16) ^ row
+    int voff[4];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+        const uint32_t row = 4u * (uint32_t)ii + (lane >> 4);
+        voff[ii] = (int)(row * rowbytes + (((lane & 15u) ^ row) * 16u));
+    }
+
+    auto issue = [&](uint32_t i, u32x4v (&sc)[T]) {
+        const uint32_t step = i % S;
+        const uint32_t tile0 = i < total ? t0 + (i / S) * T : 0u;
+        const uint32_t rows = i < total ? min((uint32_t)T * 16u, min(t1 * 16u, N) - tile0 * 16u) : 0u;
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)tile0 * 16u * W, rows * rowbytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + tile0 * 16u, step == S - 1u ? rows * 4u : 0u);
+        uint8_t* sb = wst + (i % (uint32_t)D) * ((uint32_t)T * kDmaTileBytes);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int so = (int)((uint32_t)t * 16u * rowbytes + step * 256u);
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    wrs, (__attribute__((address_space(3))) void*)(sb + (uint32_t)t * kDmaTileBytes + (uint32_t)ii * 1024u),
+                    16, voff[ii], so, 0, kCachePolicyNT);
+            sc[t] = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(((uint32_t)t * 16u + r_lane) * 4u), 0, 0);
+        }
+    };
+
+    constexpr int XU = 16;
+    const uint32_t kq4 = Kp / 4u;
+    const uint32_t n4 = MC * kq4;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x + (size_t)m0 * K, MC * K * 4u);
+    u32x4v xv[XU];
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+        const uint32_t idx = threadIdx.x + (uint32_t)u * 256u;
+        const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
+        const int off = idx < n4 ? (int)((m * K + k) * 4u) : (int)0x7ffffff0;
+        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+    }
+    u32x4v sbuf[D][T];
+#pragma unroll
+    for (int q = 0; q < D - 1; ++q) issue((uint32_t)q, sbuf[q]);
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+        const uint32_t idx = threadIdx.x + (uint32_t)u * 256u;
+        if (idx < n4) {
+            const uint32_t m = idx / kq4;
+            store_x_parts(xparts, MC, Kp, K, m, (idx - m * kq4) * 4u, xv[u]);
+        }
+    }
+    for (uint32_t idx = threadIdx.x + XU * 256u; idx < n4; idx += 256u) {
+        const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
+        store_x_parts(xparts, MC, Kp, K, m, k, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((m * K + k) * 4u), 0, 0));
+    }
+    // The x parts are this workgroup's own LDS writes: wait for them and meet
+    // at a plain barrier (a fence here would also wait for the weight stages
+    // already in flight).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 hi[T], lo[T], hs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        hi[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        lo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        hs[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const uint16_t* xb = &xparts[(g * MC + jb) * 8u];
+    const uint32_t pstride = Kp * MC;
+    const uint32_t bstride = 32u * MC;
+    const uint32_t arow = (j >> 2) * 1024u + (j & 3u) * 256u;  // row j of a tile in a stage
+
+    auto compute = [&](uint32_t i, const u32x4v (&sc)[T]) {
+        const uint32_t step = i % S;
+        const uint16_t* xs = xb + step * 8u * bstride;
+        const uint8_t* sb = wst + (i % (uint32_t)D) * ((uint32_t)T * kDmaTileBytes);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            u32x4v a[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                a[t] = *reinterpret_cast<const u32x4v*>(sb + (uint32_t)t * kDmaTileBytes + arow +
+                                                        (((4u * (uint32_t)u + g) ^ j) * 16u));
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t kb = ((uint32_t)u * 2u + (uint32_t)e) * bstride;
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(xs + kb);
+                const bf16x8 bm = *reinterpret_cast<const bf16x8*>(xs + pstride + kb);
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(xs + 2u * pstride + kb);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const bf16x8 av = codes_to_bf16(a[t][2 * e], a[t][2 * e + 1]);
+                    hi[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh, hi[t], 0, 0, 0);
+                    lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bm, lo[t], 0, 0, 0);
+                    lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl, lo[t], 0, 0, 0);
+                }
+            }
+        }
+        if (step % 4u == 3u) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                hs[t] += hi[t];
+                hi[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if (step == S - 1u) {
+            const uint32_t tile0 = t0 + (i / S) * T;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const f32x4 v = (hs[t] + hi[t]) + lo[t];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) slot[j * 17u + g * 4u + (uint32_t)q] = v[q];
+                hi[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                lo[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                hs[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const uint32_t c = lane >> 2;
+                const uint32_t row0 = (tile0 + (uint32_t)t) * 16u;
+                if (c < MC && tile0 + (uint32_t)t < t1) {
+                    float* yo = y + (size_t)(m0 + c) * N + row0 + r_lane;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (row0 + r_lane + (uint32_t)q < N)
+                            yo[q] = slot[c * 17u + r_lane + (uint32_t)q] * __uint_as_float(sc[t][q]);
+                }
+            }
+        }
+    };
+
+    // vmcnt encoding (gfx9): low 4 bits in [3:0], high 2 bits in [15:14];
+    // expcnt 7 and lgkmcnt 15 leave those counters unconstrained.
+    constexpr int kAfter = (D - 1) * 5 * T;  // loads issued after a stage's own
+    constexpr int kVmWait = 0x0f70 | (kAfter & 15) | ((kAfter >> 4) << 14);
+    static_assert(kAfter < 64, "vmcnt holds at most 63");
+    for (uint32_t i = 0; i < total; i += (uint32_t)D) {
+#pragma unroll
+        for (int q = 0; q < D; ++q) {
+            // the stage refilled next was read by the previous pair: its LDS
+            // reads must have completed
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_sched_barrier(0);
+            issue(i + (uint32_t)(q + D - 1), sbuf[(q + D - 1) % D]);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(kVmWait);  // this pair's loads have landed
+            __builtin_amdgcn_sched_barrier(0);
+            if (q == 0 || i + (uint32_t)q < total) compute(i + (uint32_t)q, sbuf[q]);
         }
     }
 }
@@ -629,9 +827,12 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
         return launch_fill_scaled_zero(a.scale, a.output, a.N, a.M, stream);
     }
     if (a.M == 1) return dispatch_m1<kEpiPlain>(a, dev, stream, variant);
-    // Batched on the matrix cores when the tile's x parts fit in LDS.  Two
-    // tiles per step share each B read when the tile holds 12 or more
-    // vectors (wider B reads), one tile with a deeper pipeline otherwise.
+    // Batched on the matrix cores when the tile's x parts fit in LDS.  Up to
+    // 11 vectors per tile: weight tiles loaded straight into LDS, one tile per
+    // step up to 4 vectors, two from 5.  From 12 vectors (or when the LDS
+    // stages do not fit): weight tiles in registers, two tiles per step
+    // sharing each B read from 12 vectors, one tile with a deeper pipeline
+    // below.
     {
         const uint32_t Kp = (a.K + 255u) / 256u * 256u;
         const uint32_t MC = a.M < 16u ? a.M : 16u;
@@ -642,6 +843,26 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
             const uint32_t wgs = (uint32_t)(kMfmaLdsBytes / lds) < 2u ? (uint32_t)(kMfmaLdsBytes / lds) : 2u;
             const uint32_t grid = min((ntiles + 3u) / 4u, cus * wgs);
             const dim3 g(grid, (a.M + 15u) / 16u);
+            // Up to 11 vectors the weight tiles go straight into LDS (whole
+            // 128-byte lines per load instruction); from 12 on the x parts
+            // leave too little LDS for the stages and the register form wins.
+            if (MC <= 11u) {
+                const bool one = MC <= 4u;  // one tile per step, two stages
+                const uint64_t ldsd =
+                    3ull * MC * Kp * 2u + 4ull * 2u * (one ? 1u : 2u) * kDmaTileBytes + 4ull * kTileSlotFloats * 4u;
+                if (ldsd <= kMfmaLdsBytes) {
+                    const uint32_t wg2 = (uint32_t)(kMfmaLdsBytes / ldsd) < 2u ? 1u : 2u;
+                    const dim3 g2(min((ntiles + 3u) / 4u, cus * wg2), (a.M + 15u) / 16u);
+                    if (one)
+                        hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<1, 2>), g2, dim3(256), (size_t)ldsd, stream,
+                                           a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
+                    else
+                        hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<2, 2>), g2, dim3(256), (size_t)ldsd, stream,
+                                           a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
+                    if (variant) *variant = "mb.mfma_dma";
+                    return hipGetLastError();
+                }
+            }
             if (MC >= 12u)
                 hipLaunchKernelGGL((matvec_q8_mfma_kernel<2, 2>), g, dim3(256), (size_t)lds, stream, a.weight, a.scale,
                                    a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
