@@ -452,7 +452,7 @@ def test_quantize_exact_half_ties_after_rounded_product():
     assert packed.tolist() == [0x0000C17F, 0x0000407F, 0x0000407F]
 
 
-@pytest.mark.parametrize("D", [1, 3, 4, 5, 64, 300, 517, 1023, 2048, 4096, 4099, 5632, 6144, 9000, 20001])
+@pytest.mark.parametrize("D", [1, 3, 4, 5, 64, 300, 517, 1023, 2048, 4096, 4099, 5632, 6144, 8000, 8192, 9000, 20001])
 def test_quantize_edges_bit_exact(D):
     rng = np.random.default_rng(D)
     N = 24

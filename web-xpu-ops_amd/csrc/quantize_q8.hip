@@ -41,49 +41,34 @@ __device__ __forceinline__ int32_t js_quantize_code(float x, double inverse) {
     return (int32_t)r;  // -0 -> 0
 }
 
-// Four consecutive row values starting at column 4w (zero past K).
-__device__ __forceinline__ f32x4_a4 load_row4(const float* __restrict__ xr, uint32_t K, uint32_t w) {
-    const uint32_t k = 4u * w;
-    if (k + 4u <= K) return load_f32x4(xr + k);
-    f32x4_a4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (k + 0u < K) v.x = xr[k + 0];
-    if (k + 1u < K) v.y = xr[k + 1];
-    if (k + 2u < K) v.z = xr[k + 2];
-    return v;
-}
-
-__device__ __forceinline__ uint32_t abs_bits_max(f32x4_a4 v, uint32_t m) {
-    m = max(m, __float_as_uint(v.x) & 0x7fffffffu);
-    m = max(m, __float_as_uint(v.y) & 0x7fffffffu);
-    m = max(m, __float_as_uint(v.z) & 0x7fffffffu);
-    m = max(m, __float_as_uint(v.w) & 0x7fffffffu);
+__device__ __forceinline__ uint32_t abs_bits_max(u32x4v v, uint32_t m) {
+    m = max(m, v.x & 0x7fffffffu);
+    m = max(m, v.y & 0x7fffffffu);
+    m = max(m, v.z & 0x7fffffffu);
+    m = max(m, v.w & 0x7fffffffu);
     return m;
 }
 
+// Codes of word w of a row (four values, 0 past K) to the packed word and/or
+// the int32 codes.  Stores go through resources that span exactly the row's
+// words / codes, so the pieces past W or K are dropped without a branch.
 template <bool CODES, bool PACK>
-__device__ __forceinline__ void emit_word(f32x4_a4 v, double inverse, uint32_t row, uint32_t w, uint32_t K,
-                                          uint32_t W, int32_t* __restrict__ codes, uint32_t* __restrict__ packed) {
-    const int32_t c0 = js_quantize_code(v.x, inverse);
-    const int32_t c1 = js_quantize_code(v.y, inverse);
-    const int32_t c2 = js_quantize_code(v.z, inverse);
-    const int32_t c3 = js_quantize_code(v.w, inverse);
-    const uint32_t k = 4u * w;
+__device__ __forceinline__ void emit_word(u32x4v v, double inverse, uint32_t w, __amdgpu_buffer_rsrc_t crs,
+                                          __amdgpu_buffer_rsrc_t prs) {
+    const int32_t c0 = js_quantize_code(__uint_as_float(v.x), inverse);
+    const int32_t c1 = js_quantize_code(__uint_as_float(v.y), inverse);
+    const int32_t c2 = js_quantize_code(__uint_as_float(v.z), inverse);
+    const int32_t c3 = js_quantize_code(__uint_as_float(v.w), inverse);
     if constexpr (PACK) {
         // Pad lanes past K were loaded as 0.0 and quantize to 0 (0 * inverse
         // is 0 or NaN), so the word's unused high bytes are zero as packQ8's.
         const uint32_t word = ((uint32_t)c0 & 0xffu) | (((uint32_t)c1 & 0xffu) << 8) |
                               (((uint32_t)c2 & 0xffu) << 16) | (((uint32_t)c3 & 0xffu) << 24);
-        packed[(size_t)row * W + w] = word;
+        __builtin_amdgcn_raw_buffer_store_b32(word, prs, (int)(w * 4u), 0, 0);
     }
     if constexpr (CODES) {
-        int32_t* out = codes + (size_t)row * K + k;
-        if (k + 4u <= K) {
-            *reinterpret_cast<i32x4_a4*>(out) = i32x4_a4{c0, c1, c2, c3};
-        } else {
-            if (k + 0u < K) out[0] = c0;
-            if (k + 1u < K) out[1] = c1;
-            if (k + 2u < K) out[2] = c2;
-        }
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4v{(uint32_t)c0, (uint32_t)c1, (uint32_t)c2, (uint32_t)c3}, crs,
+                                               (int)(w * 16u), 0, 0);
     }
 }
 
@@ -101,30 +86,47 @@ __device__ __forceinline__ void row_scale(uint32_t amax, float* scale, double* i
     }
 }
 
-// WPL > 0: the row's words l, l+64, ... (WPL of them) stay in VGPRs.
-// WPL == 0: any K; two passes over the row.
+// One wave per row.  Every load is a raw-buffer dwordx4 through a resource
+// spanning exactly the row's K floats: gfx950 clamps per dword, so entries
+// past K read as 0 and there is no per-lane tail branch (such a branch makes
+// the compiler join load sequences of different length and wait for each
+// load in turn, one memory round trip per word).
+// WPL > 0: the row's words l, l+64, ... (WPL of them) are all requested at
+// once and stay in VGPRs.  WPL == 0: any K; two passes over the row, four
+// words per lane in flight per pass step.
 template <int WPL, bool CODES, bool PACK>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ input, uint32_t N,
                                                             uint32_t K, uint32_t W, int32_t* __restrict__ codes,
                                                             uint32_t* __restrict__ packed,
                                                             float* __restrict__ scales) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t row = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= N) return;  // wave-uniform; no barriers in this kernel
-    const float* xr = input + (size_t)row * K;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(input + (size_t)row * K, K * 4u);
+    const __amdgpu_buffer_rsrc_t crs = make_rsrc(CODES ? (const void*)(codes + (size_t)row * K) : nullptr,
+                                                 CODES ? K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(PACK ? (const void*)(packed + (size_t)row * W) : nullptr,
+                                                 PACK ? W * 4u : 0u);
 
     uint32_t m = 0;
     constexpr int S = WPL > 0 ? WPL : 1;
-    f32x4_a4 v[S];
+    u32x4v v[S];
     if constexpr (WPL > 0) {
 #pragma unroll
-        for (int i = 0; i < WPL; ++i) {
-            const uint32_t w = lane + 64u * (uint32_t)i;
-            v[i] = (w < W) ? load_row4(xr, K, w) : f32x4_a4{0.0f, 0.0f, 0.0f, 0.0f};
-            m = abs_bits_max(v[i], m);
-        }
+        for (int i = 0; i < WPL; ++i)
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((lane + 64u * (uint32_t)i) * 16u), 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < WPL; ++i) m = abs_bits_max(v[i], m);
     } else {
-        for (uint32_t w = lane; w < W; w += 64u) m = abs_bits_max(load_row4(xr, K, w), m);
+        for (uint32_t w = lane; w < W; w += 256u) {
+            u32x4v t[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                t[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((w + 64u * (uint32_t)i) * 16u), 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m = abs_bits_max(t[i], m);
+        }
     }
     const uint32_t amax = wave_max_u32(m);
     float scale;
@@ -134,13 +136,128 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
 
     if constexpr (WPL > 0) {
 #pragma unroll
-        for (int i = 0; i < WPL; ++i) {
-            const uint32_t w = lane + 64u * (uint32_t)i;
-            if (w < W) emit_word<CODES, PACK>(v[i], inverse, row, w, K, W, codes, packed);
+        for (int i = 0; i < WPL; ++i) emit_word<CODES, PACK>(v[i], inverse, lane + 64u * (uint32_t)i, crs, prs);
+    } else {
+        for (uint32_t w = lane; w < W; w += 256u) {
+            u32x4v t[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                t[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((w + 64u * (uint32_t)i) * 16u), 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) emit_word<CODES, PACK>(t[i], inverse, w + 64u * (uint32_t)i, crs, prs);
+        }
+    }
+}
+
+// f32 fast path for one word's codes, exact by construction.  With
+// inv32 = fl32(inverse), v32 = fl32(x * inv32) differs from JS's
+// v = fl64(x * inverse) by at most 2^-24 |v| (product) + 2^-24 |v| (inverse)
+// + 2^-53 |v| < 2^-15 for |v| <= 128, so rint(v32) is the integer nearest v,
+// and equals Math.round(v), unless v32 lies within 2^-15 of a half-integer.
+// Those words (any lane of the wave) are redone in f64.  The caller uses this
+// only when inverse is finite in f32.
+template <bool CODES, bool PACK>
+__device__ __forceinline__ void emit_word_fast(u32x4v v, float inv32, double inverse, uint32_t w,
+                                               __amdgpu_buffer_rsrc_t crs, __amdgpu_buffer_rsrc_t prs) {
+    int32_t c[4];
+    bool near = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x = __uint_as_float(v[e]);
+        const float p = x * inv32;
+        const float r = rintf(p);
+        near |= fabsf(fabsf(p - r) - 0.5f) < 0x1p-15f;
+        const int32_t ci = (int32_t)(p == p ? r : 0.0f);  // NaN -> 0 (Int32Array store), |r| <= 128
+        c[e] = min(max(ci, -127), 127);
+    }
+    if (__builtin_amdgcn_ballot_w64(near) != 0ull) {  // wave-uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c[e] = js_quantize_code(__uint_as_float(v[e]), inverse);
+    }
+    if constexpr (PACK) {
+        const uint32_t word = ((uint32_t)c[0] & 0xffu) | (((uint32_t)c[1] & 0xffu) << 8) |
+                              (((uint32_t)c[2] & 0xffu) << 16) | (((uint32_t)c[3] & 0xffu) << 24);
+        __builtin_amdgcn_raw_buffer_store_b32(word, prs, (int)(w * 4u), 0, 0);
+    }
+    if constexpr (CODES) {
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4v{(uint32_t)c[0], (uint32_t)c[1], (uint32_t)c[2], (uint32_t)c[3]},
+                                               crs, (int)(w * 16u), 0, 0);
+    }
+}
+
+// One 256-thread workgroup per row: thread t owns words t, t + 256, ...
+// (WPT of them, requested at once through the row's buffer resource), the
+// four waves' absmax meet in LDS, and every thread derives scale and inverse
+// itself.  A quarter of the codes per lane of the one-wave form keeps the
+// compute left after a row's last bytes arrive short.  WPT == 0: any K, two
+// passes over the row.
+template <int WPT, bool CODES, bool PACK>
+__global__ __launch_bounds__(256) void quantize_row_wg_kernel(const float* __restrict__ input, uint32_t N,
+                                                              uint32_t K, uint32_t W, int32_t* __restrict__ codes,
+                                                              uint32_t* __restrict__ packed,
+                                                              float* __restrict__ scales) {
+    __shared__ uint32_t wmax[4];
+    const uint32_t t = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(input + (size_t)row * K, K * 4u);
+    const __amdgpu_buffer_rsrc_t crs = make_rsrc(CODES ? (const void*)(codes + (size_t)row * K) : nullptr,
+                                                 CODES ? K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(PACK ? (const void*)(packed + (size_t)row * W) : nullptr,
+                                                 PACK ? W * 4u : 0u);
+    uint32_t m = 0;
+    constexpr int S = WPT > 0 ? WPT : 1;
+    u32x4v v[S];
+    if constexpr (WPT > 0) {
+#pragma unroll
+        for (int i = 0; i < WPT; ++i)
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((t + 256u * (uint32_t)i) * 16u), 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) m = abs_bits_max(v[i], m);
+    } else {
+        for (uint32_t w = t; w < W; w += 1024u) {
+            u32x4v q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                q[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((w + 256u * (uint32_t)i) * 16u), 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m = abs_bits_max(q[i], m);
+        }
+    }
+    m = wave_max_u32(m);
+    if ((t & 63u) == 0u) wmax[t >> 6] = m;
+    __syncthreads();
+    const uint32_t amax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+    float scale;
+    double inverse;
+    row_scale(amax, &scale, &inverse);
+    if (t == 0) scales[row] = scale;
+    const float inv32 = (float)inverse;
+    const bool fast = !isinf(inv32);  // row-uniform
+
+    if constexpr (WPT > 0) {
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) {
+            const uint32_t w = t + 256u * (uint32_t)i;
+            if (fast)
+                emit_word_fast<CODES, PACK>(v[i], inv32, inverse, w, crs, prs);
+            else
+                emit_word<CODES, PACK>(v[i], inverse, w, crs, prs);
         }
     } else {
-        for (uint32_t w = lane; w < W; w += 64u)
-            emit_word<CODES, PACK>(load_row4(xr, K, w), inverse, row, w, K, W, codes, packed);
+        for (uint32_t w = t; w < W; w += 1024u) {
+            u32x4v q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                q[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((w + 256u * (uint32_t)i) * 16u), 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (fast)
+                    emit_word_fast<CODES, PACK>(q[i], inv32, inverse, w + 256u * (uint32_t)i, crs, prs);
+                else
+                    emit_word<CODES, PACK>(q[i], inverse, w + 256u * (uint32_t)i, crs, prs);
+            }
+        }
     }
 }
 
@@ -156,20 +273,32 @@ hipError_t launch_q(const float* input, uint32_t N, uint32_t K, int32_t* codes, 
     return hipGetLastError();
 }
 
+template <int WPT, bool CODES, bool PACK>
+hipError_t launch_qwg(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed, float* scales,
+                      hipStream_t stream) {
+    const uint32_t W = (K + 3u) / 4u;
+    hipLaunchKernelGGL((quantize_row_wg_kernel<WPT, CODES, PACK>), dim3(N), dim3(256), 0, stream, input, N, K, W,
+                       codes, packed, scales);
+    return hipGetLastError();
+}
+
 template <bool CODES, bool PACK>
 hipError_t dispatch_q(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed, float* scales,
                       hipStream_t stream, const char** variant) {
     const uint32_t W = (K + 3u) / 4u;
-    const uint32_t wpl = (W + 63u) / 64u;
-    if (variant) *variant = "rows.reg";
-    if (wpl <= 1) return launch_q<1, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (wpl <= 2) return launch_q<2, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (wpl <= 4) return launch_q<4, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (wpl <= 8) return launch_q<8, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (wpl <= 16) return launch_q<16, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (wpl <= 24) return launch_q<24, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (variant) *variant = "rows.twopass";
-    return launch_q<0, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (variant) *variant = "row.wg";
+    // Short rows: one wave per row (a workgroup per row would leave most of
+    // its lanes without a word).
+    if (W <= 64u) return launch_q<1, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (W <= 128u) return launch_q<2, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    const uint32_t wpt = (W + 255u) / 256u;
+    if (wpt <= 1) return launch_qwg<1, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (wpt <= 2) return launch_qwg<2, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (wpt <= 4) return launch_qwg<4, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (wpt <= 6) return launch_qwg<6, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (wpt <= 8) return launch_qwg<8, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (variant) *variant = "row.wg.twopass";
+    return launch_qwg<0, CODES, PACK>(input, N, K, codes, packed, scales, stream);
 }
 
 }  // namespace

@@ -108,6 +108,8 @@ int validate_matvec(const uint32_t* w, const float* s, const float* x, const flo
 }
 
 int validate_rows(const void* in, uint32_t N, uint32_t K, const char* in_name) {
+    // Kernels address one row with 32-bit buffer offsets.
+    if (K >= (1u << 27)) return fail(WXO_ERR_INVALID, "row length %u exceeds the supported maximum 2^27 - 1", K);
     if (too_big(N, K)) return fail(WXO_ERR_INVALID, "sizes N=%u K=%u exceed 2^40 elements", N, K);
     return check_ptr(in, (uint64_t)N * K, in_name);
 }
