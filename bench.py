@@ -248,6 +248,53 @@ def run_suite(stream, steps, warmup):
         scale.free()
     del mats, srcs, outs
 
+    # Resident weight load (the engine's create(): llm/engine-q8-resident.ts:521-538
+    # packs each projection on the CPU, ~0.62 GB/s per README.md:1809-1813): the
+    # seven cfg4 matrices' int8 codes from host memory to packed resident
+    # weights.  K % 4 == 0 here, so the packed layout is the codes' bytes and
+    # the upload is the pack; wall clock, pageable host memory, then the
+    # packInt8Rows kernel alone on a ragged device-resident matrix (cfg3 shape).
+    mats, _, _ = wl.make_decoder_layer()
+    host_codes = []
+    for _, N, K, wf in mats:
+        host_codes.append((N, K, np.ascontiguousarray(
+            np.random.default_rng(N + K).integers(-127, 128, N * K).astype(np.int8))))
+    dev_w = [wxo_q8.DeviceBuffer(N * ((K + 3) // 4) * 4) for N, K, _ in host_codes]
+    code_bytes = sum(c.nbytes for _, _, c in host_codes)
+    reps = 20
+    for r in range(reps + 2):
+        if r == 2:
+            stream.synchronize()
+            t0 = time.perf_counter()
+        for (N, K, c), d in zip(host_codes, dev_w):
+            check(L.wxo_memcpy_htod(d.ptr, c.ctypes.data, c.nbytes, sp))
+    stream.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / reps
+    gbs = code_bytes / (us * 1e-6) / 1e9
+    results.append({"case": "resident load: cfg4's 7 matrices, int8 codes on the host -> packed resident weights "
+                            "(upload is the pack for K % 4 == 0; pageable host memory)", "bytes": code_bytes,
+                    "us": round(us, 3), "GB/s": round(gbs, 2), "reference_cpu_packInt8Rows_GB/s": 0.62})
+    log(f"suite resident load cfg4: {us:.1f} us  {gbs:.1f} GB/s (reference CPU packInt8Rows 0.62 GB/s)")
+    for d in dev_w:
+        d.free()
+    N3, K3 = 4096, 4099
+    W3 = (K3 + 3) // 4
+    copies3 = max(1, -(-rot_target // (N3 * W3 * 4)))
+    src3 = wxo_q8.DeviceBuffer.from_array(np.random.default_rng(3).integers(-127, 128, N3 * K3 * copies3)
+                                          .astype(np.int8), stream)
+    dst3 = wxo_q8.DeviceBuffer(N3 * W3 * 4 * copies3)
+    us = time_loop(stream, lambda i: check(L.wxo_pack_int8_rows(src3.ptr + (i % copies3) * N3 * K3, N3, K3,
+                                                                dst3.ptr + (i % copies3) * N3 * W3 * 4, sp)),
+                   max(1, steps // 4), max(1, warmup // 4))
+    pbytes = N3 * K3 + N3 * W3 * 4
+    gbs = pbytes / (us * 1e-6) / 1e9
+    results.append({"case": "packInt8Rows on the GPU, device-resident codes, N=4096 K=4099 (ragged)", "bytes": pbytes,
+                    "us": round(us, 3), "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
+    log(f"suite packInt8Rows ragged 4096x4099: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM")
+    src3.free()
+    dst3.free()
+    del mats, host_codes
+
     # cfg5: vocab head N=151936, K=1024, M in {1, 4, 8, 16}.
     for M in (1, 4, 8, 16):
         c5 = wl.make_config("cfg5", M=M)

@@ -6,6 +6,7 @@ export type ResidentQ8Op =
   | { kind: "matvecQ8"; weight: ResidentBuffer; scale: ResidentBuffer; vector: ResidentBuffer; output: ResidentBuffer; N: number; K: number; M?: number }
   | { kind: "matvecQ8Ffn"; weightGate: ResidentBuffer; scaleGate: ResidentBuffer; weightUp: ResidentBuffer; scaleUp: ResidentBuffer; vector: ResidentBuffer; output: ResidentBuffer; N: number; K: number }
   | { kind: "matvecQ8Residual"; weight: ResidentBuffer; scale: ResidentBuffer; vector: ResidentBuffer; residual: ResidentBuffer; output: ResidentBuffer; N: number; K: number }
+  | { kind: "packInt8Rows"; codes: ResidentBuffer; N: number; K: number; packed: ResidentBuffer }
   | { kind: "quantizePackQ8"; input: ResidentBuffer; N: number; K: number; packed: ResidentBuffer; scales: ResidentBuffer }
   | { kind: "copy"; src: ResidentBuffer; srcOffset: number; dst: ResidentBuffer; dstOffset: number; size: number };
 export interface ResidentQ8Readback {

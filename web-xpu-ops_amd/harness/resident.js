@@ -45,6 +45,7 @@ export class ResidentQ8Device {
    *      { kind: "matvecQ8Ffn", weightGate, scaleGate, weightUp, scaleUp, vector, output, N, K }
    *      { kind: "matvecQ8Residual", weight, scale, vector, residual, output, N, K }
    *        (output may be the residual buffer: the residual stream updated in place)
+   *      { kind: "packInt8Rows", codes, N, K, packed }   (int8 codes -> packed words)
    *      { kind: "quantizePackQ8", input, N, K, packed, scales }
    *      { kind: "copy", src, srcOffset, dst, dstOffset, size }
    * readback: { source, sourceOffset, length, type: "f32" | "i32" | "u32" }
@@ -83,6 +84,12 @@ export class ResidentQ8Device {
           need(op.output, op.N * 4, "output");
           a.matvecQ8ResidualDevice(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.residual.ptr, op.output.ptr, op.N,
                                    op.K);
+          break;
+        }
+        case "packInt8Rows": {
+          need(op.codes, op.N * op.K, "codes");
+          need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
+          a.packInt8RowsDevice(op.codes.ptr, op.N, op.K, op.packed.ptr);
           break;
         }
         case "quantizePackQ8": {
