@@ -86,18 +86,46 @@ def test_no_gpu_fails_loudly():
         wxo_q8.quantize(input=np.ones(8, np.float32), N=2, D=4)
 
 
+def _device_asm(tmp, src):
+    """gfx950 assembly of one HIP source, built with the library's own flags."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("wxo_build", os.path.join(ROOT, "web-xpu-ops_amd", "build.py"))
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    out = os.path.join(tmp, src + ".s")
+    flags = [f for f in build.HIP_FLAGS if f != "-fPIC"] + build.PER_FILE_FLAGS.get(src, [])
+    subprocess.run(["/opt/rocm/bin/hipcc", *flags, "--cuda-device-only", "-S",
+                    "-I", os.path.join(ROOT, "include"), "-I", CSRC, os.path.join(CSRC, src), "-o", out],
+                   check=True, capture_output=True)
+    return open(out).read()
+
+
 def test_device_code_has_no_packed_fp32():
     # Every HIP source compiled to gfx950 assembly: no v_pk_add/mul/fma_f32.
-    hipcc = "/opt/rocm/bin/hipcc"
     with tempfile.TemporaryDirectory() as tmp:
         for src in ("matvec_q8.hip", "quantize_q8.hip"):
-            out = os.path.join(tmp, src + ".s")
-            subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only", "-S",
-                            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-                            "-I", os.path.join(ROOT, "include"), "-I", CSRC, os.path.join(CSRC, src), "-o", out],
-                           check=True, capture_output=True)
-            asm = open(out).read()
+            asm = _device_asm(tmp, src)
             assert re.search(r"v_pk_(add|mul|fma)_f32", asm) is None, src
             # no register spills in any kernel
             spills = [int(v) for v in re.findall(r"\.vgpr_spill_count:\s+(\d+)", asm)]
             assert spills and max(spills) == 0, src
+
+
+def test_single_vector_kernel_arguments_are_preloaded():
+    # The M = 1 kernels take scalar arguments so that the weight, scale,
+    # vector and output pointers and N, K, W arrive in SGPRs at wave launch.
+    with tempfile.TemporaryDirectory() as tmp:
+        asm = _device_asm(tmp, "matvec_q8.hip")
+    lengths = {}
+    kernel = None
+    for line in asm.splitlines():
+        m = re.match(r"\s*\.amdhsa_kernel\s+(\S+)", line)
+        if m:
+            kernel = m.group(1)
+        m = re.match(r"\s*\.amdhsa_user_sgpr_kernarg_preload_length\s+(\d+)", line)
+        if m and kernel:
+            lengths[kernel] = int(m.group(1))
+    m1 = {k: v for k, v in lengths.items() if "matvec_q8_m1_kernel" in k}
+    assert m1, "no single-vector kernels found"
+    # 4 pointers + N, K, W = 11 SGPRs at least
+    assert min(m1.values()) >= 11, m1

@@ -34,6 +34,12 @@ HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    # gfx950 firmware loads the first kernel arguments (up to 16 SGPRs) into
+    # SGPRs at wave launch, so a wave's first buffer loads do not wait on a
+    # kernarg fetch from memory.  Only scalar (non-struct) arguments qualify.
+    # The code object keeps a prologue that loads them itself for firmware
+    # without the feature.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 # quantize must round x * inverse before comparing its fraction (JS semantics):
 # no multiply-add contraction in that file.

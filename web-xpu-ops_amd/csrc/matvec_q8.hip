@@ -103,23 +103,32 @@ __device__ __forceinline__ float residual_epilogue(float r, float projected) {
 //                 u = du * su, silu evaluated in f64 and rounded to f32 as
 //                 ops/activation/reference.ts:91-92 does, then one f32 product
 //                 (ops/matvec/reference.ts:196-207)
+//
+// Arguments are scalars, not a struct: the build preloads the leading kernel
+// arguments into SGPRs (-amdgpu-kernarg-preload-count), which LLVM does only
+// for non-aggregate arguments.  Each wave then builds its buffer resources and
+// issues its first loads without waiting on a kernarg fetch from memory
+// (measured 0.33 us per call at N=11008, K=4096).  `aux` is the up
+// projection's scale (kEpiFfn) or the residual (kEpiResidual); the plain form
+// ignores weight2 and aux.
 template <int WAVES, int CPW, int R, int EPI>
-__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(M1Params p) {
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* y, uint32_t N, uint32_t K, uint32_t W, const uint32_t* __restrict__ weight2, const float* aux) {
     constexpr int NWT = EPI == kEpiFfn ? 2 : 1;  // weights streamed
     constexpr int V = R * NWT;                     // dot products per block
     constexpr int SHIFT = 6 - ilog2(V);
     constexpr int XS = CPW > 0 ? CPW : 1;
-    const uint32_t N = p.N, K = p.K, W = p.W;
     const int lane = (int)(threadIdx.x & 63u);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t C = (W + kChunkWords - 1) / kChunkWords;
     const uint32_t row0 = blockIdx.x * (uint32_t)R;
     const uint32_t rows = min((uint32_t)R, N - row0);  // >= 1
     const uint32_t rowbytes = W * 4u;
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.weight + (size_t)row0 * W, rows * rowbytes);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)row0 * W, rows * rowbytes);
     const __amdgpu_buffer_rsrc_t wrs2 =
-        NWT == 2 ? make_rsrc(p.weight2 + (size_t)row0 * W, rows * rowbytes) : wrs;
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.x, K * 4u);
+        NWT == 2 ? make_rsrc(weight2 + (size_t)row0 * W, rows * rowbytes) : wrs;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, K * 4u);
 
     float xr[XS][16];
     if constexpr (CPW > 0) {
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(M1Params p) {
     const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
     const uint32_t rr = (uint32_t)lane >> SHIFT;
     if constexpr (WAVES == 1 && EPI == kEpiPlain) {
-        if (leader && rr < rows) p.y[row0 + rr] = acc[0] * p.scale[row0 + rr];
+        if (leader && rr < rows) y[row0 + rr] = acc[0] * scale[row0 + rr];
     } else {
         __shared__ float part[WAVES][V];
         if (leader) part[wave][rr] = acc[0];
@@ -182,14 +191,14 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(M1Params p) {
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) d += part[w][t];
             if constexpr (EPI == kEpiPlain) {
-                p.y[row] = d * p.scale[row];
+                y[row] = d * scale[row];
             } else if constexpr (EPI == kEpiResidual) {
-                p.y[row] = residual_epilogue(p.residual[row], __fmul_rn(d, p.scale[row]));
+                y[row] = residual_epilogue(aux[row], __fmul_rn(d, scale[row]));
             } else {
                 float du = part[0][R + t];
 #pragma unroll
                 for (int w = 1; w < WAVES; ++w) du += part[w][R + t];
-                p.y[row] = ffn_epilogue(__fmul_rn(d, p.scale[row]), __fmul_rn(du, p.scale2[row]));
+                y[row] = ffn_epilogue(__fmul_rn(d, scale[row]), __fmul_rn(du, aux[row]));
             }
         }
     }
@@ -736,8 +745,9 @@ uint32_t grid_for(uint32_t nblocks, uint32_t max_groups) {
 template <int WAVES, int CPW, int R, int EPI>
 hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
-    const M1Params p{a.weight, a.scale, a.weight2, a.scale2, a.vector, a.residual, a.output, a.N, a.K, a.W};
-    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI>), dim3(nblocks), dim3(WAVES * 64), 0, stream, p);
+    const float* aux = EPI == kEpiFfn ? a.scale2 : EPI == kEpiResidual ? a.residual : nullptr;
+    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
+                       a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.weight2, aux);
     if (variant) *variant = CPW > 0 ? "m1.xreg" : "m1.xstream";
     return hipGetLastError();
 }
