@@ -300,7 +300,89 @@ def run_suite(stream, steps, warmup):
         c5 = wl.make_config("cfg5", M=M)
         matvec_case(f"cfg5 LM head M={M}", c5["N"], c5["K"], M, c5["w"], c5["x"])
         del c5
+
+    run_prefill_suite(stream, steps, warmup, results, check)
     return results
+
+
+def run_prefill_suite(stream, steps, warmup, results, check):
+    """The prefill side (the next rows after the decode path): matmulQ8 over
+    one decoder layer's seven projections for a 512-token prompt, then the
+    dequant / gather ops.  matmulQ8 is compute-bound: its bound is the bf16
+    matrix-core rate at three products per code (the exact split of each
+    activation), i.e. 3 x 2 N M K flops; TFLOP/s counts the 2 N M K useful
+    flops."""
+    L = wxo_q8.lib()
+    sp = stream.handle
+    T = wl.PREFILL_TOKENS
+    mats, _, _ = wl.make_decoder_layer()
+    rng = np.random.default_rng(7)
+    a_h = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(T * 2048, dtype=np.float32), stream)
+    a_f = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(T * 5632, dtype=np.float32), stream)
+    out = wxo_q8.DeviceBuffer(T * 5632 * 4)
+    prepared = []
+    for name, N, K, wf in mats:
+        src = wxo_q8.DeviceBuffer.from_array(wf, stream)
+        packed = wxo_q8.DeviceBuffer(N * ((K + 3) // 4) * 4)
+        scale = wxo_q8.DeviceBuffer(N * 4)
+        wxo_q8.quantize_pack_q8_device(src, N, K, packed, scale, stream)
+        stream.synchronize()
+        src.free()
+        prepared.append((name, N, K, packed, scale))
+    total_flops = 0.0
+    total_us = 0.0
+    for name, N, K, packed, scale in prepared:
+        a = a_f if K == 5632 else a_h
+        us = time_loop(stream, lambda i: check(L.wxo_matmul_q8(a.ptr, packed.ptr, scale.ptr, out.ptr, T, N, K, sp)),
+                       max(1, steps // 20), max(1, warmup // 20))
+        flops = 2.0 * T * N * K
+        bound_us = 3.0 * flops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6
+        total_flops += flops
+        total_us += us
+        results.append({"case": f"prefill matmulQ8 {name}: tokens={T} M={N} K={K}", "us": round(us, 3),
+                        "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1), "bound": "mfma_bf16 (x3 exact split)",
+                        "pct_of_bound": round(100 * bound_us / us, 1)})
+        log(f"suite prefill matmulQ8 {name} {T}x{N}x{K}: {us:.2f} us  {flops / (us * 1e-6) / 1e12:.1f} TFLOP/s  "
+            f"{100 * bound_us / us:.1f}% of the x3 bf16 bound")
+    bound_us = 3.0 * total_flops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6
+    results.append({"case": f"prefill matmulQ8: one decoder layer's 7 projections, {T} tokens", "us": round(total_us, 3),
+                    "TFLOP/s": round(total_flops / (total_us * 1e-6) / 1e12, 1),
+                    "pct_of_bound": round(100 * bound_us / total_us, 1)})
+    log(f"suite prefill layer: {total_us:.1f} us  {total_flops / (total_us * 1e-6) / 1e12:.1f} TFLOP/s")
+
+    # dequantizePackedQ8 and dequantTranspose of the gate projection, gather of
+    # the prompt's rows from a 32000 x 2048 int8 embedding table
+    _, N, K, packed, scale = prepared[4]
+    W = (K + 3) // 4
+    dq_bytes = N * W * 4 + 4 * N + 4 * N * K
+    for case, fn in (("dequantizePackedQ8", lambda i: check(L.wxo_dequantize_packed_q8(packed.ptr, scale.ptr, N, K,
+                                                                                         out2.ptr, sp))),
+                     ("dequantTranspose", lambda i: check(L.wxo_dequant_transpose(packed.ptr, scale.ptr, N, K,
+                                                                                    out2.ptr, sp)))):
+        out2 = wxo_q8.DeviceBuffer(N * K * 4)
+        us = time_loop(stream, fn, max(1, steps // 20), max(1, warmup // 20))
+        gbs = dq_bytes / (us * 1e-6) / 1e9
+        results.append({"case": f"{case} N={N} K={K}", "bytes": dq_bytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+                        "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
+        log(f"suite {case} {N}x{K}: {us:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% HBM")
+        out2.free()
+    rows, D = 32000, 2048
+    table = wxo_q8.DeviceBuffer.from_array(rng.integers(-127, 128, rows * D).astype(np.int8), stream)
+    tscale = wxo_q8.DeviceBuffer.from_array(rng.uniform(0.001, 0.02, rows).astype(np.float32), stream)
+    idx = wxo_q8.DeviceBuffer.from_array(rng.integers(0, rows, T).astype(np.int64), stream)
+    g_bytes = T * (D + 4 + 8 + 4 * D)
+    us = time_loop(stream, lambda i: check(L.wxo_gather_dequant_rows(table.ptr, tscale.ptr, rows, D, idx.ptr, T,
+                                                                     out.ptr, sp)),
+                   max(1, steps // 20), max(1, warmup // 20))
+    gbs = g_bytes / (us * 1e-6) / 1e9
+    results.append({"case": f"gatherDequantRows {T} rows of a {rows}x{D} table", "bytes": g_bytes, "us": round(us, 3),
+                    "GB/s": round(gbs, 1)})
+    log(f"suite gatherDequantRows {T} of {rows}x{D}: {us:.2f} us  {gbs:.0f} GB/s")
+    for b in (a_h, a_f, out, table, tscale, idx):
+        b.free()
+    for _, _, _, packed, scale in prepared:
+        packed.free()
+        scale.free()
 
 
 def main() -> int:
@@ -313,6 +395,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--suite", metavar="PATH", default=None,
                     help="also measure every BASELINE configuration and write the table (JSON) to PATH")
+    ap.add_argument("--prefill-suite", metavar="PATH", default=None,
+                    help="measure only the prefill-side ops (matmulQ8, dequant, gather) and write them to PATH")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="after timing, run this many device copies of the packed weight (counter calibration)")
     args = ap.parse_args()
@@ -326,6 +410,17 @@ def main() -> int:
 
     wxo_q8.init()
     log(wxo_q8.describe())
+    if args.prefill_suite:
+        stream = wxo_q8.Stream()
+        table = []
+
+        def check(st):
+            if st != 0:
+                raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
+        run_prefill_suite(stream, args.steps, args.warmup, table, check)
+        with open(args.prefill_suite, "w") as f:
+            json.dump(table, f, indent=1)
+        return 0
     cfg = wl.CONFIGS["cfg2"]
     N, K, M = cfg["N"], cfg["K"], 1
     W = (K + 3) // 4

@@ -23,6 +23,15 @@
  *   wxo_pack_int8_rows        llm/weights-q8.ts:137-139 (packInt8Rows)
  *   wxo_quantize_pack_q8      packQ8(quantize(w).output, N, K) + quantize(w).scales
  *                             in one pass (the composition at ops/matvec/reference.ts:87-90)
+ *   wxo_matmul_q8             ops/matmul/reference.ts:124-137 (matmulQ8, the prefill
+ *                             GEMM over the same packed weight) and its WGSL dispatch
+ *                             ops/matmul/wgsl/q8.wgsl:26-35 bindings {a, weight, scale,
+ *                             output, {N,M,K}}, called from llm/engine-q8-resident.ts:1078
+ *                             (runPrefillResident's projections)
+ *   wxo_dequantize_packed_q8  llm/weights-q8.ts:161-177 (dequantizePackedQ8)
+ *   wxo_dequant_transpose     ops/dequant_transpose/reference.ts:40-59 (dequantTranspose)
+ *   wxo_gather_dequant_rows   llm/weights-q8.ts:207-222 (gatherDequantRows, the
+ *                             embedding gather of llm/engine-q8-resident.ts before decode)
  *   wxo_*_host                the same ops on host arrays, synchronous: the TS op
  *                             API's calling convention (typed arrays in, fresh
  *                             typed arrays out)
@@ -138,6 +147,30 @@ int wxo_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* pa
 int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* packed, float* scales,
                          wxo_stream_t stream);
 
+/* matmulQ8: output[n*M + m] = (sum_{k<K} a[n*K + k] * sext8(byte k of weight row m)) * scale[m]
+ * for n < N (tokens), m < M (weight rows).  a f32 [N, K], weight u32 [M, ceil(K/4)],
+ * scale f32 [M], output f32 [N, M].  f32 accumulation on the matrix cores (exact
+ * products); |y - y_ref| <= 1e-5 * sum_k |a * q * s| + 1e-7 against the reference's f64
+ * sum of per-term dequantized products.  K = 0 gives zeros.  K <= 2^22. */
+int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* output, uint32_t N,
+                  uint32_t M, uint32_t K, wxo_stream_t stream);
+
+/* dequantizePackedQ8: output f32 [N, K], output[n*K + k] = q[n, k] * scale[n] rounded to
+ * f32 once (bit-exact to the reference). */
+int wxo_dequantize_packed_q8(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K, float* output,
+                             wxo_stream_t stream);
+
+/* dequantTranspose: output f32 [in_features, out_features],
+ * output[k*out_features + n] = q[n, k] * scale[n] (bit-exact). */
+int wxo_dequant_transpose(const uint32_t* weight, const float* scale, uint32_t out_features,
+                          uint32_t in_features, float* output, wxo_stream_t stream);
+
+/* gatherDequantRows: codes int8 [rows, D] (the unpacked table), scale f32 [rows],
+ * indices int64 [count] -> output f32 [count, D]; row i is codes[indices[i]] * scale
+ * (bit-exact), or zeros when indices[i] is outside [0, rows). */
+int wxo_gather_dequant_rows(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
+                            const int64_t* indices, uint32_t count, float* output, wxo_stream_t stream);
+
 /* ---- the same ops on host arrays (synchronous; copy in, run, copy out) ----- */
 int wxo_matvec_q8_host(const uint32_t* weight, const float* scale, const float* vector, float* output,
                        uint32_t N, uint32_t K, uint32_t M);
@@ -150,6 +183,14 @@ int wxo_pack_q8_host(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* pac
 int wxo_pack_int8_rows_host(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed);
 int wxo_quantize_pack_q8_host(const float* input, uint32_t N, uint32_t K, uint32_t* packed,
                               float* scales);
+int wxo_matmul_q8_host(const float* a, const uint32_t* weight, const float* scale, float* output, uint32_t N,
+                       uint32_t M, uint32_t K);
+int wxo_dequantize_packed_q8_host(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K,
+                                  float* output);
+int wxo_dequant_transpose_host(const uint32_t* weight, const float* scale, uint32_t out_features,
+                               uint32_t in_features, float* output);
+int wxo_gather_dequant_rows_host(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
+                                 const int64_t* indices, uint32_t count, float* output);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,11 @@ Functions mirror the reference's TypeScript definitions:
   matvec_q8_ffn       ops/matvec/reference.ts:196-207 (matvecQ8Ffn)
   silu                ops/activation/reference.ts:91-92
   absterm             sum_k |s*q*x| per row in f64 (tolerance base)
+  matmul_q8           ops/matmul/reference.ts:124-137 (matmulQ8)
+  matmul_absterm      sum_k |a * fround(q*s)| per output in f64 (tolerance base)
+  dequantize_packed_q8 llm/weights-q8.ts:161-177 (dequantizePackedQ8)
+  dequant_transpose   ops/dequant_transpose/reference.ts:40-59 (dequantTranspose)
+  gather_dequant_rows llm/weights-q8.ts:207-222 (gatherDequantRows)
 """
 from __future__ import annotations
 
@@ -54,9 +59,15 @@ def _load():
     lib.q8o_matvec_q8_ffn.argtypes = [p, p, p, p, p, sz, sz, p]
     lib.q8o_silu.argtypes = [ctypes.c_float]
     lib.q8o_silu.restype = ctypes.c_float
+    lib.q8o_matmul_q8.argtypes = [p, p, p, sz, sz, sz, p]
+    lib.q8o_matmul_q8_absterm.argtypes = [p, p, p, sz, sz, sz, p]
+    lib.q8o_dequantize_packed_q8.argtypes = [p, p, sz, sz, p]
+    lib.q8o_dequant_transpose.argtypes = [p, p, sz, sz, p]
+    lib.q8o_gather_dequant_rows.argtypes = [p, p, sz, sz, p, sz, p]
     for name in ("q8o_quantize", "q8o_pack_q8", "q8o_pack_int8_rows", "q8o_matvec_q8",
                  "q8o_matvec_q8_batched", "q8o_matvec_q8_absterm", "q8o_matvec_q8_residual",
-                 "q8o_matvec_q8_ffn"):
+                 "q8o_matvec_q8_ffn", "q8o_matmul_q8", "q8o_matmul_q8_absterm", "q8o_dequantize_packed_q8",
+                 "q8o_dequant_transpose", "q8o_gather_dequant_rows"):
         getattr(lib, name).restype = None
     _lib = lib
     return lib
@@ -153,6 +164,54 @@ def absterm(weight, scale, vector, N: int, K: int) -> np.ndarray:
     v = np.ascontiguousarray(vector, dtype=np.float32).reshape(-1)
     out = np.empty(N, dtype=np.float64)
     _load().q8o_matvec_q8_absterm(_ptr(w), _ptr(s), _ptr(v), N, K, _ptr(out))
+    return out
+
+
+def matmul_q8(a, weight, scale, N: int, M: int, K: int) -> np.ndarray:
+    """ops/matmul/reference.ts:124-137: a [N, K], weight [M, W] -> f32 [N, M]."""
+    av = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    assert av.size >= N * K and w.size >= M * words_per_row(K) and s.size >= M
+    out = np.empty(N * M, dtype=np.float32)
+    _load().q8o_matmul_q8(_ptr(av), _ptr(w), _ptr(s), N, M, K, _ptr(out))
+    return out.reshape(N, M)
+
+
+def matmul_absterm(a, weight, scale, N: int, M: int, K: int) -> np.ndarray:
+    av = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    out = np.empty(N * M, dtype=np.float64)
+    _load().q8o_matmul_q8_absterm(_ptr(av), _ptr(w), _ptr(s), N, M, K, _ptr(out))
+    return out.reshape(N, M)
+
+
+def dequantize_packed_q8(weight, scale, N: int, K: int) -> np.ndarray:
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    assert w.size >= N * words_per_row(K) and s.size >= N
+    out = np.empty(N * K, dtype=np.float32)
+    _load().q8o_dequantize_packed_q8(_ptr(w), _ptr(s), N, K, _ptr(out))
+    return out
+
+
+def dequant_transpose(weight, scale, out_features: int, in_features: int) -> np.ndarray:
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    assert w.size >= out_features * words_per_row(in_features) and s.size >= out_features
+    out = np.empty(out_features * in_features, dtype=np.float32)
+    _load().q8o_dequant_transpose(_ptr(w), _ptr(s), out_features, in_features, _ptr(out))
+    return out
+
+
+def gather_dequant_rows(codes, scale, rows: int, D: int, indices) -> np.ndarray:
+    c = np.ascontiguousarray(codes, dtype=np.int8).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    ix = np.ascontiguousarray(indices, dtype=np.int64).reshape(-1)
+    assert c.size >= rows * D and s.size >= rows
+    out = np.empty(ix.size * D, dtype=np.float32)
+    _load().q8o_gather_dequant_rows(_ptr(c), _ptr(s), rows, D, _ptr(ix), ix.size, _ptr(out))
     return out
 
 

@@ -176,3 +176,81 @@ void q8o_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, con
         output[row] = (float)((double)q8o_silu(output[row]) * (double)up[row]);
     free(up);
 }
+
+/* The f32 that a Float32Array store of unpackI8(byte) * s holds: the product
+ * of an int8 and an f32 is exact in f64, so this is one rounding to f32. */
+static float dequant_term(uint32_t word, size_t lane, float s) {
+    const uint32_t byte = (word >> (lane * 8)) & 0xffu;
+    return (float)((double)unpack_i8(byte) * (double)s);
+}
+
+/* ops/matmul/reference.ts:124-137 (matmulQ8): b[k * M + row] =
+ * Float32Array(unpackI8(byte) * scale[row]) for the weight's M rows, then
+ * matmul({a, b, M: N, N: M, K}) (:37-49): for each output element, an f64
+ * sum over k left to right of a[row * K + k] * b[k * M + col], stored to a
+ * Float32Array.  output is [N, M]. */
+void q8o_matmul_q8(const float* a, const uint32_t* weight, const float* scale, size_t N, size_t M, size_t K,
+                   float* output) {
+    const size_t W = (K + 3) / 4;
+    float* b = (float*)malloc((K * M != 0 ? K * M : 1) * sizeof(float));
+    for (size_t row = 0; row < M; ++row)
+        for (size_t k = 0; k < K; ++k)
+            b[k * M + row] = dequant_term(weight[row * W + (k >> 2)], k & 3, scale[row]);
+    for (size_t row = 0; row < N; ++row) {
+        for (size_t col = 0; col < M; ++col) {
+            double sum = 0.0;
+            for (size_t k = 0; k < K; ++k) sum += (double)a[row * K + k] * (double)b[k * M + col];
+            output[row * M + col] = (float)sum;
+        }
+    }
+    free(b);
+}
+
+/* sum_k |a[n, k] * b[k, m]| in f64 with b the dequantized term above: the
+ * magnitude the f32 kernel's rounding error is measured against. */
+void q8o_matmul_q8_absterm(const float* a, const uint32_t* weight, const float* scale, size_t N, size_t M,
+                           size_t K, double* bound) {
+    const size_t W = (K + 3) / 4;
+    for (size_t n = 0; n < N; ++n)
+        for (size_t m = 0; m < M; ++m) {
+            double sum = 0.0;
+            for (size_t k = 0; k < K; ++k)
+                sum += fabs((double)a[n * K + k] * (double)dequant_term(weight[m * W + (k >> 2)], k & 3, scale[m]));
+            bound[n * M + m] = sum;
+        }
+}
+
+/* llm/weights-q8.ts:161-177 (dequantizePackedQ8): output[row * K + col] =
+ * signed byte col of the row times scale[row], stored to a Float32Array. */
+void q8o_dequantize_packed_q8(const uint32_t* weight, const float* scale, size_t N, size_t K, float* output) {
+    const size_t W = (K + 3) / 4;
+    for (size_t row = 0; row < N; ++row)
+        for (size_t col = 0; col < K; ++col)
+            output[row * K + col] = dequant_term(weight[row * W + (col >> 2)], col & 3, scale[row]);
+}
+
+/* ops/dequant_transpose/reference.ts:40-59 (dequantTranspose): output
+ * [inFeatures, outFeatures], output[col * outFeatures + row] = unpackI8 * s.
+ * (The reference's length checks at :42-47 are the C ABI's validation.) */
+void q8o_dequant_transpose(const uint32_t* weight, const float* scale, size_t out_features, size_t in_features,
+                           float* output) {
+    const size_t W = (in_features + 3) / 4;
+    for (size_t row = 0; row < out_features; ++row)
+        for (size_t col = 0; col < in_features; ++col)
+            output[col * out_features + row] = dequant_term(weight[row * W + (col >> 2)], col & 3, scale[row]);
+}
+
+/* llm/weights-q8.ts:207-222 (gatherDequantRows): rows of an int8 table in
+ * request order; an index outside [0, rows) leaves its output row zero (the
+ * output starts zeroed, :211). */
+void q8o_gather_dequant_rows(const int8_t* codes, const float* scale, size_t rows, size_t D,
+                             const int64_t* indices, size_t count, float* output) {
+    for (size_t i = 0; i < count; ++i) {
+        const int64_t r = indices[i];
+        for (size_t c = 0; c < D; ++c) output[i * D + c] = 0.0f;
+        if (r < 0 || (uint64_t)r >= (uint64_t)rows) continue;
+        const float s = scale[r];
+        for (size_t c = 0; c < D; ++c)
+            output[i * D + c] = (float)((double)codes[(size_t)r * D + c] * (double)s);
+    }
+}

@@ -18,6 +18,12 @@
  *   q8o_silu              ops/activation/reference.ts:91-92 (silu)
  *   q8o_matvec_q8_absterm sum_k |s_n * q_nk * x_k| in f64: the per-row bound
  *                         the f32 kernels are judged against
+ *   q8o_matmul_q8         ops/matmul/reference.ts:124-137 (matmulQ8: per-term
+ *                         dequant into matmul's b, then matmul :37-49)
+ *   q8o_matmul_q8_absterm sum_k |a_nk * fround(q_mk * s_m)| in f64 per output
+ *   q8o_dequantize_packed_q8 llm/weights-q8.ts:161-177 (dequantizePackedQ8)
+ *   q8o_dequant_transpose ops/dequant_transpose/reference.ts:40-59 (dequantTranspose)
+ *   q8o_gather_dequant_rows llm/weights-q8.ts:207-222 (gatherDequantRows)
  *
  * Batched matvecQ8 (M vectors) has no reference function; it is M
  * independent matvecQ8 calls by definition, so the checker loops M times.
@@ -49,6 +55,16 @@ void q8o_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, con
                        const float* scale_up, const float* vector, size_t N, size_t K, float* output);
 void q8o_matvec_q8_absterm(const uint32_t* weight, const float* scale, const float* vector,
                            size_t N, size_t K, double* bound);
+
+void q8o_matmul_q8(const float* a, const uint32_t* weight, const float* scale, size_t N, size_t M, size_t K,
+                   float* output);
+void q8o_matmul_q8_absterm(const float* a, const uint32_t* weight, const float* scale, size_t N, size_t M,
+                           size_t K, double* bound);
+void q8o_dequantize_packed_q8(const uint32_t* weight, const float* scale, size_t N, size_t K, float* output);
+void q8o_dequant_transpose(const uint32_t* weight, const float* scale, size_t out_features, size_t in_features,
+                           float* output);
+void q8o_gather_dequant_rows(const int8_t* codes, const float* scale, size_t rows, size_t D,
+                             const int64_t* indices, size_t count, float* output);
 
 #ifdef __cplusplus
 }

@@ -16,6 +16,10 @@
  *   matvecQ8       ops/matvec/reference.ts:113-131
  *   matvecQ8Ffn    ops/matvec/reference.ts:196-207, silu from ops/activation/reference.ts:91-92
  *   matvecQ8Residual ops/matvec/reference.ts:235-243
+ *   matmulQ8       ops/matmul/reference.ts:124-137 (with matmul :37-49)
+ *   dequantizePackedQ8 llm/weights-q8.ts:161-177
+ *   dequantTranspose ops/dequant_transpose/reference.ts:40-59
+ *   gatherDequantRows llm/weights-q8.ts:207-222
  */
 
 /** ops/quantize/reference.ts:13-38 */
@@ -102,5 +106,71 @@ export function matvecQ8Residual({ weight, scale, vector, residual, N, K }) {
   const projected = matvecQ8({ weight, scale, vector, N, K });
   const output = new Float32Array(N);
   for (let row = 0; row < N; row += 1) output[row] = residual[row] + projected[row];
+  return output;
+}
+
+const unpackI8 = (word, lane) => {
+  const byte = (word >>> (lane * 8)) & 0xff;
+  return byte >= 128 ? byte - 256 : byte;
+};
+
+/** ops/matmul/reference.ts:37-49: f64 triple loop, C stored to a Float32Array. */
+export function matmul({ a, b, M, N, K }) {
+  const output = new Float32Array(M * N);
+  for (let row = 0; row < M; row += 1) {
+    for (let col = 0; col < N; col += 1) {
+      let sum = 0;
+      for (let k = 0; k < K; k += 1) sum += a[row * K + k] * b[k * N + col];
+      output[row * N + col] = sum;
+    }
+  }
+  return output;
+}
+
+/** ops/matmul/reference.ts:124-137: the weight dequantized per term into matmul's b [K, M], then matmul. */
+export function matmulQ8({ a, weight, scale, N, M, K }) {
+  const wordsPerRow = Math.ceil(K / 4);
+  const b = new Float32Array(K * M);
+  for (let row = 0; row < M; row += 1) {
+    const s = scale[row];
+    for (let k = 0; k < K; k += 1) b[k * M + row] = unpackI8(weight[row * wordsPerRow + (k >> 2)], k & 3) * s;
+  }
+  return matmul({ a, b, M: N, N: M, K });
+}
+
+/** llm/weights-q8.ts:161-177 */
+export function dequantizePackedQ8(weight, scale, N, K) {
+  const wordsPerRow = Math.ceil(K / 4);
+  const output = new Float32Array(N * K);
+  for (let row = 0; row < N; row += 1) {
+    const s = scale[row];
+    for (let col = 0; col < K; col += 1) output[row * K + col] = unpackI8(weight[row * wordsPerRow + (col >> 2)], col & 3) * s;
+  }
+  return output;
+}
+
+/** ops/dequant_transpose/reference.ts:40-59 -> [inFeatures, outFeatures] */
+export function dequantTranspose({ weight, scale, outFeatures, inFeatures }) {
+  const wordsPerRow = Math.ceil(inFeatures / 4);
+  const output = new Float32Array(inFeatures * outFeatures);
+  for (let row = 0; row < outFeatures; row += 1) {
+    const s = scale[row];
+    for (let col = 0; col < inFeatures; col += 1) {
+      output[col * outFeatures + row] = unpackI8(weight[row * wordsPerRow + (col >> 2)], col & 3) * s;
+    }
+  }
+  return output;
+}
+
+/** llm/weights-q8.ts:207-222: table = { codes: Int8Array [rows, D], scale: Float32Array [rows] } */
+export function gatherDequantRows(table, indices, D) {
+  const rows = table.scale.length;
+  const output = new Float32Array(indices.length * D);
+  indices.forEach((rowIndex, i) => {
+    if (rowIndex < 0 || rowIndex >= rows) return;
+    const s = table.scale[rowIndex];
+    const base = rowIndex * D;
+    for (let c = 0; c < D; c += 1) output[i * D + c] = table.codes[base + c] * s;
+  });
   return output;
 }

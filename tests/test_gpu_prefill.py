@@ -1,0 +1,261 @@
+"""Parity of the gfx950 prefill-side ops with the oracle, through the C ABI.
+
+  * matmulQ8 (ops/matmul/reference.ts:124-137): |y - y_ref| <= 1e-5 * sum_k
+    |a * fround(q * s)| + 1e-7 per output element, y_ref the reference's f64
+    sum of per-term dequantized products.  That bar is tighter than the
+    reference's own GPU test tolerance (rel 1e-4 or abs 6e-4,
+    ops/matmul/q8.wgsl.test.ts:33); shapes follow that file and
+    q8-edges.wgsl.test.ts, plus tile-boundary sweeps and the decoder layer's
+    projections at a 512-token prompt.
+  * dequantizePackedQ8, dequantTranspose, gatherDequantRows: bit-exact
+    (ops/dequant_transpose/wgsl.test.ts:37 holds its kernel to rel 0, abs 0).
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import wxo_q8
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    wxo_q8.init()
+
+
+def kat():
+    with open(os.path.join(GOLDEN, "kat.json")) as f:
+        return json.load(f)
+
+
+def assert_bits_equal(got, want, what):
+    got = np.asarray(got).reshape(-1)
+    want = np.asarray(want).reshape(-1)
+    assert got.shape == want.shape, what
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[0]}: got {got[bad[0]]!r} want {want[bad[0]]!r}"
+
+
+def assert_matmul(got, a, w, s, N, M, K, rows=None):
+    """Checks output rows `rows` (all by default) against the oracle."""
+    got = np.asarray(got).reshape(N, M)
+    rows = np.arange(N) if rows is None else np.asarray(rows)
+    asub = np.ascontiguousarray(np.asarray(a, np.float32).reshape(N, K)[rows])
+    want = oracle.matmul_q8(asub, w, s, len(rows), M, K)
+    bound = oracle.matmul_absterm(asub, w, s, len(rows), M, K)
+    ok, msg = oracle.check_matvec(got[rows].reshape(-1), want.reshape(-1), bound.reshape(-1))
+    assert ok, f"N={N} M={M} K={K}: {msg}"
+
+
+def sin_wave(n, k, mul):
+    return np.array([math.sin(i * k) * mul for i in range(n)], dtype=np.float32)
+
+
+def code_wave(n, k):
+    return np.array([int(oracle.js_round(math.sin(i * k) * 100)) for i in range(n)], dtype=np.int32)
+
+
+def scale_wave(n):
+    return np.array([0.02 * (i + 1) + 0.007 for i in range(n)], dtype=np.float32)
+
+
+# ---------------------------------------------------------------- matmulQ8
+
+def test_matmul_hand_kat():
+    c = kat()["matmul_q8"][1]
+    w = oracle.pack_q8(np.array(c["codes"], np.int32), c["M"], c["K"])
+    y = wxo_q8.matmulQ8(a=np.array(c["a"], np.float32), weight=w, scale=np.array(c["scale"], np.float32),
+                        N=c["N"], M=c["M"], K=c["K"])
+    assert y.reshape(-1).tolist() == c["want"]
+
+
+@pytest.mark.parametrize("shape", kat()["matmul_q8"][0]["shapes"], ids=lambda s: "x".join(map(str, s)))
+def test_matmul_reference_shapes(shape):
+    N, M, K = shape
+    a = sin_wave(N * K, 0.37, 1.5)
+    w = oracle.pack_q8(code_wave(M * K, 0.19), M, K)
+    s = scale_wave(M)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    if K == 0:
+        assert np.array_equal(y, np.zeros((N, M), np.float32))
+    assert_matmul(y, a, w, s, N, M, K)
+
+
+def test_matmul_does_not_read_past_a_ragged_row():
+    # q8-edges.wgsl.test.ts:29-74: K = 19, sentinel words after the weight
+    N, M, K = 5, 7, 19
+    a = sin_wave(N * K, 0.41, 1.5)
+    w = oracle.pack_q8(code_wave(M * K, 0.23), M, K)
+    padded = np.concatenate([w, np.full(64, 0x7F7F7F7F, np.uint32)])
+    s = scale_wave(M)
+    y = wxo_q8.matmulQ8(a=a, weight=padded, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+
+
+def test_matmul_own_scale_per_feature():
+    # q8-edges.wgsl.test.ts:110-139: identical code rows, scales 0.03 and 0.11
+    N, M, K = 2, 2, 12
+    shared = code_wave(K, 0.27)
+    w = oracle.pack_q8(np.concatenate([shared, shared]), M, K)
+    a = sin_wave(N * K, 0.5, 1.5)
+    s = np.array([0.03, 0.11], np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+    assert not np.allclose(y[:, 0], y[:, 1])
+
+
+def test_matmul_writes_nothing_past_the_output():
+    # q8-edges.wgsl.test.ts:76-108 (M = TILE + 1), on device buffers with a
+    # sentinel after the output and in the pad lanes of the weight
+    rng = np.random.default_rng(1)
+    for N, M, K in [(4, 17, 8), (65, 129, 70), (1, 3, 5)]:
+        a = rng.standard_normal(N * K).astype(np.float32)
+        w = oracle.pack_q8(rng.integers(-128, 128, M * K).astype(np.int32), M, K)
+        s = rng.uniform(0.01, 0.1, M).astype(np.float32)
+        da = wxo_q8.DeviceBuffer.from_array(a)
+        dw = wxo_q8.DeviceBuffer.from_array(w)
+        ds = wxo_q8.DeviceBuffer.from_array(s)
+        sentinel = np.full(N * M + 256, 12345.0, np.float32)
+        dy = wxo_q8.DeviceBuffer.from_array(sentinel)
+        wxo_q8.matmul_q8_device(da, dw, ds, dy, N, M, K)
+        out = dy.download(np.float32, N * M + 256)
+        assert np.all(out[N * M:] == 12345.0), (N, M, K)
+        assert_matmul(out[:N * M], a, w, s, N, M, K)
+
+
+@pytest.mark.parametrize("K", [1, 3, 4, 5, 63, 64, 65, 127, 255, 256, 257, 1030])
+@pytest.mark.parametrize("N,M", [(1, 1), (63, 31), (64, 64), (65, 127), (130, 129), (7, 300)])
+def test_matmul_tile_boundaries(N, M, K):
+    rng = np.random.default_rng(N * 7919 + M * 31 + K)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    w = rng.integers(0, 2 ** 32, M * ((K + 3) // 4), dtype=np.uint64).astype(np.uint32)  # any byte, -128 included
+    s = rng.uniform(-0.05, 0.05, M).astype(np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+
+
+def test_matmul_nonfinite_activations():
+    rng = np.random.default_rng(2)
+    N, M, K = 70, 40, 200
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[3] = np.inf                     # token 0
+    a[K + 5] = -np.inf                # token 1
+    a[2 * K + 7] = np.nan             # token 2
+    a[3 * K + 1] = np.uint32(0x7F800001).view(np.float32)  # token 3: a NaN whose top bits read as Inf
+    a[4 * K + 2], a[4 * K + 9] = np.inf, -np.inf  # token 4: Inf - Inf
+    a[5 * K:6 * K] = 1e-40            # token 5: subnormal row
+    codes = rng.integers(1, 128, M * K).astype(np.int32)  # no zero code: Inf * q stays infinite
+    codes[::3] *= -1
+    w = oracle.pack_q8(codes, M, K)
+    s = rng.uniform(0.01, 0.1, M).astype(np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+    assert np.isnan(y[3]).all() and np.isnan(y[2]).all() and np.isinf(y[0]).all()
+
+
+@pytest.mark.parametrize("K", [4096, 11008])
+def test_matmul_same_sign_long_k(K):
+    # all terms positive: no cancellation hides accumulated rounding
+    rng = np.random.default_rng(K)
+    N, M = 64, 128
+    a = rng.uniform(0.0, 2.0, N * K).astype(np.float32)
+    w = oracle.pack_q8(rng.integers(0, 128, M * K).astype(np.int32), M, K)
+    s = rng.uniform(0.001, 0.01, M).astype(np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K, rows=np.arange(0, N, 9))
+
+
+def test_matmul_k_zero_gives_zeros():
+    s = np.array([np.inf, np.nan, 1.0], np.float32)
+    y = wxo_q8.matmulQ8(a=np.zeros(0, np.float32), weight=np.zeros(0, np.uint32), scale=s, N=4, M=3, K=0)
+    assert np.array_equal(y, np.zeros((4, 3), np.float32)) and not np.signbit(y).any()
+
+
+@pytest.mark.parametrize("M,K", [(2048, 2048), (5632, 2048), (2048, 5632)])
+def test_matmul_prefill_layer_projection(M, K):
+    # one decoder layer's projections (hidden 2048, FFN 5632) on a 512-token
+    # prompt, W ~ N(0, 0.02) quantized by the product; a sample of tokens is
+    # checked against the oracle (each output row depends on its token only)
+    N = 512
+    rng = np.random.default_rng(M + K)
+    wf = (rng.standard_normal(M * K, dtype=np.float32) * np.float32(0.02))
+    w, s = wxo_q8.quantizePackQ8(input=wf, N=M, K=K)
+    a = rng.standard_normal(N * K, dtype=np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K, rows=[0, 1, 63, 64, 200, 511])
+
+
+def test_matmul_invalid_sizes_raise():
+    with pytest.raises(wxo_q8.WxoError):
+        wxo_q8.matmulQ8(a=np.zeros(4, np.float32), weight=np.zeros(1, np.uint32), scale=np.zeros(1, np.float32),
+                        N=2, M=1, K=4)  # a too short
+    # a K beyond 2^22 is refused before any launch
+    assert wxo_q8.lib().wxo_matmul_q8(None, None, None, None, 1, 1, (1 << 22) + 1, None) == wxo_q8.WXO_ERR_INVALID
+    assert "2^22" in wxo_q8.lib().wxo_last_error().decode()
+
+
+# ---------------------------------------------------------------- dequant / gather
+
+@pytest.mark.parametrize("N,K", [(1, 1), (3, 5), (4, 9), (7, 64), (5, 1027), (300, 4099), (2048, 2048)])
+def test_dequantize_packed_bit_exact(N, K):
+    rng = np.random.default_rng(N + K)
+    w = rng.integers(0, 2 ** 32, N * ((K + 3) // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(-1, 1, N).astype(np.float32)
+    s[0] = np.inf
+    got = wxo_q8.dequantizePackedQ8(w, s, N, K)
+    want = oracle.dequantize_packed_q8(w, s, N, K)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    got[nan] = 0
+    want[nan] = 0
+    assert_bits_equal(got, want, f"dequantizePackedQ8 N={N} K={K}")
+
+
+def test_dequantize_packed_kats():
+    c = kat()["dequantize_packed_q8"][1]
+    w = oracle.pack_int8_rows(np.array(c["codes"], np.int8), c["N"], c["K"])
+    assert wxo_q8.dequantizePackedQ8(w, np.array(c["scale"], np.float32), c["N"], c["K"]).tolist() == c["want"]
+
+
+@pytest.mark.parametrize("outF,inF", [(1, 1), (5, 3), (3, 8), (16, 112), (512, 1792), (67, 1027), (2048, 5632)])
+def test_dequant_transpose_bit_exact(outF, inF):
+    codes = np.array([((i * 37) % 200) - 100 for i in range(outF * inF)], dtype=np.int8) if outF * inF < 10 ** 6 \
+        else np.random.default_rng(0).integers(-128, 128, outF * inF).astype(np.int8)
+    s = np.array([0.01 + i * 1e-4 for i in range(outF)], dtype=np.float32)
+    w = oracle.pack_int8_rows(codes, outF, inF)
+    got = wxo_q8.dequantTranspose(weight=w, scale=s, outFeatures=outF, inFeatures=inF)
+    assert_bits_equal(got, oracle.dequant_transpose(w, s, outF, inF), f"dequantTranspose {outF}x{inF}")
+
+
+def test_dequant_transpose_size_errors():
+    c = kat()["dequant_transpose"][1]
+    w = oracle.pack_int8_rows(np.zeros(15, np.int8), 3, 5)
+    wxo_q8.dequantTranspose(weight=w, scale=np.zeros(3, np.float32), outFeatures=3, inFeatures=5)
+    with pytest.raises(wxo_q8.WxoError, match=c["errors"][0]):
+        wxo_q8.dequantTranspose(weight=w, scale=np.zeros(3, np.float32), outFeatures=4, inFeatures=5)
+    with pytest.raises(wxo_q8.WxoError, match=c["errors"][1]):
+        wxo_q8.dequantTranspose(weight=w, scale=np.zeros(2, np.float32), outFeatures=3, inFeatures=5)
+
+
+@pytest.mark.parametrize("case", kat()["gather_dequant_rows"], ids=lambda c: c["source"].split(" ")[0])
+def test_gather_kat(case):
+    got = wxo_q8.gatherDequantRows((np.array(case["codes"], np.int8), np.array(case["scale"], np.float32)),
+                                   case["indices"], case["D"])
+    assert got.tolist() == case["want"]
+
+
+@pytest.mark.parametrize("rows,D", [(37, 70), (1000, 2048), (300, 4099), (5, 16)])
+def test_gather_bit_exact(rows, D):
+    rng = np.random.default_rng(rows + D)
+    codes = rng.integers(-128, 128, rows * D).astype(np.int8)
+    s = rng.uniform(0.001, 0.1, rows).astype(np.float32)
+    idx = np.concatenate([rng.integers(0, rows, 50), [-1, rows, 2 ** 40, -(2 ** 40), 0, rows - 1, 0]]).astype(np.int64)
+    got = wxo_q8.gatherDequantRows((codes, s), idx, D)
+    assert_bits_equal(got, oracle.gather_dequant_rows(codes, s, rows, D, idx), f"gather rows={rows} D={D}")

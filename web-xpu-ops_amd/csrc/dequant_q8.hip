@@ -1,0 +1,202 @@
+// dequant_q8.hip -- packed int8 weights back to f32 on gfx950.
+//
+// Reference semantics (all bit-exact: one f32 product of an int8 code and
+// its row's scale, which is what the reference's f64 product stored to a
+// Float32Array rounds to):
+//   dequantize_packed   llm/weights-q8.ts:161-177 (dequantizePackedQ8):
+//                       out[n, k] = q[n, k] * s[n], f32 [N, K]
+//   dequant_transpose   ops/dequant_transpose/reference.ts:40-59
+//                       (dequantTranspose): out[k, n] = q[n, k] * s[n],
+//                       f32 [inFeatures, outFeatures]
+//   gather_dequant_rows llm/weights-q8.ts:207-222 (gatherDequantRows): rows
+//                       of an int8 [rows, D] table in request order, indices
+//                       outside [0, rows) give a row of zeros
+//
+// All three are HBM-bound byte work: the codes are read once and the f32
+// output (4x the bytes) is written once, in 16-byte stores wherever the row
+// layout allows.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.hpp"
+#include "wave_ops.hpp"
+
+namespace wxo {
+
+namespace {
+
+__device__ __forceinline__ float dq(uint32_t word, int lane, float s) {
+    // sign-extended byte `lane` of the word times the scale, one f32 rounding
+    return __fmul_rn((float)(int32_t)((int32_t)(word << (24 - 8 * lane)) >> 24), s);
+}
+
+// out [N, K]: each thread owns 4 consecutive packed words (16 codes) of one
+// row.  K % 16 == 0 rows are stored as four 16-byte stores; otherwise the
+// row start is only 4-byte aligned and the codes past K are not stored.
+__global__ __launch_bounds__(256) void dequantize_packed_kernel(const uint32_t* __restrict__ weight,
+                                                                const float* __restrict__ scale,
+                                                                float* __restrict__ out, uint32_t N, uint32_t K,
+                                                                uint32_t W) {
+    const uint32_t G = (W + 3u) / 4u;  // 4-word groups per row
+    const uint64_t total = (uint64_t)N * G;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t row = (uint32_t)(i / G), grp = (uint32_t)(i - (uint64_t)row * G);
+        const uint32_t w0 = grp * 4u;
+        const uint32_t* wr = weight + (size_t)row * W;
+        const float s = scale[row];
+        float* o = out + (size_t)row * K + (size_t)w0 * 4u;
+        if ((K & 15u) == 0u) {
+            const u32x4_a4 v = load_u32x4(wr + w0);
+            const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                f32x4_a4 f;
+                f.x = dq(ws[q], 0, s);
+                f.y = dq(ws[q], 1, s);
+                f.z = dq(ws[q], 2, s);
+                f.w = dq(ws[q], 3, s);
+                *reinterpret_cast<f32x4_a4*>(o + 4 * q) = f;
+            }
+        } else {
+            for (uint32_t q = 0; q < 4u && w0 + q < W; ++q) {
+                const uint32_t word = wr[w0 + q];
+#pragma unroll
+                for (int l = 0; l < 4; ++l) {
+                    const uint32_t k = (w0 + q) * 4u + (uint32_t)l;
+                    if (k < K) o[q * 4u + (uint32_t)l] = dq(word, l, s);
+                }
+            }
+        }
+    }
+}
+
+// out [K, N] (inFeatures x outFeatures).  A workgroup transposes one tile of
+// 64 rows (n) x 64 codes (k) through LDS: each thread reads one packed word
+// of 4 rows, writes the dequantized values transposed, and after the barrier
+// stores 4 floats of a k-row, so both the word reads and the f32 writes are
+// contiguous runs.
+constexpr uint32_t kTrTile = 64u;
+
+__global__ __launch_bounds__(256) void dequant_transpose_kernel(const uint32_t* __restrict__ weight,
+                                                                const float* __restrict__ scale,
+                                                                float* __restrict__ out, uint32_t N, uint32_t K,
+                                                                uint32_t W) {
+    __shared__ float tile[kTrTile][kTrTile + 1];
+    const uint32_t n0 = blockIdx.x * kTrTile, k0 = blockIdx.y * kTrTile;
+    const uint32_t t = threadIdx.x;
+    // load: word column wc = t % 16 (codes k0 + 4 wc .. +3), rows r = t / 16 + 16 j
+    {
+        const uint32_t wc = t & 15u;
+        const uint32_t w = k0 / 4u + wc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t r = (t >> 4) + 16u * (uint32_t)j;
+            const uint32_t n = n0 + r;
+            uint32_t word = 0u;
+            float s = 0.0f;
+            if (n < N && w < W) {
+                word = weight[(size_t)n * W + w];
+                s = scale[n];
+            }
+#pragma unroll
+            for (int l = 0; l < 4; ++l) tile[wc * 4u + (uint32_t)l][r] = dq(word, l, s);
+        }
+    }
+    __syncthreads();
+    // store: k-row kr = t / 16 + 16 j, columns 4 (t % 16) .. +3
+    const uint32_t c4 = (t & 15u) * 4u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t kr = (t >> 4) + 16u * (uint32_t)j;
+        const uint32_t k = k0 + kr;
+        if (k >= K) continue;
+        float* o = out + (size_t)k * N + n0 + c4;
+        if ((N & 3u) == 0u && n0 + c4 + 3u < N) {
+            f32x4_a4 f;
+            f.x = tile[kr][c4];
+            f.y = tile[kr][c4 + 1u];
+            f.z = tile[kr][c4 + 2u];
+            f.w = tile[kr][c4 + 3u];
+            *reinterpret_cast<f32x4_a4*>(o) = f;
+        } else {
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q)
+                if (n0 + c4 + q < N) o[q] = tile[kr][c4 + q];
+        }
+    }
+}
+
+// out [count, D]: one workgroup per requested row, 16 codes per thread per
+// pass.  An index outside [0, rows) writes zeros.
+__global__ __launch_bounds__(256) void gather_dequant_rows_kernel(const int8_t* __restrict__ codes,
+                                                                  const float* __restrict__ scale,
+                                                                  const int64_t* __restrict__ indices,
+                                                                  float* __restrict__ out, uint32_t rows,
+                                                                  uint32_t D, uint32_t count) {
+    for (uint32_t i = blockIdx.x; i < count; i += gridDim.x) {
+        const int64_t idx = indices[i];
+        const bool valid = idx >= 0 && idx < (int64_t)rows;
+        const float s = valid ? scale[idx] : 0.0f;
+        const int8_t* src = codes + (valid ? (size_t)idx * D : 0);
+        float* o = out + (size_t)i * D;
+        if (valid && (D & 15u) == 0u && ((uintptr_t)src & 15u) == 0u) {
+            for (uint32_t c = threadIdx.x * 16u; c < D; c += blockDim.x * 16u) {
+                const u32x4v v = *reinterpret_cast<const u32x4v*>(src + c);
+                const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    f32x4_a4 f;
+                    f.x = dq(ws[q], 0, s);
+                    f.y = dq(ws[q], 1, s);
+                    f.z = dq(ws[q], 2, s);
+                    f.w = dq(ws[q], 3, s);
+                    *reinterpret_cast<f32x4_a4*>(o + c + 4u * (uint32_t)q) = f;
+                }
+            }
+        } else {
+            for (uint32_t c = threadIdx.x; c < D; c += blockDim.x)
+                o[c] = valid ? __fmul_rn((float)src[c], s) : 0.0f;
+        }
+    }
+}
+
+uint32_t grid_cap(uint64_t items, uint32_t per_block, const DeviceInfo& dev) {
+    const uint64_t want = (items + per_block - 1) / per_block;
+    const uint64_t cap = (uint64_t)(dev.cu_count > 0 ? dev.cu_count : 256) * 16u;
+    return (uint32_t)(want < cap ? (want > 0 ? want : 1) : cap);
+}
+
+}  // namespace
+
+hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K,
+                                    float* out, const DeviceInfo& dev, hipStream_t stream) {
+    if (N == 0 || K == 0) return hipSuccess;
+    const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
+    const uint64_t items = (uint64_t)N * ((W + 3u) / 4u);
+    hipLaunchKernelGGL(dequantize_packed_kernel, dim3(grid_cap(items, 256, dev)), dim3(256), 0, stream, weight,
+                       scale, out, N, K, W);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_transpose(const uint32_t* weight, const float* scale, uint32_t out_features,
+                                    uint32_t in_features, float* out, hipStream_t stream) {
+    if (out_features == 0 || in_features == 0) return hipSuccess;
+    const uint32_t W = (uint32_t)(((uint64_t)in_features + 3) / 4);
+    const dim3 grid((out_features + kTrTile - 1) / kTrTile, (in_features + kTrTile - 1) / kTrTile);
+    hipLaunchKernelGGL(dequant_transpose_kernel, grid, dim3(256), 0, stream, weight, scale, out, out_features,
+                       in_features, W);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_dequant_rows(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
+                                      const int64_t* indices, uint32_t count, float* out, const DeviceInfo& dev,
+                                      hipStream_t stream) {
+    if (count == 0 || D == 0) return hipSuccess;
+    const uint32_t cap = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256) * 8u;
+    hipLaunchKernelGGL(gather_dequant_rows_kernel, dim3(count < cap ? count : cap), dim3(256), 0, stream, codes,
+                       scale, indices, out, rows, D, count);
+    return hipGetLastError();
+}
+
+}  // namespace wxo

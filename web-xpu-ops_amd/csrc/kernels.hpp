@@ -61,4 +61,18 @@ hipError_t launch_pack_q8(const int32_t* codes, uint32_t N, uint32_t K, uint32_t
 hipError_t launch_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed,
                                  const DeviceInfo& dev, hipStream_t stream);
 
+// matmulQ8 (matmul_q8.hip): a f32 [N, K] x packed weight [M, ceil(K/4)] ->
+// out f32 [N, M].  K <= 2^22.
+hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
+                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, const char** variant);
+
+// dequant_q8.hip
+hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K,
+                                    float* out, const DeviceInfo& dev, hipStream_t stream);
+hipError_t launch_dequant_transpose(const uint32_t* weight, const float* scale, uint32_t out_features,
+                                    uint32_t in_features, float* out, hipStream_t stream);
+hipError_t launch_gather_dequant_rows(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
+                                      const int64_t* indices, uint32_t count, float* out, const DeviceInfo& dev,
+                                      hipStream_t stream);
+
 }  // namespace wxo

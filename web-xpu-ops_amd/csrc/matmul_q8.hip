@@ -1,0 +1,347 @@
+// matmul_q8.hip -- W8A32 GEMM (prefill) for gfx950 on the matrix cores:
+// out[n, m] = (sum_k a[n, k] * q[m, k]) * s[m], a f32 [N, K] (tokens),
+// weight [M, ceil(K/4)] packed int8 (matvecQ8's wire format), out f32 [N, M].
+//
+// Reference: ops/matmul/reference.ts:124-137 (matmulQ8) -- the reference
+// dequantizes each weight term to f32 (fround(q * s)) and runs the f64 triple
+// loop of matmul (:37-49); its own doc defines the op as "N independent
+// matvecQ8 calls against the same weight" (:76-77).  This kernel computes
+// that matvecQ8 form: the exact dot product of codes and activations, then
+// the row scale once.  Against the reference's per-term form the two differ
+// by at most one f32 rounding of each term, 2^-24 of sum |a * q * s|, far
+// inside the 1e-5 bar the tests hold.
+//
+// Exactness on bf16 matrix cores: a code q in [-128, 127] is exact in bf16;
+// each activation a is split by truncation into a = h + m + l, three bf16
+// parts of 8 significant bits each (a non-finite a stays whole in h, with a
+// canonical quiet NaN), so every product q * part is exact in f32 and
+// v_mfma_f32_16x16x32_bf16 sums them in f32.  Each 256-code slice of K is
+// summed in the matrix-core accumulator (24 accumulations) and then folded
+// into an outer f32 sum, so no rounding chain exceeds ~24 + K/256 steps:
+// for K = 11008 that is under 70 roundings, 4e-6 of sum |terms|.
+//
+// Tiling: a workgroup (4 waves, 2 x 2) owns BM = 32 FB weight rows x BN = 64
+// tokens and walks K in steps of 64 codes.  Each step, every thread loads
+// BM / 64 dwordx4 of packed codes and 4 dwordx4 of activations (one token,
+// 16 consecutive k), converts them once (codes -> bf16, activations -> three
+// bf16 parts) into LDS, and after one barrier every wave reads its operand
+// fragments with ds_read_b128 and issues FB x 2 x 2 x 3 matrix-core ops.
+// The LDS holds two stages, so the next step's conversion overlaps the
+// current step's reads; the next step's global loads are issued before the
+// current step's matrix work.  Rows of 64 codes (128 bytes of bf16) are
+// stored with their 16-byte pieces XOR-swizzled by row, so the 16 rows one
+// fragment read touches fall in distinct bank groups.
+//
+// Operand layout of v_mfma_f32_16x16x32_bf16 (probed on gfx950): A lane l
+// holds A[l % 16][8 (l / 16) + e], B lane l holds B[8 (l / 16) + e][l % 16],
+// C lane l holds C[4 (l / 16) + v][l % 16].  A = weight rows (16 features),
+// B = activations (16 tokens), so a lane's C values are 4 consecutive
+// features of one token: one 16-byte store into out[token, :].
+//
+// Workgroups are numbered so that the 8 XCDs (which take workgroups
+// round-robin) each hold a contiguous run of tiles that share activation
+// tiles in that XCD's L2.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.hpp"
+#include "wave_ops.hpp"
+
+namespace wxo {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kBK = 64;            // codes per K step
+constexpr uint32_t kBN = 64;            // tokens per workgroup
+constexpr uint32_t kRowBytes = kBK * 2; // one LDS row: 64 bf16
+constexpr uint32_t kFoldSteps = 4;      // fold the accumulator every 256 codes
+
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
+    // upper halves of two f32 bit patterns, a in the low half
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// 16 codes (4 packed words) -> 16 bf16 in two 16-byte pieces.
+__device__ __forceinline__ void codes16_to_bf16(u32x4v w, u32x4v& lo, u32x4v& hi) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    uint32_t r[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float c0 = (float)(int8_t)(ws[q]);
+        const float c1 = (float)(int8_t)(ws[q] >> 8);
+        const float c2 = (float)(int8_t)(ws[q] >> 16);
+        const float c3 = (float)((int32_t)ws[q] >> 24);
+        r[2 * q] = hi_pair(__float_as_uint(c0), __float_as_uint(c1));
+        r[2 * q + 1] = hi_pair(__float_as_uint(c2), __float_as_uint(c3));
+    }
+    lo = u32x4v{r[0], r[1], r[2], r[3]};
+    hi = u32x4v{r[4], r[5], r[6], r[7]};
+}
+
+// Splits one activation into bf16 parts h + m + l (bit patterns in the upper
+// halves).  Finite values split exactly; a non-finite value keeps all of
+// itself in h (NaN canonicalised so truncation cannot turn it into Inf).
+__device__ __forceinline__ void split3(uint32_t bits, bool finite_all, uint32_t& h, uint32_t& m, uint32_t& l) {
+    if (finite_all) {
+        h = bits & 0xffff0000u;
+        const float r = __uint_as_float(bits) - __uint_as_float(h);  // exact
+        m = __float_as_uint(r) & 0xffff0000u;
+        l = __float_as_uint(r - __uint_as_float(m));                 // exact, <= 8 significant bits
+    } else {
+        const float a = __uint_as_float(bits);
+        if (isfinite(a)) {
+            h = bits & 0xffff0000u;
+            const float r = a - __uint_as_float(h);
+            m = __float_as_uint(r) & 0xffff0000u;
+            l = __float_as_uint(r - __uint_as_float(m));
+        } else {
+            h = isnan(a) ? 0x7fc00000u : bits;
+            m = 0u;
+            l = 0u;
+        }
+    }
+}
+
+template <int FB>
+__global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict__ a,
+                                                        const uint32_t* __restrict__ weight,
+                                                        const float* __restrict__ scale, float* __restrict__ out,
+                                                        uint32_t N, uint32_t M, uint32_t K, uint32_t W,
+                                                        uint32_t mtiles, uint32_t ntiles) {
+    constexpr uint32_t BM = 32u * FB;                 // weight rows per workgroup
+    constexpr uint32_t AST = BM * kRowBytes;          // bytes of one A stage
+    constexpr uint32_t BST = 3u * kBN * kRowBytes;    // bytes of one B stage (three parts)
+    constexpr int AL = (int)(BM / 64u);               // A loads per thread per step
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [A0 A1 B0 B1]
+
+    // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
+    // contiguous run of the (token-major) tile sequence.
+    const uint32_t total = mtiles * ntiles;
+    const uint32_t per = (total + 7u) / 8u;
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t lin = xcd * per + slot;
+    if (lin >= total) return;  // whole workgroup: no barrier is skipped by part of it
+    const uint32_t nt = lin / mtiles, mt = lin - nt * mtiles;
+    const uint32_t m0 = mt * BM, n0 = nt * kBN;
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t wm = (wv & 1u) * (BM / 2u);  // wave's first weight row in the tile
+    const uint32_t wn = (wv >> 1) * 32u;        // wave's first token in the tile
+    const uint32_t j = lane & 15u, g = lane >> 4;
+
+    const uint32_t mrows = min(BM, M - m0);
+    const uint32_t ntok = min(kBN, N - n0);
+    const uint32_t rowbytes = W * 4u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)m0 * W, mrows * rowbytes);
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a + (size_t)n0 * K, ntok * K * 4u);
+
+    // Global load assignment.  A: thread t, load u -> row t / 4 + 64 u, codes
+    // 16 (t % 4) .. +15 of the step.  B: token t / 4, k 16 (t % 4) .. +15.
+    const uint32_t ac = t & 3u;
+    const uint32_t ar = t >> 2;
+    const uint32_t btok = t >> 2;
+    const int boff = (int)((btok * K + ac * 16u) * 4u);
+
+    u32x4v ga[AL], gb[4];
+    auto issue = [&](uint32_t k0) {
+#pragma unroll
+        for (int u = 0; u < AL; ++u)
+            ga[u] = load_nt_b128(wrs, (int)((ar + 64u * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            gb[q] = __builtin_amdgcn_raw_buffer_load_b128(ars, boff + 16 * q, (int)(k0 * 4u), 0);
+    };
+
+    // Writes the converted step into stage s.  Row r's 16-byte piece p sits at
+    // piece p ^ (r & 7).
+    auto convert_store = [&](uint32_t s, uint32_t k0) {
+        uint8_t* as = lds + s * AST;
+        uint8_t* bs = lds + 2u * AST + s * BST;
+#pragma unroll
+        for (int u = 0; u < AL; ++u) {
+            const uint32_t r = ar + 64u * (uint32_t)u;
+            u32x4v lo, hi;
+            codes16_to_bf16(ga[u], lo, hi);
+            const uint32_t p0 = (2u * ac) ^ (r & 7u), p1 = (2u * ac + 1u) ^ (r & 7u);
+            *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p0 * 16u) = lo;
+            *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p1 * 16u) = hi;
+        }
+        // activations: zero the entries at k >= K (they belong to the next token)
+        uint32_t v[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[4 * q] = gb[q].x;
+            v[4 * q + 1] = gb[q].y;
+            v[4 * q + 2] = gb[q].z;
+            v[4 * q + 3] = gb[q].w;
+        }
+        const uint32_t kb = k0 + ac * 16u;
+        if (k0 + kBK > K) {  // wave-uniform: only the last step can be ragged
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                if (kb + (uint32_t)e >= K) v[e] = 0u;
+        }
+        // one vote per thread: are all 16 finite?
+        uint32_t expmax = 0u;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) expmax = max(expmax, v[e] & 0x7f800000u);
+        const bool fin = expmax != 0x7f800000u;
+        uint32_t hp[8], mp[8], lp[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            uint32_t h0, m0_, l0, h1, m1, l1;
+            split3(v[e], fin, h0, m0_, l0);
+            split3(v[e + 1], fin, h1, m1, l1);
+            hp[e / 2] = hi_pair(h0, h1);
+            mp[e / 2] = hi_pair(m0_, m1);
+            lp[e / 2] = hi_pair(l0, l1);
+        }
+        const uint32_t p0 = (2u * ac) ^ (btok & 7u), p1 = (2u * ac + 1u) ^ (btok & 7u);
+        uint8_t* row = bs + btok * kRowBytes;
+        *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{hp[0], hp[1], hp[2], hp[3]};
+        *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{hp[4], hp[5], hp[6], hp[7]};
+        row += kBN * kRowBytes;
+        *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{mp[0], mp[1], mp[2], mp[3]};
+        *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{mp[4], mp[5], mp[6], mp[7]};
+        row += kBN * kRowBytes;
+        *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{lp[0], lp[1], lp[2], lp[3]};
+        *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{lp[4], lp[5], lp[6], lp[7]};
+    };
+
+    f32x4 acc[FB][2], sum[FB][2];
+#pragma unroll
+    for (int f = 0; f < FB; ++f)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            sum[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+    // Matrix work of one stage: two 32-code substeps.
+    auto compute = [&](uint32_t s) {
+        const uint8_t* as = lds + s * AST;
+        const uint8_t* bs = lds + 2u * AST + s * BST;
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+            const uint32_t piece = 4u * (uint32_t)ss + g;
+            bf16x8 af[FB], bf[2][3];
+#pragma unroll
+            for (int f = 0; f < FB; ++f) {
+                const uint32_t r = wm + 16u * (uint32_t)f + j;
+                af[f] = *reinterpret_cast<const bf16x8*>(as + r * kRowBytes + ((piece ^ (r & 7u)) * 16u));
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const uint32_t tk = wn + 16u * (uint32_t)b + j;
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    bf[b][p] = *reinterpret_cast<const bf16x8*>(bs + ((uint32_t)p * kBN + tk) * kRowBytes +
+                                                                ((piece ^ (tk & 7u)) * 16u));
+            }
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int f = 0; f < FB; ++f)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+                        acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[f], bf[b][p], acc[f][b], 0, 0, 0);
+        }
+    };
+
+    const uint32_t steps = (K + kBK - 1u) / kBK;
+    issue(0u);
+    for (uint32_t i = 0; i < steps; ++i) {
+        const uint32_t s = i & 1u;
+        convert_store(s, i * kBK);
+        if (i + 1u < steps) issue((i + 1u) * kBK);
+        __syncthreads();
+        compute(s);
+        if ((i + 1u) % kFoldSteps == 0u || i + 1u == steps) {  // uniform
+#pragma unroll
+            for (int f = 0; f < FB; ++f)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    sum[f][b] += acc[f][b];
+                    acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    }
+
+    // Epilogue: lane (j, g) of block (f, b) holds features m0 + wm + 16 f +
+    // 4 g .. +3 of token n0 + wn + 16 b + j.
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + m0, mrows * 4u);
+#pragma unroll
+    for (int f = 0; f < FB; ++f) {
+        const uint32_t fm = wm + 16u * (uint32_t)f + 4u * g;  // within the tile
+        const u32x4v sv = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const uint32_t tok = wn + 16u * (uint32_t)b + j;
+            if (tok >= ntok) continue;
+            f32x4 y;
+            y[0] = sum[f][b][0] * __uint_as_float(sv.x);
+            y[1] = sum[f][b][1] * __uint_as_float(sv.y);
+            y[2] = sum[f][b][2] * __uint_as_float(sv.z);
+            y[3] = sum[f][b][3] * __uint_as_float(sv.w);
+            float* o = out + (size_t)(n0 + tok) * M + m0 + fm;
+            if (fm + 3u < mrows) {
+                *reinterpret_cast<f32x4_a4*>(o) = f32x4_a4{y[0], y[1], y[2], y[3]};
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (fm + (uint32_t)q < mrows) o[q] = y[q];
+            }
+        }
+    }
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = 0.0f;
+}
+
+template <int FB>
+hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N, uint32_t M,
+                     uint32_t K, hipStream_t stream) {
+    constexpr uint32_t BM = 32u * FB;
+    const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
+    const uint32_t mtiles = (M + BM - 1u) / BM, ntiles = (N + kBN - 1u) / kBN;
+    const uint32_t total = mtiles * ntiles;
+    const uint32_t grid = ((total + 7u) / 8u) * 8u;
+    const size_t lds = 2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes;
+    hipLaunchKernelGGL((matmul_q8_kernel<FB>), dim3(grid), dim3(256), lds, stream, a, weight, scale, out, N, M, K, W,
+                       mtiles, ntiles);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
+                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    if (N == 0 || M == 0) return hipSuccess;
+    if (K == 0) {
+        // matmul over an empty K: every sum is 0 (ops/matmul/reference.ts:17-18)
+        const size_t n = (size_t)N * M;
+        const uint32_t grid = (uint32_t)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
+        hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, stream, out, n);
+        if (variant) *variant = "matmul.zero";
+        return hipGetLastError();
+    }
+    // 128 weight rows per workgroup when that still gives every CU a tile,
+    // otherwise 64.
+    const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    const uint32_t ntiles = (N + kBN - 1u) / kBN;
+    if ((uint64_t)((M + 127u) / 128u) * ntiles >= cus) {
+        if (variant) *variant = "matmul.mfma128";
+        return launch_fb<4>(a, weight, scale, out, N, M, K, stream);
+    }
+    if (variant) *variant = "matmul.mfma64";
+    return launch_fb<2>(a, weight, scale, out, N, M, K, stream);
+}
+
+}  // namespace wxo

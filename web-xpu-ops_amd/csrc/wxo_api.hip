@@ -114,6 +114,39 @@ int validate_rows(const void* in, uint32_t N, uint32_t K, const char* in_name) {
     return check_ptr(in, (uint64_t)N * K, in_name);
 }
 
+int validate_matmul(const float* a, const uint32_t* w, const float* s, const float* y, uint32_t N, uint32_t M,
+                    uint32_t K) {
+    // A workgroup addresses 64 activation rows and 128 weight rows with 32-bit
+    // buffer offsets.
+    if (K > (1u << 22)) return fail(WXO_ERR_INVALID, "K=%u exceeds the supported maximum 2^22 for matmulQ8", K);
+    const uint64_t W = ((uint64_t)K + 3) / 4;
+    if (too_big(N, K) || too_big(M, W) || too_big(N, M))
+        return fail(WXO_ERR_INVALID, "sizes N=%u M=%u K=%u exceed 2^40 elements", N, M, K);
+    WXO_TRY(check_ptr(a, (uint64_t)N * K, "a"));
+    WXO_TRY(check_ptr(w, (uint64_t)M * W, "weight"));
+    WXO_TRY(check_ptr(s, M, "scale"));
+    WXO_TRY(check_ptr(y, (uint64_t)N * M, "output"));
+    return WXO_OK;
+}
+
+int validate_dequant(const uint32_t* w, const float* s, const float* y, uint32_t N, uint32_t K) {
+    const uint64_t W = ((uint64_t)K + 3) / 4;
+    if (too_big(N, K)) return fail(WXO_ERR_INVALID, "sizes N=%u K=%u exceed 2^40 elements", N, K);
+    WXO_TRY(check_ptr(w, (uint64_t)N * W, "weight"));
+    WXO_TRY(check_ptr(s, N, "scale"));
+    return check_ptr(y, (uint64_t)N * K, "output");
+}
+
+int validate_gather(const int8_t* codes, const float* s, const int64_t* idx, const float* y, uint32_t rows,
+                    uint32_t D, uint32_t count) {
+    if (too_big(rows, D) || too_big(count, D))
+        return fail(WXO_ERR_INVALID, "sizes rows=%u D=%u count=%u exceed 2^40 elements", rows, D, count);
+    WXO_TRY(check_ptr(codes, (uint64_t)rows * D, "codes"));
+    WXO_TRY(check_ptr(s, rows, "scale"));
+    WXO_TRY(check_ptr(idx, count, "indices"));
+    return check_ptr(y, (uint64_t)count * D, "output");
+}
+
 hipStream_t as_hip(wxo_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 // RAII device buffer for the *_host entry points.
@@ -167,7 +200,7 @@ const char* wxo_describe(void) {
     snprintf(g_describe, sizeof g_describe,
              "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(plain|"
              "residual|ffn),matvec_q8_mfma(bf16x3),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,"
-             "pack_int8_rows",
+             "pack_int8_rows,matmul_q8(bf16x3),dequantize_packed,dequant_transpose,gather_dequant_rows",
              WXO_ABI_VERSION, WXO_BUILD_ID, d->ordinal, d->name, d->arch, d->cu_count,
              (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0));
     return g_describe;
@@ -366,6 +399,42 @@ int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* p
     return e == hipSuccess ? ok() : hip_fail(e, "quantize_pack_q8 launch");
 }
 
+int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* output, uint32_t N, uint32_t M,
+                  uint32_t K, wxo_stream_t stream) {
+    WXO_TRY(validate_matmul(a, weight, scale, output, N, M, K));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_matmul_q8(a, weight, scale, output, N, M, K, *d, as_hip(stream), nullptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "matmul_q8 launch");
+}
+
+int wxo_dequantize_packed_q8(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K, float* output,
+                             wxo_stream_t stream) {
+    WXO_TRY(validate_dequant(weight, scale, output, N, K));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_dequantize_packed(weight, scale, N, K, output, *d, as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "dequantize_packed_q8 launch");
+}
+
+int wxo_dequant_transpose(const uint32_t* weight, const float* scale, uint32_t out_features, uint32_t in_features,
+                          float* output, wxo_stream_t stream) {
+    WXO_TRY(validate_dequant(weight, scale, output, out_features, in_features));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_dequant_transpose(weight, scale, out_features, in_features, output, as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "dequant_transpose launch");
+}
+
+int wxo_gather_dequant_rows(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
+                            const int64_t* indices, uint32_t count, float* output, wxo_stream_t stream) {
+    WXO_TRY(validate_gather(codes, scale, indices, output, rows, D, count));
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = wxo::launch_gather_dequant_rows(codes, scale, rows, D, indices, count, output, *d, as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "gather_dequant_rows launch");
+}
+
 // ---- host-array forms ----------------------------------------------------------
 
 int wxo_matvec_q8_host(const uint32_t* weight, const float* scale, const float* vector, float* output, uint32_t N,
@@ -483,6 +552,70 @@ int wxo_quantize_pack_q8_host(const float* input, uint32_t N, uint32_t K, uint32
     WXO_TRY(wxo_quantize_pack_q8((const float*)in.p, N, K, (uint32_t*)p.p, (float*)sc.p, nullptr));
     WXO_TRY(p.download(packed, (size_t)N * W * 4));
     WXO_TRY(sc.download(scales, (size_t)N * 4));
+    return ok();
+}
+
+int wxo_matmul_q8_host(const float* a, const uint32_t* weight, const float* scale, float* output, uint32_t N,
+                       uint32_t M, uint32_t K) {
+    WXO_TRY(validate_matmul(a, weight, scale, output, N, M, K));
+    const size_t W = ((size_t)K + 3) / 4;
+    DevBuf da, w, s, y;
+    WXO_TRY(da.alloc((size_t)N * K * 4));
+    WXO_TRY(w.alloc((size_t)M * W * 4));
+    WXO_TRY(s.alloc((size_t)M * 4));
+    WXO_TRY(y.alloc((size_t)N * M * 4));
+    WXO_TRY(da.upload(a, (size_t)N * K * 4));
+    WXO_TRY(w.upload(weight, (size_t)M * W * 4));
+    WXO_TRY(s.upload(scale, (size_t)M * 4));
+    WXO_TRY(wxo_matmul_q8((const float*)da.p, (const uint32_t*)w.p, (const float*)s.p, (float*)y.p, N, M, K, nullptr));
+    WXO_TRY(y.download(output, (size_t)N * M * 4));
+    return ok();
+}
+
+int wxo_dequantize_packed_q8_host(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K, float* output) {
+    WXO_TRY(validate_dequant(weight, scale, output, N, K));
+    const size_t W = ((size_t)K + 3) / 4;
+    DevBuf w, s, y;
+    WXO_TRY(w.alloc((size_t)N * W * 4));
+    WXO_TRY(s.alloc((size_t)N * 4));
+    WXO_TRY(y.alloc((size_t)N * K * 4));
+    WXO_TRY(w.upload(weight, (size_t)N * W * 4));
+    WXO_TRY(s.upload(scale, (size_t)N * 4));
+    WXO_TRY(wxo_dequantize_packed_q8((const uint32_t*)w.p, (const float*)s.p, N, K, (float*)y.p, nullptr));
+    WXO_TRY(y.download(output, (size_t)N * K * 4));
+    return ok();
+}
+
+int wxo_dequant_transpose_host(const uint32_t* weight, const float* scale, uint32_t out_features,
+                               uint32_t in_features, float* output) {
+    WXO_TRY(validate_dequant(weight, scale, output, out_features, in_features));
+    const size_t W = ((size_t)in_features + 3) / 4;
+    DevBuf w, s, y;
+    WXO_TRY(w.alloc((size_t)out_features * W * 4));
+    WXO_TRY(s.alloc((size_t)out_features * 4));
+    WXO_TRY(y.alloc((size_t)out_features * in_features * 4));
+    WXO_TRY(w.upload(weight, (size_t)out_features * W * 4));
+    WXO_TRY(s.upload(scale, (size_t)out_features * 4));
+    WXO_TRY(wxo_dequant_transpose((const uint32_t*)w.p, (const float*)s.p, out_features, in_features, (float*)y.p,
+                                  nullptr));
+    WXO_TRY(y.download(output, (size_t)out_features * in_features * 4));
+    return ok();
+}
+
+int wxo_gather_dequant_rows_host(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
+                                 const int64_t* indices, uint32_t count, float* output) {
+    WXO_TRY(validate_gather(codes, scale, indices, output, rows, D, count));
+    DevBuf c, s, ix, y;
+    WXO_TRY(c.alloc((size_t)rows * D));
+    WXO_TRY(s.alloc((size_t)rows * 4));
+    WXO_TRY(ix.alloc((size_t)count * 8));
+    WXO_TRY(y.alloc((size_t)count * D * 4));
+    WXO_TRY(c.upload(codes, (size_t)rows * D));
+    WXO_TRY(s.upload(scale, (size_t)rows * 4));
+    WXO_TRY(ix.upload(indices, (size_t)count * 8));
+    WXO_TRY(wxo_gather_dequant_rows((const int8_t*)c.p, (const float*)s.p, rows, D, (const int64_t*)ix.p, count,
+                                    (float*)y.p, nullptr));
+    WXO_TRY(y.download(output, (size_t)count * D * 4));
     return ok();
 }
 

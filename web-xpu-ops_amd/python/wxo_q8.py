@@ -7,6 +7,11 @@ argument meaning:
     packQ8(codes=, N=, K=)                      -> u32 [N*W]   ops/matvec/reference.ts:267
     quantize(input=, N=, D=)                    -> (i32 codes, f32 scales)  ops/quantize/reference.ts:13
     packInt8Rows(codes, N, K)                   -> u32 [N*W]   llm/weights-q8.ts:137
+    matmulQ8(a=, weight=, scale=, N=, M=, K=)   -> f32 [N, M]  ops/matmul/reference.ts:124
+    dequantizePackedQ8(weight, scale, N, K)     -> f32 [N*K]   llm/weights-q8.ts:161
+    dequantTranspose(weight=, scale=, outFeatures=, inFeatures=) -> f32 [inF*outF]
+                                                               ops/dequant_transpose/reference.ts:40
+    gatherDequantRows(table, indices, D)        -> f32 [len*D] llm/weights-q8.ts:207
 
 plus the batched form matvecQ8Batched (M vectors), the fused
 quantizePackQ8, and device-resident buffers (DeviceBuffer) with
@@ -71,6 +76,14 @@ SIGNATURES = {
     "wxo_pack_q8_host": ([_P, _U32, _U32, _P], _I),
     "wxo_pack_int8_rows_host": ([_P, _U32, _U32, _P], _I),
     "wxo_quantize_pack_q8_host": ([_P, _U32, _U32, _P, _P], _I),
+    "wxo_matmul_q8": ([_P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
+    "wxo_dequantize_packed_q8": ([_P, _P, _U32, _U32, _P, _P], _I),
+    "wxo_dequant_transpose": ([_P, _P, _U32, _U32, _P, _P], _I),
+    "wxo_gather_dequant_rows": ([_P, _P, _U32, _U32, _P, _U32, _P, _P], _I),
+    "wxo_matmul_q8_host": ([_P, _P, _P, _P, _U32, _U32, _U32], _I),
+    "wxo_dequantize_packed_q8_host": ([_P, _P, _U32, _U32, _P], _I),
+    "wxo_dequant_transpose_host": ([_P, _P, _U32, _U32, _P], _I),
+    "wxo_gather_dequant_rows_host": ([_P, _P, _U32, _U32, _P, _U32, _P], _I),
 }
 
 
@@ -336,3 +349,69 @@ def quantizePackQ8(*, input, N: int, K: int) -> tuple[np.ndarray, np.ndarray]:
     scales = np.empty(N, dtype=np.float32)
     _check(lib().wxo_quantize_pack_q8_host(x.ctypes.data, N, K, packed.ctypes.data, scales.ctypes.data))
     return packed, scales
+
+
+def matmul_q8_device(a, weight, scale, output, N: int, M: int, K: int, stream=None) -> None:
+    _check(lib().wxo_matmul_q8(_addr(a), _addr(weight), _addr(scale), _addr(output), N, M, K, _stream_ptr(stream)))
+
+
+def dequantize_packed_q8_device(weight, scale, N: int, K: int, output, stream=None) -> None:
+    _check(lib().wxo_dequantize_packed_q8(_addr(weight), _addr(scale), N, K, _addr(output), _stream_ptr(stream)))
+
+
+def dequant_transpose_device(weight, scale, out_features: int, in_features: int, output, stream=None) -> None:
+    _check(lib().wxo_dequant_transpose(_addr(weight), _addr(scale), out_features, in_features, _addr(output),
+                                       _stream_ptr(stream)))
+
+
+def gather_dequant_rows_device(codes, scale, rows: int, D: int, indices, count: int, output, stream=None) -> None:
+    _check(lib().wxo_gather_dequant_rows(_addr(codes), _addr(scale), rows, D, _addr(indices), count, _addr(output),
+                                         _stream_ptr(stream)))
+
+
+def matmulQ8(*, a, weight, scale, N: int, M: int, K: int) -> np.ndarray:
+    """ops/matmul/reference.ts:124 -- a [N, K] against the packed weight [M, ceil(K/4)]: f32 [N, M]."""
+    av = _need(a, np.float32, N * K, "a")
+    w = _need(weight, np.uint32, M * words_per_row(K), "weight")
+    s = _need(scale, np.float32, M, "scale")
+    out = np.empty(N * M, dtype=np.float32)
+    _check(lib().wxo_matmul_q8_host(av.ctypes.data, w.ctypes.data, s.ctypes.data, out.ctypes.data, N, M, K))
+    return out.reshape(N, M)
+
+
+def dequantizePackedQ8(weight, scale, N: int, K: int) -> np.ndarray:
+    """llm/weights-q8.ts:161 -- packed [N, ceil(K/4)] -> f32 [N*K]."""
+    w = _need(weight, np.uint32, N * words_per_row(K), "weight")
+    s = _need(scale, np.float32, N, "scale")
+    out = np.empty(N * K, dtype=np.float32)
+    _check(lib().wxo_dequantize_packed_q8_host(w.ctypes.data, s.ctypes.data, N, K, out.ctypes.data))
+    return out
+
+
+def dequantTranspose(*, weight, scale, outFeatures: int, inFeatures: int) -> np.ndarray:
+    """ops/dequant_transpose/reference.ts:40 -- f32 [inFeatures * outFeatures].  Like the
+    reference, the weight and scale lengths must match exactly."""
+    w = np.ascontiguousarray(weight, dtype=np.uint32).reshape(-1)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    if w.size != outFeatures * words_per_row(inFeatures):
+        raise WxoError(WXO_ERR_INVALID, f"dequantTranspose(): expected {outFeatures * words_per_row(inFeatures)} "
+                                        f"packed words, got {w.size}")
+    if s.size != outFeatures:
+        raise WxoError(WXO_ERR_INVALID, f"dequantTranspose(): expected {outFeatures} scales, got {s.size}")
+    out = np.empty(outFeatures * inFeatures, dtype=np.float32)
+    _check(lib().wxo_dequant_transpose_host(w.ctypes.data, s.ctypes.data, outFeatures, inFeatures, out.ctypes.data))
+    return out
+
+
+def gatherDequantRows(table, indices, D: int) -> np.ndarray:
+    """llm/weights-q8.ts:207 -- table = (codes int8 [rows*D], scale f32 [rows]); rows of the
+    table in request order, zeros for indices outside [0, rows)."""
+    codes, scale = table
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    rows = s.size
+    c = _need(codes, np.int8, rows * D, "codes")
+    ix = np.ascontiguousarray(indices, dtype=np.int64).reshape(-1)
+    out = np.empty(ix.size * D, dtype=np.float32)
+    _check(lib().wxo_gather_dequant_rows_host(c.ctypes.data, s.ctypes.data, rows, D, ix.ctypes.data, ix.size,
+                                              out.ctypes.data))
+    return out

@@ -29,6 +29,8 @@ DECODER_LAYER = [  # cfg4: (name, N, K)
     ("wGate", 5632, 2048), ("wUp", 5632, 2048), ("wDown", 2048, 5632),
 ]
 DECODER_SEED = 4
+# prefill (matmulQ8): tokens in the prompt run through the cfg4 projections
+PREFILL_TOKENS = 512
 
 
 def weights_f32(rng: np.random.Generator, N: int, K: int, std: float = 0.02) -> np.ndarray:
