@@ -30,43 +30,32 @@ __device__ __forceinline__ float dq(uint32_t word, int lane, float s) {
     return __fmul_rn((float)(int32_t)((int32_t)(word << (24 - 8 * lane)) >> 24), s);
 }
 
-// out [N, K]: each thread owns 4 consecutive packed words (16 codes) of one
-// row.  K % 16 == 0 rows are stored as four 16-byte stores; otherwise the
-// row start is only 4-byte aligned and the codes past K are not stored.
+// out [N, K]: one packed word per thread per pass, consecutive threads on
+// consecutive words.  With K % 4 == 0 the output is the words' flat image, 16
+// bytes per word, so a wave stores 1 KiB contiguous; otherwise a row's output
+// stride is K floats and the codes past K are not stored.
 __global__ __launch_bounds__(256) void dequantize_packed_kernel(const uint32_t* __restrict__ weight,
                                                                 const float* __restrict__ scale,
                                                                 float* __restrict__ out, uint32_t N, uint32_t K,
                                                                 uint32_t W) {
-    const uint32_t G = (W + 3u) / 4u;  // 4-word groups per row
-    const uint64_t total = (uint64_t)N * G;
+    const uint64_t total = (uint64_t)N * W;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t row = (uint32_t)(i / G), grp = (uint32_t)(i - (uint64_t)row * G);
-        const uint32_t w0 = grp * 4u;
-        const uint32_t* wr = weight + (size_t)row * W;
+        const uint32_t row = (uint32_t)(i / W), w = (uint32_t)(i - (uint64_t)row * W);
+        const uint32_t word = weight[i];
         const float s = scale[row];
-        float* o = out + (size_t)row * K + (size_t)w0 * 4u;
-        if ((K & 15u) == 0u) {
-            const u32x4_a4 v = load_u32x4(wr + w0);
-            const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                f32x4_a4 f;
-                f.x = dq(ws[q], 0, s);
-                f.y = dq(ws[q], 1, s);
-                f.z = dq(ws[q], 2, s);
-                f.w = dq(ws[q], 3, s);
-                *reinterpret_cast<f32x4_a4*>(o + 4 * q) = f;
-            }
+        if ((K & 3u) == 0u) {
+            f32x4_a4 f;
+            f.x = dq(word, 0, s);
+            f.y = dq(word, 1, s);
+            f.z = dq(word, 2, s);
+            f.w = dq(word, 3, s);
+            *reinterpret_cast<f32x4_a4*>(out + 4u * i) = f;
         } else {
-            for (uint32_t q = 0; q < 4u && w0 + q < W; ++q) {
-                const uint32_t word = wr[w0 + q];
+            float* o = out + (size_t)row * K + (size_t)w * 4u;
 #pragma unroll
-                for (int l = 0; l < 4; ++l) {
-                    const uint32_t k = (w0 + q) * 4u + (uint32_t)l;
-                    if (k < K) o[q * 4u + (uint32_t)l] = dq(word, l, s);
-                }
-            }
+            for (int l = 0; l < 4; ++l)
+                if (w * 4u + (uint32_t)l < K) o[l] = dq(word, l, s);
         }
     }
 }
@@ -173,7 +162,7 @@ hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, 
                                     float* out, const DeviceInfo& dev, hipStream_t stream) {
     if (N == 0 || K == 0) return hipSuccess;
     const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
-    const uint64_t items = (uint64_t)N * ((W + 3u) / 4u);
+    const uint64_t items = (uint64_t)N * W;
     hipLaunchKernelGGL(dequantize_packed_kernel, dim3(grid_cap(items, 256, dev)), dim3(256), 0, stream, weight,
                        scale, out, N, K, W);
     return hipGetLastError();

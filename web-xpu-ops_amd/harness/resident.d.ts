@@ -8,6 +8,9 @@ export type ResidentQ8Op =
   | { kind: "matvecQ8Residual"; weight: ResidentBuffer; scale: ResidentBuffer; vector: ResidentBuffer; residual: ResidentBuffer; output: ResidentBuffer; N: number; K: number }
   | { kind: "packInt8Rows"; codes: ResidentBuffer; N: number; K: number; packed: ResidentBuffer }
   | { kind: "quantizePackQ8"; input: ResidentBuffer; N: number; K: number; packed: ResidentBuffer; scales: ResidentBuffer }
+  | { kind: "matmulQ8"; a: ResidentBuffer; weight: ResidentBuffer; scale: ResidentBuffer; output: ResidentBuffer; N: number; M: number; K: number }
+  | { kind: "dequantTranspose"; weight: ResidentBuffer; scale: ResidentBuffer; outFeatures: number; inFeatures: number; output: ResidentBuffer }
+  | { kind: "gatherDequantRows"; codes: ResidentBuffer; scale: ResidentBuffer; rows: number; D: number; indices: ResidentBuffer; count: number; output: ResidentBuffer }
   | { kind: "copy"; src: ResidentBuffer; srcOffset: number; dst: ResidentBuffer; dstOffset: number; size: number };
 export interface ResidentQ8Readback {
   source: ResidentBuffer;

@@ -2,7 +2,8 @@
 // engine, the MI355X counterpart of the reference's ResidentDevice
 // (harness/resident.ts:98-145, createResidentDevice :148, batch :231-382)
 // restricted to what the matvecQ8 path needs: storage buffers, uploads,
-// matvecQ8 (plain, fused FFN, fused residual) / quantize+packQ8 ops and device
+// matvecQ8 (plain, fused FFN, fused residual) / quantize+packQ8 ops, the
+// prefill-side matmulQ8 / dequantTranspose / gatherDequantRows ops and device
 // copies recorded into one batch,
 // one synchronisation per batch, selective readback.
 //
@@ -47,6 +48,10 @@ export class ResidentQ8Device {
    *        (output may be the residual buffer: the residual stream updated in place)
    *      { kind: "packInt8Rows", codes, N, K, packed }   (int8 codes -> packed words)
    *      { kind: "quantizePackQ8", input, N, K, packed, scales }
+   *      { kind: "matmulQ8", a, weight, scale, output, N, M, K }   (prefill GEMM, output [N, M])
+   *      { kind: "dequantTranspose", weight, scale, outFeatures, inFeatures, output }
+   *      { kind: "gatherDequantRows", codes, scale, rows, D, indices, count, output }
+   *        (indices: an int64 buffer of `count` row ids)
    *      { kind: "copy", src, srcOffset, dst, dstOffset, size }
    * readback: { source, sourceOffset, length, type: "f32" | "i32" | "u32" }
    */
@@ -97,6 +102,29 @@ export class ResidentQ8Device {
           need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
           need(op.scales, op.N * 4, "scales");
           a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
+          break;
+        }
+        case "matmulQ8": {
+          need(op.a, op.N * op.K * 4, "a");
+          need(op.weight, op.M * Math.ceil(op.K / 4) * 4, "weight");
+          need(op.scale, op.M * 4, "scale");
+          need(op.output, op.N * op.M * 4, "output");
+          a.matmulQ8Device(op.a.ptr, op.weight.ptr, op.scale.ptr, op.output.ptr, op.N, op.M, op.K);
+          break;
+        }
+        case "dequantTranspose": {
+          need(op.weight, op.outFeatures * Math.ceil(op.inFeatures / 4) * 4, "weight");
+          need(op.scale, op.outFeatures * 4, "scale");
+          need(op.output, op.outFeatures * op.inFeatures * 4, "output");
+          a.dequantTransposeDevice(op.weight.ptr, op.scale.ptr, op.outFeatures, op.inFeatures, op.output.ptr);
+          break;
+        }
+        case "gatherDequantRows": {
+          need(op.codes, op.rows * op.D, "codes");
+          need(op.scale, op.rows * 4, "scale");
+          need(op.indices, op.count * 8, "indices");
+          need(op.output, op.count * op.D * 4, "output");
+          a.gatherDequantRowsDevice(op.codes.ptr, op.scale.ptr, op.rows, op.D, op.indices.ptr, op.count, op.output.ptr);
           break;
         }
         case "copy": {

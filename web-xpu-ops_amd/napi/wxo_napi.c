@@ -16,12 +16,18 @@
  *   packQ8(codes: Int32Array, N, K) -> Uint32Array
  *   packInt8Rows(codes: Int8Array, N, K) -> Uint32Array
  *   quantizePackQ8(input: Float32Array, N, K) -> { weight: Uint32Array, scale: Float32Array }
+ *   matmulQ8(a: Float32Array, weight: Uint32Array, scale: Float32Array, N, M, K) -> Float32Array [N*M]
+ *   dequantizePackedQ8(weight, scale, N, K) -> Float32Array [N*K]
+ *   dequantTranspose(weight, scale, outFeatures, inFeatures) -> Float32Array [inF*outF]
+ *   gatherDequantRows(codes: Int8Array, scale: Float32Array, indices, D) -> Float32Array
  * Device-resident functions take BigInt device addresses (from malloc):
  *   malloc(bytes) -> bigint, free(ptr), upload(ptr, typedArray),
  *   download(ptr, typedArray), copy(dst, src, bytes), synchronize(),
  *   matvecQ8Device(w, s, x, y, N, K, M), quantizeDevice(in, N, D, out, scales),
  *   packQ8Device(codes, N, K, packed), packInt8RowsDevice(codes, N, K, packed),
- *   quantizePackQ8Device(in, N, K, packed, scales)
+ *   quantizePackQ8Device(in, N, K, packed, scales), matmulQ8Device(a, w, s, y, N, M, K),
+ *   dequantizePackedQ8Device(w, s, N, K, y), dequantTransposeDevice(w, s, outF, inF, y),
+ *   gatherDequantRowsDevice(codes, s, rows, D, indices, count, y)
  * Device functions are stream-ordered on the null stream; synchronize()
  * (or any download) waits for them.
  * Errors: a TypeError/RangeError for bad arguments, an Error carrying
@@ -30,6 +36,7 @@
 #include <node_api.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "wxo_q8.h"
@@ -349,6 +356,162 @@ static napi_value js_quantize_pack_q8(napi_env env, napi_callback_info info) {
     return obj;
 }
 
+/* matmulQ8(a f32 [N*K], weight u32 [M*ceil(K/4)], scale f32 [M], N, M, K) -> Float32Array [N*M] */
+static napi_value js_matmul_q8(napi_env env, napi_callback_info info) {
+    size_t argc = 6;
+    napi_value argv[6];
+    if (!get_args(env, info, 6, &argc, argv)) return NULL;
+    void *a, *w, *s;
+    size_t la, lw, ls;
+    uint32_t N, M, K;
+    if (!get_typed(env, argv[0], napi_float32_array, &a, &la, "a") ||
+        !get_typed(env, argv[1], napi_uint32_array, &w, &lw, "weight") ||
+        !get_typed(env, argv[2], napi_float32_array, &s, &ls, "scale") || !get_u32(env, argv[3], &N, "N") ||
+        !get_u32(env, argv[4], &M, "M") || !get_u32(env, argv[5], &K, "K"))
+        return NULL;
+    if (!need_len(env, la, (uint64_t)N * K, "a") || !need_len(env, lw, (uint64_t)M * words_per_row(K), "weight") ||
+        !need_len(env, ls, M, "scale"))
+        return NULL;
+    void* y;
+    napi_value out = new_typed(env, napi_float32_array, 4, (size_t)N * M, &y);
+    if (!out) return NULL;
+    int st = wxo_matmul_q8_host(a, w, s, y, N, M, K);
+    if (st != WXO_OK) return throw_status(env, st, "matmulQ8");
+    return out;
+}
+
+/* dequantizePackedQ8(weight u32, scale f32, N, K) -> Float32Array [N*K];
+ * dequantTranspose(weight u32, scale f32, outFeatures, inFeatures) -> Float32Array
+ * [inFeatures*outFeatures], with the reference's exact-length checks
+ * (ops/dequant_transpose/reference.ts:42-47) */
+static napi_value dequant_common(napi_env env, napi_callback_info info, int transpose) {
+    size_t argc = 4;
+    napi_value argv[4];
+    if (!get_args(env, info, 4, &argc, argv)) return NULL;
+    void *w, *s;
+    size_t lw, ls;
+    uint32_t N, K;
+    if (!get_typed(env, argv[0], napi_uint32_array, &w, &lw, "weight") ||
+        !get_typed(env, argv[1], napi_float32_array, &s, &ls, "scale") ||
+        !get_u32(env, argv[2], &N, transpose ? "outFeatures" : "N") ||
+        !get_u32(env, argv[3], &K, transpose ? "inFeatures" : "K"))
+        return NULL;
+    if (transpose) {
+        char msg[160];
+        if ((uint64_t)lw != (uint64_t)N * words_per_row(K)) {
+            snprintf(msg, sizeof msg, "dequantTranspose(): expected %llu packed words, got %zu",
+                     (unsigned long long)((uint64_t)N * words_per_row(K)), lw);
+            napi_throw_error(env, NULL, msg);
+            return NULL;
+        }
+        if ((uint64_t)ls != N) {
+            snprintf(msg, sizeof msg, "dequantTranspose(): expected %u scales, got %zu", N, ls);
+            napi_throw_error(env, NULL, msg);
+            return NULL;
+        }
+    } else if (!need_len(env, lw, (uint64_t)N * words_per_row(K), "weight") || !need_len(env, ls, N, "scale")) {
+        return NULL;
+    }
+    void* y;
+    napi_value out = new_typed(env, napi_float32_array, 4, (size_t)N * K, &y);
+    if (!out) return NULL;
+    int st = transpose ? wxo_dequant_transpose_host(w, s, N, K, y) : wxo_dequantize_packed_q8_host(w, s, N, K, y);
+    if (st != WXO_OK) return throw_status(env, st, transpose ? "dequantTranspose" : "dequantizePackedQ8");
+    return out;
+}
+
+static napi_value js_dequantize_packed_q8(napi_env env, napi_callback_info info) {
+    return dequant_common(env, info, 0);
+}
+static napi_value js_dequant_transpose(napi_env env, napi_callback_info info) { return dequant_common(env, info, 1); }
+
+/* Request indices as int64: a JS array of integers or an Int32Array /
+ * Uint32Array / BigInt64Array.  Returns a malloc'd array (caller frees). */
+static int64_t* get_indices(napi_env env, napi_value v, uint32_t* count) {
+    bool is_array = false, is_typed = false;
+    napi_is_array(env, v, &is_array);
+    napi_is_typedarray(env, v, &is_typed);
+    if (is_array) {
+        uint32_t n = 0;
+        napi_get_array_length(env, v, &n);
+        int64_t* out = (int64_t*)malloc((n ? n : 1) * sizeof(int64_t));
+        for (uint32_t i = 0; i < n; ++i) {
+            napi_value e;
+            napi_get_element(env, v, i, &e);
+            napi_valuetype t;
+            napi_typeof(env, e, &t);
+            double d;
+            if (t != napi_number || napi_get_value_double(env, e, &d) != napi_ok || d != d || d < -9.0e15 ||
+                d > 9.0e15 || d != (double)(int64_t)d) {
+                free(out);
+                napi_throw_type_error(env, NULL, "indices must hold integers");
+                return NULL;
+            }
+            out[i] = (int64_t)d;
+        }
+        *count = n;
+        return out;
+    }
+    if (is_typed) {
+        napi_typedarray_type t;
+        size_t n;
+        void* data;
+        napi_value ab;
+        size_t off;
+        napi_get_typedarray_info(env, v, &t, &n, &data, &ab, &off);
+        if (n > 0xffffffffu) {
+            napi_throw_range_error(env, NULL, "too many indices");
+            return NULL;
+        }
+        if (t != napi_int32_array && t != napi_uint32_array && t != napi_bigint64_array) {
+            napi_throw_type_error(env, NULL, "indices must be an array, Int32Array, Uint32Array or BigInt64Array");
+            return NULL;
+        }
+        int64_t* out = (int64_t*)malloc((n ? n : 1) * sizeof(int64_t));
+        for (size_t i = 0; i < n; ++i)
+            out[i] = t == napi_int32_array ? (int64_t)((const int32_t*)data)[i]
+                     : t == napi_uint32_array ? (int64_t)((const uint32_t*)data)[i]
+                                              : ((const int64_t*)data)[i];
+        *count = (uint32_t)n;
+        return out;
+    }
+    napi_throw_type_error(env, NULL, "indices must be an array, Int32Array, Uint32Array or BigInt64Array");
+    return NULL;
+}
+
+/* gatherDequantRows(codes Int8Array [rows*D], scale Float32Array [rows], indices, D)
+ * -> Float32Array [indices.length * D]; rows = scale.length (llm/weights-q8.ts:207-222) */
+static napi_value js_gather_dequant_rows(napi_env env, napi_callback_info info) {
+    size_t argc = 4;
+    napi_value argv[4];
+    if (!get_args(env, info, 4, &argc, argv)) return NULL;
+    void *c, *s;
+    size_t lc, ls;
+    uint32_t D;
+    if (!get_typed(env, argv[0], napi_int8_array, &c, &lc, "codes") ||
+        !get_typed(env, argv[1], napi_float32_array, &s, &ls, "scale") || !get_u32(env, argv[3], &D, "D"))
+        return NULL;
+    if (ls > 0xffffffffu) {
+        range_error(env, "too many rows");
+        return NULL;
+    }
+    const uint32_t rows = (uint32_t)ls;
+    if (!need_len(env, lc, (uint64_t)rows * D, "codes")) return NULL;
+    uint32_t count = 0;
+    int64_t* idx = get_indices(env, argv[2], &count);
+    if (!idx) return NULL;
+    void* y;
+    napi_value out = new_typed(env, napi_float32_array, 4, (size_t)count * D, &y);
+    if (!out) {
+        free(idx);
+        return NULL;
+    }
+    int st = wxo_gather_dequant_rows_host(c, s, rows, D, idx, count, y);
+    free(idx);
+    if (st != WXO_OK) return throw_status(env, st, "gatherDequantRows");
+    return out;
+}
+
 /* ---------------------------------------------------------------- device memory */
 
 static napi_value js_malloc(napi_env env, napi_callback_info info) {
@@ -546,6 +709,64 @@ static napi_value js_quantize_pack_q8_device(napi_env env, napi_callback_info in
     return NULL;
 }
 
+/* matmulQ8Device(a, weight, scale, output, N, M, K): device addresses */
+static napi_value js_matmul_q8_device(napi_env env, napi_callback_info info) {
+    size_t argc = 7;
+    napi_value argv[7];
+    uint64_t a, w, s, y;
+    uint32_t N, M, K;
+    if (!get_args(env, info, 7, &argc, argv) || !get_ptr(env, argv[0], &a, "a") ||
+        !get_ptr(env, argv[1], &w, "weight") || !get_ptr(env, argv[2], &s, "scale") ||
+        !get_ptr(env, argv[3], &y, "output") || !get_u32(env, argv[4], &N, "N") || !get_u32(env, argv[5], &M, "M") ||
+        !get_u32(env, argv[6], &K, "K"))
+        return NULL;
+    int st = wxo_matmul_q8((const float*)(uintptr_t)a, (const uint32_t*)(uintptr_t)w, (const float*)(uintptr_t)s,
+                           (float*)(uintptr_t)y, N, M, K, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "matmulQ8Device");
+    return NULL;
+}
+
+/* dequantizePackedQ8Device / dequantTransposeDevice(weight, scale, N, K, output) */
+static napi_value dequant_device_common(napi_env env, napi_callback_info info, int transpose) {
+    size_t argc = 5;
+    napi_value argv[5];
+    uint64_t w, s, y;
+    uint32_t N, K;
+    if (!get_args(env, info, 5, &argc, argv) || !get_ptr(env, argv[0], &w, "weight") ||
+        !get_ptr(env, argv[1], &s, "scale") || !get_u32(env, argv[2], &N, "N") || !get_u32(env, argv[3], &K, "K") ||
+        !get_ptr(env, argv[4], &y, "output"))
+        return NULL;
+    const uint32_t* wp = (const uint32_t*)(uintptr_t)w;
+    const float* sp = (const float*)(uintptr_t)s;
+    int st = transpose ? wxo_dequant_transpose(wp, sp, N, K, (float*)(uintptr_t)y, NULL)
+                       : wxo_dequantize_packed_q8(wp, sp, N, K, (float*)(uintptr_t)y, NULL);
+    if (st != WXO_OK) return throw_status(env, st, transpose ? "dequantTransposeDevice" : "dequantizePackedQ8Device");
+    return NULL;
+}
+static napi_value js_dequantize_packed_q8_device(napi_env env, napi_callback_info info) {
+    return dequant_device_common(env, info, 0);
+}
+static napi_value js_dequant_transpose_device(napi_env env, napi_callback_info info) {
+    return dequant_device_common(env, info, 1);
+}
+
+/* gatherDequantRowsDevice(codes, scale, rows, D, indices (int64 device array), count, output) */
+static napi_value js_gather_dequant_rows_device(napi_env env, napi_callback_info info) {
+    size_t argc = 7;
+    napi_value argv[7];
+    uint64_t c, s, ix, y;
+    uint32_t rows, D, count;
+    if (!get_args(env, info, 7, &argc, argv) || !get_ptr(env, argv[0], &c, "codes") ||
+        !get_ptr(env, argv[1], &s, "scale") || !get_u32(env, argv[2], &rows, "rows") || !get_u32(env, argv[3], &D, "D") ||
+        !get_ptr(env, argv[4], &ix, "indices") || !get_u32(env, argv[5], &count, "count") ||
+        !get_ptr(env, argv[6], &y, "output"))
+        return NULL;
+    int st = wxo_gather_dequant_rows((const int8_t*)(uintptr_t)c, (const float*)(uintptr_t)s, rows, D,
+                                     (const int64_t*)(uintptr_t)ix, count, (float*)(uintptr_t)y, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "gatherDequantRowsDevice");
+    return NULL;
+}
+
 /* ---------------------------------------------------------------- module */
 
 static napi_value init_module(napi_env env, napi_value exports) {
@@ -574,6 +795,14 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"packQ8Device", NULL, js_pack_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"packInt8RowsDevice", NULL, js_pack_int8_rows_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"quantizePackQ8Device", NULL, js_quantize_pack_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matmulQ8", NULL, js_matmul_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"dequantizePackedQ8", NULL, js_dequantize_packed_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"dequantTranspose", NULL, js_dequant_transpose, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"gatherDequantRows", NULL, js_gather_dequant_rows, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matmulQ8Device", NULL, js_matmul_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"dequantizePackedQ8Device", NULL, js_dequantize_packed_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"dequantTransposeDevice", NULL, js_dequant_transpose_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"gatherDequantRowsDevice", NULL, js_gather_dequant_rows_device, NULL, NULL, NULL, napi_enumerable, NULL},
     };
     if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;
     return exports;
