@@ -15,10 +15,10 @@
 // each activation a is split by truncation into a = h + m + l, three bf16
 // parts of 8 significant bits each (a non-finite a stays whole in h, with a
 // canonical quiet NaN), so every product q * part is exact in f32 and
-// v_mfma_f32_16x16x32_bf16 sums them in f32.  Each 256-code slice of K is
-// summed in the matrix-core accumulator (24 accumulations) and then folded
-// into an outer f32 sum, so no rounding chain exceeds ~24 + K/256 steps:
-// for K = 11008 that is under 70 roundings, 4e-6 of sum |terms|.
+// v_mfma_f32_16x16x32_bf16 sums them in f32.  Each 1024-code slice of K is
+// summed in the matrix-core accumulator (96 accumulations) and then folded
+// into an outer f32 sum, so no rounding chain exceeds ~96 + K/1024 steps:
+// for K = 11008 that is under 110 roundings, 7e-6 of sum |terms|.
 //
 // Tiling: a workgroup (4 waves, 2 x 2) owns BM = 32 FB weight rows x BN = 64
 // tokens and walks K in steps of 64 codes.  Each step, every thread loads
@@ -26,9 +26,10 @@
 // 16 consecutive k), converts them once (codes -> bf16, activations -> three
 // bf16 parts) into LDS, and after one barrier every wave reads its operand
 // fragments with ds_read_b128 and issues FB x 2 x 2 x 3 matrix-core ops.
-// The LDS holds two stages, so the next step's conversion overlaps the
-// current step's reads; the next step's global loads are issued before the
-// current step's matrix work.  Rows of 64 codes (128 bytes of bf16) are
+// The LDS holds two stages: while a wave's matrix cores work on step i, its
+// VALU converts step i + 1 into the other stage, and global loads run two
+// steps ahead of their conversion in two register sets.  The non-finite handling of the split is a wave-uniform branch taken
+// only by waves that hold an Inf or NaN.  Rows of 64 codes (128 bytes of bf16) are
 // stored with their 16-byte pieces XOR-swizzled by row, so the 16 rows one
 // fragment read touches fall in distinct bank groups.
 //
@@ -57,7 +58,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kBK = 64;            // codes per K step
 constexpr uint32_t kBN = 64;            // tokens per workgroup
 constexpr uint32_t kRowBytes = kBK * 2; // one LDS row: 64 bf16
-constexpr uint32_t kFoldSteps = 4;      // fold the accumulator every 256 codes
+constexpr uint32_t kFoldSteps = 16;     // fold the accumulator every 1024 codes
 
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
     // upper halves of two f32 bit patterns, a in the low half
@@ -81,28 +82,27 @@ __device__ __forceinline__ void codes16_to_bf16(u32x4v w, u32x4v& lo, u32x4v& hi
     hi = u32x4v{r[4], r[5], r[6], r[7]};
 }
 
-// Splits one activation into bf16 parts h + m + l (bit patterns in the upper
-// halves).  Finite values split exactly; a non-finite value keeps all of
-// itself in h (NaN canonicalised so truncation cannot turn it into Inf).
-__device__ __forceinline__ void split3(uint32_t bits, bool finite_all, uint32_t& h, uint32_t& m, uint32_t& l) {
-    if (finite_all) {
-        h = bits & 0xffff0000u;
-        const float r = __uint_as_float(bits) - __uint_as_float(h);  // exact
-        m = __float_as_uint(r) & 0xffff0000u;
-        l = __float_as_uint(r - __uint_as_float(m));                 // exact, <= 8 significant bits
-    } else {
-        const float a = __uint_as_float(bits);
-        if (isfinite(a)) {
-            h = bits & 0xffff0000u;
-            const float r = a - __uint_as_float(h);
-            m = __float_as_uint(r) & 0xffff0000u;
-            l = __float_as_uint(r - __uint_as_float(m));
-        } else {
-            h = isnan(a) ? 0x7fc00000u : bits;
-            m = 0u;
-            l = 0u;
-        }
-    }
+// Splits activations into bf16 parts h + m + l (bit patterns in the upper
+// halves).  Finite values split exactly by truncation: h keeps the top 8
+// significant bits, r = a - h is exact, m keeps r's top 8, l = r - m is exact
+// with at most 8 significant bits.  A non-finite value keeps all of itself in
+// h (a NaN canonicalised, so truncating its payload cannot make it Inf) and
+// m = l = 0, so Inf and NaN reach the products as IEEE arithmetic has them.
+__device__ __forceinline__ void split3_fast(uint32_t bits, uint32_t& h, uint32_t& m, uint32_t& l, float& r) {
+    h = bits & 0xffff0000u;
+    r = __uint_as_float(bits) - __uint_as_float(h);
+    m = __float_as_uint(r) & 0xffff0000u;
+    l = __float_as_uint(r - __uint_as_float(m));
+}
+
+__device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t& m, uint32_t& l) {
+    const bool finite = (bits & 0x7f800000u) != 0x7f800000u;
+    const bool nan = (bits & 0x7fffffffu) > 0x7f800000u;
+    const uint32_t hf = bits & 0xffff0000u;
+    const float r = finite ? __uint_as_float(bits) - __uint_as_float(hf) : 0.0f;
+    h = finite ? hf : (nan ? 0x7fc00000u : bits);
+    m = __float_as_uint(r) & 0xffff0000u;
+    l = __float_as_uint(r - __uint_as_float(m));
 }
 
 template <int FB>
@@ -147,62 +147,45 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
     const uint32_t btok = t >> 2;
     const int boff = (int)((btok * K + ac * 16u) * 4u);
 
-    u32x4v ga[AL], gb[4];
-    auto issue = [&](uint32_t k0) {
+    // Two register sets of global loads: step i's data sits in set i & 1,
+    // loaded two steps ahead.
+    u32x4v ga[2][AL], gb[2][4];
+    auto issue = [&](int b, uint32_t k0) {
 #pragma unroll
         for (int u = 0; u < AL; ++u)
-            ga[u] = load_nt_b128(wrs, (int)((ar + 64u * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
+            ga[b][u] = load_nt_b128(wrs, (int)((ar + 64u * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            gb[q] = __builtin_amdgcn_raw_buffer_load_b128(ars, boff + 16 * q, (int)(k0 * 4u), 0);
+            gb[b][q] = __builtin_amdgcn_raw_buffer_load_b128(ars, boff + 16 * q, (int)(k0 * 4u), 0);
     };
 
-    // Writes the converted step into stage s.  Row r's 16-byte piece p sits at
-    // piece p ^ (r & 7).
-    auto convert_store = [&](uint32_t s, uint32_t k0) {
-        uint8_t* as = lds + s * AST;
-        uint8_t* bs = lds + 2u * AST + s * BST;
-#pragma unroll
-        for (int u = 0; u < AL; ++u) {
-            const uint32_t r = ar + 64u * (uint32_t)u;
-            u32x4v lo, hi;
-            codes16_to_bf16(ga[u], lo, hi);
-            const uint32_t p0 = (2u * ac) ^ (r & 7u), p1 = (2u * ac + 1u) ^ (r & 7u);
-            *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p0 * 16u) = lo;
-            *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p1 * 16u) = hi;
-        }
-        // activations: zero the entries at k >= K (they belong to the next token)
-        uint32_t v[16];
+    // Zeroes, in register set s, the activations at k >= K of step k0 (they
+    // belong to the next token).  Only the last step of a ragged K needs it;
+    // the caller branches before the matrix work, so the conversion that
+    // follows stays in one block with it.
+    auto mask_b = [&](int s, uint32_t k0) {
+        const uint32_t kb = k0 + ac * 16u;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            v[4 * q] = gb[q].x;
-            v[4 * q + 1] = gb[q].y;
-            v[4 * q + 2] = gb[q].z;
-            v[4 * q + 3] = gb[q].w;
+            if (kb + 4u * (uint32_t)q >= K) gb[s][q].x = 0u;
+            if (kb + 4u * (uint32_t)q + 1u >= K) gb[s][q].y = 0u;
+            if (kb + 4u * (uint32_t)q + 2u >= K) gb[s][q].z = 0u;
+            if (kb + 4u * (uint32_t)q + 3u >= K) gb[s][q].w = 0u;
         }
-        const uint32_t kb = k0 + ac * 16u;
-        if (k0 + kBK > K) {  // wave-uniform: only the last step can be ragged
+    };
+    auto load_b = [&](int s, uint32_t (&v)[16]) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                if (kb + (uint32_t)e >= K) v[e] = 0u;
+        for (int q = 0; q < 4; ++q) {
+            v[4 * q] = gb[s][q].x;
+            v[4 * q + 1] = gb[s][q].y;
+            v[4 * q + 2] = gb[s][q].z;
+            v[4 * q + 3] = gb[s][q].w;
         }
-        // one vote per thread: are all 16 finite?
-        uint32_t expmax = 0u;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) expmax = max(expmax, v[e] & 0x7f800000u);
-        const bool fin = expmax != 0x7f800000u;
-        uint32_t hp[8], mp[8], lp[8];
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-            uint32_t h0, m0_, l0, h1, m1, l1;
-            split3(v[e], fin, h0, m0_, l0);
-            split3(v[e + 1], fin, h1, m1, l1);
-            hp[e / 2] = hi_pair(h0, h1);
-            mp[e / 2] = hi_pair(m0_, m1);
-            lp[e / 2] = hi_pair(l0, l1);
-        }
+    };
+    // The three parts of the thread's 16 activations into stage s.
+    auto store_b = [&](int s, const uint32_t (&hp)[8], const uint32_t (&mp)[8], const uint32_t (&lp)[8]) {
         const uint32_t p0 = (2u * ac) ^ (btok & 7u), p1 = (2u * ac + 1u) ^ (btok & 7u);
-        uint8_t* row = bs + btok * kRowBytes;
+        uint8_t* row = lds + 2u * AST + (uint32_t)s * BST + btok * kRowBytes;
         *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{hp[0], hp[1], hp[2], hp[3]};
         *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{hp[4], hp[5], hp[6], hp[7]};
         row += kBN * kRowBytes;
@@ -211,6 +194,59 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
         row += kBN * kRowBytes;
         *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{lp[0], lp[1], lp[2], lp[3]};
         *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{lp[4], lp[5], lp[6], lp[7]};
+    };
+    // Writes the converted step into stage s and returns the thread's
+    // non-finite indicator.  Row r's 16-byte piece p sits at piece p ^ (r & 7).
+    auto convert_store = [&](int s) -> float {
+        uint8_t* as = lds + (uint32_t)s * AST;
+#pragma unroll
+        for (int u = 0; u < AL; ++u) {
+            const uint32_t r = ar + 64u * (uint32_t)u;
+            u32x4v lo, hi;
+            codes16_to_bf16(ga[s][u], lo, hi);
+            const uint32_t p0 = (2u * ac) ^ (r & 7u), p1 = (2u * ac + 1u) ^ (r & 7u);
+            *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p0 * 16u) = lo;
+            *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p1 * 16u) = hi;
+        }
+        uint32_t v[16];
+        load_b(s, v);
+        // Split all 16 the fast way.  r = a - h is NaN exactly when a is not
+        // finite, so the sum of the r's tells whether this thread needs the
+        // slower split; the caller redoes the stage for a wave that does
+        // (nonfinite_fixup), outside the block the scheduler interleaves with
+        // the matrix work.
+        uint32_t hp[8], mp[8], lp[8];
+        float rsum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            uint32_t h0, m0_, l0, h1, m1, l1;
+            float r0, r1;
+            split3_fast(v[e], h0, m0_, l0, r0);
+            split3_fast(v[e + 1], h1, m1, l1, r1);
+            rsum += r0 + r1;
+            hp[e / 2] = hi_pair(h0, h1);
+            mp[e / 2] = hi_pair(m0_, m1);
+            lp[e / 2] = hi_pair(l0, l1);
+        }
+        store_b(s, hp, mp, lp);
+        return rsum;
+    };
+
+    // The same activation conversion for every value, Inf and NaN included.
+    auto nonfinite_fixup = [&](int s) {
+        uint32_t v[16];
+        load_b(s, v);
+        uint32_t hp[8], mp[8], lp[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+            uint32_t h0, m0_, l0, h1, m1, l1;
+            split3_any(v[e], h0, m0_, l0);
+            split3_any(v[e + 1], h1, m1, l1);
+            hp[e / 2] = hi_pair(h0, h1);
+            mp[e / 2] = hi_pair(m0_, m1);
+            lp[e / 2] = hi_pair(l0, l1);
+        }
+        store_b(s, hp, mp, lp);
     };
 
     f32x4 acc[FB][2], sum[FB][2];
@@ -223,9 +259,9 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
         }
 
     // Matrix work of one stage: two 32-code substeps.
-    auto compute = [&](uint32_t s) {
-        const uint8_t* as = lds + s * AST;
-        const uint8_t* bs = lds + 2u * AST + s * BST;
+    auto compute = [&](int s) {
+        const uint8_t* as = lds + (uint32_t)s * AST;
+        const uint8_t* bs = lds + 2u * AST + (uint32_t)s * BST;
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss) {
             const uint32_t piece = 4u * (uint32_t)ss + g;
@@ -253,23 +289,51 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
         }
     };
 
+    // Software pipeline, one barrier per step: iteration i converts step
+    // i + 1 (register set and LDS stage (i + 1) & 1) and refills that set
+    // with step i + 3, then runs step i's matrix work on stage i & 1.  The
+    // conversion (VALU) and the matrix work are independent, so a wave
+    // overlaps them.  Past the last step the conversion writes a stage nobody
+    // reads and the loads fall outside the buffer resources (they return 0).
     const uint32_t steps = (K + kBK - 1u) / kBK;
-    issue(0u);
-    for (uint32_t i = 0; i < steps; ++i) {
-        const uint32_t s = i & 1u;
-        convert_store(s, i * kBK);
-        if (i + 1u < steps) issue((i + 1u) * kBK);
+    const bool ragged = (K % kBK) != 0u;
+    auto convert_checked = [&](int b) {
+        const float rsum = convert_store(b);
+        if (__builtin_amdgcn_ballot_w64(__builtin_isnan(rsum)) != 0) nonfinite_fixup(b);  // uniform
+    };
+    issue(0, 0u);
+    issue(1, kBK);
+    if (ragged && steps == 1u) mask_b(0, 0u);
+    convert_checked(0);
+    issue(0, 2u * kBK);
+    __syncthreads();
+    // The matrix work comes first in program order: its LDS reads then need
+    // not wait behind the conversion's LDS writes, and the scheduler can fill
+    // the matrix-core latency with the conversion's VALU work.
+    auto iter = [&](int b, uint32_t i) {
+        if (ragged && i + 2u == steps) mask_b(b ^ 1, (i + 1u) * kBK);  // uniform
+        compute(b);
+        convert_checked(b ^ 1);
+        issue(b ^ 1, (i + 3u) * kBK);
         __syncthreads();
-        compute(s);
-        if ((i + 1u) % kFoldSteps == 0u || i + 1u == steps) {  // uniform
-#pragma unroll
-            for (int f = 0; f < FB; ++f)
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    sum[f][b] += acc[f][b];
-                    acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-                }
+    };
+    // Steps run in groups of kFoldSteps (an even count, so a group starts on
+    // stage 0); the accumulator is folded into the outer sum after each group.
+    for (uint32_t g0 = 0; g0 < steps; g0 += kFoldSteps) {
+        const uint32_t gend = min(g0 + kFoldSteps, steps);
+        uint32_t i = g0;
+        for (; i + 1u < gend; i += 2u) {
+            iter(0, i);
+            iter(1, i + 1u);
         }
+        if (i < gend) iter(0, i);
+#pragma unroll
+        for (int f = 0; f < FB; ++f)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                sum[f][b] += acc[f][b];
+                acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
     }
 
     // Epilogue: lane (j, g) of block (f, b) holds features m0 + wm + 16 f +
