@@ -20,12 +20,16 @@
 // into an outer f32 sum, so no rounding chain exceeds ~96 + K/1024 steps:
 // for K = 11008 that is under 110 roundings, 7e-6 of sum |terms|.
 //
-// Tiling: a workgroup (4 waves, 2 x 2) owns BM = 32 FB weight rows x BN = 64
-// tokens and walks K in steps of 64 codes.  Each step, every thread loads
-// BM / 64 dwordx4 of packed codes and 4 dwordx4 of activations (one token,
-// 16 consecutive k), converts them once (codes -> bf16, activations -> three
-// bf16 parts) into LDS, and after one barrier every wave reads its operand
-// fragments with ds_read_b128 and issues FB x 2 x 2 x 3 matrix-core ops.
+// Tiling: a workgroup of NW = 8 waves (2 over the weight rows x 4 over the
+// tokens; 4 waves, 2 x 2, also build) owns BM = 32 FB weight rows x BN = 64
+// tokens and walks K in steps of 64 codes.  Each step, the threads load the
+// tile's packed codes (one dwordx4 of 16 codes per chunk) and activations
+// (one token's 64 / NW consecutive k per thread), convert them once (codes ->
+// bf16, activations -> three bf16 parts) into LDS, and after one barrier
+// every wave reads its operand fragments with ds_read_b128 and issues
+// FB x (4 / (NW / 2)) x 2 x 3 matrix-core ops.  Two waves per SIMD let one
+// wave's LDS and barrier waits overlap the other's work (measured: 357 ->
+// 310 us for a 512-token layer against 4 waves).
 // The LDS holds two stages: while a wave's matrix cores work on step i, its
 // VALU converts step i + 1 into the other stage, and global loads run two
 // steps ahead of their conversion in two register sets.  The non-finite handling of the split is a wave-uniform branch taken
@@ -59,6 +63,9 @@ constexpr uint32_t kBK = 64;            // codes per K step
 constexpr uint32_t kBN = 64;            // tokens per workgroup
 constexpr uint32_t kRowBytes = kBK * 2; // one LDS row: 64 bf16
 constexpr uint32_t kFoldSteps = 16;     // fold the accumulator every 1024 codes
+#ifndef WXO_MM_NW
+#define WXO_MM_NW 8
+#endif
 
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
     // upper halves of two f32 bit patterns, a in the low half
@@ -105,8 +112,8 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
     l = __float_as_uint(r - __uint_as_float(m));
 }
 
-template <int FB>
-__global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict__ a,
+template <int FB, int NW>
+__global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restrict__ a,
                                                         const uint32_t* __restrict__ weight,
                                                         const float* __restrict__ scale, float* __restrict__ out,
                                                         uint32_t N, uint32_t M, uint32_t K, uint32_t W,
@@ -114,7 +121,13 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
     constexpr uint32_t BM = 32u * FB;                 // weight rows per workgroup
     constexpr uint32_t AST = BM * kRowBytes;          // bytes of one A stage
     constexpr uint32_t BST = 3u * kBN * kRowBytes;    // bytes of one B stage (three parts)
-    constexpr int AL = (int)(BM / 64u);               // A loads per thread per step
+    constexpr uint32_t NT = 64u * NW;                 // threads
+    constexpr uint32_t ACH = BM * 4u;                 // 16-code chunks of A per step
+    constexpr int AL = (int)((ACH + NT - 1u) / NT);   // A loads per thread per step
+    constexpr uint32_t FPT = 64u / NW;                // activations per thread per step (16 or 8)
+    constexpr int BL = (int)(FPT / 4u);               // B loads (dwordx4) per thread per step
+    constexpr int TB = (int)(4u / (NW / 2u));         // 16-token blocks per wave (2 or 1)
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [A0 A1 B0 B1]
 
     // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
@@ -130,8 +143,8 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
     const uint32_t t = threadIdx.x;
     const uint32_t lane = t & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t wm = (wv & 1u) * (BM / 2u);  // wave's first weight row in the tile
-    const uint32_t wn = (wv >> 1) * 32u;        // wave's first token in the tile
+    const uint32_t wm = (wv & 1u) * (BM / 2u);            // wave's first weight row in the tile
+    const uint32_t wn = (wv >> 1) * (16u * (uint32_t)TB);  // wave's first token in the tile
     const uint32_t j = lane & 15u, g = lane >> 4;
 
     const uint32_t mrows = min(BM, M - m0);
@@ -140,22 +153,26 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)m0 * W, mrows * rowbytes);
     const __amdgpu_buffer_rsrc_t ars = make_rsrc(a + (size_t)n0 * K, ntok * K * 4u);
 
-    // Global load assignment.  A: thread t, load u -> row t / 4 + 64 u, codes
-    // 16 (t % 4) .. +15 of the step.  B: token t / 4, k 16 (t % 4) .. +15.
+    // Global load assignment.  A: thread t, load u -> chunk t + NT u: row
+    // chunk / 4, codes 16 (chunk % 4) .. +15 of the step (threads past the
+    // tile's chunks load nothing; with BM = 64 and 8 waves that is waves 4-7,
+    // a wave-uniform split).  B: token t / NW, k FPT (t % NW) .. +FPT-1.
     const uint32_t ac = t & 3u;
     const uint32_t ar = t >> 2;
-    const uint32_t btok = t >> 2;
-    const int boff = (int)((btok * K + ac * 16u) * 4u);
+    const uint32_t btok = t / NW;
+    const uint32_t bc = t % NW;
+    const int boff = (int)((btok * K + bc * FPT) * 4u);
 
     // Two register sets of global loads: step i's data sits in set i & 1,
     // loaded two steps ahead.
-    u32x4v ga[2][AL], gb[2][4];
+    u32x4v ga[2][AL], gb[2][BL];
     auto issue = [&](int b, uint32_t k0) {
 #pragma unroll
         for (int u = 0; u < AL; ++u)
-            ga[b][u] = load_nt_b128(wrs, (int)((ar + 64u * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
+            if (ACH % NT == 0u || t + NT * (uint32_t)u < ACH)  // wave-uniform
+                ga[b][u] = load_nt_b128(wrs, (int)((ar + (NT / 4u) * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < BL; ++q)
             gb[b][q] = __builtin_amdgcn_raw_buffer_load_b128(ars, boff + 16 * q, (int)(k0 * 4u), 0);
     };
 
@@ -164,36 +181,38 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
     // the caller branches before the matrix work, so the conversion that
     // follows stays in one block with it.
     auto mask_b = [&](int s, uint32_t k0) {
-        const uint32_t kb = k0 + ac * 16u;
+        const uint32_t kb = k0 + bc * FPT;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < BL; ++q) {
             if (kb + 4u * (uint32_t)q >= K) gb[s][q].x = 0u;
             if (kb + 4u * (uint32_t)q + 1u >= K) gb[s][q].y = 0u;
             if (kb + 4u * (uint32_t)q + 2u >= K) gb[s][q].z = 0u;
             if (kb + 4u * (uint32_t)q + 3u >= K) gb[s][q].w = 0u;
         }
     };
-    auto load_b = [&](int s, uint32_t (&v)[16]) {
+    auto load_b = [&](int s, uint32_t (&v)[FPT]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < BL; ++q) {
             v[4 * q] = gb[s][q].x;
             v[4 * q + 1] = gb[s][q].y;
             v[4 * q + 2] = gb[s][q].z;
             v[4 * q + 3] = gb[s][q].w;
         }
     };
-    // The three parts of the thread's 16 activations into stage s.
-    auto store_b = [&](int s, const uint32_t (&hp)[8], const uint32_t (&mp)[8], const uint32_t (&lp)[8]) {
-        const uint32_t p0 = (2u * ac) ^ (btok & 7u), p1 = (2u * ac + 1u) ^ (btok & 7u);
+    // The three parts of the thread's FPT activations into stage s: FPT / 8
+    // 16-byte pieces per part, starting at piece bc * FPT / 8 of the row.
+    auto store_b = [&](int s, const uint32_t (&hp)[FPT / 2], const uint32_t (&mp)[FPT / 2],
+                       const uint32_t (&lp)[FPT / 2]) {
         uint8_t* row = lds + 2u * AST + (uint32_t)s * BST + btok * kRowBytes;
-        *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{hp[0], hp[1], hp[2], hp[3]};
-        *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{hp[4], hp[5], hp[6], hp[7]};
-        row += kBN * kRowBytes;
-        *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{mp[0], mp[1], mp[2], mp[3]};
-        *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{mp[4], mp[5], mp[6], mp[7]};
-        row += kBN * kRowBytes;
-        *reinterpret_cast<u32x4v*>(row + p0 * 16u) = u32x4v{lp[0], lp[1], lp[2], lp[3]};
-        *reinterpret_cast<u32x4v*>(row + p1 * 16u) = u32x4v{lp[4], lp[5], lp[6], lp[7]};
+#pragma unroll
+        for (uint32_t q = 0; q < FPT / 8u; ++q) {
+            const uint32_t pc = ((bc * (FPT / 8u) + q) ^ (btok & 7u)) * 16u;
+            *reinterpret_cast<u32x4v*>(row + pc) = u32x4v{hp[4 * q], hp[4 * q + 1], hp[4 * q + 2], hp[4 * q + 3]};
+            *reinterpret_cast<u32x4v*>(row + kBN * kRowBytes + pc) =
+                u32x4v{mp[4 * q], mp[4 * q + 1], mp[4 * q + 2], mp[4 * q + 3]};
+            *reinterpret_cast<u32x4v*>(row + 2u * kBN * kRowBytes + pc) =
+                u32x4v{lp[4 * q], lp[4 * q + 1], lp[4 * q + 2], lp[4 * q + 3]};
+        }
     };
     // Writes the converted step into stage s and returns the thread's
     // non-finite indicator.  Row r's 16-byte piece p sits at piece p ^ (r & 7).
@@ -201,24 +220,25 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
         uint8_t* as = lds + (uint32_t)s * AST;
 #pragma unroll
         for (int u = 0; u < AL; ++u) {
-            const uint32_t r = ar + 64u * (uint32_t)u;
+            if (!(ACH % NT == 0u || t + NT * (uint32_t)u < ACH)) continue;  // wave-uniform
+            const uint32_t r = ar + (NT / 4u) * (uint32_t)u;
             u32x4v lo, hi;
             codes16_to_bf16(ga[s][u], lo, hi);
             const uint32_t p0 = (2u * ac) ^ (r & 7u), p1 = (2u * ac + 1u) ^ (r & 7u);
             *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p0 * 16u) = lo;
             *reinterpret_cast<u32x4v*>(as + r * kRowBytes + p1 * 16u) = hi;
         }
-        uint32_t v[16];
+        uint32_t v[FPT];
         load_b(s, v);
-        // Split all 16 the fast way.  r = a - h is NaN exactly when a is not
+        // Split all FPT the fast way.  r = a - h is NaN exactly when a is not
         // finite, so the sum of the r's tells whether this thread needs the
         // slower split; the caller redoes the stage for a wave that does
         // (nonfinite_fixup), outside the block the scheduler interleaves with
         // the matrix work.
-        uint32_t hp[8], mp[8], lp[8];
+        uint32_t hp[FPT / 2], mp[FPT / 2], lp[FPT / 2];
         float rsum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 16; e += 2) {
+        for (int e = 0; e < (int)FPT; e += 2) {
             uint32_t h0, m0_, l0, h1, m1, l1;
             float r0, r1;
             split3_fast(v[e], h0, m0_, l0, r0);
@@ -234,11 +254,11 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
 
     // The same activation conversion for every value, Inf and NaN included.
     auto nonfinite_fixup = [&](int s) {
-        uint32_t v[16];
+        uint32_t v[FPT];
         load_b(s, v);
-        uint32_t hp[8], mp[8], lp[8];
+        uint32_t hp[FPT / 2], mp[FPT / 2], lp[FPT / 2];
 #pragma unroll
-        for (int e = 0; e < 16; e += 2) {
+        for (int e = 0; e < (int)FPT; e += 2) {
             uint32_t h0, m0_, l0, h1, m1, l1;
             split3_any(v[e], h0, m0_, l0);
             split3_any(v[e + 1], h1, m1, l1);
@@ -249,11 +269,11 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
         store_b(s, hp, mp, lp);
     };
 
-    f32x4 acc[FB][2], sum[FB][2];
+    f32x4 acc[FB][TB], sum[FB][TB];
 #pragma unroll
     for (int f = 0; f < FB; ++f)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < TB; ++b) {
             acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
             sum[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
@@ -265,14 +285,14 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss) {
             const uint32_t piece = 4u * (uint32_t)ss + g;
-            bf16x8 af[FB], bf[2][3];
+            bf16x8 af[FB], bf[TB][3];
 #pragma unroll
             for (int f = 0; f < FB; ++f) {
                 const uint32_t r = wm + 16u * (uint32_t)f + j;
                 af[f] = *reinterpret_cast<const bf16x8*>(as + r * kRowBytes + ((piece ^ (r & 7u)) * 16u));
             }
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < TB; ++b) {
                 const uint32_t tk = wn + 16u * (uint32_t)b + j;
 #pragma unroll
                 for (int p = 0; p < 3; ++p)
@@ -284,7 +304,7 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
 #pragma unroll
                 for (int f = 0; f < FB; ++f)
 #pragma unroll
-                    for (int b = 0; b < 2; ++b)
+                    for (int b = 0; b < TB; ++b)
                         acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[f], bf[b][p], acc[f][b], 0, 0, 0);
         }
     };
@@ -330,7 +350,7 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
 #pragma unroll
         for (int f = 0; f < FB; ++f)
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < TB; ++b) {
                 sum[f][b] += acc[f][b];
                 acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
@@ -344,7 +364,7 @@ __global__ __launch_bounds__(256) void matmul_q8_kernel(const float* __restrict_
         const uint32_t fm = wm + 16u * (uint32_t)f + 4u * g;  // within the tile
         const u32x4v sv = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < TB; ++b) {
             const uint32_t tok = wn + 16u * (uint32_t)b + j;
             if (tok >= ntok) continue;
             f32x4 y;
@@ -369,7 +389,7 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
-template <int FB>
+template <int FB, int NW>
 hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N, uint32_t M,
                      uint32_t K, hipStream_t stream) {
     constexpr uint32_t BM = 32u * FB;
@@ -378,8 +398,8 @@ hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale,
     const uint32_t total = mtiles * ntiles;
     const uint32_t grid = ((total + 7u) / 8u) * 8u;
     const size_t lds = 2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes;
-    hipLaunchKernelGGL((matmul_q8_kernel<FB>), dim3(grid), dim3(256), lds, stream, a, weight, scale, out, N, M, K, W,
-                       mtiles, ntiles);
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW>), dim3(grid), dim3(64 * NW), lds, stream, a, weight, scale, out, N,
+                       M, K, W, mtiles, ntiles);
     return hipGetLastError();
 }
 
@@ -402,10 +422,10 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
     const uint32_t ntiles = (N + kBN - 1u) / kBN;
     if ((uint64_t)((M + 127u) / 128u) * ntiles >= cus) {
         if (variant) *variant = "matmul.mfma128";
-        return launch_fb<4>(a, weight, scale, out, N, M, K, stream);
+        return launch_fb<4, WXO_MM_NW>(a, weight, scale, out, N, M, K, stream);
     }
     if (variant) *variant = "matmul.mfma64";
-    return launch_fb<2>(a, weight, scale, out, N, M, K, stream);
+    return launch_fb<2, WXO_MM_NW>(a, weight, scale, out, N, M, K, stream);
 }
 
 }  // namespace wxo
