@@ -551,6 +551,9 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
 // loads issued after it; vector stores count there too, which can only make
 // the wait longer).
 constexpr uint32_t kDmaTileBytes = 16u * 256u;
+// Stages per wave.  Three or four (more weight bytes in flight per wave,
+// fewer workgroups per CU) measured slower at every M from 2 to 14.
+constexpr int kDmaStages = 2;
 
 template <int T, int D>
 __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
@@ -853,21 +856,26 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
             const uint32_t wgs = (uint32_t)(kMfmaLdsBytes / lds) < 2u ? (uint32_t)(kMfmaLdsBytes / lds) : 2u;
             const uint32_t grid = min((ntiles + 3u) / 4u, cus * wgs);
             const dim3 g(grid, (a.M + 15u) / 16u);
-            // Up to 11 vectors the weight tiles go straight into LDS (whole
-            // 128-byte lines per load instruction); from 12 on the x parts
-            // leave too little LDS for the stages and the register form wins.
-            if (MC <= 11u) {
-                const bool one = MC <= 4u;  // one tile per step, two stages
-                const uint64_t ldsd =
-                    3ull * MC * Kp * 2u + 4ull * 2u * (one ? 1u : 2u) * kDmaTileBytes + 4ull * kTileSlotFloats * 4u;
-                if (ldsd <= kMfmaLdsBytes) {
+            // The weight tiles go straight into LDS (whole 128-byte lines per
+            // load instruction) whenever the stages fit beside the x parts:
+            // two tiles per step (one B read serves both) from 5 vectors,
+            // one tile per step below that or when two do not fit.
+            {
+                const uint64_t xbytes = 3ull * MC * Kp * 2u + 4ull * kTileSlotFloats * 4u;
+                const uint64_t lds1 = xbytes + 4ull * kDmaStages * 1u * kDmaTileBytes;
+                const uint64_t lds2 = xbytes + 4ull * kDmaStages * 2u * kDmaTileBytes;
+                const bool two = MC > 4u && lds2 <= kMfmaLdsBytes;
+                const uint64_t ldsd = two ? lds2 : lds1;
+                // one tile per step pays a B read per tile: from 5 vectors the
+                // register form (two tiles per step) is faster than that
+                if (two || (MC <= 4u && ldsd <= kMfmaLdsBytes)) {
                     const uint32_t wg2 = (uint32_t)(kMfmaLdsBytes / ldsd) < 2u ? 1u : 2u;
                     const dim3 g2(min((ntiles + 3u) / 4u, cus * wg2), (a.M + 15u) / 16u);
-                    if (one)
-                        hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<1, 2>), g2, dim3(256), (size_t)ldsd, stream,
+                    if (!two)
+                        hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<1, kDmaStages>), g2, dim3(256), (size_t)ldsd, stream,
                                            a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
                     else
-                        hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<2, 2>), g2, dim3(256), (size_t)ldsd, stream,
+                        hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<2, kDmaStages>), g2, dim3(256), (size_t)ldsd, stream,
                                            a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
                     if (variant) *variant = "mb.mfma_dma";
                     return hipGetLastError();
