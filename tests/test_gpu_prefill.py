@@ -141,6 +141,17 @@ def test_matmul_tile_boundaries(N, M, K):
     assert_matmul(y, a, w, s, N, M, K)
 
 
+@pytest.mark.parametrize("N,M,K", [(3, 5, 4097), (65, 70, 4100), (64, 129, 5000), (7, 33, 8191), (130, 64, 6000)])
+def test_matmul_long_ragged_k(N, M, K):
+    # K > 4096 with 64-row tiles runs 128-code steps: their ragged last step
+    rng = np.random.default_rng(N + M + K)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    w = rng.integers(0, 2 ** 32, M * ((K + 3) // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(-0.05, 0.05, M).astype(np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+
+
 def test_matmul_nonfinite_activations():
     rng = np.random.default_rng(2)
     N, M, K = 70, 40, 200

@@ -59,13 +59,10 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kBK = 64;            // codes per K step
 constexpr uint32_t kBN = 64;            // tokens per workgroup
-constexpr uint32_t kRowBytes = kBK * 2; // one LDS row: 64 bf16
-constexpr uint32_t kFoldSteps = 16;     // fold the accumulator every 1024 codes
-#ifndef WXO_MM_NW
-#define WXO_MM_NW 8
-#endif
+constexpr uint32_t kFoldCodes = 1024;   // fold the accumulator every 1024 codes
+
+
 
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
     // upper halves of two f32 bit patterns, a in the low half
@@ -112,22 +109,28 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
     l = __float_as_uint(r - __uint_as_float(m));
 }
 
-template <int FB, int NW>
+template <int FB, int NW, int BK>
 __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restrict__ a,
                                                         const uint32_t* __restrict__ weight,
                                                         const float* __restrict__ scale, float* __restrict__ out,
                                                         uint32_t N, uint32_t M, uint32_t K, uint32_t W,
                                                         uint32_t mtiles, uint32_t ntiles) {
     constexpr uint32_t BM = 32u * FB;                 // weight rows per workgroup
+    constexpr uint32_t kBK = (uint32_t)BK;            // codes per K step
+    constexpr uint32_t kRowBytes = kBK * 2u;          // one LDS row: BK bf16
+    constexpr uint32_t kFoldSteps = kFoldCodes / kBK;
+    constexpr uint32_t CPR = kBK / 16u;               // 16-code chunks per row and step
     constexpr uint32_t AST = BM * kRowBytes;          // bytes of one A stage
     constexpr uint32_t BST = 3u * kBN * kRowBytes;    // bytes of one B stage (three parts)
     constexpr uint32_t NT = 64u * NW;                 // threads
-    constexpr uint32_t ACH = BM * 4u;                 // 16-code chunks of A per step
+    constexpr uint32_t ACH = BM * CPR;                // 16-code chunks of A per step
     constexpr int AL = (int)((ACH + NT - 1u) / NT);   // A loads per thread per step
-    constexpr uint32_t FPT = 64u / NW;                // activations per thread per step (16 or 8)
+    constexpr uint32_t FPT = kBK / NW;                // activations per thread per step
     constexpr int BL = (int)(FPT / 4u);               // B loads (dwordx4) per thread per step
     constexpr int TB = (int)(4u / (NW / 2u));         // 16-token blocks per wave (2 or 1)
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static_assert(BK == 64 || BK == 128, "64- or 128-code steps");
+    static_assert(kFoldSteps % 2u == 0u, "a fold group starts on stage 0");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [A0 A1 B0 B1]
 
     // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
@@ -157,8 +160,8 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     // chunk / 4, codes 16 (chunk % 4) .. +15 of the step (threads past the
     // tile's chunks load nothing; with BM = 64 and 8 waves that is waves 4-7,
     // a wave-uniform split).  B: token t / NW, k FPT (t % NW) .. +FPT-1.
-    const uint32_t ac = t & 3u;
-    const uint32_t ar = t >> 2;
+    const uint32_t ac = t % CPR;
+    const uint32_t ar = t / CPR;
     const uint32_t btok = t / NW;
     const uint32_t bc = t % NW;
     const int boff = (int)((btok * K + bc * FPT) * 4u);
@@ -170,7 +173,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
 #pragma unroll
         for (int u = 0; u < AL; ++u)
             if (ACH % NT == 0u || t + NT * (uint32_t)u < ACH)  // wave-uniform
-                ga[b][u] = load_nt_b128(wrs, (int)((ar + (NT / 4u) * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
+                ga[b][u] = load_nt_b128(wrs, (int)((ar + (NT / CPR) * (uint32_t)u) * rowbytes + ac * 16u), (int)k0);
 #pragma unroll
         for (int q = 0; q < BL; ++q)
             gb[b][q] = __builtin_amdgcn_raw_buffer_load_b128(ars, boff + 16 * q, (int)(k0 * 4u), 0);
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
 #pragma unroll
         for (int u = 0; u < AL; ++u) {
             if (!(ACH % NT == 0u || t + NT * (uint32_t)u < ACH)) continue;  // wave-uniform
-            const uint32_t r = ar + (NT / 4u) * (uint32_t)u;
+            const uint32_t r = ar + (NT / CPR) * (uint32_t)u;
             u32x4v lo, hi;
             codes16_to_bf16(ga[s][u], lo, hi);
             const uint32_t p0 = (2u * ac) ^ (r & 7u), p1 = (2u * ac + 1u) ^ (r & 7u);
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
         const uint8_t* as = lds + (uint32_t)s * AST;
         const uint8_t* bs = lds + 2u * AST + (uint32_t)s * BST;
 #pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
+        for (int ss = 0; ss < BK / 32; ++ss) {
             const uint32_t piece = 4u * (uint32_t)ss + g;
             bf16x8 af[FB], bf[TB][3];
 #pragma unroll
@@ -389,17 +392,18 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
-template <int FB, int NW>
+template <int FB, int NW, int BK>
 hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N, uint32_t M,
                      uint32_t K, hipStream_t stream) {
+    constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
     constexpr uint32_t BM = 32u * FB;
     const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
     const uint32_t mtiles = (M + BM - 1u) / BM, ntiles = (N + kBN - 1u) / kBN;
     const uint32_t total = mtiles * ntiles;
     const uint32_t grid = ((total + 7u) / 8u) * 8u;
     const size_t lds = 2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes;
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW>), dim3(grid), dim3(64 * NW), lds, stream, a, weight, scale, out, N,
-                       M, K, W, mtiles, ntiles);
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK>), dim3(grid), dim3(64 * NW), lds, stream, a, weight, scale, out,
+                       N, M, K, W, mtiles, ntiles);
     return hipGetLastError();
 }
 
@@ -417,15 +421,22 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
         return hipGetLastError();
     }
     // 128 weight rows per workgroup when that still gives every CU a tile,
-    // otherwise 64.
+    // otherwise 64.  128-code steps halve the barriers and load round trips
+    // per unit of work; they pay off for long K with 64-row tiles (measured:
+    // 512 x 2048 x 5632 in 71 us against 79), while with 128-row tiles the
+    // two stages fill all 160 KB of LDS and leave one workgroup per CU.
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const uint32_t ntiles = (N + kBN - 1u) / kBN;
     if ((uint64_t)((M + 127u) / 128u) * ntiles >= cus) {
         if (variant) *variant = "matmul.mfma128";
-        return launch_fb<4, WXO_MM_NW>(a, weight, scale, out, N, M, K, stream);
+        return launch_fb<4, 8, 64>(a, weight, scale, out, N, M, K, stream);
+    }
+    if (K > 4096u) {
+        if (variant) *variant = "matmul.mfma64.k128";
+        return launch_fb<2, 8, 128>(a, weight, scale, out, N, M, K, stream);
     }
     if (variant) *variant = "matmul.mfma64";
-    return launch_fb<2, WXO_MM_NW>(a, weight, scale, out, N, M, K, stream);
+    return launch_fb<2, 8, 64>(a, weight, scale, out, N, M, K, stream);
 }
 
 }  // namespace wxo
