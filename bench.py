@@ -302,7 +302,48 @@ def run_suite(stream, steps, warmup):
         del c5
 
     run_prefill_suite(stream, steps, warmup, results, check)
+    results.extend(cpu_reference_ops(budget_s=1.0))
     return results
+
+
+def cpu_reference_ops(budget_s):
+    """The reference's CPU path for each measured op, restated in ECMAScript
+    (oracle/q8_oracle.mjs) and timed under node on one host core over a
+    bounded sample of the suite's shapes (oracle/cpu_baseline_ops.mjs).
+    Reported beside the GPU numbers; not a target."""
+    node = shutil.which("node")
+    if node is None:
+        return []
+    out = []
+    # op -> (algorithmic bytes of the sample, useful flops of the sample)
+    for op in ("quantize_pack", "pack_int8_rows", "ffn", "matmul", "dequantize", "dequant_transpose", "gather"):
+        proc = subprocess.run([node, os.path.join(ROOT, "oracle", "cpu_baseline_ops.mjs"), op, str(budget_s)],
+                              capture_output=True, text=True, timeout=budget_s * 20 + 120)
+        if proc.returncode != 0:
+            log(f"cpu reference {op} failed: {proc.stderr.strip()[-200:]}")
+            continue
+        r = json.loads(proc.stdout.strip().splitlines()[-1])
+        us = r["median_us"]
+        entry = {"case": f"CPU reference, one core (node {r['node']}): {r['op']}", "us": round(us, 1),
+                 "sample": {k: r[k] for k in ("N", "M", "K", "rows", "D", "T") if k in r}, "runs": r["runs"],
+                 "cores": 1}
+        if op == "quantize_pack":
+            entry["GB/s"] = round(wl.quantize_pack_bytes(r["N"], r["K"]) / (us * 1e-6) / 1e9, 3)
+        elif op == "pack_int8_rows":
+            entry["GB/s"] = round((r["N"] * r["K"] + r["N"] * ((r["K"] + 3) // 4) * 4) / (us * 1e-6) / 1e9, 3)
+        elif op == "ffn":
+            entry["GB/s"] = round(2 * wl.matvec_bytes(r["N"], r["K"]) / (us * 1e-6) / 1e9, 3)
+        elif op == "matmul":
+            entry["GFLOP/s"] = round(2.0 * r["N"] * r["M"] * r["K"] / (us * 1e-6) / 1e9, 3)
+        elif op in ("dequantize", "dequant_transpose"):
+            W = (r["K"] + 3) // 4
+            entry["GB/s"] = round((r["N"] * W * 4 + 4 * r["N"] + 4 * r["N"] * r["K"]) / (us * 1e-6) / 1e9, 3)
+        elif op == "gather":
+            entry["GB/s"] = round(r["T"] * (r["D"] + 4 + 8 + 4 * r["D"]) / (us * 1e-6) / 1e9, 3)
+        out.append(entry)
+        log(f"cpu reference {op}: {us:.0f} us per call ({entry.get('GB/s', entry.get('GFLOP/s'))} "
+            f"{'GB/s' if 'GB/s' in entry else 'GFLOP/s'}) on {entry['sample']}")
+    return out
 
 
 def run_prefill_suite(stream, steps, warmup, results, check):
@@ -418,6 +459,8 @@ def main() -> int:
             if st != 0:
                 raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
         run_prefill_suite(stream, args.steps, args.warmup, table, check)
+        if not args.no_cpu_baseline:
+            table.extend(cpu_reference_ops(budget_s=1.0))
         with open(args.prefill_suite, "w") as f:
             json.dump(table, f, indent=1)
         return 0
