@@ -24,6 +24,7 @@ Prints one JSON line:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import re
@@ -223,6 +224,37 @@ def run_suite(stream, steps, warmup):
                             "+ 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3), "GB/s": round(gbs, 1),
                     "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
     log(f"suite cfg4 layer fused: {us:.2f} us/layer  {gbs:.0f} GB/s")
+
+    # The same again as the resident batch issues it: the three same-vector
+    # projections wq/wk/wv coalesced into one wxo_matvec_q8_multi launch.
+    P3 = ctypes.c_void_p * 3
+    ns3 = (ctypes.c_uint32 * 3)(2048, 2048, 2048)
+    qkv_out = wxo_q8.DeviceBuffer(3 * 2048 * 4)
+    outs3 = P3(qkv_out.ptr, qkv_out.ptr + 2048 * 4, qkv_out.ptr + 2 * 2048 * 4)
+
+    def coalesced_step(i):
+        li = i % layers
+
+        def wp(name):
+            _, N, K, _ = mats[by[name]]
+            packed, scale = prepared[by[name]]
+            return packed.ptr + li * N * ((K + 3) // 4) * 4, scale.ptr
+
+        q, k, v = wp("wq"), wp("wk"), wp("wv")
+        check(L.wxo_matvec_q8_multi(P3(q[0], k[0], v[0]), P3(q[1], k[1], v[1]), outs3, ns3, 3, vh.ptr, 2048, sp))
+        w, sc = wp("wo")
+        check(L.wxo_matvec_q8_residual(w, sc, vh.ptr, resid.ptr, resid.ptr, 2048, 2048, sp))
+        (wg, sg), (wu, su) = wp("wGate"), wp("wUp")
+        check(L.wxo_matvec_q8_ffn(wg, sg, wu, su, vh.ptr, hidden.ptr, 5632, 2048, sp))
+        w, sc = wp("wDown")
+        check(L.wxo_matvec_q8_residual(w, sc, vf.ptr, resid.ptr, resid.ptr, 2048, 5632, sp))
+    us = time_loop(stream, coalesced_step, max(1, steps // 7), max(1, warmup // 7))
+    gbs = layer_bytes / (us * 1e-6) / 1e9
+    results.append({"case": "cfg4 decoder layer as the resident batch issues it: wq/wk/wv in one matvecQ8 multi "
+                            "launch + 2 matvecQ8Residual + 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3),
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
+    log(f"suite cfg4 layer coalesced: {us:.2f} us/layer  {gbs:.0f} GB/s")
+    qkv_out.free()
     resid.free()
     hidden.free()
     for packed, scale in prepared:

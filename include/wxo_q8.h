@@ -12,6 +12,11 @@
  *                             called from llm/kernels.ts:195-211 (runMatVecQ8) and
  *                             llm/engine-q8-resident.ts:1843-1845, :1869
  *                             M > 1: M independent matvecQ8 calls on one weight
+ *   wxo_matvec_q8_multi       several consecutive matvecQ8 dispatches on one vector, as
+ *                             the resident decode issues them: wq/wk/wv at
+ *                             llm/engine-q8-resident.ts:1843-1845 and the lm_head
+ *                             chunks at :1869 (each a q8.wgsl dispatch); one launch
+ *                             for up to 4 projections (no single reference function)
  *   wxo_matvec_q8_residual    ops/matvec/reference.ts:235-243 (matvecQ8Residual) and
  *                             its WGSL form ops/matvec/wgsl/q8_residual.wgsl, used for
  *                             o_proj / down_proj at llm/engine-q8-resident.ts:1857, :1866
@@ -114,6 +119,18 @@ int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
  * against the reference's f64 sum. */
 int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output,
                   uint32_t N, uint32_t K, uint32_t M, wxo_stream_t stream);
+
+/* Several projections of one vector: for p < count, outputs[p][n] =
+ * matvecQ8(weights[p], scales[p], vector, Ns[p], K)[n], exactly what count
+ * wxo_matvec_q8 calls with M = 1 would write (same kernel body, same
+ * tolerance).  The arrays of pointers and row counts are host memory; the
+ * operands are device memory.  Up to 4 projections share one launch (more
+ * are run 4 at a time).  Outputs run concurrently, so an output that
+ * overlaps the vector or another output is rejected.  A projection with
+ * Ns[p] = 0 is skipped. */
+int wxo_matvec_q8_multi(const uint32_t* const* weights, const float* const* scales,
+                        float* const* outputs, const uint32_t* Ns, uint32_t count,
+                        const float* vector, uint32_t K, wxo_stream_t stream);
 
 /* matvecQ8Residual: output[n] = residual[n] + (matvecQ8 row n), the sum rounded
  * to f32 after the scaled dot product is (two roundings, as the reference).

@@ -260,3 +260,51 @@ gpuTest(F, "ResidentQ8Device: fused FFN and an in-place residual add in one batc
   assert.strictEqual(W * 4 * N, wg.byteLength);
   dev.destroy();
 });
+
+gpuTest(F, "ResidentQ8Device: same-vector matvecQ8 runs share one launch and give the separate ops' results", async () => {
+  // The engine's decode order (llm/engine-q8-resident.ts:1843-1845): wq, wk, wv
+  // on one vector, then ops that depend on earlier outputs.
+  const K = 1030, W = Math.ceil(K / 4);
+  const shapes = { q: 256, k: 64, v: 64 };
+  const mats = {};
+  let p = 0;
+  for (const [name, N] of Object.entries(shapes)) {
+    mats[name] = { N, weight: matvec.packQ8({ codes: codeWave(N * K, 0.29 + 0.05 * p, p), N, K }), scale: scaleWave(N) };
+    p += 1;
+  }
+  const Nd = 100, Kd = shapes.q;  // reads q's output as its vector
+  const wd = matvec.packQ8({ codes: codeWave(Nd * Kd, 0.43), N: Nd, K: Kd }), sd = scaleWave(Nd);
+  const vector = wave(K, 0.11);
+  for (const coalesce of [true, false]) {
+    const dev = await createResidentQ8Device({ coalesce });
+    const buf = (a) => { const b = dev.createStorageBuffer(a.byteLength); dev.upload(b, 0, a); return b; };
+    const bx = buf(vector);
+    const ops = [];
+    const outs = {};
+    for (const [name, m] of Object.entries(mats)) {
+      outs[name] = dev.createStorageBuffer(m.N * 4);
+      ops.push({ kind: "matvecQ8", weight: buf(m.weight), scale: buf(m.scale), vector: bx, output: outs[name], N: m.N, K });
+    }
+    const yd = dev.createStorageBuffer(Nd * 4);
+    ops.push({ kind: "matvecQ8", weight: buf(wd), scale: buf(sd), vector: outs.q, output: yd, N: Nd, K: Kd });
+    // two ops on the same vector writing one output: in order, the second wins
+    const yk2 = dev.createStorageBuffer(shapes.k * 4);
+    const kop = ops[1];
+    ops.push({ ...kop, output: yk2 }, { ...ops[0], N: shapes.k, output: yk2 });
+    const launches0 = dev.stats.launches;
+    const [q, k, v, d, k2] = await dev.batch(ops, [outs.q, outs.k, outs.v, yd, yk2].map(
+      (b) => ({ source: b, sourceOffset: 0, length: b.size / 4, type: "f32" })));
+    const got = { q, k, v };
+    for (const [name, m] of Object.entries(mats)) {
+      const args = { weight: m.weight, scale: m.scale, vector, N: m.N, K };
+      assertMatvecAgrees(got[name], oracle.matvecQ8(args), args, `${name} coalesce=${coalesce}`);
+    }
+    const dargs = { weight: wd, scale: sd, vector: q, N: Nd, K: Kd };
+    assertMatvecAgrees(d, oracle.matvecQ8(dargs), dargs, `dependent op coalesce=${coalesce}`);
+    const qargs = { weight: mats.q.weight, scale: mats.q.scale, vector, N: shapes.k, K };
+    assertMatvecAgrees(k2, oracle.matvecQ8(qargs), qargs, `last writer coalesce=${coalesce}`);
+    // q/k/v in one launch; the dependent op and the two same-output ops alone
+    assert.strictEqual(dev.stats.launches - launches0, coalesce ? 4 : 6);
+    dev.destroy();
+  }
+});

@@ -68,6 +68,16 @@ def test_validation_happens_before_device_access():
     assert L.wxo_pack_q8(None, 3, 5, None, None) == wxo_q8.WXO_ERR_INVALID
     assert L.wxo_pack_int8_rows(None, 3, 5, None, None) == wxo_q8.WXO_ERR_INVALID
     assert L.wxo_quantize_pack_q8(None, 3, 5, None, None, None) == wxo_q8.WXO_ERR_INVALID
+    # multi-projection: arrays, per-projection sizes, overlapping outputs
+    assert L.wxo_matvec_q8_multi(None, None, None, None, 0, None, 8, None) == wxo_q8.WXO_OK
+    assert L.wxo_matvec_q8_multi(None, None, None, None, 2, None, 8, None) == wxo_q8.WXO_ERR_INVALID
+    with pytest.raises(wxo_q8.WxoError, match="projection 1: weight is NULL"):
+        wxo_q8.matvec_q8_multi_device([(16, 16, 0x10000, 4), (0, 16, 0x20000, 4)], 0x30000, 8)
+    with pytest.raises(wxo_q8.WxoError, match="outputs of projections 0 and 2 overlap"):
+        wxo_q8.matvec_q8_multi_device([(16, 16, 0x10000, 4), (16, 16, 0x20000, 4), (16, 16, 0x1000c, 4)],
+                                      0x30000, 8)
+    with pytest.raises(wxo_q8.WxoError, match="projection 0: output overlaps the vector"):
+        wxo_q8.matvec_q8_multi_device([(16, 16, 0x3001c, 4)], 0x30000, 8)
     with pytest.raises(wxo_q8.WxoError, match="weight has 3 elements"):
         wxo_q8.matvecQ8(weight=np.zeros(3, np.uint32), scale=np.ones(2, np.float32),
                         vector=np.ones(8, np.float32), N=2, K=8)

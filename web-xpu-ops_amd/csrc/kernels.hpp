@@ -50,6 +50,18 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
 // matvecQ8Residual (epi = kEpiResidual) or matvecQ8Ffn (kEpiFfn), M = 1.
 hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo& dev, hipStream_t stream,
                                   const char** variant);
+// Several single-vector projections of one vector x [K]: output_p =
+// matvecQ8(weight_p, scale_p, x, N_p, K), count <= kMaxProjections, in one
+// launch.  Outputs must be disjoint from each other and from x.
+constexpr uint32_t kMaxProjections = 4;
+struct Projection {
+    const uint32_t* weight;
+    const float* scale;
+    float* output;
+    uint32_t N;
+};
+hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count, const float* x, uint32_t K,
+                                  const DeviceInfo& dev, hipStream_t stream, const char** variant);
 hipError_t launch_fused_zero(const MatvecArgs& a, int epi, hipStream_t stream);
 hipError_t launch_fill_scaled_zero(const float* scale, float* y, uint32_t N, uint32_t M, hipStream_t stream);
 

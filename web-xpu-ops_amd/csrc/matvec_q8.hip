@@ -111,10 +111,14 @@ __device__ __forceinline__ float residual_epilogue(float r, float projected) {
 // (measured 0.33 us per call at N=11008, K=4096).  `aux` is the up
 // projection's scale (kEpiFfn) or the residual (kEpiResidual); the plain form
 // ignores weight2 and aux.
+//
+// The body is a device function over row block `block` so that the
+// multi-projection kernel below runs the same code on its own row blocks.
 template <int WAVES, int CPW, int R, int EPI>
-__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
-    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
-    float* y, uint32_t N, uint32_t K, uint32_t W, const uint32_t* __restrict__ weight2, const float* aux) {
+__device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight, const float* __restrict__ scale,
+                                             const float* __restrict__ x, float* y, uint32_t N, uint32_t K,
+                                             uint32_t W, const uint32_t* __restrict__ weight2, const float* aux,
+                                             uint32_t block) {
     constexpr int NWT = EPI == kEpiFfn ? 2 : 1;  // weights streamed
     constexpr int V = R * NWT;                     // dot products per block
     constexpr int SHIFT = 6 - ilog2(V);
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
     const int lane = (int)(threadIdx.x & 63u);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t C = (W + kChunkWords - 1) / kChunkWords;
-    const uint32_t row0 = blockIdx.x * (uint32_t)R;
+    const uint32_t row0 = block * (uint32_t)R;
     const uint32_t rows = min((uint32_t)R, N - row0);  // >= 1
     const uint32_t rowbytes = W * 4u;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)row0 * W, rows * rowbytes);
@@ -202,6 +206,39 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
             }
         }
     }
+}
+
+template <int WAVES, int CPW, int R, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* y, uint32_t N, uint32_t K, uint32_t W, const uint32_t* __restrict__ weight2, const float* aux) {
+    m1_row_block<WAVES, CPW, R, EPI>(weight, scale, x, y, N, K, W, weight2, aux, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// Several projections of one vector in one launch (up to kMaxProjections):
+// y_p = matvecQ8(weight_p, scale_p, x, N_p, K) for each p, all with the same
+// x and K.  The grid is the projections' row blocks laid end to end;
+// projection p owns blocks [start_p, start_{p+1}) (start_0 = 0, an unused
+// projection starts at 0xffffffff), so a block picks its projection with
+// wave-uniform compares and then runs the single-vector body unchanged.  One
+// launch instead of several saves each later launch's start-up and tail
+// (about 1.5 us each), which is most of a small projection's time.
+template <int WAVES, int CPW, int R>
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_multi_kernel(
+    const float* __restrict__ x, uint32_t K, uint32_t W, uint32_t start1, uint32_t start2, uint32_t start3,
+    const uint32_t* w0, const float* s0, float* y0, uint32_t n0, const uint32_t* w1, const float* s1, float* y1,
+    uint32_t n1, const uint32_t* w2, const float* s2, float* y2, uint32_t n2, const uint32_t* w3,
+    const float* s3, float* y3, uint32_t n3) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t* w = w0;
+    const float* s = s0;
+    float* y = y0;
+    uint32_t n = n0, start = 0;
+    if (b >= start1) { w = w1; s = s1; y = y1; n = n1; start = start1; }
+    if (b >= start2) { w = w2; s = s2; y = y2; n = n2; start = start2; }
+    if (b >= start3) { w = w3; s = s3; y = y3; n = n3; start = start3; }
+    m1_row_block<WAVES, CPW, R, kEpiPlain>(w, s, x, y, n, K, W, nullptr, nullptr, b - start);
 }
 
 // ---------------------------------------------------------------------------
@@ -918,6 +955,86 @@ hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo
     if (a.K == 0) return launch_fused_zero(a, epi, stream);
     return epi == kEpiFfn ? dispatch_m1<kEpiFfn>(a, dev, stream, variant)
                           : dispatch_m1<kEpiResidual>(a, dev, stream, variant);
+}
+
+namespace {
+
+template <int WAVES, int CPW, int R>
+hipError_t launch_multi(const Projection* p, uint32_t count, const float* x, uint32_t K, hipStream_t stream,
+                        const char** variant) {
+    Projection q[kMaxProjections] = {};
+    uint32_t start[kMaxProjections + 1];
+    start[0] = 0;
+    for (uint32_t i = 0; i < kMaxProjections; ++i) {
+        if (i < count) q[i] = p[i];
+        start[i + 1] = start[i] + (q[i].N + R - 1) / R;
+    }
+    const uint32_t nblocks = start[count];
+    for (uint32_t i = count; i < kMaxProjections; ++i) start[i] = 0xffffffffu;
+    hipLaunchKernelGGL((matvec_q8_multi_kernel<WAVES, CPW, R>), dim3(nblocks), dim3(WAVES * 64), 0, stream, x, K,
+                       (K + 3) / 4, start[1], start[2], start[3], q[0].weight, q[0].scale, q[0].output, q[0].N,
+                       q[1].weight, q[1].scale, q[1].output, q[1].N, q[2].weight, q[2].scale, q[2].output, q[2].N,
+                       q[3].weight, q[3].scale, q[3].output, q[3].N);
+    if (variant) *variant = CPW > 0 ? "multi.xreg" : "multi.xstream";
+    return hipGetLastError();
+}
+
+template <int WAVES, int CPW, int RMAX>
+hipError_t dispatch_multi_rows(const Projection* p, uint32_t count, const float* x, uint32_t K,
+                               const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    // The rows-per-block rule of the single-vector kernel, over the
+    // projections' blocks together.
+    const uint64_t want = 2u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    auto blocks = [&](uint32_t R) {
+        uint64_t b = 0;
+        for (uint32_t i = 0; i < count; ++i) b += (p[i].N + (uint64_t)R - 1) / R;
+        return b;
+    };
+    if constexpr (RMAX >= 16) {
+        if (blocks(16) >= want) return launch_multi<WAVES, CPW, 16>(p, count, x, K, stream, variant);
+    }
+    if constexpr (RMAX >= 8) {
+        if (blocks(8) >= want) return launch_multi<WAVES, CPW, 8>(p, count, x, K, stream, variant);
+    }
+    if constexpr (RMAX >= 4) {
+        if (blocks(4) >= want) return launch_multi<WAVES, CPW, 4>(p, count, x, K, stream, variant);
+    }
+    return launch_multi<WAVES, CPW, 2>(p, count, x, K, stream, variant);
+}
+
+}  // namespace
+
+hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count, const float* x, uint32_t K,
+                                  const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    Projection p[kMaxProjections];
+    uint32_t n = 0;
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (projections[i].N == 0) continue;
+        if (n == kMaxProjections) return hipErrorInvalidValue;
+        p[n++] = projections[i];
+        rows += projections[i].N;
+    }
+    if (n == 0) return hipSuccess;
+    // One projection, no vector terms, or a grid past 2^31 - 1 blocks (the
+    // blocks hold at least 2 rows each): the single-vector path per
+    // projection.
+    if (n == 1 || K == 0 || rows / 2 + kMaxProjections >= 0x7fffffffu) {
+        for (uint32_t i = 0; i < n; ++i) {
+            MatvecArgs a{p[i].weight, p[i].scale, x, p[i].output, p[i].N, K, 1, (K + 3) / 4};
+            const hipError_t e = launch_matvec_q8(a, dev, stream, variant);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const uint32_t C = ((K + 3) / 4 + kChunkWords - 1) / kChunkWords;
+    if (C == 1) return dispatch_multi_rows<1, 1, 16>(p, n, x, K, dev, stream, variant);
+    if (C == 2) return dispatch_multi_rows<2, 1, 16>(p, n, x, K, dev, stream, variant);
+    if (C == 3) return dispatch_multi_rows<3, 1, 16>(p, n, x, K, dev, stream, variant);
+    if (C == 4) return dispatch_multi_rows<4, 1, 16>(p, n, x, K, dev, stream, variant);
+    if (C <= 8) return dispatch_multi_rows<4, 2, 8>(p, n, x, K, dev, stream, variant);
+    if (C <= 16) return dispatch_multi_rows<4, 4, 4>(p, n, x, K, dev, stream, variant);
+    return dispatch_multi_rows<4, 0, 4>(p, n, x, K, dev, stream, variant);
 }
 
 // K = 0: every dot product is 0.

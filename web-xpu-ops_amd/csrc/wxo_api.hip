@@ -199,7 +199,7 @@ const char* wxo_describe(void) {
     }
     snprintf(g_describe, sizeof g_describe,
              "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(plain|"
-             "residual|ffn),matvec_q8_mfma(bf16x3),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,"
+             "residual|ffn),matvec_q8_multi,matvec_q8_mfma(bf16x3),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,"
              "pack_int8_rows,matmul_q8(bf16x3),dequantize_packed,dequant_transpose,gather_dequant_rows",
              WXO_ABI_VERSION, WXO_BUILD_ID, d->ordinal, d->name, d->arch, d->cu_count,
              (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0));
@@ -331,6 +331,43 @@ int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vecto
     wxo::MatvecArgs a{weight, scale, vector, output, N, K, M, (uint32_t)(((uint64_t)K + 3) / 4)};
     hipError_t e = wxo::launch_matvec_q8(a, *d, as_hip(stream), nullptr);
     return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8 launch");
+}
+
+int wxo_matvec_q8_multi(const uint32_t* const* weights, const float* const* scales, float* const* outputs,
+                        const uint32_t* Ns, uint32_t count, const float* vector, uint32_t K, wxo_stream_t stream) {
+    if (count == 0) return ok();
+    if (!weights || !scales || !outputs || !Ns) return fail(WXO_ERR_INVALID, "projection arrays are NULL");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (validate_matvec(weights[i], scales[i], vector, outputs[i], Ns[i], K, 1) != WXO_OK) {
+            char why[256];
+            snprintf(why, sizeof why, "%s", g_error);
+            return fail(WXO_ERR_INVALID, "projection %u: %s", i, why);
+        }
+    }
+    // The projections run concurrently: an output that overlaps the vector
+    // or another output would make the result depend on the schedule.
+    const auto lo = [](const void* p) { return (uintptr_t)p; };
+    for (uint32_t i = 0; i < count; ++i) {
+        if (Ns[i] == 0) continue;
+        const uintptr_t a0 = lo(outputs[i]), a1 = a0 + (uintptr_t)Ns[i] * 4u;
+        if (K > 0 && a0 < lo(vector) + (uintptr_t)K * 4u && lo(vector) < a1)
+            return fail(WXO_ERR_INVALID, "projection %u: output overlaps the vector", i);
+        for (uint32_t j = 0; j < i; ++j) {
+            if (Ns[j] == 0) continue;
+            const uintptr_t b0 = lo(outputs[j]), b1 = b0 + (uintptr_t)Ns[j] * 4u;
+            if (a0 < b1 && b0 < a1) return fail(WXO_ERR_INVALID, "outputs of projections %u and %u overlap", j, i);
+        }
+    }
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    for (uint32_t g = 0; g < count; g += wxo::kMaxProjections) {
+        wxo::Projection p[wxo::kMaxProjections];
+        const uint32_t n = count - g < wxo::kMaxProjections ? count - g : wxo::kMaxProjections;
+        for (uint32_t i = 0; i < n; ++i) p[i] = {weights[g + i], scales[g + i], outputs[g + i], Ns[g + i]};
+        hipError_t e = wxo::launch_matvec_q8_multi(p, n, vector, K, *d, as_hip(stream), nullptr);
+        if (e != hipSuccess) return hip_fail(e, "matvec_q8_multi launch");
+    }
+    return ok();
 }
 
 int wxo_matvec_q8_residual(const uint32_t* weight, const float* scale, const float* vector, const float* residual,

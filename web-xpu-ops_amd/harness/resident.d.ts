@@ -18,11 +18,16 @@ export interface ResidentQ8Readback {
   length: number;
   type: "f32" | "i32" | "u32";
 }
+export interface ResidentQ8Options {
+  /** Run consecutive same-vector matvecQ8 ops as one launch (default true). */
+  coalesce?: boolean;
+}
 export declare class ResidentQ8Device {
-  readonly stats: { buffersCreated: number; submits: number };
+  constructor(options?: ResidentQ8Options);
+  readonly stats: { buffersCreated: number; submits: number; launches: number };
   createStorageBuffer(bytes: number): ResidentBuffer;
   upload(buffer: ResidentBuffer, offset: number, data: ArrayBufferView): void;
   batch(ops: ResidentQ8Op[], readback?: ResidentQ8Readback[]): Promise<(Float32Array | Int32Array | Uint32Array)[]>;
   destroy(): void;
 }
-export declare function createResidentQ8Device(): Promise<ResidentQ8Device | null>;
+export declare function createResidentQ8Device(options?: ResidentQ8Options): Promise<ResidentQ8Device | null>;

@@ -11,15 +11,24 @@
 // by destroy(); ops are enqueued in order on the device's stream as batch()
 // walks them, so nothing is allocated inside a decode loop's steady state
 // (`stats.buffersCreated` stays flat, as the reference's test checks).
+//
+// Consecutive single-vector matvecQ8 ops on the same vector (the engine's
+// wq/wk/wv projections, llm/engine-q8-resident.ts:1843-1845, and its lm_head
+// chunks, :1869) run as one launch of matvecQ8MultiDevice when nothing in the
+// run depends on another op of the run: outputs disjoint from each other, from
+// the vector and from the run's weights and scales.  The results are those of
+// the separate ops; only the launch count changes (`stats.launches`).  Pass
+// `{ coalesce: false }` to the constructor to issue every op on its own.
 import { native } from "../native/index.js";
 
 const TYPED = { f32: Float32Array, i32: Int32Array, u32: Uint32Array };
 
 export class ResidentQ8Device {
-  constructor() {
+  constructor(options = {}) {
     this.addon = native();
     this.addon.init();
-    this.stats = { buffersCreated: 0, submits: 0 };
+    this.coalesce = options.coalesce !== false;
+    this.stats = { buffersCreated: 0, submits: 0, launches: 0 };
     this.buffers = new Set();
   }
 
@@ -57,16 +66,22 @@ export class ResidentQ8Device {
    */
   async batch(ops, readback = []) {
     const a = this.addon;
-    for (const op of ops) {
+    for (let i = 0; i < ops.length; i += 1) {
+      const op = ops[i];
+      this.stats.launches += 1;
       switch (op.kind) {
         case "matvecQ8": {
           const M = op.M === undefined ? 1 : op.M;
-          const W = Math.ceil(op.K / 4);
-          need(op.weight, op.N * W * 4, "weight");
-          need(op.scale, op.N * 4, "scale");
-          need(op.vector, M * op.K * 4, "vector");
-          need(op.output, M * op.N * 4, "output");
-          a.matvecQ8Device(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.output.ptr, op.N, op.K, M);
+          checkMatvec(op, M);
+          const run = this.coalesce && M === 1 ? sameVectorRun(ops, i) : 1;
+          if (run > 1) {
+            const group = ops.slice(i, i + run);
+            a.matvecQ8MultiDevice(group.map((g) => [g.weight.ptr, g.scale.ptr, g.output.ptr, g.N]), op.vector.ptr,
+                                  op.K);
+            i += run - 1;
+          } else {
+            a.matvecQ8Device(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.output.ptr, op.N, op.K, M);
+          }
           break;
         }
         case "matvecQ8Ffn": {
@@ -155,14 +170,60 @@ export class ResidentQ8Device {
   }
 }
 
+function checkMatvec(op, M) {
+  const W = Math.ceil(op.K / 4);
+  need(op.weight, op.N * W * 4, "weight");
+  need(op.scale, op.N * 4, "scale");
+  need(op.vector, M * op.K * 4, "vector");
+  need(op.output, M * op.N * 4, "output");
+}
+
+/** [start, end) byte range of `bytes` bytes at a resident buffer's address. */
+function span(buffer, bytes) {
+  return [buffer.ptr, buffer.ptr + BigInt(bytes)];
+}
+
+function overlaps(x, y) {
+  return x[0] < y[1] && y[0] < x[1] && x[0] < x[1] && y[0] < y[1];
+}
+
+/**
+ * How many ops from `start` on (at least 1) form a run of single-vector
+ * matvecQ8 ops on the same vector and K with no op of the run reading what
+ * another writes, so that one launch gives what the ops in order would.
+ */
+function sameVectorRun(ops, start) {
+  const first = ops[start];
+  const vec = span(first.vector, first.K * 4);
+  const outs = [];
+  const ins = [];
+  let n = 0;
+  for (let j = start; j < ops.length; j += 1) {
+    const op = ops[j];
+    if (op.kind !== "matvecQ8" || (op.M !== undefined && op.M !== 1)) break;
+    if (j > start) checkMatvec(op, 1);
+    if (op.K !== first.K || op.vector.ptr !== first.vector.ptr) break;
+    const out = span(op.output, op.N * 4);
+    const reads = [span(op.weight, op.N * Math.ceil(op.K / 4) * 4), span(op.scale, op.N * 4)];
+    if (overlaps(out, vec) || outs.some((o) => overlaps(o, out)) ||
+        reads.some((r) => outs.some((o) => overlaps(o, r))) || ins.some((r) => overlaps(r, out))) {
+      break;
+    }
+    outs.push(out);
+    ins.push(...reads);
+    n += 1;
+  }
+  return Math.max(n, 1);
+}
+
 function need(buffer, bytes, name) {
   if (!buffer || typeof buffer.ptr !== "bigint") throw new TypeError(`${name} must be a resident buffer`);
   if (bytes > buffer.size) throw new RangeError(`${name} buffer holds ${buffer.size} B, ${bytes} B needed`);
 }
 
 /** Resolves to null when no gfx950 device is visible (as harness/resident.ts:148 does without an adapter). */
-export async function createResidentQ8Device() {
+export async function createResidentQ8Device(options = {}) {
   const a = native();
   if (a.deviceCount() === 0) return null;
-  return new ResidentQ8Device();
+  return new ResidentQ8Device(options);
 }

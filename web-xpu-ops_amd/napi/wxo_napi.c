@@ -625,6 +625,57 @@ static napi_value js_matvec_q8_device(napi_env env, napi_callback_info info) {
     return NULL;
 }
 
+/* matvecQ8MultiDevice([[weight, scale, output, N], ...], vector, K): several
+ * projections of one vector (device addresses), one launch per 4. */
+static napi_value js_matvec_q8_multi_device(napi_env env, napi_callback_info info) {
+    size_t argc = 3;
+    napi_value argv[3];
+    uint64_t x;
+    uint32_t K, count = 0;
+    bool is_array = false;
+    if (!get_args(env, info, 3, &argc, argv)) return NULL;
+    if (napi_is_array(env, argv[0], &is_array) != napi_ok || !is_array)
+        return type_error(env, "%s must be an array of [weight, scale, output, N]", "projections"), NULL;
+    if (!get_ptr(env, argv[1], &x, "vector") || !get_u32(env, argv[2], &K, "K")) return NULL;
+    napi_get_array_length(env, argv[0], &count);
+    const size_t n = count > 0 ? count : 1;
+    const uint32_t** ws = (const uint32_t**)calloc(n, sizeof *ws);
+    const float** ss = (const float**)calloc(n, sizeof *ss);
+    float** ys = (float**)calloc(n, sizeof *ys);
+    uint32_t* ns = (uint32_t*)calloc(n, sizeof *ns);
+    napi_value result = NULL;
+    int okay = ws && ss && ys && ns;
+    if (!okay) napi_throw_error(env, NULL, "matvecQ8MultiDevice: out of host memory");
+    for (uint32_t i = 0; okay && i < count; ++i) {
+        napi_value e, f[4];
+        uint32_t len = 0;
+        uint64_t w, sc, y;
+        okay = napi_get_element(env, argv[0], i, &e) == napi_ok && napi_is_array(env, e, &is_array) == napi_ok &&
+               is_array && napi_get_array_length(env, e, &len) == napi_ok && len == 4;
+        if (!okay) {
+            char idx[16];
+            snprintf(idx, sizeof idx, "%u", i);
+            type_error(env, "projection %s must be [weight, scale, output, N]", idx);
+            break;
+        }
+        for (uint32_t j = 0; j < 4; ++j) napi_get_element(env, e, j, &f[j]);
+        okay = get_ptr(env, f[0], &w, "weight") && get_ptr(env, f[1], &sc, "scale") &&
+               get_ptr(env, f[2], &y, "output") && get_u32(env, f[3], &ns[i], "N");
+        ws[i] = (const uint32_t*)(uintptr_t)w;
+        ss[i] = (const float*)(uintptr_t)sc;
+        ys[i] = (float*)(uintptr_t)y;
+    }
+    if (okay) {
+        int st = wxo_matvec_q8_multi(ws, ss, ys, ns, count, (const float*)(uintptr_t)x, K, NULL);
+        if (st != WXO_OK) throw_status(env, st, "matvecQ8MultiDevice");
+    }
+    free(ws);
+    free(ss);
+    free(ys);
+    free(ns);
+    return result;
+}
+
 /* matvecQ8ResidualDevice(weight, scale, vector, residual, output, N, K): device addresses */
 static napi_value js_matvec_q8_residual_device(napi_env env, napi_callback_info info) {
     size_t argc = 7;
@@ -789,6 +840,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
         {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8MultiDevice", NULL, js_matvec_q8_multi_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8ResidualDevice", NULL, js_matvec_q8_residual_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8FfnDevice", NULL, js_matvec_q8_ffn_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"quantizeDevice", NULL, js_quantize_device, NULL, NULL, NULL, napi_enumerable, NULL},

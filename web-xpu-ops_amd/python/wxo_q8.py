@@ -63,6 +63,7 @@ SIGNATURES = {
     "wxo_event_synchronize": ([_P], _I),
     "wxo_event_elapsed_ms": ([ctypes.POINTER(ctypes.c_float), _P, _P], _I),
     "wxo_matvec_q8": ([_P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
+    "wxo_matvec_q8_multi": ([_P, _P, _P, _P, _U32, _P, _U32, _P], _I),
     "wxo_matvec_q8_residual": ([_P, _P, _P, _P, _P, _U32, _U32, _P], _I),
     "wxo_matvec_q8_ffn": ([_P, _P, _P, _P, _P, _P, _U32, _U32, _P], _I),
     "wxo_quantize": ([_P, _U32, _U32, _P, _P, _P], _I),
@@ -238,6 +239,16 @@ def _addr(x) -> int:
 def matvec_q8_device(weight, scale, vector, output, N: int, K: int, M: int = 1, stream=None) -> None:
     _check(lib().wxo_matvec_q8(_addr(weight), _addr(scale), _addr(vector), _addr(output), N, K, M,
                                _stream_ptr(stream)))
+
+
+def matvec_q8_multi_device(projections, vector, K: int, stream=None) -> None:
+    """projections: a sequence of (weight, scale, output, N); one launch per 4."""
+    n = len(projections)
+    ws = (ctypes.c_void_p * max(n, 1))(*[_addr(p[0]) for p in projections])
+    ss = (ctypes.c_void_p * max(n, 1))(*[_addr(p[1]) for p in projections])
+    ys = (ctypes.c_void_p * max(n, 1))(*[_addr(p[2]) for p in projections])
+    ns = (ctypes.c_uint32 * max(n, 1))(*[int(p[3]) for p in projections])
+    _check(lib().wxo_matvec_q8_multi(ws, ss, ys, ns, n, _addr(vector), K, _stream_ptr(stream)))
 
 
 def matvec_q8_residual_device(weight, scale, vector, residual, output, N: int, K: int, stream=None) -> None:
