@@ -254,6 +254,63 @@ def test_batched_same_sign_long_k(M, K):
         assert_matvec(ys[m], w, s, xs[m], N, K)
 
 
+@pytest.mark.parametrize("M,K", [(5, 1030), (8, 64), (12, 2048), (13, 4099), (16, 1024), (17, 1500), (32, 520),
+                                 (6, 3000)])
+def test_batched_matrix_core_shapes(M, K):
+    # From 16384 rows and 5 vectors the batched call runs on the matrix cores
+    # (when the tile's x parts fit in LDS); smaller shapes take the VALU path,
+    # which the other batched tests cover.  Ragged row tail (N % 16 != 0),
+    # ragged K, vector tiles past 16, full-range codes (-128 included).
+    rng = np.random.default_rng(M * 1009 + K)
+    N = 16397
+    w = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
+
+
+@pytest.mark.parametrize("M,K", [(5, 5376), (16, 1536)])
+def test_batched_matrix_core_same_sign_long_k(M, K):
+    # The longest K whose x parts still fit in LDS for the tile, all terms
+    # positive: the matrix cores' longest accumulation chains.
+    rng = np.random.default_rng(K + M)
+    N = 16400
+    codes = rng.integers(64, 128, size=(N, K)).astype(np.int32)
+    w = oracle.pack_q8(codes.reshape(-1), N, K)
+    s = rng.uniform(0.5, 1.0, N).astype(np.float32)
+    xs = rng.uniform(1.0, 2.0, (M, K)).astype(np.float32)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
+
+
+@pytest.mark.parametrize("M,K,N", [(M, K, 37) for M in (2, 4, 8, 12, 16) for K in (1030, 4096)]
+                         + [(M, 1030, 16397) for M in (5, 8, 12, 16)] + [(6, 4096, 16397)])
+def test_batched_nonfinite_vectors(M, K, N):
+    # Inf and NaN entries reach every row as the reference's f64 sum has them
+    # (q * Inf = +-Inf, 0 * Inf = NaN), including NaNs whose payload sits only
+    # in the low 16 bits, which a bf16 truncation would turn into infinities
+    # (N = 16397 with 5 or more vectors runs on the matrix cores, which split
+    # x into bf16 parts).
+    rng = np.random.default_rng(M * 13 + K)
+    codes = rng.integers(-127, 128, N * K, dtype=np.int32)
+    codes[::5] = 0
+    w = oracle.pack_q8(codes, N, K)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    bits = xs.view(np.uint32)
+    specials = [(0, 5, 0x7F800001), (1, 100, 0xFF800000), (0, K - 1, 0xFF800001), (1, 7, 0x7FC00000),
+                (M - 1, 64, 0x7F800000), (M - 1, 65, 0x7FBFFFFF)]
+    for m, k, b in specials:
+        bits[m, k] = b
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
+    assert np.isnan(ys[0]).all()  # every row meets a NaN in vector 0
+
+
 @pytest.mark.parametrize("M", [1, 4, 8, 16])
 def test_batched_lm_head(M):
     c = wl.make_config("cfg5", M=M)

@@ -21,8 +21,9 @@
 //    the pad bytes hold contributes q * 0 = 0; words past the row end and
 //    vector entries past K are never loaded.
 //
-// The small-M batched kernel reuses every loaded word for MT vectors: one
-// unpack per code, MT FMAs, with the MT vector slices in VGPRs.
+// The small-M batched VALU kernel reuses every loaded word for up to 8
+// vectors (one unpack per code, one FMA per vector, the vector slices in
+// VGPRs); large weights with 5 or more vectors go to the matrix cores.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -216,6 +217,108 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// A few vectors (M <= MV) on the single-vector kernel's streaming loop: the
+// same chunk loads (a whole 1 KiB of one row per instruction), one code
+// conversion per code and MV FMAs, the MV vector slices of each owned chunk in
+// VGPRs.  Costs 1 + MV VALU operations per code, so it pays only while that
+// stays under the streaming time (small MV); R * MV dot products per block
+// reduce across the wave as in the single-vector kernel.
+template <int WAVES, int CPW, int R, int MV>
+__global__ __launch_bounds__(WAVES * 64) void matvec_q8_mv_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M) {
+    constexpr int V = R * MV;
+    constexpr int XS = CPW > 0 ? CPW : 1;
+    static_assert(V <= 64, "R * MV values per lane are reduced across the wave");
+    constexpr int SHIFT = 6 - ilog2(V);
+    const int lane = (int)(threadIdx.x & 63u);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t C = (W + kChunkWords - 1) / kChunkWords;
+    const uint32_t row0 = blockIdx.x * (uint32_t)R;
+    const uint32_t rows = min((uint32_t)R, N - row0);
+    const uint32_t rowbytes = W * 4u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)row0 * W, rows * rowbytes);
+    // grid y: groups of MV vectors
+    x += (size_t)blockIdx.y * MV * K;
+    y += (size_t)blockIdx.y * MV * N;
+    M -= blockIdx.y * MV;
+
+    // vectors past M read as 0 (an empty resource)
+    __amdgpu_buffer_rsrc_t xrs[MV];
+#pragma unroll
+    for (int m = 0; m < MV; ++m) xrs[m] = make_rsrc(x + (size_t)m * K, (uint32_t)m < M ? K * 4u : 0u);
+    // CPW > 0: the slices of CPW chunk slots loaded once; CPW == 0: any K,
+    // one slot at a time with its slices
+    float xr[XS][MV][16];
+    if constexpr (CPW > 0) {
+#pragma unroll
+        for (int m = 0; m < MV; ++m)
+#pragma unroll
+            for (int j = 0; j < CPW; ++j) load_x16_rsrc(xrs[m], wave + (uint32_t)j * WAVES, lane, xr[j][m]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    const int slots = CPW > 0 ? CPW : (int)((C + WAVES - 1) / WAVES);
+#pragma unroll
+    for (int j = 0; j < slots; ++j) {
+        const uint32_t c = wave + (uint32_t)j * WAVES;
+        if (CPW != 1 && c >= C) break;  // wave-uniform
+        const int voff = (int)(c * kChunkWords * 4u + (uint32_t)lane * 16u);
+        u32x4v v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = load_nt_b128(wrs, voff, (int)(r * rowbytes));
+        __builtin_amdgcn_sched_barrier(0);
+        const int js = CPW > 0 ? j : 0;
+        if constexpr (CPW == 0) {
+#pragma unroll
+            for (int m = 0; m < MV; ++m) load_x16_rsrc(xrs[m], c, lane, xr[0][m]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+                const uint32_t w = v[r][wd];
+                const float q0 = (float)(int8_t)(w), q1 = (float)(int8_t)(w >> 8);
+                const float q2 = (float)(int8_t)(w >> 16), q3 = (float)((int32_t)w >> 24);
+#pragma unroll
+                for (int m = 0; m < MV; ++m) {
+                    float a = acc[r * MV + m];
+                    a = __builtin_fmaf(q0, xr[js][m][4 * wd], a);
+                    a = __builtin_fmaf(q1, xr[js][m][4 * wd + 1], a);
+                    a = __builtin_fmaf(q2, xr[js][m][4 * wd + 2], a);
+                    a = __builtin_fmaf(q3, xr[js][m][4 * wd + 3], a);
+                    acc[r * MV + m] = a;
+                }
+            }
+        }
+    }
+
+    wave_reduce_rows<V>(acc, lane);
+    const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
+    const uint32_t idx = (uint32_t)lane >> SHIFT;  // r * MV + m
+    if constexpr (WAVES == 1) {
+        const uint32_t r = idx / MV, m = idx % MV;
+        if (leader && r < rows && m < M) y[(size_t)m * N + row0 + r] = acc[0] * scale[row0 + r];
+    } else {
+        __shared__ float part[WAVES][V];
+        if (leader) part[wave][idx] = acc[0];
+        __syncthreads();
+        if (threadIdx.x < (unsigned)V) {
+            const uint32_t r = threadIdx.x / MV, m = threadIdx.x % MV;
+            if (r < rows && m < M) {
+                float d = part[0][threadIdx.x];
+#pragma unroll
+                for (int w = 1; w < WAVES; ++w) d += part[w][threadIdx.x];
+                y[(size_t)m * N + row0 + r] = d * scale[row0 + r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Several projections of one vector in one launch (up to kMaxProjections):
 // y_p = matvecQ8(weight_p, scale_p, x, N_p, K) for each p, all with the same
 // x and K.  The grid is the projections' row blocks laid end to end;
@@ -239,94 +342,6 @@ __global__ __launch_bounds__(WAVES * 64) void matvec_q8_multi_kernel(
     if (b >= start2) { w = w2; s = s2; y = y2; n = n2; start = start2; }
     if (b >= start3) { w = w3; s = s3; y = y3; n = n3; start = start3; }
     m1_row_block<WAVES, CPW, R, kEpiPlain>(w, s, x, y, n, K, W, nullptr, nullptr, b - start);
-}
-
-// ---------------------------------------------------------------------------
-// Small-M batched: MT vectors per pass.  Lane l owns 4 codes (one word) per
-// 64-word chunk; the MT x 4 vector values of each owned word sit in VGPRs.
-// Each wave takes chunks c = wave, wave + WAVES, ... (CPW of them).
-template <int WAVES, int CPW, int R, int MT>
-__global__ __launch_bounds__(WAVES * 64) void matvec_q8_mb_kernel(
-    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
-    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M, uint32_t nblocks) {
-    constexpr uint32_t CW = 64;  // words per chunk: one dword per lane
-    constexpr int SHIFT = 6 - ilog2(R * MT);
-    static_assert(R * MT <= 64, "R * MT values per lane are reduced across the wave");
-    const int lane = (int)(threadIdx.x & 63u);
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t C = (W + CW - 1) / CW;
-    const uint32_t m0 = blockIdx.y * (uint32_t)MT;
-
-    float xr[CPW][4][MT];
-#pragma unroll
-    for (int j = 0; j < CPW; ++j) {
-        const uint32_t c = wave + (uint32_t)j * WAVES;
-        const uint32_t k0 = (c * CW + (uint32_t)lane) * 4u;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                const uint32_t k = k0 + (uint32_t)e;
-                const uint32_t mm = m0 + (uint32_t)m;
-                xr[j][e][m] = (c < C && k < K && mm < M) ? x[(size_t)mm * K + k] : 0.0f;
-            }
-    }
-
-    __shared__ float part[2][WAVES][R * MT];
-    uint32_t it = 0;
-    for (uint32_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x, ++it) {
-        const uint32_t r0 = blk * (uint32_t)R;
-        float acc[R * MT];
-#pragma unroll
-        for (int i = 0; i < R * MT; ++i) acc[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPW; ++j) {
-            const uint32_t c = wave + (uint32_t)j * WAVES;
-            if (c >= C) break;
-            const uint32_t w = c * CW + (uint32_t)lane;
-            uint32_t v[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t row = r0 + (uint32_t)r;
-                v[r] = (row < N && w < W) ? weight[(size_t)row * W + w] : 0u;
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float q0 = (float)(int8_t)(v[r]);
-                const float q1 = (float)(int8_t)(v[r] >> 8);
-                const float q2 = (float)(int8_t)(v[r] >> 16);
-                const float q3 = (float)((int32_t)v[r] >> 24);
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    float a = acc[r * MT + m];
-                    a = __builtin_fmaf(q0, xr[j][0][m], a);
-                    a = __builtin_fmaf(q1, xr[j][1][m], a);
-                    a = __builtin_fmaf(q2, xr[j][2][m], a);
-                    a = __builtin_fmaf(q3, xr[j][3][m], a);
-                    acc[r * MT + m] = a;
-                }
-            }
-        }
-        wave_reduce_rows<R * MT>(acc, lane);
-        const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
-        const uint32_t idx = (uint32_t)lane >> SHIFT;  // = r * MT + m
-        if constexpr (WAVES == 1) {
-            const uint32_t row = r0 + idx / MT, mm = m0 + idx % MT;
-            if (leader && row < N && mm < M) y[(size_t)mm * N + row] = acc[0] * scale[row];
-        } else {
-            if (leader) part[it & 1][wave][idx] = acc[0];
-            __syncthreads();
-            if (threadIdx.x < (unsigned)(R * MT)) {
-                const uint32_t row = r0 + threadIdx.x / MT, mm = m0 + threadIdx.x % MT;
-                if (row < N && mm < M) {
-                    float s = part[it & 1][0][threadIdx.x];
-#pragma unroll
-                    for (int w2 = 1; w2 < WAVES; ++w2) s += part[it & 1][w2][threadIdx.x];
-                    y[(size_t)mm * N + row] = s * scale[row];
-                }
-            }
-        }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -362,6 +377,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kMfmaLdsBytes = 160u * 1024u;  // gfx950: 160 KB of LDS per CU, all usable by one workgroup
+constexpr uint32_t kMfmaMinRows = 16384;  // batched rows from which the matrix-core path pays
 
 
 __device__ __forceinline__ uint32_t bf16_hi_pair(float a, float b) {
@@ -400,7 +416,9 @@ __device__ __forceinline__ void store_x_parts(uint16_t* xparts, uint32_t MC, uin
     for (int e = 0; e < 4; ++e) {
         // entries past K belong to the next vector (or read 0): zero them
         const float xe = (k + (uint32_t)e < K) ? __uint_as_float(v[e]) : 0.0f;
-        const uint32_t hb = __float_as_uint(xe) & 0xffff0000u;
+        // a NaN whose payload sits in the low 16 bits would truncate to an
+        // infinity: it becomes the canonical quiet NaN instead
+        const uint32_t hb = __builtin_isnan(xe) ? 0x7fc00000u : __float_as_uint(xe) & 0xffff0000u;
         uint32_t mb = 0u, lb = 0u;
         if (isfinite(xe)) {
             const float r1 = xe - __uint_as_float(hb);  // exact
@@ -774,14 +792,6 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
 
 namespace {
 
-uint32_t grid_for(uint32_t nblocks, uint32_t max_groups) {
-    if (nblocks <= max_groups) return nblocks;
-    // Equal block counts per workgroup: every workgroup runs the same number
-    // of iterations, so none is left streaming alone at the end.
-    const uint32_t iters = (nblocks + max_groups - 1) / max_groups;
-    return (nblocks + iters - 1) / iters;
-}
-
 template <int WAVES, int CPW, int R, int EPI>
 hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
@@ -824,47 +834,58 @@ hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t s
     return dispatch_m1_rows<4, 0, 4, EPI>(a, dev, stream, variant);
 }
 
-template <int WAVES, int CPW, int R, int MT>
-hipError_t launch_mb(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+template <int WAVES, int CPW, int R, int MV>
+hipError_t launch_mv(const MatvecArgs& a, hipStream_t stream, const char** variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
-    const uint32_t mtiles = (a.M + MT - 1) / MT;
-    const uint32_t max_groups = (uint32_t)dev.cu_count * (uint32_t)(8 / WAVES > 0 ? 8 / WAVES : 1);
-    const uint32_t grid = grid_for(nblocks, max_groups);
-    hipLaunchKernelGGL((matvec_q8_mb_kernel<WAVES, CPW, R, MT>), dim3(grid, mtiles), dim3(WAVES * 64), 0,
-                       stream, a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, nblocks);
-    if (variant) *variant = "mb.xreg";
-    return hipGetLastError();
+    // groups of MV vectors on grid y, at most 65535 per launch
+    const uint32_t groups = (a.M + MV - 1) / MV;
+    for (uint32_t g0 = 0; g0 < groups; g0 += 65535u) {
+        const uint32_t gy = groups - g0 < 65535u ? groups - g0 : 65535u;
+        const uint32_t m0 = g0 * (uint32_t)MV;
+        hipLaunchKernelGGL((matvec_q8_mv_kernel<WAVES, CPW, R, MV>), dim3(nblocks, gy), dim3(WAVES * 64), 0, stream,
+                           a.weight, a.scale, a.vector + (size_t)m0 * a.K, a.output + (size_t)m0 * a.N, a.N, a.K, a.W,
+                           a.M - m0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (variant) *variant = "mb.valu";
+    return hipSuccess;
 }
 
-template <int MT, int CPW>
-hipError_t dispatch_mb(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
-    // 64-word chunks (one dword per lane), split over up to 4 waves x CPW slots.
-    constexpr int R = (64 / MT) < 16 ? 64 / MT : 16;
-    const uint32_t C = (a.W + 63) / 64;
-    if constexpr (CPW == 1) {
-        if (C <= 1) return launch_mb<1, 1, R, MT>(a, dev, stream, variant);
-        if (C <= 2) return launch_mb<2, 1, R, MT>(a, dev, stream, variant);
-        return launch_mb<4, 1, R, MT>(a, dev, stream, variant);
-    } else {
-        return launch_mb<4, CPW, R, MT>(a, dev, stream, variant);
+// Rows per workgroup: the largest R (up to RMAX) that still gives every SIMD
+// a wave; fewer, fatter blocks load each vector slice fewer times.
+template <int WAVES, int CPW, int RMAX, int MV>
+hipError_t dispatch_mv_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    const uint64_t want = 4u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
+    if constexpr (RMAX >= 16) {
+        if (waves(16) >= want) return launch_mv<WAVES, CPW, 16, MV>(a, stream, variant);
     }
+    if constexpr (RMAX >= 8) {
+        if (waves(8) >= want) return launch_mv<WAVES, CPW, 8, MV>(a, stream, variant);
+    }
+    return launch_mv<WAVES, CPW, 4, MV>(a, stream, variant);
 }
 
-// Vector-tile width for batched calls: the tile's vector slices take
-// 4 * MT * CPW VGPRs per lane, kept at <= 64 (MT * CPW <= 16).
-template <int CPW>
-hipError_t dispatch_mb_tile(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream,
-                            const char** variant) {
-    constexpr int MT_MAX = 16 / CPW;
-    if (a.M <= 2 || MT_MAX <= 2) return dispatch_mb<2, CPW>(a, dev, stream, variant);
-    if constexpr (MT_MAX >= 4) {
-        if (a.M <= 4 || MT_MAX <= 4) return dispatch_mb<4, CPW>(a, dev, stream, variant);
+// Waves per workgroup and vector-slice form by the number of 1 KiB chunks per
+// row, as for one vector; slices stay in VGPRs while they take at most 128
+// per lane (CPW * MV * 16), otherwise each slot loads its own.
+template <int MV>
+hipError_t dispatch_mv(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    constexpr int RM = MV >= 8 ? 8 : 16;
+    const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
+    if (C == 1) return dispatch_mv_rows<1, 1, RM, MV>(a, dev, stream, variant);
+    if (C == 2) return dispatch_mv_rows<2, 1, RM, MV>(a, dev, stream, variant);
+    if (C == 3) return dispatch_mv_rows<3, 1, RM, MV>(a, dev, stream, variant);
+    if (C == 4) return dispatch_mv_rows<4, 1, RM, MV>(a, dev, stream, variant);
+    // two or more slots per wave: at most 8 rows per block (VGPRs)
+    if constexpr (MV <= 4) {
+        if (C <= 8) return dispatch_mv_rows<4, 2, 8, MV>(a, dev, stream, variant);
     }
-    if constexpr (MT_MAX >= 8) {
-        if (a.M <= 8 || MT_MAX <= 8) return dispatch_mb<8, CPW>(a, dev, stream, variant);
+    if constexpr (MV <= 2) {
+        if (C <= 16) return dispatch_mv_rows<4, 4, 8, MV>(a, dev, stream, variant);
     }
-    if constexpr (MT_MAX >= 16) return dispatch_mb<16, CPW>(a, dev, stream, variant);
-    return hipErrorNotSupported;
+    return dispatch_mv_rows<4, 0, 8, MV>(a, dev, stream, variant);
 }
 
 }  // namespace
@@ -877,17 +898,18 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
         return launch_fill_scaled_zero(a.scale, a.output, a.N, a.M, stream);
     }
     if (a.M == 1) return dispatch_m1<kEpiPlain>(a, dev, stream, variant);
-    // Batched on the matrix cores when the tile's x parts fit in LDS.  Up to
-    // 11 vectors per tile: weight tiles loaded straight into LDS, one tile per
-    // step up to 4 vectors, two from 5.  From 12 vectors (or when the LDS
-    // stages do not fit): weight tiles in registers, two tiles per step
-    // sharing each B read from 12 vectors, one tile with a deeper pipeline
-    // below.
+    // Batched.  The matrix-core kernels pay a per-workgroup prologue (the x
+    // parts of the whole K for their 16-vector tile, written to LDS) and a
+    // 64-byte-per-row load pattern; they win only on large weights with at
+    // least 5 vectors, where each workgroup streams many tiles and the VALU
+    // path's 1 + M operations per code no longer hide under the streaming.
+    // Everything else runs on the VALU path (up to 8 vectors per pass).
+    // Measured on MI355X over N = 2048 .. 151936, K = 1024 .. 20000, M = 2 .. 16.
     {
         const uint32_t Kp = (a.K + 255u) / 256u * 256u;
         const uint32_t MC = a.M < 16u ? a.M : 16u;
         const uint64_t lds = 3ull * MC * Kp * 2u + 4ull * kTileSlotFloats * 4u;
-        if (lds <= kMfmaLdsBytes) {
+        if (a.M >= 5u && a.N >= kMfmaMinRows && lds <= kMfmaLdsBytes && (a.M + 15u) / 16u <= 65535u) {
             const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
             const uint32_t ntiles = (a.N + 15u) / 16u;
             const uint32_t wgs = (uint32_t)(kMfmaLdsBytes / lds) < 2u ? (uint32_t)(kMfmaLdsBytes / lds) : 2u;
@@ -895,8 +917,8 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
             const dim3 g(grid, (a.M + 15u) / 16u);
             // The weight tiles go straight into LDS (whole 128-byte lines per
             // load instruction) whenever the stages fit beside the x parts:
-            // two tiles per step (one B read serves both) from 5 vectors,
-            // one tile per step below that or when two do not fit.
+            // two tiles per step (one B read serves both) when they fit, one
+            // tile per step up to 4 vectors in a tile.
             {
                 const uint64_t xbytes = 3ull * MC * Kp * 2u + 4ull * kTileSlotFloats * 4u;
                 const uint64_t lds1 = xbytes + 4ull * kDmaStages * 1u * kDmaTileBytes;
@@ -928,24 +950,9 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
             return hipGetLastError();
         }
     }
-    // Batched: vectors in tiles of up to 16 (blockIdx.y), each tile reading
-    // the weight once; K up to 32 x 256 codes keeps the tile's vector slices
-    // in VGPRs, larger K falls back to M independent single-vector passes.
-    const uint32_t C = (a.W + 63) / 64;
-    if (C <= 4) return dispatch_mb_tile<1>(a, dev, stream, variant);
-    if (C <= 8) return dispatch_mb_tile<2>(a, dev, stream, variant);
-    if (C <= 16) return dispatch_mb_tile<4>(a, dev, stream, variant);
-    if (C <= 32) return dispatch_mb_tile<8>(a, dev, stream, variant);
-    for (uint32_t m = 0; m < a.M; ++m) {
-        MatvecArgs one = a;
-        one.vector = a.vector + (size_t)m * a.K;
-        one.output = a.output + (size_t)m * a.N;
-        one.M = 1;
-        hipError_t e = launch_matvec_q8(one, dev, stream, variant);
-        if (e != hipSuccess) return e;
-    }
-    if (variant) *variant = "mb.loop_m1";
-    return hipSuccess;
+    if (a.M <= 2) return dispatch_mv<2>(a, dev, stream, variant);
+    if (a.M <= 4) return dispatch_mv<4>(a, dev, stream, variant);
+    return dispatch_mv<8>(a, dev, stream, variant);
 }
 
 hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo& dev, hipStream_t stream,

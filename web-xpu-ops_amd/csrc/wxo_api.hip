@@ -199,7 +199,7 @@ const char* wxo_describe(void) {
     }
     snprintf(g_describe, sizeof g_describe,
              "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(plain|"
-             "residual|ffn),matvec_q8_multi,matvec_q8_mfma(bf16x3),matvec_q8_mb(xreg),quantize_rows(reg|twopass),pack_q8,"
+             "residual|ffn),matvec_q8_multi,matvec_q8_mv(valu),matvec_q8_mfma(bf16x3),quantize_rows(reg|twopass),pack_q8,"
              "pack_int8_rows,matmul_q8(bf16x3),dequantize_packed,dequant_transpose,gather_dequant_rows",
              WXO_ABI_VERSION, WXO_BUILD_ID, d->ordinal, d->name, d->arch, d->cu_count,
              (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0));
