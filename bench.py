@@ -274,6 +274,22 @@ def run_suite(stream, steps, warmup):
     results.append({"case": "cfg4 quantize+packQ8 (fused) of the 7 matrices", "bytes": qbytes, "us": round(us, 3),
                     "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
     log(f"suite cfg4 quantize+pack: {us:.2f} us  {gbs:.0f} GB/s")
+
+    # The same seven as the resident batch issues them: matrices with one K
+    # in one wxo_quantize_pack_q8_multi launch (K = 2048 x 6, K = 5632 x 1).
+    by_k = {}
+    for (N, K, src), (packed, scale) in zip(srcs, outs):
+        by_k.setdefault(K, []).append((src, N, packed, scale))
+
+    def quant_multi_step(i):
+        for K, group in by_k.items():
+            wxo_q8.quantize_pack_q8_multi_device(group, K, stream)
+    us = time_loop(stream, quant_multi_step, max(1, steps // 20), 2)
+    gbs = qbytes / (us * 1e-6) / 1e9
+    results.append({"case": f"cfg4 quantize+packQ8 of the 7 matrices as the resident batch issues them "
+                            f"({len(by_k)} launches, one per K)", "bytes": qbytes, "us": round(us, 3),
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
+    log(f"suite cfg4 quantize+pack coalesced: {us:.2f} us  {gbs:.0f} GB/s")
     for (_, _, src), (packed, scale) in zip(srcs, outs):
         src.free()
         packed.free()

@@ -28,6 +28,9 @@
  *   wxo_pack_int8_rows        llm/weights-q8.ts:137-139 (packInt8Rows)
  *   wxo_quantize_pack_q8      packQ8(quantize(w).output, N, K) + quantize(w).scales
  *                             in one pass (the composition at ops/matvec/reference.ts:87-90)
+ *   wxo_quantize_pack_q8_multi  several consecutive quantize+packQ8 of matrices with one
+ *                             K in one launch (no single reference function; each
+ *                             matrix is wxo_quantize_pack_q8's result)
  *   wxo_matmul_q8             ops/matmul/reference.ts:124-137 (matmulQ8, the prefill
  *                             GEMM over the same packed weight) and its WGSL dispatch
  *                             ops/matmul/wgsl/q8.wgsl:26-35 bindings {a, weight, scale,
@@ -163,6 +166,15 @@ int wxo_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* pa
  * scales f32 [N]; bit-exact to packQ8(quantize(w).output, N, K). */
 int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* packed, float* scales,
                          wxo_stream_t stream);
+
+/* quantize+packQ8 of several matrices with the same row length K: matrix p
+ * (inputs[p] f32 [Ns[p], K]) gets packed[p] u32 [Ns[p], ceil(K/4)] and
+ * scales[p] f32 [Ns[p]], bit-exact to wxo_quantize_pack_q8 on it alone.  The
+ * arrays of pointers and row counts are host memory.  Up to 8 matrices share
+ * one launch (more run 8 at a time); the matrices run concurrently, so an
+ * output that overlaps any input or another output is rejected. */
+int wxo_quantize_pack_q8_multi(const float* const* inputs, const uint32_t* Ns, uint32_t* const* packed,
+                               float* const* scales, uint32_t count, uint32_t K, wxo_stream_t stream);
 
 /* matmulQ8: output[n*M + m] = (sum_{k<K} a[n*K + k] * sext8(byte k of weight row m)) * scale[m]
  * for n < N (tokens), m < M (weight rows).  a f32 [N, K], weight u32 [M, ceil(K/4)],

@@ -308,3 +308,31 @@ gpuTest(F, "ResidentQ8Device: same-vector matvecQ8 runs share one launch and giv
     dev.destroy();
   }
 });
+
+gpuTest(F, "ResidentQ8Device: consecutive quantizePackQ8 ops with one K share a launch, bit-exact per matrix", async () => {
+  const K = 520, W = Math.ceil(K / 4);
+  const Ns = [40, 3, 17];
+  const inputs = Ns.map((N, m) => Float32Array.from({ length: N * K }, (_, i) => Math.sin(i * 0.013 + m) * 0.02));
+  inputs[0].fill(0, K, 2 * K);  // an all-zero row: scale 1, codes 0
+  for (const coalesce of [true, false]) {
+    const dev = await createResidentQ8Device({ coalesce });
+    const ops = [], outs = [];
+    Ns.forEach((N, m) => {
+      const input = dev.createStorageBuffer(N * K * 4);
+      dev.upload(input, 0, inputs[m]);
+      const packed = dev.createStorageBuffer(N * W * 4), scales = dev.createStorageBuffer(N * 4);
+      ops.push({ kind: "quantizePackQ8", input, N, K, packed, scales });
+      outs.push({ source: packed, sourceOffset: 0, length: N * W, type: "u32" },
+                { source: scales, sourceOffset: 0, length: N, type: "f32" });
+    });
+    const launches0 = dev.stats.launches;
+    const got = await dev.batch(ops, outs);
+    Ns.forEach((N, m) => {
+      const want = oracle.quantize({ input: inputs[m], N, D: K });
+      assertBitsEqual(got[2 * m], oracle.packQ8({ codes: want.output, N, K }), `packed ${m} coalesce=${coalesce}`);
+      assertBitsEqual(got[2 * m + 1], want.scales, `scales ${m} coalesce=${coalesce}`);
+    });
+    assert.strictEqual(dev.stats.launches - launches0, coalesce ? 1 : 3);
+    dev.destroy();
+  }
+});

@@ -78,6 +78,13 @@ def test_validation_happens_before_device_access():
                                       0x30000, 8)
     with pytest.raises(wxo_q8.WxoError, match="projection 0: output overlaps the vector"):
         wxo_q8.matvec_q8_multi_device([(16, 16, 0x3001c, 4)], 0x30000, 8)
+    assert L.wxo_quantize_pack_q8_multi(None, None, None, None, 0, 8, None) == wxo_q8.WXO_OK
+    with pytest.raises(wxo_q8.WxoError, match="matrix 1: input is NULL"):
+        wxo_q8.quantize_pack_q8_multi_device([(0x10000, 2, 0x20000, 0x30000), (0, 2, 0x40000, 0x50000)], 8)
+    with pytest.raises(wxo_q8.WxoError, match="outputs of matrix 1 overlap the input of matrix 0"):
+        wxo_q8.quantize_pack_q8_multi_device([(0x10000, 2, 0x20000, 0x30000), (0x40000, 2, 0x10010, 0x50000)], 8)
+    with pytest.raises(wxo_q8.WxoError, match="packed and scales overlap"):
+        wxo_q8.quantize_pack_q8_multi_device([(0x10000, 2, 0x20000, 0x20004)], 8)
     with pytest.raises(wxo_q8.WxoError, match="weight has 3 elements"):
         wxo_q8.matvecQ8(weight=np.zeros(3, np.uint32), scale=np.ones(2, np.float32),
                         vector=np.ones(8, np.float32), N=2, K=8)
@@ -113,7 +120,7 @@ def _device_asm(tmp, src):
 def test_device_code_has_no_packed_fp32():
     # Every HIP source compiled to gfx950 assembly: no v_pk_add/mul/fma_f32.
     with tempfile.TemporaryDirectory() as tmp:
-        for src in ("matvec_q8.hip", "quantize_q8.hip"):
+        for src in ("matvec_q8.hip", "quantize_q8.hip", "matmul_q8.hip", "dequant_q8.hip"):
             asm = _device_asm(tmp, src)
             assert re.search(r"v_pk_(add|mul|fma)_f32", asm) is None, src
             # no register spills in any kernel

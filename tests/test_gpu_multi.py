@@ -1,8 +1,13 @@
-"""wxo_matvec_q8_multi: several projections of one vector in one launch, the
-form the resident decode takes for wq/wk/wv (llm/engine-q8-resident.ts:1843-1845)
-and the lm_head chunks (:1869).  Every output must meet the matvecQ8 bar
-against the oracle (|y - y_ref| <= 1e-5 * sum_k |s q x| + 1e-7), the same
-as separate wxo_matvec_q8 calls, and nothing outside the outputs is written.
+"""Several operations in one launch.
+
+wxo_matvec_q8_multi: several projections of one vector, the form the resident
+decode takes for wq/wk/wv (llm/engine-q8-resident.ts:1843-1845) and the
+lm_head chunks (:1869).  Every output must meet the matvecQ8 bar against the
+oracle (|y - y_ref| <= 1e-5 * sum_k |s q x| + 1e-7), the same as separate
+wxo_matvec_q8 calls, and nothing outside the outputs is written.
+
+wxo_quantize_pack_q8_multi: quantize + packQ8 of several matrices with one K;
+every matrix bit-exact to the oracle's quantize + packQ8 of it alone.
 """
 import numpy as np
 import pytest
@@ -159,4 +164,59 @@ def test_multi_rejects_overlapping_outputs():
     with pytest.raises(wxo_q8.WxoError, match="overlaps the vector"):
         wxo_q8.matvec_q8_multi_device([(bw, bs, bx, 64)], bx, 64)
     for b in (bw, bs, bx, by):
+        b.free()
+
+
+# ------------------------------------------------ quantize + packQ8 of several matrices
+
+def quantize_multi(mats, K):
+    """mats: list of f32 arrays [N, K]; returns [(packed, scales)] from one multi call."""
+    bufs = []
+    for a in mats:
+        N = a.shape[0]
+        bufs.append((wxo_q8.DeviceBuffer.from_array(a.reshape(-1)) if a.size else None, N,
+                     wxo_q8.DeviceBuffer(max(4, N * ((K + 3) // 4) * 4)), wxo_q8.DeviceBuffer(max(4, 4 * N))))
+    wxo_q8.quantize_pack_q8_multi_device([(b[0].ptr if b[0] else 0, b[1], b[2], b[3]) for b in bufs], K)
+    wxo_q8.synchronize()
+    out = []
+    for (bi, N, bp, bs) in bufs:
+        out.append((bp.download(np.uint32, N * ((K + 3) // 4)), bs.download(np.float32, N)))
+        for b in (bi, bp, bs):
+            if b:
+                b.free()
+    return out
+
+
+@pytest.mark.parametrize("K,Ns", [(2048, (2048, 2048, 2048, 2048, 5632, 5632)), (5632, (2048, 1)),
+                                  (4099, (7, 0, 300, 1)), (300, (5, 9)), (1030, (3,) * 11), (40000, (2, 3))])
+def test_quantize_pack_multi_bit_exact(K, Ns):
+    # every matrix equals the oracle's quantize + packQ8 of it alone, bit for
+    # bit: cfg4's six K = 2048 matrices, ragged K, an empty matrix, short rows
+    # (one launch per matrix), more than 8 matrices, rows read twice (K > 8192)
+    rng = np.random.default_rng(K + len(Ns))
+    mats = []
+    for i, N in enumerate(Ns):
+        a = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        if N > 2:
+            a[1, :] = 0.0                      # all-zero row: scale 1, codes 0
+            a[2, K // 2] = np.float32(3.5)    # outlier row
+        mats.append(a)
+    got = quantize_multi(mats, K)
+    for a, (packed, scales) in zip(mats, got):
+        N = a.shape[0]
+        codes, want_scales = oracle.quantize(a.reshape(-1), N, K)
+        want_packed = oracle.pack_q8(codes, N, K)
+        np.testing.assert_array_equal(packed, want_packed)
+        np.testing.assert_array_equal(scales.view(np.uint32), want_scales.view(np.uint32))
+
+
+def test_quantize_pack_multi_rejects_overlap():
+    a = wxo_q8.DeviceBuffer(4 * 4 * 512)
+    p = wxo_q8.DeviceBuffer(4 * 512 * 2)
+    s = wxo_q8.DeviceBuffer(64)
+    with pytest.raises(wxo_q8.WxoError, match="overlap the input"):
+        wxo_q8.quantize_pack_q8_multi_device([(a, 4, a, s)], 512)
+    with pytest.raises(wxo_q8.WxoError, match="outputs of matrices 0 and 1 overlap"):
+        wxo_q8.quantize_pack_q8_multi_device([(a, 2, p, s), (a.ptr + 2 * 512 * 4, 2, p.ptr + 4, s.ptr + 32)], 512)
+    for b in (a, p, s):
         b.free()

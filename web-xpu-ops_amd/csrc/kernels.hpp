@@ -68,6 +68,12 @@ hipError_t launch_fill_scaled_zero(const float* scale, float* y, uint32_t N, uin
 // quantize (codes != nullptr) and/or packQ8 (packed != nullptr) of f32 rows.
 hipError_t launch_quantize_rows(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed,
                                 float* scales, const DeviceInfo& dev, hipStream_t stream, const char** variant);
+// quantize + packQ8 of several matrices with the same K (count <= 8), one
+// launch for rows of more than 128 words.
+constexpr uint32_t kMaxQuantizeMatrices = 8;
+hipError_t launch_quantize_pack_multi(const float* const* inputs, const uint32_t* Ns, uint32_t* const* packed,
+                                      float* const* scales, uint32_t count, uint32_t K, const DeviceInfo& dev,
+                                      hipStream_t stream);
 hipError_t launch_pack_q8(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed, const DeviceInfo& dev,
                           hipStream_t stream);
 hipError_t launch_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed,

@@ -191,14 +191,15 @@ __device__ __forceinline__ void emit_word_fast(u32x4v v, float inv32, double inv
 // itself.  A quarter of the codes per lane of the one-wave form keeps the
 // compute left after a row's last bytes arrive short.  WPT == 0: any K, two
 // passes over the row.
+//
+// The body is a device function of the row so that the multi-matrix kernel
+// below runs it on its own rows.
 template <int WPT, bool CODES, bool PACK>
-__global__ __launch_bounds__(256) void quantize_row_wg_kernel(const float* __restrict__ input, uint32_t N,
-                                                              uint32_t K, uint32_t W, int32_t* __restrict__ codes,
-                                                              uint32_t* __restrict__ packed,
-                                                              float* __restrict__ scales) {
+__device__ __forceinline__ void quantize_row_wg(const float* __restrict__ input, uint32_t K, uint32_t W,
+                                                int32_t* __restrict__ codes, uint32_t* __restrict__ packed,
+                                                float* __restrict__ scales, uint32_t row) {
     __shared__ uint32_t wmax[4];
     const uint32_t t = threadIdx.x;
-    const uint32_t row = blockIdx.x;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(input + (size_t)row * K, K * 4u);
     const __amdgpu_buffer_rsrc_t crs = make_rsrc(CODES ? (const void*)(codes + (size_t)row * K) : nullptr,
                                                  CODES ? K * 4u : 0u);
@@ -261,6 +262,36 @@ __global__ __launch_bounds__(256) void quantize_row_wg_kernel(const float* __res
     }
 }
 
+template <int WPT, bool CODES, bool PACK>
+__global__ __launch_bounds__(256) void quantize_row_wg_kernel(const float* __restrict__ input, uint32_t N,
+                                                              uint32_t K, uint32_t W, int32_t* __restrict__ codes,
+                                                              uint32_t* __restrict__ packed,
+                                                              float* __restrict__ scales) {
+    (void)N;
+    quantize_row_wg<WPT, CODES, PACK>(input, K, W, codes, packed, scales, blockIdx.x);
+}
+
+// Several matrices with the same K in one launch (quantize + packQ8): the
+// grid is their rows laid end to end, matrix i owning blocks
+// [start[i], start[i + 1]); unused entries start at 0xffffffff.  A block
+// finds its matrix with wave-uniform compares and runs the one-row body.
+struct QuantizeSegments {
+    const float* input[kMaxQuantizeMatrices];
+    uint32_t* packed[kMaxQuantizeMatrices];
+    float* scales[kMaxQuantizeMatrices];
+    uint32_t start[kMaxQuantizeMatrices];
+};
+
+template <int WPT>
+__global__ __launch_bounds__(256) void quantize_pack_multi_kernel(QuantizeSegments seg, uint32_t K, uint32_t W) {
+    const uint32_t b = blockIdx.x;
+    uint32_t i = 0;
+#pragma unroll
+    for (uint32_t j = 1; j < kMaxQuantizeMatrices; ++j)
+        if (b >= seg.start[j]) i = j;
+    quantize_row_wg<WPT, false, true>(seg.input[i], K, W, nullptr, seg.packed[i], seg.scales[i], b - seg.start[i]);
+}
+
 namespace {
 
 template <int WPL, bool CODES, bool PACK>
@@ -302,6 +333,61 @@ hipError_t dispatch_q(const float* input, uint32_t N, uint32_t K, int32_t* codes
 }
 
 }  // namespace
+
+namespace {
+
+template <int WPT>
+hipError_t launch_qmulti(const QuantizeSegments& seg, uint32_t blocks, uint32_t K, hipStream_t stream) {
+    hipLaunchKernelGGL((quantize_pack_multi_kernel<WPT>), dim3(blocks), dim3(256), 0, stream, seg, K, (K + 3u) / 4u);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quantize_pack_multi(const float* const* inputs, const uint32_t* Ns, uint32_t* const* packed,
+                                      float* const* scales, uint32_t count, uint32_t K, const DeviceInfo& dev,
+                                      hipStream_t stream) {
+    const uint32_t W = (K + 3u) / 4u;
+    QuantizeSegments seg;
+    uint32_t n = 0;
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (Ns[i] == 0) continue;
+        if (n == kMaxQuantizeMatrices) return hipErrorInvalidValue;
+        seg.input[n] = inputs[i];
+        seg.packed[n] = packed[i];
+        seg.scales[n] = scales[i];
+        seg.start[n] = (uint32_t)rows;
+        rows += Ns[i];
+        ++n;
+    }
+    if (n == 0) return hipSuccess;
+    // Short rows (one wave per row), one matrix, or a grid past 2^31 - 1:
+    // one launch per matrix.
+    if (W <= 128u || n == 1 || rows >= 0x7fffffffu) {
+        for (uint32_t i = 0; i < count; ++i) {
+            if (Ns[i] == 0) continue;
+            const hipError_t e = launch_quantize_rows(inputs[i], Ns[i], K, nullptr, packed[i], scales[i], dev, stream,
+                                                      nullptr);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    for (uint32_t i = n; i < kMaxQuantizeMatrices; ++i) {
+        seg.input[i] = nullptr;
+        seg.packed[i] = nullptr;
+        seg.scales[i] = nullptr;
+        seg.start[i] = 0xffffffffu;
+    }
+    const uint32_t blocks = (uint32_t)rows;
+    const uint32_t wpt = (W + 255u) / 256u;
+    if (wpt <= 1) return launch_qmulti<1>(seg, blocks, K, stream);
+    if (wpt <= 2) return launch_qmulti<2>(seg, blocks, K, stream);
+    if (wpt <= 4) return launch_qmulti<4>(seg, blocks, K, stream);
+    if (wpt <= 6) return launch_qmulti<6>(seg, blocks, K, stream);
+    if (wpt <= 8) return launch_qmulti<8>(seg, blocks, K, stream);
+    return launch_qmulti<0>(seg, blocks, K, stream);
+}
 
 hipError_t launch_quantize_rows(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed,
                                 float* scales, const DeviceInfo& dev, hipStream_t stream, const char** variant) {

@@ -436,6 +436,52 @@ int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* p
     return e == hipSuccess ? ok() : hip_fail(e, "quantize_pack_q8 launch");
 }
 
+int wxo_quantize_pack_q8_multi(const float* const* inputs, const uint32_t* Ns, uint32_t* const* packed,
+                               float* const* scales, uint32_t count, uint32_t K, wxo_stream_t stream) {
+    if (count == 0) return ok();
+    if (!inputs || !Ns || !packed || !scales) return fail(WXO_ERR_INVALID, "matrix arrays are NULL");
+    const uint64_t W = ((uint64_t)K + 3) / 4;
+    for (uint32_t i = 0; i < count; ++i) {
+        int st = validate_rows(inputs[i], Ns[i], K, "input");
+        if (st == WXO_OK) st = check_ptr(packed[i], (uint64_t)Ns[i] * W, "packed");
+        if (st == WXO_OK) st = check_ptr(scales[i], Ns[i], "scales");
+        if (st != WXO_OK) {
+            char why[256];
+            snprintf(why, sizeof why, "%s", g_error);
+            return fail(st, "matrix %u: %s", i, why);
+        }
+    }
+    // The matrices run concurrently: nothing one of them writes may overlap
+    // what another reads or writes.
+    struct Span {
+        uintptr_t lo, hi;
+    };
+    const auto span = [](const void* p, uint64_t bytes) { return Span{(uintptr_t)p, (uintptr_t)p + bytes}; };
+    const auto meet = [](Span a, Span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; };
+    for (uint32_t i = 0; i < count; ++i) {
+        const Span outs[2] = {span(packed[i], (uint64_t)Ns[i] * W * 4), span(scales[i], (uint64_t)Ns[i] * 4)};
+        if (meet(outs[0], outs[1])) return fail(WXO_ERR_INVALID, "matrix %u: packed and scales overlap", i);
+        for (uint32_t j = 0; j < count; ++j) {
+            const Span in = span(inputs[j], (uint64_t)Ns[j] * K * 4);
+            for (const Span& o : outs) {
+                if (meet(o, in)) return fail(WXO_ERR_INVALID, "outputs of matrix %u overlap the input of matrix %u", i, j);
+                if (j < i && (meet(o, span(packed[j], (uint64_t)Ns[j] * W * 4)) ||
+                              meet(o, span(scales[j], (uint64_t)Ns[j] * 4))))
+                    return fail(WXO_ERR_INVALID, "outputs of matrices %u and %u overlap", j, i);
+            }
+        }
+    }
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    for (uint32_t g = 0; g < count; g += wxo::kMaxQuantizeMatrices) {
+        const uint32_t n = count - g < wxo::kMaxQuantizeMatrices ? count - g : wxo::kMaxQuantizeMatrices;
+        hipError_t e = wxo::launch_quantize_pack_multi(inputs + g, Ns + g, packed + g, scales + g, n, K, *d,
+                                                       as_hip(stream));
+        if (e != hipSuccess) return hip_fail(e, "quantize_pack_q8_multi launch");
+    }
+    return ok();
+}
+
 int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* output, uint32_t N, uint32_t M,
                   uint32_t K, wxo_stream_t stream) {
     WXO_TRY(validate_matmul(a, weight, scale, output, N, M, K));

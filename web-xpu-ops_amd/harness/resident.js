@@ -16,9 +16,11 @@
 // wq/wk/wv projections, llm/engine-q8-resident.ts:1843-1845, and its lm_head
 // chunks, :1869) run as one launch of matvecQ8MultiDevice when nothing in the
 // run depends on another op of the run: outputs disjoint from each other, from
-// the vector and from the run's weights and scales.  The results are those of
-// the separate ops; only the launch count changes (`stats.launches`).  Pass
-// `{ coalesce: false }` to the constructor to issue every op on its own.
+// the vector and from the run's weights and scales.  Consecutive
+// quantizePackQ8 ops with one K run as one quantizePackQ8MultiDevice launch
+// under the same condition.  The results are those of the separate ops; only
+// the launch count changes (`stats.launches`).  Pass `{ coalesce: false }` to
+// the constructor to issue every op on its own.
 import { native } from "../native/index.js";
 
 const TYPED = { f32: Float32Array, i32: Int32Array, u32: Uint32Array };
@@ -113,10 +115,15 @@ export class ResidentQ8Device {
           break;
         }
         case "quantizePackQ8": {
-          need(op.input, op.N * op.K * 4, "input");
-          need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
-          need(op.scales, op.N * 4, "scales");
-          a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
+          checkQuantize(op);
+          const run = this.coalesce ? quantizeRun(ops, i) : 1;
+          if (run > 1) {
+            const group = ops.slice(i, i + run);
+            a.quantizePackQ8MultiDevice(group.map((g) => [g.input.ptr, g.N, g.packed.ptr, g.scales.ptr]), op.K);
+            i += run - 1;
+          } else {
+            a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
+          }
           break;
         }
         case "matmulQ8": {
@@ -176,6 +183,39 @@ function checkMatvec(op, M) {
   need(op.scale, op.N * 4, "scale");
   need(op.vector, M * op.K * 4, "vector");
   need(op.output, M * op.N * 4, "output");
+}
+
+function checkQuantize(op) {
+  need(op.input, op.N * op.K * 4, "input");
+  need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
+  need(op.scales, op.N * 4, "scales");
+}
+
+/**
+ * How many ops from `start` on (at least 1) form a run of quantizePackQ8 ops
+ * with the same K, none writing what another of the run reads or writes.
+ */
+function quantizeRun(ops, start) {
+  const K = ops[start].K;
+  const ins = [];
+  const outs = [];
+  let n = 0;
+  for (let j = start; j < ops.length; j += 1) {
+    const op = ops[j];
+    if (op.kind !== "quantizePackQ8") break;
+    if (j > start) checkQuantize(op);
+    if (op.K !== K) break;
+    const input = span(op.input, op.N * op.K * 4);
+    const own = [span(op.packed, op.N * Math.ceil(op.K / 4) * 4), span(op.scales, op.N * 4)];
+    if (overlaps(own[0], own[1]) || own.some((o) => overlaps(o, input) || ins.some((r) => overlaps(o, r)) ||
+        outs.some((w) => overlaps(o, w))) || outs.some((w) => overlaps(w, input))) {
+      break;
+    }
+    ins.push(input);
+    outs.push(...own);
+    n += 1;
+  }
+  return Math.max(n, 1);
 }
 
 /** [start, end) byte range of `bytes` bytes at a resident buffer's address. */

@@ -676,6 +676,55 @@ static napi_value js_matvec_q8_multi_device(napi_env env, napi_callback_info inf
     return result;
 }
 
+/* quantizePackQ8MultiDevice([[input, N, packed, scales], ...], K): quantize +
+ * packQ8 of several matrices with one K (device addresses), one launch per 8. */
+static napi_value js_quantize_pack_q8_multi_device(napi_env env, napi_callback_info info) {
+    size_t argc = 2;
+    napi_value argv[2];
+    uint32_t K, count = 0;
+    bool is_array = false;
+    if (!get_args(env, info, 2, &argc, argv)) return NULL;
+    if (napi_is_array(env, argv[0], &is_array) != napi_ok || !is_array)
+        return type_error(env, "%s must be an array of [input, N, packed, scales]", "matrices"), NULL;
+    if (!get_u32(env, argv[1], &K, "K")) return NULL;
+    napi_get_array_length(env, argv[0], &count);
+    const size_t n = count > 0 ? count : 1;
+    const float** ins = (const float**)calloc(n, sizeof *ins);
+    uint32_t* ns = (uint32_t*)calloc(n, sizeof *ns);
+    uint32_t** ps = (uint32_t**)calloc(n, sizeof *ps);
+    float** ss = (float**)calloc(n, sizeof *ss);
+    int okay = ins && ns && ps && ss;
+    if (!okay) napi_throw_error(env, NULL, "quantizePackQ8MultiDevice: out of host memory");
+    for (uint32_t i = 0; okay && i < count; ++i) {
+        napi_value e, f[4];
+        uint32_t len = 0;
+        uint64_t in, p, sc;
+        okay = napi_get_element(env, argv[0], i, &e) == napi_ok && napi_is_array(env, e, &is_array) == napi_ok &&
+               is_array && napi_get_array_length(env, e, &len) == napi_ok && len == 4;
+        if (!okay) {
+            char idx[16];
+            snprintf(idx, sizeof idx, "%u", i);
+            type_error(env, "matrix %s must be [input, N, packed, scales]", idx);
+            break;
+        }
+        for (uint32_t j = 0; j < 4; ++j) napi_get_element(env, e, j, &f[j]);
+        okay = get_ptr(env, f[0], &in, "input") && get_u32(env, f[1], &ns[i], "N") &&
+               get_ptr(env, f[2], &p, "packed") && get_ptr(env, f[3], &sc, "scales");
+        ins[i] = (const float*)(uintptr_t)in;
+        ps[i] = (uint32_t*)(uintptr_t)p;
+        ss[i] = (float*)(uintptr_t)sc;
+    }
+    if (okay) {
+        int st = wxo_quantize_pack_q8_multi(ins, ns, ps, ss, count, K, NULL);
+        if (st != WXO_OK) throw_status(env, st, "quantizePackQ8MultiDevice");
+    }
+    free(ins);
+    free(ns);
+    free(ps);
+    free(ss);
+    return NULL;
+}
+
 /* matvecQ8ResidualDevice(weight, scale, vector, residual, output, N, K): device addresses */
 static napi_value js_matvec_q8_residual_device(napi_env env, napi_callback_info info) {
     size_t argc = 7;
@@ -842,6 +891,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8MultiDevice", NULL, js_matvec_q8_multi_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8ResidualDevice", NULL, js_matvec_q8_residual_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"quantizePackQ8MultiDevice", NULL, js_quantize_pack_q8_multi_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8FfnDevice", NULL, js_matvec_q8_ffn_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"quantizeDevice", NULL, js_quantize_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"packQ8Device", NULL, js_pack_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},

@@ -19,6 +19,7 @@ export interface WxoAddon {
   copy(dst: bigint, src: bigint, bytes: number): void;
   matvecQ8Device(weight: bigint, scale: bigint, vector: bigint, output: bigint, N: number, K: number, M?: number): void;
   matvecQ8MultiDevice(projections: [bigint, bigint, bigint, number][], vector: bigint, K: number): void;
+  quantizePackQ8MultiDevice(matrices: [bigint, number, bigint, bigint][], K: number): void;
   matvecQ8ResidualDevice(weight: bigint, scale: bigint, vector: bigint, residual: bigint, output: bigint, N: number, K: number): void;
   matvecQ8FfnDevice(weightGate: bigint, scaleGate: bigint, weightUp: bigint, scaleUp: bigint, vector: bigint, output: bigint, N: number, K: number): void;
   quantizeDevice(input: bigint, N: number, D: number, output: bigint, scales: bigint): void;

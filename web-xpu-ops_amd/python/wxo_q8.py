@@ -78,6 +78,7 @@ SIGNATURES = {
     "wxo_pack_int8_rows_host": ([_P, _U32, _U32, _P], _I),
     "wxo_quantize_pack_q8_host": ([_P, _U32, _U32, _P, _P], _I),
     "wxo_matmul_q8": ([_P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
+    "wxo_quantize_pack_q8_multi": ([_P, _P, _P, _P, _U32, _U32, _P], _I),
     "wxo_dequantize_packed_q8": ([_P, _P, _U32, _U32, _P, _P], _I),
     "wxo_dequant_transpose": ([_P, _P, _U32, _U32, _P, _P], _I),
     "wxo_gather_dequant_rows": ([_P, _P, _U32, _U32, _P, _U32, _P, _P], _I),
@@ -264,6 +265,16 @@ def matvec_q8_ffn_device(weight_gate, scale_gate, weight_up, scale_up, vector, o
 
 def quantize_device(inp, N: int, D: int, output, scales, stream=None) -> None:
     _check(lib().wxo_quantize(_addr(inp), N, D, _addr(output), _addr(scales), _stream_ptr(stream)))
+
+
+def quantize_pack_q8_multi_device(matrices, K: int, stream=None) -> None:
+    """matrices: a sequence of (input, N, packed, scales); one launch per 8."""
+    n = len(matrices)
+    ins = (ctypes.c_void_p * max(n, 1))(*[_addr(m[0]) for m in matrices])
+    ns = (ctypes.c_uint32 * max(n, 1))(*[int(m[1]) for m in matrices])
+    ps = (ctypes.c_void_p * max(n, 1))(*[_addr(m[2]) for m in matrices])
+    ss = (ctypes.c_void_p * max(n, 1))(*[_addr(m[3]) for m in matrices])
+    _check(lib().wxo_quantize_pack_q8_multi(ins, ns, ps, ss, n, K, _stream_ptr(stream)))
 
 
 def pack_q8_device(codes, N: int, K: int, packed, stream=None) -> None:
