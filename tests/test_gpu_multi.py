@@ -68,18 +68,21 @@ def run_multi(rng, Ns, K, guard=64):
 
 # K over every vector-slice class of the single-vector kernel (1, 2, 3, 4,
 # <= 8, <= 16 and > 16 chunks of 1024 codes), ragged ends included.
-@pytest.mark.parametrize("K", [3, 1000, 2048, 3000, 4096, 4099, 8000, 11008, 20000])
+@pytest.mark.parametrize("K", [3, 1000, 2048, 3000, 4096, 4099, 5632, 7000, 8000, 11008, 20000])
 def test_multi_matches_oracle(K):
     rng = np.random.default_rng(K)
     run_multi(rng, (300, 17, 1, 64), K)
 
 
-@pytest.mark.parametrize("Ns", [(5,), (16, 16), (2048, 512, 512), (0, 33, 0, 7), (9, 1, 130, 0, 77, 3, 40)])
-def test_multi_projection_counts(Ns):
-    # one projection, the engine's GQA shape, empty projections, and more than
-    # the four a launch takes (run four at a time)
+@pytest.mark.parametrize("Ns,K", [((5,), 1030), ((16, 16), 1030), ((2048, 512, 512), 2048), ((0, 33, 0, 7), 1030),
+                                  ((9, 1, 130, 0, 77, 3, 40), 1030), ((4096, 1024, 1024), 5632),
+                                  ((2048, 2048, 2048), 8192)])
+def test_multi_projection_counts(Ns, K):
+    # one projection, the engine's GQA shape, empty projections, more than
+    # the four a launch takes (run four at a time), and 5 to 8 chunks per row
+    # (one wave per chunk) at sizes that pick 16 and 8 rows per block
     rng = np.random.default_rng(len(Ns))
-    run_multi(rng, Ns, 2048 if max(Ns) >= 512 else 1030)
+    run_multi(rng, Ns, K)
 
 
 def test_multi_cfg4_qkv_and_lm_head_chunks():

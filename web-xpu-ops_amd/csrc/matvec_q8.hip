@@ -822,6 +822,27 @@ hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
     return launch_m1<WAVES, CPW, 2, EPI>(a, stream, variant);
 }
 
+// One wave per chunk for 5 to 8 chunks (rows of 4097 .. 8192 codes): the
+// chunks load side by side instead of one wave walking a second slot after
+// its first (6-10 % faster from K = 4099 to 8192, same-process timings).
+// Rows per block: the largest R that still gives 6 waves per CU.
+template <int WAVES, int RMAX, int EPI>
+hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    constexpr int RM = EPI == kEpiFfn ? RMAX / 2 : RMAX;
+    const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
+    if constexpr (RM >= 16) {
+        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI>(a, stream, variant);
+    }
+    if constexpr (RM >= 8) {
+        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI>(a, stream, variant);
+    }
+    if constexpr (RM >= 4) {
+        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI>(a, stream, variant);
+    }
+    return launch_m1<WAVES, 1, 2, EPI>(a, stream, variant);
+}
+
 template <int EPI>
 hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
     const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
@@ -829,7 +850,10 @@ hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t s
     if (C == 2) return dispatch_m1_rows<2, 1, 16, EPI>(a, dev, stream, variant);
     if (C == 3) return dispatch_m1_rows<3, 1, 16, EPI>(a, dev, stream, variant);
     if (C == 4) return dispatch_m1_rows<4, 1, 16, EPI>(a, dev, stream, variant);
-    if (C <= 8) return dispatch_m1_rows<4, 2, 8, EPI>(a, dev, stream, variant);
+    if (C == 5) return dispatch_m1_wide<5, 16, EPI>(a, dev, stream, variant);
+    if (C == 6) return dispatch_m1_wide<6, 16, EPI>(a, dev, stream, variant);
+    if (C == 7) return dispatch_m1_wide<7, 16, EPI>(a, dev, stream, variant);
+    if (C == 8) return dispatch_m1_wide<8, 16, EPI>(a, dev, stream, variant);
     if (C <= 16) return dispatch_m1_rows<4, 4, 4, EPI>(a, dev, stream, variant);
     return dispatch_m1_rows<4, 0, 4, EPI>(a, dev, stream, variant);
 }
@@ -1009,6 +1033,22 @@ hipError_t dispatch_multi_rows(const Projection* p, uint32_t count, const float*
     return launch_multi<WAVES, CPW, 2>(p, count, x, K, stream, variant);
 }
 
+// 5 to 8 chunks: one wave per chunk, as for a single projection.
+template <int WAVES>
+hipError_t dispatch_multi_wide(const Projection* p, uint32_t count, const float* x, uint32_t K,
+                               const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    auto waves = [&](uint32_t R) {
+        uint64_t b = 0;
+        for (uint32_t i = 0; i < count; ++i) b += (p[i].N + (uint64_t)R - 1) / R;
+        return b * WAVES;
+    };
+    if (waves(16) >= want) return launch_multi<WAVES, 1, 16>(p, count, x, K, stream, variant);
+    if (waves(8) >= want) return launch_multi<WAVES, 1, 8>(p, count, x, K, stream, variant);
+    if (waves(4) >= want) return launch_multi<WAVES, 1, 4>(p, count, x, K, stream, variant);
+    return launch_multi<WAVES, 1, 2>(p, count, x, K, stream, variant);
+}
+
 }  // namespace
 
 hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count, const float* x, uint32_t K,
@@ -1039,7 +1079,10 @@ hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count,
     if (C == 2) return dispatch_multi_rows<2, 1, 16>(p, n, x, K, dev, stream, variant);
     if (C == 3) return dispatch_multi_rows<3, 1, 16>(p, n, x, K, dev, stream, variant);
     if (C == 4) return dispatch_multi_rows<4, 1, 16>(p, n, x, K, dev, stream, variant);
-    if (C <= 8) return dispatch_multi_rows<4, 2, 8>(p, n, x, K, dev, stream, variant);
+    if (C == 5) return dispatch_multi_wide<5>(p, n, x, K, dev, stream, variant);
+    if (C == 6) return dispatch_multi_wide<6>(p, n, x, K, dev, stream, variant);
+    if (C == 7) return dispatch_multi_wide<7>(p, n, x, K, dev, stream, variant);
+    if (C == 8) return dispatch_multi_wide<8>(p, n, x, K, dev, stream, variant);
     if (C <= 16) return dispatch_multi_rows<4, 4, 4>(p, n, x, K, dev, stream, variant);
     return dispatch_multi_rows<4, 0, 4>(p, n, x, K, dev, stream, variant);
 }
