@@ -76,7 +76,7 @@ def test_multi_matches_oracle(K):
 
 @pytest.mark.parametrize("Ns,K", [((5,), 1030), ((16, 16), 1030), ((2048, 512, 512), 2048), ((0, 33, 0, 7), 1030),
                                   ((9, 1, 130, 0, 77, 3, 40), 1030), ((4096, 1024, 1024), 5632),
-                                  ((2048, 2048, 2048), 8192)])
+                                  ((2048, 2048, 2048), 8192), ((4096, 1024, 1024), 11008)])
 def test_multi_projection_counts(Ns, K):
     # one projection, the engine's GQA shape, empty projections, more than
     # the four a launch takes (run four at a time), and 5 to 8 chunks per row

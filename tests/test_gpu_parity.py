@@ -146,10 +146,10 @@ def test_matvec_k_sweep(N, K):
     assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
 
 
-@pytest.mark.parametrize("K", [4100, 5000, 5632, 7000, 8192])
+@pytest.mark.parametrize("K", [4100, 5000, 5632, 7000, 8192, 9000, 11008, 12288, 16384])
 @pytest.mark.parametrize("N", [100, 1000, 4097, 11008])
 def test_matvec_one_wave_per_chunk(N, K):
-    # 5 to 8 chunks of 1024 codes run one wave per chunk; N spans every
+    # 5 to 16 chunks of 1024 codes run one wave per chunk; N spans every
     # rows-per-block choice (16, 8, 4, 2), ragged K and row tails included
     rng = np.random.default_rng(N * 7 + K)
     w = random_weights(rng, N, K, full_range=(K % 2 == 0))
@@ -375,7 +375,8 @@ def test_residual_kat(case):
 
 
 FUSED_SHAPES = [(1, 1), (1, 4), (3, 7), (37, 64), (100, 1024), (9, 1030), (70, 2048), (21, 4099), (513, 4096),
-                (5, 8200), (3, 20000), (2000, 300), (4097, 1000), (2048, 5632), (700, 7000), (4097, 8192)]
+                (5, 8200), (3, 20000), (2000, 300), (4097, 1000), (2048, 5632), (700, 7000), (4097, 8192), (4096, 11008),
+                (300, 16384)]
 
 
 @pytest.mark.parametrize("N,K", FUSED_SHAPES)

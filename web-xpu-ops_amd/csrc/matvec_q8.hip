@@ -843,6 +843,21 @@ hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
     return launch_m1<WAVES, 1, 2, EPI>(a, stream, variant);
 }
 
+// 9 to 16 chunks (K up to 16384): one wave per chunk as well, at most 8 rows
+// per block and the largest R that still gives every CU a workgroup (4-12 %
+// faster than 4 waves of 4 chunk slots each, same-process timings from
+// K = 9000 to 16384).
+template <int WAVES, int EPI>
+hipError_t dispatch_m1_wider(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    constexpr int RM = EPI == kEpiFfn ? 4 : 8;
+    const uint32_t want = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    if constexpr (RM >= 8) {
+        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, 1, 8, EPI>(a, stream, variant);
+    }
+    if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, 1, 4, EPI>(a, stream, variant);
+    return launch_m1<WAVES, 1, 2, EPI>(a, stream, variant);
+}
+
 template <int EPI>
 hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
     const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
@@ -854,7 +869,17 @@ hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t s
     if (C == 6) return dispatch_m1_wide<6, 16, EPI>(a, dev, stream, variant);
     if (C == 7) return dispatch_m1_wide<7, 16, EPI>(a, dev, stream, variant);
     if (C == 8) return dispatch_m1_wide<8, 16, EPI>(a, dev, stream, variant);
-    if (C <= 16) return dispatch_m1_rows<4, 4, 4, EPI>(a, dev, stream, variant);
+    switch (C) {
+        case 9: return dispatch_m1_wider<9, EPI>(a, dev, stream, variant);
+        case 10: return dispatch_m1_wider<10, EPI>(a, dev, stream, variant);
+        case 11: return dispatch_m1_wider<11, EPI>(a, dev, stream, variant);
+        case 12: return dispatch_m1_wider<12, EPI>(a, dev, stream, variant);
+        case 13: return dispatch_m1_wider<13, EPI>(a, dev, stream, variant);
+        case 14: return dispatch_m1_wider<14, EPI>(a, dev, stream, variant);
+        case 15: return dispatch_m1_wider<15, EPI>(a, dev, stream, variant);
+        case 16: return dispatch_m1_wider<16, EPI>(a, dev, stream, variant);
+        default: break;
+    }
     return dispatch_m1_rows<4, 0, 4, EPI>(a, dev, stream, variant);
 }
 
@@ -1049,6 +1074,21 @@ hipError_t dispatch_multi_wide(const Projection* p, uint32_t count, const float*
     return launch_multi<WAVES, 1, 2>(p, count, x, K, stream, variant);
 }
 
+// 9 to 16 chunks: one wave per chunk, as for a single projection.
+template <int WAVES>
+hipError_t dispatch_multi_wider(const Projection* p, uint32_t count, const float* x, uint32_t K,
+                                const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    const uint64_t want = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    auto blocks = [&](uint32_t R) {
+        uint64_t b = 0;
+        for (uint32_t i = 0; i < count; ++i) b += (p[i].N + (uint64_t)R - 1) / R;
+        return b;
+    };
+    if (blocks(8) >= want) return launch_multi<WAVES, 1, 8>(p, count, x, K, stream, variant);
+    if (blocks(4) >= want) return launch_multi<WAVES, 1, 4>(p, count, x, K, stream, variant);
+    return launch_multi<WAVES, 1, 2>(p, count, x, K, stream, variant);
+}
+
 }  // namespace
 
 hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count, const float* x, uint32_t K,
@@ -1083,7 +1123,17 @@ hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count,
     if (C == 6) return dispatch_multi_wide<6>(p, n, x, K, dev, stream, variant);
     if (C == 7) return dispatch_multi_wide<7>(p, n, x, K, dev, stream, variant);
     if (C == 8) return dispatch_multi_wide<8>(p, n, x, K, dev, stream, variant);
-    if (C <= 16) return dispatch_multi_rows<4, 4, 4>(p, n, x, K, dev, stream, variant);
+    switch (C) {
+        case 9: return dispatch_multi_wider<9>(p, n, x, K, dev, stream, variant);
+        case 10: return dispatch_multi_wider<10>(p, n, x, K, dev, stream, variant);
+        case 11: return dispatch_multi_wider<11>(p, n, x, K, dev, stream, variant);
+        case 12: return dispatch_multi_wider<12>(p, n, x, K, dev, stream, variant);
+        case 13: return dispatch_multi_wider<13>(p, n, x, K, dev, stream, variant);
+        case 14: return dispatch_multi_wider<14>(p, n, x, K, dev, stream, variant);
+        case 15: return dispatch_multi_wider<15>(p, n, x, K, dev, stream, variant);
+        case 16: return dispatch_multi_wider<16>(p, n, x, K, dev, stream, variant);
+        default: break;
+    }
     return dispatch_multi_rows<4, 0, 4>(p, n, x, K, dev, stream, variant);
 }
 
