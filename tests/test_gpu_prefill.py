@@ -152,9 +152,22 @@ def test_matmul_long_ragged_k(N, M, K):
     assert_matmul(y, a, w, s, N, M, K)
 
 
-def test_matmul_nonfinite_activations():
+@pytest.mark.parametrize("N,M,K", [(N, M, K) for N in (1, 2, 5, 8, 16, 17, 31, 32, 33) for M, K in ((300, 1030), (20000, 520))])
+def test_matmul_small_token_counts(N, M, K):
+    # up to 32 tokens run on the batched single-vector kernels (VALU, or the
+    # matrix cores from 5 tokens on 16384+ rows), from 33 on the GEMM
+    rng = np.random.default_rng(N * 131 + M + K)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    w = rng.integers(0, 2 ** 32, M * ((K + 3) // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(-0.05, 0.05, M).astype(np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+
+
+@pytest.mark.parametrize("N", [70, 8])
+def test_matmul_nonfinite_activations(N):
     rng = np.random.default_rng(2)
-    N, M, K = 70, 40, 200
+    M, K = 40, 200
     a = rng.standard_normal(N * K).astype(np.float32)
     a[3] = np.inf                     # token 0
     a[K + 5] = -np.inf                # token 1

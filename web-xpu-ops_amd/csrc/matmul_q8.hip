@@ -109,7 +109,7 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
     l = __float_as_uint(r - __uint_as_float(m));
 }
 
-template <int FB, int NW, int BK>
+template <int FB, int NW, int BK, int PD>
 __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restrict__ a,
                                                         const uint32_t* __restrict__ weight,
                                                         const float* __restrict__ scale, float* __restrict__ out,
@@ -130,7 +130,8 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     constexpr int TB = (int)(4u / (NW / 2u));         // 16-token blocks per wave (2 or 1)
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(BK == 64 || BK == 128, "64- or 128-code steps");
-    static_assert(kFoldSteps % 2u == 0u, "a fold group starts on stage 0");
+    static_assert(PD == 2 || PD == 4, "2 or 4 register sets of loads in flight");
+    static_assert(kFoldSteps % (uint32_t)PD == 0u, "a fold group starts on register set 0 and stage 0");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [A0 A1 B0 B1]
 
     // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
@@ -166,9 +167,9 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     const uint32_t bc = t % NW;
     const int boff = (int)((btok * K + bc * FPT) * 4u);
 
-    // Two register sets of global loads: step i's data sits in set i & 1,
-    // loaded two steps ahead.
-    u32x4v ga[2][AL], gb[2][BL];
+    // PD register sets of global loads: step i's data sits in set i % PD,
+    // loaded PD steps ahead of its conversion.
+    u32x4v ga[PD][AL], gb[PD][BL];
     auto issue = [&](int b, uint32_t k0) {
 #pragma unroll
         for (int u = 0; u < AL; ++u)
@@ -219,8 +220,8 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     };
     // Writes the converted step into stage s and returns the thread's
     // non-finite indicator.  Row r's 16-byte piece p sits at piece p ^ (r & 7).
-    auto convert_store = [&](int s) -> float {
-        uint8_t* as = lds + (uint32_t)s * AST;
+    auto convert_store = [&](int s, int st) -> float {
+        uint8_t* as = lds + (uint32_t)st * AST;
 #pragma unroll
         for (int u = 0; u < AL; ++u) {
             if (!(ACH % NT == 0u || t + NT * (uint32_t)u < ACH)) continue;  // wave-uniform
@@ -251,12 +252,12 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
             mp[e / 2] = hi_pair(m0_, m1);
             lp[e / 2] = hi_pair(l0, l1);
         }
-        store_b(s, hp, mp, lp);
+        store_b(st, hp, mp, lp);
         return rsum;
     };
 
     // The same activation conversion for every value, Inf and NaN included.
-    auto nonfinite_fixup = [&](int s) {
+    auto nonfinite_fixup = [&](int s, int st) {
         uint32_t v[FPT];
         load_b(s, v);
         uint32_t hp[FPT / 2], mp[FPT / 2], lp[FPT / 2];
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
             mp[e / 2] = hi_pair(m0_, m1);
             lp[e / 2] = hi_pair(l0, l1);
         }
-        store_b(s, hp, mp, lp);
+        store_b(st, hp, mp, lp);
     };
 
     f32x4 acc[FB][TB], sum[FB][TB];
@@ -313,43 +314,48 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     };
 
     // Software pipeline, one barrier per step: iteration i converts step
-    // i + 1 (register set and LDS stage (i + 1) & 1) and refills that set
-    // with step i + 3, then runs step i's matrix work on stage i & 1.  The
+    // i + 1 (register set (i + 1) % PD, LDS stage (i + 1) & 1) and refills
+    // that set with step i + 1 + PD, then runs step i's matrix work on stage
+    // i & 1.  A step's loads thus have PD iterations to arrive.  The
     // conversion (VALU) and the matrix work are independent, so a wave
     // overlaps them.  Past the last step the conversion writes a stage nobody
     // reads and the loads fall outside the buffer resources (they return 0).
     const uint32_t steps = (K + kBK - 1u) / kBK;
     const bool ragged = (K % kBK) != 0u;
-    auto convert_checked = [&](int b) {
-        const float rsum = convert_store(b);
-        if (__builtin_amdgcn_ballot_w64(__builtin_isnan(rsum)) != 0) nonfinite_fixup(b);  // uniform
+    auto convert_checked = [&](int s, int st) {
+        const float rsum = convert_store(s, st);
+        if (__builtin_amdgcn_ballot_w64(__builtin_isnan(rsum)) != 0) nonfinite_fixup(s, st);  // uniform
     };
-    issue(0, 0u);
-    issue(1, kBK);
+#pragma unroll
+    for (int q = 0; q < PD; ++q) issue(q, (uint32_t)q * kBK);
     if (ragged && steps == 1u) mask_b(0, 0u);
-    convert_checked(0);
-    issue(0, 2u * kBK);
+    convert_checked(0, 0);
+    issue(0, (uint32_t)PD * kBK);
     __syncthreads();
     // The matrix work comes first in program order: its LDS reads then need
     // not wait behind the conversion's LDS writes, and the scheduler can fill
-    // the matrix-core latency with the conversion's VALU work.
-    auto iter = [&](int b, uint32_t i) {
-        if (ragged && i + 2u == steps) mask_b(b ^ 1, (i + 1u) * kBK);  // uniform
-        compute(b);
-        convert_checked(b ^ 1);
-        issue(b ^ 1, (i + 3u) * kBK);
+    // the matrix-core latency with the conversion's VALU work.  q = i % PD.
+    auto iter = [&](int q, uint32_t i) {
+        const int nx = (q + 1) % PD;
+        if (ragged && i + 2u == steps) mask_b(nx, (i + 1u) * kBK);  // uniform
+        compute(q & 1);
+        convert_checked(nx, (q + 1) & 1);
+        issue(nx, (i + 1u + (uint32_t)PD) * kBK);
         __syncthreads();
     };
-    // Steps run in groups of kFoldSteps (an even count, so a group starts on
-    // stage 0); the accumulator is folded into the outer sum after each group.
+    // Steps run in groups of kFoldSteps (a multiple of PD, so a group starts
+    // on register set 0 and stage 0); the accumulator is folded into the
+    // outer sum after each group.
     for (uint32_t g0 = 0; g0 < steps; g0 += kFoldSteps) {
         const uint32_t gend = min(g0 + kFoldSteps, steps);
         uint32_t i = g0;
-        for (; i + 1u < gend; i += 2u) {
-            iter(0, i);
-            iter(1, i + 1u);
+        for (; i + (uint32_t)PD <= gend; i += (uint32_t)PD) {
+#pragma unroll
+            for (int q = 0; q < PD; ++q) iter(q, i + (uint32_t)q);
         }
-        if (i < gend) iter(0, i);
+#pragma unroll
+        for (int q = 0; q < PD - 1; ++q)
+            if (i + (uint32_t)q < gend) iter(q, i + (uint32_t)q);
 #pragma unroll
         for (int f = 0; f < FB; ++f)
 #pragma unroll
@@ -392,7 +398,7 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
-template <int FB, int NW, int BK>
+template <int FB, int NW, int BK, int PD = 2>
 hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N, uint32_t M,
                      uint32_t K, hipStream_t stream) {
     constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
@@ -402,7 +408,7 @@ hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale,
     const uint32_t total = mtiles * ntiles;
     const uint32_t grid = ((total + 7u) / 8u) * 8u;
     const size_t lds = 2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes;
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK>), dim3(grid), dim3(64 * NW), lds, stream, a, weight, scale, out,
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD>), dim3(grid), dim3(64 * NW), lds, stream, a, weight, scale, out,
                        N, M, K, W, mtiles, ntiles);
     return hipGetLastError();
 }
@@ -420,23 +426,31 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
         if (variant) *variant = "matmul.zero";
         return hipGetLastError();
     }
+    // Up to 32 tokens: the batched single-vector path, one token per vector
+    // (out[n, m] is y[vector n][row m], the same layout).  The GEMM walks all
+    // of K in a serial chain of steps per workgroup whatever the token count
+    // (20 us for 1 token at 2048 x 2048); the batched path streams the weight
+    // once per 8 or 16 tokens (3.6 us for 1 token, 12 us for 32; the GEMM
+    // wins from about 64 tokens).  Both compute the matvecQ8 form.
+    if (N <= 32u) {
+        MatvecArgs mv{weight, scale, a, out, M, K, N, (uint32_t)(((uint64_t)K + 3) / 4)};
+        const hipError_t e = launch_matvec_q8(mv, dev, stream, variant);
+        if (variant) *variant = "matmul.batched_matvec";
+        return e;
+    }
     // 128 weight rows per workgroup when that still gives every CU a tile,
-    // otherwise 64.  128-code steps halve the barriers and load round trips
-    // per unit of work; they pay off for long K with 64-row tiles (measured:
-    // 512 x 2048 x 5632 in 71 us against 79), while with 128-row tiles the
-    // two stages fill all 160 KB of LDS and leave one workgroup per CU.
+    // otherwise 64 rows with four register sets of loads in flight (6-16 %
+    // faster than two at 64-row tiles from K = 2048 to 11008, and faster than
+    // 128-code steps; with 128-row tiles the extra registers cost more than
+    // they save).
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const uint32_t ntiles = (N + kBN - 1u) / kBN;
     if ((uint64_t)((M + 127u) / 128u) * ntiles >= cus) {
         if (variant) *variant = "matmul.mfma128";
-        return launch_fb<4, 8, 64>(a, weight, scale, out, N, M, K, stream);
-    }
-    if (K > 4096u) {
-        if (variant) *variant = "matmul.mfma64.k128";
-        return launch_fb<2, 8, 128>(a, weight, scale, out, N, M, K, stream);
+        return launch_fb<4, 8, 64, 2>(a, weight, scale, out, N, M, K, stream);
     }
     if (variant) *variant = "matmul.mfma64";
-    return launch_fb<2, 8, 64>(a, weight, scale, out, N, M, K, stream);
+    return launch_fb<2, 8, 64, 4>(a, weight, scale, out, N, M, K, stream);
 }
 
 }  // namespace wxo
