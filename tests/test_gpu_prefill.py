@@ -164,6 +164,19 @@ def test_matmul_small_token_counts(N, M, K):
     assert_matmul(y, a, w, s, N, M, K)
 
 
+@pytest.mark.parametrize("N,M,K", [(400, 3000, 300), (450, 4096, 1030), (200, 700, 2061), (40, 64, 64)])
+def test_matmul_kernel_variants(N, M, K):
+    # every GEMM form: 64-row tiles with one K group (more tiles than CUs) and
+    # with two (the K steps split in halves, an odd count included), 128-row
+    # tiles with two K groups (exactly one tile per CU), one K step
+    rng = np.random.default_rng(N + M + K)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    w = rng.integers(0, 2 ** 32, M * ((K + 3) // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(-0.05, 0.05, M).astype(np.float32)
+    y = wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=N, M=M, K=K)
+    assert_matmul(y, a, w, s, N, M, K)
+
+
 @pytest.mark.parametrize("N", [70, 8])
 def test_matmul_nonfinite_activations(N):
     rng = np.random.default_rng(2)

@@ -109,8 +109,8 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
     l = __float_as_uint(r - __uint_as_float(m));
 }
 
-template <int FB, int NW, int BK, int PD>
-__global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restrict__ a,
+template <int FB, int NW, int BK, int PD, int KS>
+__global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a,
                                                         const uint32_t* __restrict__ weight,
                                                         const float* __restrict__ scale, float* __restrict__ out,
                                                         uint32_t N, uint32_t M, uint32_t K, uint32_t W,
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     constexpr uint32_t CPR = kBK / 16u;               // 16-code chunks per row and step
     constexpr uint32_t AST = BM * kRowBytes;          // bytes of one A stage
     constexpr uint32_t BST = 3u * kBN * kRowBytes;    // bytes of one B stage (three parts)
-    constexpr uint32_t NT = 64u * NW;                 // threads
+    constexpr uint32_t NT = 64u * NW;                 // threads of one K group
     constexpr uint32_t ACH = BM * CPR;                // 16-code chunks of A per step
     constexpr int AL = (int)((ACH + NT - 1u) / NT);   // A loads per thread per step
     constexpr uint32_t FPT = kBK / NW;                // activations per thread per step
@@ -132,7 +132,9 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     static_assert(BK == 64 || BK == 128, "64- or 128-code steps");
     static_assert(PD == 2 || PD == 4, "2 or 4 register sets of loads in flight");
     static_assert(kFoldSteps % (uint32_t)PD == 0u, "a fold group starts on register set 0 and stage 0");
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // [A0 A1 B0 B1]
+    static_assert(KS == 1 || KS == 2, "K split over 1 or 2 groups of NW waves");
+    // Per K group: [A0 A1 B0 B1]
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
     // contiguous run of the (token-major) tile sequence.
@@ -144,7 +146,11 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     const uint32_t nt = lin / mtiles, mt = lin - nt * mtiles;
     const uint32_t m0 = mt * BM, n0 = nt * kBN;
 
-    const uint32_t t = threadIdx.x;
+    // KS groups of NW waves share the tile and split its K steps in halves;
+    // their sums meet in LDS at the end.
+    const uint32_t kg = KS == 1 ? 0u : __builtin_amdgcn_readfirstlane(threadIdx.x / NT);
+    const uint32_t gbase = kg * (2u * AST + 2u * BST);  // this group's stages (0 for KS = 1)
+    const uint32_t t = KS == 1 ? threadIdx.x : threadIdx.x % NT;
     const uint32_t lane = t & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t wm = (wv & 1u) * (BM / 2u);            // wave's first weight row in the tile
@@ -207,7 +213,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     // 16-byte pieces per part, starting at piece bc * FPT / 8 of the row.
     auto store_b = [&](int s, const uint32_t (&hp)[FPT / 2], const uint32_t (&mp)[FPT / 2],
                        const uint32_t (&lp)[FPT / 2]) {
-        uint8_t* row = lds + 2u * AST + (uint32_t)s * BST + btok * kRowBytes;
+        uint8_t* row = lds + gbase + 2u * AST + (uint32_t)s * BST + btok * kRowBytes;
 #pragma unroll
         for (uint32_t q = 0; q < FPT / 8u; ++q) {
             const uint32_t pc = ((bc * (FPT / 8u) + q) ^ (btok & 7u)) * 16u;
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     // Writes the converted step into stage s and returns the thread's
     // non-finite indicator.  Row r's 16-byte piece p sits at piece p ^ (r & 7).
     auto convert_store = [&](int s, int st) -> float {
-        uint8_t* as = lds + (uint32_t)st * AST;
+        uint8_t* as = lds + gbase + (uint32_t)st * AST;
 #pragma unroll
         for (int u = 0; u < AL; ++u) {
             if (!(ACH % NT == 0u || t + NT * (uint32_t)u < ACH)) continue;  // wave-uniform
@@ -284,8 +290,8 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
 
     // Matrix work of one stage: two 32-code substeps.
     auto compute = [&](int s) {
-        const uint8_t* as = lds + (uint32_t)s * AST;
-        const uint8_t* bs = lds + 2u * AST + (uint32_t)s * BST;
+        const uint8_t* as = lds + gbase + (uint32_t)s * AST;
+        const uint8_t* bs = lds + gbase + 2u * AST + (uint32_t)s * BST;
 #pragma unroll
         for (int ss = 0; ss < BK / 32; ++ss) {
             const uint32_t piece = 4u * (uint32_t)ss + g;
@@ -322,32 +328,37 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
     // reads and the loads fall outside the buffer resources (they return 0).
     const uint32_t steps = (K + kBK - 1u) / kBK;
     const bool ragged = (K % kBK) != 0u;
+    // This group's steps: [s0, s0 + gs); every group runs `iters` iterations
+    // (the same barriers), skipping the matrix work past its own steps.
+    const uint32_t iters = KS == 1 ? steps : (steps + KS - 1u) / KS;
+    const uint32_t s0 = kg * iters;
+    const uint32_t gs = KS == 1 ? steps : (s0 < steps ? min(iters, steps - s0) : 0u);
     auto convert_checked = [&](int s, int st) {
         const float rsum = convert_store(s, st);
         if (__builtin_amdgcn_ballot_w64(__builtin_isnan(rsum)) != 0) nonfinite_fixup(s, st);  // uniform
     };
 #pragma unroll
-    for (int q = 0; q < PD; ++q) issue(q, (uint32_t)q * kBK);
-    if (ragged && steps == 1u) mask_b(0, 0u);
+    for (int q = 0; q < PD; ++q) issue(q, (s0 + (uint32_t)q) * kBK);
+    if (ragged && s0 + 1u == steps) mask_b(0, s0 * kBK);
     convert_checked(0, 0);
-    issue(0, (uint32_t)PD * kBK);
+    issue(0, (s0 + (uint32_t)PD) * kBK);
     __syncthreads();
     // The matrix work comes first in program order: its LDS reads then need
     // not wait behind the conversion's LDS writes, and the scheduler can fill
     // the matrix-core latency with the conversion's VALU work.  q = i % PD.
     auto iter = [&](int q, uint32_t i) {
         const int nx = (q + 1) % PD;
-        if (ragged && i + 2u == steps) mask_b(nx, (i + 1u) * kBK);  // uniform
-        compute(q & 1);
+        if (ragged && s0 + i + 2u == steps) mask_b(nx, (s0 + i + 1u) * kBK);  // uniform
+        if (KS == 1 || i < gs) compute(q & 1);                                 // uniform
         convert_checked(nx, (q + 1) & 1);
-        issue(nx, (i + 1u + (uint32_t)PD) * kBK);
+        issue(nx, (s0 + i + 1u + (uint32_t)PD) * kBK);
         __syncthreads();
     };
     // Steps run in groups of kFoldSteps (a multiple of PD, so a group starts
     // on register set 0 and stage 0); the accumulator is folded into the
     // outer sum after each group.
-    for (uint32_t g0 = 0; g0 < steps; g0 += kFoldSteps) {
-        const uint32_t gend = min(g0 + kFoldSteps, steps);
+    for (uint32_t g0 = 0; g0 < iters; g0 += kFoldSteps) {
+        const uint32_t gend = min(g0 + kFoldSteps, iters);
         uint32_t i = g0;
         for (; i + (uint32_t)PD <= gend; i += (uint32_t)PD) {
 #pragma unroll
@@ -363,6 +374,30 @@ __global__ __launch_bounds__(64 * NW) void matmul_q8_kernel(const float* __restr
                 sum[f][b] += acc[f][b];
                 acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
+    }
+
+    if constexpr (KS > 1) {
+        // Group 1's sums through LDS (its stages are done) into group 0's.
+        constexpr uint32_t E = (uint32_t)(FB * TB * 4);
+        float* red = reinterpret_cast<float*>(lds);
+        __syncthreads();
+        if (kg == 1u) {
+#pragma unroll
+            for (int f = 0; f < FB; ++f)
+#pragma unroll
+                for (int b = 0; b < TB; ++b)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) red[((uint32_t)((f * TB + b) * 4 + v)) * NT + t] = sum[f][b][v];
+        }
+        __syncthreads();
+        if (kg != 0u) return;  // after the last barrier
+#pragma unroll
+        for (int f = 0; f < FB; ++f)
+#pragma unroll
+            for (int b = 0; b < TB; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) sum[f][b][v] += red[((uint32_t)((f * TB + b) * 4 + v)) * NT + t];
+        static_assert(E * NT * 4u <= 2u * AST + 2u * BST, "the reduction fits in group 0's stages");
     }
 
     // Epilogue: lane (j, g) of block (f, b) holds features m0 + wm + 16 f +
@@ -398,7 +433,7 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
-template <int FB, int NW, int BK, int PD = 2>
+template <int FB, int NW, int BK, int PD, int KS = 1>
 hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N, uint32_t M,
                      uint32_t K, hipStream_t stream) {
     constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
@@ -407,8 +442,8 @@ hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale,
     const uint32_t mtiles = (M + BM - 1u) / BM, ntiles = (N + kBN - 1u) / kBN;
     const uint32_t total = mtiles * ntiles;
     const uint32_t grid = ((total + 7u) / 8u) * 8u;
-    const size_t lds = 2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes;
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD>), dim3(grid), dim3(64 * NW), lds, stream, a, weight, scale, out,
+    const size_t lds = (size_t)KS * (2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes);
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS>), dim3(grid), dim3(64 * NW * KS), lds, stream, a, weight, scale, out,
                        N, M, K, W, mtiles, ntiles);
     return hipGetLastError();
 }
@@ -442,15 +477,21 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
     // otherwise 64 rows with four register sets of loads in flight (6-16 %
     // faster than two at 64-row tiles from K = 2048 to 11008, and faster than
     // 128-code steps; with 128-row tiles the extra registers cost more than
-    // they save).
+    // they save).  When the tiles fit in one workgroup per CU, two groups of
+    // 8 waves split each tile's K steps (half the serial chain; 8-15 %
+    // faster, 512 x 4096 x 11008 in 172 us against 197); with more tiles the
+    // smaller one-group workgroups (two per CU) win.
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
-    const uint32_t ntiles = (N + kBN - 1u) / kBN;
-    if ((uint64_t)((M + 127u) / 128u) * ntiles >= cus) {
-        if (variant) *variant = "matmul.mfma128";
-        return launch_fb<4, 8, 64, 2>(a, weight, scale, out, N, M, K, stream);
+    const uint64_t ntiles = (N + kBN - 1u) / kBN;
+    const uint64_t t4 = (uint64_t)((M + 127u) / 128u) * ntiles, t2 = (uint64_t)((M + 63u) / 64u) * ntiles;
+    if (t4 >= cus) {
+        if (variant) *variant = t4 <= cus ? "matmul.mfma128.ksplit" : "matmul.mfma128";
+        return t4 <= cus ? launch_fb<4, 8, 64, 2, 2>(a, weight, scale, out, N, M, K, stream)
+                         : launch_fb<4, 8, 64, 2, 1>(a, weight, scale, out, N, M, K, stream);
     }
-    if (variant) *variant = "matmul.mfma64";
-    return launch_fb<2, 8, 64, 4>(a, weight, scale, out, N, M, K, stream);
+    if (variant) *variant = t2 <= cus ? "matmul.mfma64.ksplit" : "matmul.mfma64";
+    return t2 <= cus ? launch_fb<2, 8, 64, 4, 2>(a, weight, scale, out, N, M, K, stream)
+                     : launch_fb<2, 8, 64, 4, 1>(a, weight, scale, out, N, M, K, stream);
 }
 
 }  // namespace wxo
