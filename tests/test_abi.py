@@ -78,6 +78,8 @@ def test_validation_happens_before_device_access():
                                       0x30000, 8)
     with pytest.raises(wxo_q8.WxoError, match="projection 0: output overlaps the vector"):
         wxo_q8.matvec_q8_multi_device([(16, 16, 0x3001c, 4)], 0x30000, 8)
+    with pytest.raises(wxo_q8.WxoError, match="projection 1: output overlaps the weight or scale of projection 0"):
+        wxo_q8.matvec_q8_multi_device([(0x50000, 0x60000, 0x10000, 4), (16, 16, 0x50004, 4)], 0x30000, 8)
     assert L.wxo_quantize_pack_q8_multi(None, None, None, None, 0, 8, None) == wxo_q8.WXO_OK
     with pytest.raises(wxo_q8.WxoError, match="matrix 1: input is NULL"):
         wxo_q8.quantize_pack_q8_multi_device([(0x10000, 2, 0x20000, 0x30000), (0, 2, 0x40000, 0x50000)], 8)

@@ -344,18 +344,24 @@ int wxo_matvec_q8_multi(const uint32_t* const* weights, const float* const* scal
             return fail(WXO_ERR_INVALID, "projection %u: %s", i, why);
         }
     }
-    // The projections run concurrently: an output that overlaps the vector
-    // or another output would make the result depend on the schedule.
-    const auto lo = [](const void* p) { return (uintptr_t)p; };
+    // The projections run concurrently: an output that overlaps the vector,
+    // another output or any projection's weight or scale would make the
+    // result depend on the schedule.
+    const uint64_t W = ((uint64_t)K + 3) / 4;
+    const auto meet = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
+        const uintptr_t p0 = (uintptr_t)p, q0 = (uintptr_t)q;
+        return pb > 0 && qb > 0 && p0 < q0 + qb && q0 < p0 + pb;
+    };
     for (uint32_t i = 0; i < count; ++i) {
-        if (Ns[i] == 0) continue;
-        const uintptr_t a0 = lo(outputs[i]), a1 = a0 + (uintptr_t)Ns[i] * 4u;
-        if (K > 0 && a0 < lo(vector) + (uintptr_t)K * 4u && lo(vector) < a1)
+        const uint64_t ob = (uint64_t)Ns[i] * 4u;
+        if (meet(outputs[i], ob, vector, (uint64_t)K * 4u))
             return fail(WXO_ERR_INVALID, "projection %u: output overlaps the vector", i);
-        for (uint32_t j = 0; j < i; ++j) {
-            if (Ns[j] == 0) continue;
-            const uintptr_t b0 = lo(outputs[j]), b1 = b0 + (uintptr_t)Ns[j] * 4u;
-            if (a0 < b1 && b0 < a1) return fail(WXO_ERR_INVALID, "outputs of projections %u and %u overlap", j, i);
+        for (uint32_t j = 0; j < count; ++j) {
+            if (j < i && meet(outputs[i], ob, outputs[j], (uint64_t)Ns[j] * 4u))
+                return fail(WXO_ERR_INVALID, "outputs of projections %u and %u overlap", j, i);
+            if (meet(outputs[i], ob, weights[j], (uint64_t)Ns[j] * W * 4u) ||
+                meet(outputs[i], ob, scales[j], (uint64_t)Ns[j] * 4u))
+                return fail(WXO_ERR_INVALID, "projection %u: output overlaps the weight or scale of projection %u", i, j);
         }
     }
     const wxo::DeviceInfo* d = nullptr;
