@@ -350,8 +350,28 @@ def run_suite(stream, steps, warmup):
         del c5
 
     run_prefill_suite(stream, steps, warmup, results, check)
+    results.extend(napi_end_to_end())
     results.extend(cpu_reference_ops(budget_s=1.0))
     return results
+
+
+def napi_end_to_end():
+    """What a JavaScript caller sees through the Node-API addon (launch plus
+    stream synchronisation per call, readback, the PCIe-inclusive host call and
+    a whole resident decode step): web-xpu-ops_amd/harness/napi_timing.mjs, run
+    as a child process.  Reported beside the kernel-only event timings."""
+    node = shutil.which("node")
+    if node is None:
+        return []
+    proc = subprocess.run([node, os.path.join(ROOT, "web-xpu-ops_amd", "harness", "napi_timing.mjs")],
+                          capture_output=True, text=True, timeout=300)
+    if proc.returncode != 0:
+        raise RuntimeError(f"napi_timing.mjs failed: {proc.stderr.strip()[-500:]}")
+    r = json.loads(proc.stdout.strip().splitlines()[-1])
+    for e in r["results"]:
+        e["node"] = r["node"]
+        log(f"suite {e['case']}: {e['us']} us")
+    return r["results"]
 
 
 def cpu_reference_ops(budget_s):

@@ -1,0 +1,76 @@
+"""Host <-> device copies through the C ABI on the GPU: device-to-host reads
+return the exact bytes from any source offset, for any length (sizes from one
+byte to past 4 MiB), and a stream's pending work lands before a read on that
+stream."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import wxo_q8
+
+pytestmark = pytest.mark.gpu
+
+LIMIT = 4 << 20
+
+
+@pytest.fixture(scope="module")
+def source():
+    wxo_q8.init()
+    data = np.random.default_rng(11).integers(0, 256, LIMIT + 4096, dtype=np.uint8)
+    buf = wxo_q8.DeviceBuffer.from_array(data)
+    yield data, buf
+    buf.free()
+
+
+@pytest.mark.parametrize("offset", [0, 1, 3, 4, 12, 16, 4095])
+@pytest.mark.parametrize("length", [1, 3, 4, 15, 16, 17, 44032, 65536, 65537, 600000])
+def test_read_any_offset_and_length(source, offset, length):
+    data, buf = source
+    print(f"read offset={offset} length={length}", flush=True)
+    got = buf.download(np.uint8, length, offset=offset)
+    assert np.array_equal(got, data[offset:offset + length])
+
+
+@pytest.mark.parametrize("length", [LIMIT - 16, LIMIT, LIMIT + 1, LIMIT + 4096])
+def test_read_around_4_mib(source, length):
+    data, buf = source
+    print(f"read length={length}", flush=True)
+    got = buf.download(np.uint8, length)
+    assert np.array_equal(got, data[:length])
+
+
+def test_small_reads_after_a_large_one(source):
+    data, buf = source
+    for length in (100, LIMIT, 7, 300000, 64):
+        print(f"read length={length}", flush=True)
+        assert np.array_equal(buf.download(np.uint8, length, offset=5), data[5:5 + length])
+
+
+def test_read_waits_for_the_stream():
+    # A matvec enqueued on a stream, then read back on that stream: the read
+    # sees the finished output, every call.
+    wxo_q8.init()
+    stream = wxo_q8.Stream()
+    N, K = 4096, 1024
+    W = K // 4
+    rng = np.random.default_rng(5)
+    weight = wxo_q8.DeviceBuffer.from_array(rng.integers(0, 2**32, N * W, dtype=np.uint64).astype(np.uint32))
+    scale = wxo_q8.DeviceBuffer.from_array(np.full(N, 0.5, np.float32))
+    out = wxo_q8.DeviceBuffer(N * 4)
+    L = wxo_q8.lib()
+    first = None
+    for i in range(20):
+        x = wxo_q8.DeviceBuffer.from_array(np.full(K, float(i), np.float32))
+        assert L.wxo_matvec_q8(weight.ptr, scale.ptr, x.ptr, out.ptr, N, K, 1, stream.handle) == 0
+        y = out.download(np.float32, N, stream)
+        if i == 1:
+            first = y.copy()
+        if i >= 1:
+            # y is linear in the constant vector value i
+            np.testing.assert_allclose(y, first * i, rtol=1e-5, atol=1e-3)
+        else:
+            assert np.all(y == 0)
+        x.free()
+    for b in (weight, scale, out):
+        b.free()
