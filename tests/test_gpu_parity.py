@@ -267,12 +267,14 @@ def test_batched_same_sign_long_k(M, K):
 
 
 @pytest.mark.parametrize("M,K", [(5, 1030), (8, 64), (12, 2048), (13, 4099), (16, 1024), (17, 1500), (32, 520),
-                                 (6, 3000)])
+                                 (6, 3000), (14, 1000), (16, 768), (13, 1536)])
 def test_batched_matrix_core_shapes(M, K):
     # From 16384 rows and 5 vectors the batched call runs on the matrix cores
     # (when the tile's x parts fit in LDS); smaller shapes take the VALU path,
     # which the other batched tests cover.  Ragged row tail (N % 16 != 0),
-    # ragged K, vector tiles past 16, full-range codes (-128 included).
+    # ragged K, vector tiles past 16, full-range codes (-128 included).  16
+    # vectors with K <= 1024 and 13 with 1024 < K <= 1536 take the 8-wave
+    # kernel with 128-code steps.
     rng = np.random.default_rng(M * 1009 + K)
     N = 16397
     w = random_weights(rng, N, K, full_range=True)
@@ -283,7 +285,7 @@ def test_batched_matrix_core_shapes(M, K):
         assert_matvec(ys[m], w, s, xs[m], N, K)
 
 
-@pytest.mark.parametrize("M,K", [(5, 5376), (16, 1536)])
+@pytest.mark.parametrize("M,K", [(5, 5376), (16, 1536), (16, 1024), (13, 1536)])
 def test_batched_matrix_core_same_sign_long_k(M, K):
     # The longest K whose x parts still fit in LDS for the tile, all terms
     # positive: the matrix cores' longest accumulation chains.
@@ -299,7 +301,8 @@ def test_batched_matrix_core_same_sign_long_k(M, K):
 
 
 @pytest.mark.parametrize("M,K,N", [(M, K, 37) for M in (2, 4, 8, 12, 16) for K in (1030, 4096)]
-                         + [(M, 1030, 16397) for M in (5, 8, 12, 16)] + [(6, 4096, 16397)])
+                         + [(M, 1030, 16397) for M in (5, 8, 12, 16)] + [(6, 4096, 16397), (16, 1000, 16397),
+                                                                         (13, 1500, 16397)])
 def test_batched_nonfinite_vectors(M, K, N):
     # Inf and NaN entries reach every row as the reference's f64 sum has them
     # (q * Inf = +-Inf, 0 * Inf = NaN), including NaNs whose payload sits only

@@ -595,23 +595,27 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_kernel(
 }
 
 // The same kernel with the weight tiles fetched straight into LDS
-// (buffer_load_dwordx4 ... lds): one instruction moves 4 rows x 256 bytes,
-// whole 128-byte lines, where the register form can only fetch 64 bytes of
-// each of 16 rows.  Each wave owns D stages of T x 4 KiB.  Piece q (16 bytes)
-// of row j of a tile is stored at position q ^ j of that row, so the 16 lanes
-// that read one piece of 16 different rows hit 16 different bank groups.
+// (buffer_load_dwordx4 ... lds): one instruction moves 1 KiB of whole 128-byte
+// lines (4 rows x 256 bytes, or 8 rows x 128 bytes), where the register form
+// can only fetch 64 bytes of each of 16 rows.  NWV waves (4 or 8) each own D
+// stages of T tiles of 16 rows x SC codes (SC = 256 or 128: a K step).  Piece
+// q (16 bytes) of row j of a tile is stored at position q ^ (j mod pieces per
+// row), so the lanes that read one piece of 16 different rows spread over the
+// bank groups.  128-code steps halve the stages, which lets 8 waves (two per
+// SIMD) share one copy of the x parts of up to 8 vectors: one wave's LDS and
+// load waits then overlap the other's conversion and matrix work.
 // Waits are explicit, since the compiler does not track these loads: every
 // LDS read of a stage completes (lgkmcnt(0)) before the stage is refilled,
 // and a stage is read only after its loads have landed (vmcnt, counting the
 // loads issued after it; vector stores count there too, which can only make
 // the wait longer).
-constexpr uint32_t kDmaTileBytes = 16u * 256u;
+constexpr uint32_t kDmaTileBytes = 16u * 256u;  // one tile at 256-code steps
 // Stages per wave.  Three or four (more weight bytes in flight per wave,
 // fewer workgroups per CU) measured slower at every M from 2 to 14.
 constexpr int kDmaStages = 2;
 
-template <int T, int D>
-__global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
+template <int T, int D, int NWV = 4, int SC = 256>
+__global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
     float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M, uint32_t Kp) {
     extern __shared__ __attribute__((aligned(16))) uint16_t xparts[];  // x parts, weight stages, tile slots
@@ -623,24 +627,34 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
     const uint32_t j = lane & 15u, g = lane >> 4;
     const uint32_t jb = min(j, MC - 1u);
     uint8_t* stages = reinterpret_cast<uint8_t*>(xparts + 3u * MC * Kp);
-    uint8_t* wst = stages + wv * ((uint32_t)D * T * kDmaTileBytes);
-    float* slot = reinterpret_cast<float*>(stages + 4u * D * T * kDmaTileBytes) + wv * kTileSlotFloats;
+    static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
+    static_assert(SC == 256 || SC == 128, "256- or 128-code steps");
+    constexpr uint32_t TBY = 16u * (uint32_t)SC;       // bytes of one tile per step
+    constexpr uint32_t PPR = (uint32_t)SC / 16u;        // 16-byte pieces per row
+    constexpr uint32_t RPI = 1024u / (uint32_t)SC;      // rows per load instruction
+    constexpr int LPT = SC / 64;                        // load instructions per tile
+    constexpr uint32_t NT = 64u * NWV;                  // threads
+    uint8_t* wst = stages + wv * ((uint32_t)D * T * TBY);
+    float* slot = reinterpret_cast<float*>(stages + (uint32_t)NWV * D * T * TBY) + wv * kTileSlotFloats;
     const uint32_t rowbytes = W * 4u;
     const uint32_t ntiles = (N + 15u) / 16u;
-    const uint32_t S = Kp / 256u;
+    const uint32_t S = Kp / (uint32_t)SC;
     const uint32_t b0 = (uint32_t)((uint64_t)blockIdx.x * ntiles / gridDim.x);
     const uint32_t b1 = (uint32_t)((uint64_t)(blockIdx.x + 1u) * ntiles / gridDim.x);
-    const uint32_t t0 = b0 + (b1 - b0) * wv / 4u, t1 = b0 + (b1 - b0) * (wv + 1u) / 4u;
+    const uint32_t t0 = b0 + (b1 - b0) * wv / (uint32_t)NWV, t1 = b0 + (b1 - b0) * (wv + 1u) / (uint32_t)NWV;
     const uint32_t ngroups = (t1 - t0 + T - 1) / T;
     const uint32_t total = ngroups * S;
     const uint32_t r_lane = (lane & 3u) * 4u;
-    // load instruction ii of a tile: lane -> row 4 ii + lane / 16, stored at
-    // position lane % 16, which holds piece (lane % 16) ^ row
+    // load instruction ii of a tile: lane -> row RPI ii + lane / PPR, stored
+    // at position lane % PPR, which holds piece (lane % PPR) ^ (row % PPR)
+    // (a fixed bound: a template-dependent array captured by the lambdas below
+    // makes the host-side instantiation of the kernel fail)
     int voff[4];
+    static_assert(LPT <= 4, "at most 4 load instructions per tile");
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-        const uint32_t row = 4u * (uint32_t)ii + (lane >> 4);
-        voff[ii] = (int)(row * rowbytes + (((lane & 15u) ^ row) * 16u));
+    for (int ii = 0; ii < LPT; ++ii) {
+        const uint32_t row = RPI * (uint32_t)ii + lane / PPR;
+        voff[ii] = (int)(row * rowbytes + (((lane % PPR) ^ (row % PPR)) * 16u));
     }
 
     auto issue = [&](uint32_t i, u32x4v (&sc)[T]) {
@@ -649,27 +663,27 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
         const uint32_t rows = i < total ? min((uint32_t)T * 16u, min(t1 * 16u, N) - tile0 * 16u) : 0u;
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)tile0 * 16u * W, rows * rowbytes);
         const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + tile0 * 16u, step == S - 1u ? rows * 4u : 0u);
-        uint8_t* sb = wst + (i % (uint32_t)D) * ((uint32_t)T * kDmaTileBytes);
+        uint8_t* sb = wst + (i % (uint32_t)D) * ((uint32_t)T * TBY);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int so = (int)((uint32_t)t * 16u * rowbytes + step * 256u);
+            const int so = (int)((uint32_t)t * 16u * rowbytes + step * (uint32_t)SC);
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
+            for (int ii = 0; ii < LPT; ++ii)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    wrs, (__attribute__((address_space(3))) void*)(sb + (uint32_t)t * kDmaTileBytes + (uint32_t)ii * 1024u),
+                    wrs, (__attribute__((address_space(3))) void*)(sb + (uint32_t)t * TBY + (uint32_t)ii * 1024u),
                     16, voff[ii], so, 0, kCachePolicyNT);
             sc[t] = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(((uint32_t)t * 16u + r_lane) * 4u), 0, 0);
         }
     };
 
-    constexpr int XU = 16;
+    constexpr int XU = 64 / NWV;  // x loads per thread in the first pass (16 KiB of x per pass)
     const uint32_t kq4 = Kp / 4u;
     const uint32_t n4 = MC * kq4;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x + (size_t)m0 * K, MC * K * 4u);
     u32x4v xv[XU];
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
-        const uint32_t idx = threadIdx.x + (uint32_t)u * 256u;
+        const uint32_t idx = threadIdx.x + (uint32_t)u * NT;
         const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
         const int off = idx < n4 ? (int)((m * K + k) * 4u) : (int)0x7ffffff0;
         xv[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
@@ -679,13 +693,13 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
     for (int q = 0; q < D - 1; ++q) issue((uint32_t)q, sbuf[q]);
 #pragma unroll
     for (int u = 0; u < XU; ++u) {
-        const uint32_t idx = threadIdx.x + (uint32_t)u * 256u;
+        const uint32_t idx = threadIdx.x + (uint32_t)u * NT;
         if (idx < n4) {
             const uint32_t m = idx / kq4;
             store_x_parts(xparts, MC, Kp, K, m, (idx - m * kq4) * 4u, xv[u]);
         }
     }
-    for (uint32_t idx = threadIdx.x + XU * 256u; idx < n4; idx += 256u) {
+    for (uint32_t idx = threadIdx.x + XU * NT; idx < n4; idx += NT) {
         const uint32_t m = idx / kq4, k = (idx - m * kq4) * 4u;
         store_x_parts(xparts, MC, Kp, K, m, k, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)((m * K + k) * 4u), 0, 0));
     }
@@ -707,19 +721,19 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
     const uint16_t* xb = &xparts[(g * MC + jb) * 8u];
     const uint32_t pstride = Kp * MC;
     const uint32_t bstride = 32u * MC;
-    const uint32_t arow = (j >> 2) * 1024u + (j & 3u) * 256u;  // row j of a tile in a stage
+    const uint32_t arow = j * (uint32_t)SC;  // row j of a tile in a stage
 
     auto compute = [&](uint32_t i, const u32x4v (&sc)[T]) {
         const uint32_t step = i % S;
-        const uint16_t* xs = xb + step * 8u * bstride;
-        const uint8_t* sb = wst + (i % (uint32_t)D) * ((uint32_t)T * kDmaTileBytes);
+        const uint16_t* xs = xb + step * ((uint32_t)SC / 32u) * bstride;
+        const uint8_t* sb = wst + (i % (uint32_t)D) * ((uint32_t)T * TBY);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < SC / 64; ++u) {
             u32x4v a[T];
 #pragma unroll
             for (int t = 0; t < T; ++t)
-                a[t] = *reinterpret_cast<const u32x4v*>(sb + (uint32_t)t * kDmaTileBytes + arow +
-                                                        (((4u * (uint32_t)u + g) ^ j) * 16u));
+                a[t] = *reinterpret_cast<const u32x4v*>(sb + (uint32_t)t * TBY + arow +
+                                                        (((4u * (uint32_t)u + g) ^ (j % PPR)) * 16u));
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const uint32_t kb = ((uint32_t)u * 2u + (uint32_t)e) * bstride;
@@ -735,7 +749,8 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
                 }
             }
         }
-        if (step % 4u == 3u) {
+        constexpr uint32_t kFoldSteps = 1024u / (uint32_t)SC;  // fold the h sums every 1024 codes
+        if (step % kFoldSteps == kFoldSteps - 1u) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 hs[t] += hi[t];
@@ -767,7 +782,7 @@ __global__ __launch_bounds__(256) void matvec_q8_mfma_dma_kernel(
 
     // vmcnt encoding (gfx9): low 4 bits in [3:0], high 2 bits in [15:14];
     // expcnt 7 and lgkmcnt 15 leave those counters unconstrained.
-    constexpr int kAfter = (D - 1) * 5 * T;  // loads issued after a stage's own
+    constexpr int kAfter = (D - 1) * (LPT + 1) * T;  // loads issued after a stage's own
     constexpr int kVmWait = 0x0f70 | (kAfter & 15) | ((kAfter >> 4) << 14);
     static_assert(kAfter < 64, "vmcnt holds at most 63");
     for (uint32_t i = 0; i < total; i += (uint32_t)D) {
@@ -987,6 +1002,20 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
                         hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<2, kDmaStages>), g2, dim3(256), (size_t)ldsd, stream,
                                            a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
                     if (variant) *variant = "mb.mfma_dma";
+                    return hipGetLastError();
+                }
+                // 13 to 16 vectors: two tiles per step no longer fit beside the
+                // x parts, but one tile per step in 128-code steps does, shared
+                // by 8 waves (two per SIMD): cfg5 (N = 151936, K = 1024) at
+                // 16 vectors in 42.0 us against 45-46 on the register-load
+                // kernel below.
+                const uint64_t lds8 = 3ull * MC * Kp * 2u + 8ull * kTileSlotFloats * 4u +
+                                      8ull * kDmaStages * 1u * 16u * 128u;
+                if (MC > 12u && lds8 <= kMfmaLdsBytes) {
+                    const dim3 g8(min((ntiles + 3u) / 4u, cus), (a.M + 15u) / 16u);
+                    hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<1, kDmaStages, 8, 128>), g8, dim3(512), (size_t)lds8,
+                                       stream, a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
+                    if (variant) *variant = "mb.mfma_dma8";
                     return hipGetLastError();
                 }
             }
