@@ -267,14 +267,15 @@ def test_batched_same_sign_long_k(M, K):
 
 
 @pytest.mark.parametrize("M,K", [(5, 1030), (8, 64), (12, 2048), (13, 4099), (16, 1024), (17, 1500), (32, 520),
-                                 (6, 3000), (14, 1000), (16, 768), (13, 1536)])
+                                 (6, 3000), (14, 1000), (16, 768), (13, 1536), (20, 1024), (33, 1000)])
 def test_batched_matrix_core_shapes(M, K):
     # From 16384 rows and 5 vectors the batched call runs on the matrix cores
     # (when the tile's x parts fit in LDS); smaller shapes take the VALU path,
     # which the other batched tests cover.  Ragged row tail (N % 16 != 0),
     # ragged K, vector tiles past 16, full-range codes (-128 included).  16
     # vectors with K <= 1024 and 13 with 1024 < K <= 1536 take the 8-wave
-    # kernel with 128-code steps.
+    # kernel with 128-code steps, as do 20 and 33 vectors at K <= 1024 (groups
+    # of 16 on grid y, the last one partial).
     rng = np.random.default_rng(M * 1009 + K)
     N = 16397
     w = random_weights(rng, N, K, full_range=True)
