@@ -115,7 +115,13 @@ __device__ __forceinline__ float residual_epilogue(float r, float projected) {
 //
 // The body is a device function over row block `block` so that the
 // multi-projection kernel below runs the same code on its own row blocks.
-template <int WAVES, int CPW, int R, int EPI>
+//
+// MASK (rows with a partial last chunk): lanes past the row's last word get
+// an offset past the buffer resource, which returns zeros without a memory
+// request, instead of reading the next row's words (then multiplied by zero x).
+// Same results; cfg3 (4096 x 4099) 5.02 -> 4.90 us, 4096 x 4352 4.95 -> 4.84;
+// left off for whole chunks, where the extra compare costs ~2 %.
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
 __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight, const float* __restrict__ scale,
                                              const float* __restrict__ x, float* y, uint32_t N, uint32_t K,
                                              uint32_t W, const uint32_t* __restrict__ weight2, const float* aux,
@@ -154,7 +160,8 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     for (int j = 0; j < slots; ++j) {
         const uint32_t c = wave + (uint32_t)j * WAVES;
         if (CPW != 1 && c >= C) break;  // wave-uniform; with CPW == 1 every wave owns a chunk
-        const int voff = (int)(c * kChunkWords * 4u + (uint32_t)lane * 16u);
+        const uint32_t wi = c * kChunkWords + (uint32_t)lane * 4u;  // the lane's first word
+        const int voff = (!MASK || wi < W) ? (int)(wi * 4u) : 0x40000000;
         u32x4v v[V];
 #pragma unroll
         for (int r = 0; r < R; ++r) v[r] = load_nt_b128(wrs, voff, (int)(r * rowbytes));
@@ -209,11 +216,11 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     }
 }
 
-template <int WAVES, int CPW, int R, int EPI>
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
 __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
     float* y, uint32_t N, uint32_t K, uint32_t W, const uint32_t* __restrict__ weight2, const float* aux) {
-    m1_row_block<WAVES, CPW, R, EPI>(weight, scale, x, y, N, K, W, weight2, aux, blockIdx.x);
+    m1_row_block<WAVES, CPW, R, EPI, MASK>(weight, scale, x, y, N, K, W, weight2, aux, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -807,11 +814,11 @@ __global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
 
 namespace {
 
-template <int WAVES, int CPW, int R, int EPI>
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
 hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
     const float* aux = EPI == kEpiFfn ? a.scale2 : EPI == kEpiResidual ? a.residual : nullptr;
-    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
+    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI, MASK>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
                        a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.weight2, aux);
     if (variant) *variant = CPW > 0 ? "m1.xreg" : "m1.xstream";
     return hipGetLastError();
@@ -842,21 +849,27 @@ hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
 // chunks load side by side instead of one wave walking a second slot after
 // its first (6-10 % faster from K = 4099 to 8192, same-process timings).
 // Rows per block: the largest R that still gives 6 waves per CU.
-template <int WAVES, int RMAX, int EPI>
-hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+template <int WAVES, int RMAX, int EPI, bool MASK>
+hipError_t dispatch_m1_wide_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
     constexpr int RM = EPI == kEpiFfn ? RMAX / 2 : RMAX;
     const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
     if constexpr (RM >= 16) {
-        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI>(a, stream, variant);
+        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI, MASK>(a, stream, variant);
     }
     if constexpr (RM >= 8) {
-        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI>(a, stream, variant);
+        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI, MASK>(a, stream, variant);
     }
     if constexpr (RM >= 4) {
-        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI>(a, stream, variant);
+        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI, MASK>(a, stream, variant);
     }
-    return launch_m1<WAVES, 1, 2, EPI>(a, stream, variant);
+    return launch_m1<WAVES, 1, 2, EPI, MASK>(a, stream, variant);
+}
+
+template <int WAVES, int RMAX, int EPI>
+hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+    if (a.W % kChunkWords != 0u) return dispatch_m1_wide_rows<WAVES, RMAX, EPI, true>(a, dev, stream, variant);
+    return dispatch_m1_wide_rows<WAVES, RMAX, EPI, false>(a, dev, stream, variant);
 }
 
 // 9 to 16 chunks (K up to 16384): one wave per chunk as well, at most 8 rows
