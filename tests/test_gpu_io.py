@@ -74,3 +74,4 @@ def test_read_waits_for_the_stream():
         x.free()
     for b in (weight, scale, out):
         b.free()
+    stream.destroy()
