@@ -16,8 +16,14 @@ Prints one JSON line:
   roofline       the matvec kernel: algorithmic bytes per launch / mean launch
                  duration (HIP events on the launch stream around the K
                  dispatches, which are all that stream holds); traffic = HBM
-                 bytes per launch from the committed rocprofv3
-                 FETCH_SIZE/WRITE_SIZE summary, if present
+                 bytes per launch from the committed rocprofv3 counter
+                 summary, if present (taken in its own profiler run)
+  config.variant the kernel instance that ran (wxo_last_variant)
+
+Every rotated copy is read once during set-up; the timed launches queue
+behind LEAD_STEPS untimed calls and are bracketed by timing-only events, so
+neither first touches, nor the host's launch latency, nor the events' own
+cache fences fall inside the timed region.
   cpu_baseline   the ECMAScript oracle's matvecQ8 under node on one core, on a
                  bounded row sample of the same inputs
 """
@@ -50,6 +56,9 @@ PEAK_FP32_FMA_TFLOPS = 157.3 / 2
 # and runs 16-wide vector tiles, so it issues 3 x 2 x N x K x 16 flops per tile).
 PEAK_BF16_MFMA_TFLOPS = 2500.0
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "matvec_q8_cfg2_traffic.txt")
+TRAFFIC_NOTE = ("HBM bytes per launch from the committed rocprofv3 --pmc summary "
+                "profiles/matvec_q8_cfg2_traffic.txt (not measured in this run: counters need their own "
+                "profiler process)")
 
 
 def log(msg: str) -> None:
@@ -94,12 +103,21 @@ def cpu_baseline(packed, scales, x, N, K, budget_s):
     }
 
 
+# Untimed steps enqueued after the synchronisation that opens a timed
+# sequence and before its first event: the timed launches queue behind
+# running work, so neither the host's latency to the first launch nor an idle
+# GPU's state at the start falls inside the events' interval.
+LEAD_STEPS = 10
+
+
 def time_loop(stream, launch, steps, warmup):
-    """Mean us per step over `steps` back-to-back steps (events on the stream)."""
+    """Mean us per step over `steps` back-to-back steps (timing-only events on the stream)."""
     for i in range(warmup):
         launch(i)
     stream.synchronize()
-    e0, e1 = wxo_q8.Event(), wxo_q8.Event()
+    e0, e1 = wxo_q8.Event(timer=True), wxo_q8.Event(timer=True)
+    for i in range(LEAD_STEPS):
+        launch(warmup + i)
     e0.record(stream)
     for i in range(steps):
         launch(i)
@@ -358,15 +376,15 @@ def run_suite(stream, steps, warmup):
 def napi_end_to_end():
     """What a JavaScript caller sees through the Node-API addon (launch plus
     stream synchronisation per call, readback, the PCIe-inclusive host call and
-    a whole resident decode step): web-xpu-ops_amd/harness/napi_timing.mjs, run
+    a whole resident decode step): bench_napi.mjs, run
     as a child process.  Reported beside the kernel-only event timings."""
     node = shutil.which("node")
     if node is None:
         return []
-    proc = subprocess.run([node, os.path.join(ROOT, "web-xpu-ops_amd", "harness", "napi_timing.mjs")],
+    proc = subprocess.run([node, os.path.join(ROOT, "bench_napi.mjs")],
                           capture_output=True, text=True, timeout=300)
     if proc.returncode != 0:
-        raise RuntimeError(f"napi_timing.mjs failed: {proc.stderr.strip()[-500:]}")
+        raise RuntimeError(f"bench_napi.mjs failed: {proc.stderr.strip()[-500:]}")
     r = json.loads(proc.stdout.strip().splitlines()[-1])
     for e in r["results"]:
         e["node"] = r["node"]
@@ -562,31 +580,43 @@ def main() -> int:
         if st != 0:
             raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
 
+    # Set-up, outside the warmup and the timed region: one call per rotated
+    # copy, so every copy's pages have been read once before any is timed.
+    for i in range(copies):
+        call(i)
+    stream.synchronize()
     for i in range(args.warmup):
         call(i)
     stream.synchronize()
 
-    # Timed region: K back-to-back calls, events at both ends.
-    e0, e1 = wxo_q8.Event(), wxo_q8.Event()
+    # Timed region: K back-to-back calls between two timing-only events
+    # (recording them fences nothing, so no cache write-back or invalidation
+    # lands inside the interval), synchronised on both sides.  LEAD_STEPS
+    # untimed calls are enqueued before the first event, so the timed launches
+    # queue behind running work and the host's latency to the first launch
+    # stays outside the interval.
+    e0, e1 = wxo_q8.Event(timer=True), wxo_q8.Event(timer=True)
     wxo_q8.synchronize()
+    for i in range(LEAD_STEPS):
+        call(args.warmup + i)
     e0.record(stream)
     for i in range(args.steps):
         call(i)
     e1.record(stream)
     e1.synchronize()
     wxo_q8.synchronize()
+    variant = wxo_q8.last_variant()
     total_ms = e0.elapsed_ms(e1)
     ms_per_step = total_ms / args.steps
     bytes_per_call = wl.matvec_bytes(N, K, M)
     value = bytes_per_call / (ms_per_step * 1e-3) / 1e9
 
-    # The launch stream holds nothing but these K matvec dispatches, so the
-    # timed region / K is the mean dispatch duration (the same interval
-    # rocprofv3's kernel trace reports: its per-dispatch intervals tile this
-    # timeline).  Event pairs around single launches add ~2 us of their own.
-    kern_us = ms_per_step * 1e3
-    achieved = bytes_per_call / (kern_us * 1e-6) / 1e9
-    log(f"timed region {total_ms:.3f} ms / {args.steps} calls = {kern_us:.3f} us/call")
+    # The launch stream holds nothing but these K matvec dispatches between
+    # the events, so the timed region / K is the mean launch duration,
+    # back to back (events around single launches would add ~2 us each).
+    launch_us = ms_per_step * 1e3
+    achieved = bytes_per_call / (launch_us * 1e-6) / 1e9
+    log(f"timed region {total_ms:.3f} ms / {args.steps} calls = {launch_us:.3f} us/call ({variant})")
 
     if args.calibrate_copy:
         # A plain device copy of the packed weight (rocclr's copyBuffer kernel):
@@ -623,12 +653,13 @@ def main() -> int:
         "dtype": "int8 weights x f32 vector, f32 accumulate",
         "data": "synthetic (seeded numpy PCG64: W~N(0,0.02) quantized+packed on GPU, x~N(0,1))",
         "config": {"workload": "matvecQ8 Llama-7B MLP up N=11008 K=4096 M=1 (BASELINE configs[1])",
-                   "N": N, "K": K, "M": M, "weight_copies_rotated": copies,
+                   "N": N, "K": K, "M": M, "variant": variant, "weight_copies_rotated": copies,
                    "rotated_bytes": row_bytes * copies, "bytes_per_call": bytes_per_call},
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
-            "kernel_us_mean": round(kern_us, 3),
+            "traffic_source": TRAFFIC_NOTE,
+            "launch_us_events": round(launch_us, 3),
         },
         "cpu_baseline": baseline,
     }

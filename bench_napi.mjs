@@ -14,9 +14,9 @@
 //     matvecQ8Ffn, matvecQ8Residual for down, with one synchronisation per step.
 // Prints one JSON line: {"node": ..., "results": [...]}.
 //
-//   node web-xpu-ops_amd/harness/napi_timing.mjs [calls]
-import { createResidentQ8Device } from "./resident.js";
-import { matvecQ8 } from "../ops/matvec/index.js";
+//   node bench_napi.mjs [calls]
+import { createResidentQ8Device } from "./web-xpu-ops_amd/harness/resident.js";
+import { matvecQ8 } from "./web-xpu-ops_amd/ops/matvec/index.js";
 
 const N = 11008, K = 4096, W = Math.ceil(K / 4), COPIES = 12;
 

@@ -92,9 +92,18 @@ typedef struct wxo_event_opaque* wxo_event_t;   /* hipEvent_t */
 int wxo_abi_version(void);
 /* Message for the last failing call on this thread ("" if none). */
 const char* wxo_last_error(void);
+/* The kernel instance the calling thread's last successful op launched, e.g.
+ * "matvec_q8_m1 xreg waves=4 rows=16 slots=1 vectors=1 grid=688x1" ("" before
+ * any op; "none empty" when the op had nothing to do).  The reference resolves
+ * its kernel variant explicitly and says which it picked (harness/resolve.ts:211
+ * resolve(), harness/target.ts:74-93 detectTarget()); here the choice is made per
+ * call from the shape, and this reports it.  Thread-local; valid until the
+ * thread's next call. */
+const char* wxo_last_variant(void);
 /* Initialises the HIP runtime on the current device and checks it is gfx950. */
 int wxo_init(void);
-/* One line: device name, arch, CU count, HBM size, library build, kernels. */
+/* One line: device name, arch, CU count, HBM size, library build, kernels, and
+ * the calling thread's last variant (last="..."). */
 const char* wxo_describe(void);
 int wxo_device_count(int* count);
 int wxo_set_device(int ordinal);
@@ -110,6 +119,13 @@ int wxo_stream_create(wxo_stream_t* stream);
 int wxo_stream_destroy(wxo_stream_t stream);
 int wxo_stream_synchronize(wxo_stream_t stream);
 int wxo_event_create(wxo_event_t* event);
+/* An event for timing only: recording it performs no system-scope memory
+ * fence (no cache write-back or invalidation around the timed work, which
+ * otherwise lands inside a short timed interval).  Synchronising on it still
+ * waits for the work before it; it does not make device writes visible to the
+ * host (copies do that).  The reference times with GPU timestamp queries
+ * inside its passes (harness/wgsl.ts:37-52, harness/resident.ts:75-96). */
+int wxo_event_create_timer(wxo_event_t* event);
 int wxo_event_destroy(wxo_event_t event);
 int wxo_event_record(wxo_event_t event, wxo_stream_t stream);
 int wxo_event_synchronize(wxo_event_t event);

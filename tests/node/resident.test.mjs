@@ -1,0 +1,397 @@
+// The resident device as the reference engine drives it: pipelineFor /
+// bindGroup / createUniformBuffer / upload / {kind:"dispatch"} / {kind:"copy"}
+// / batch(ops, readback, profile) (harness/resident.ts:28-145), with the
+// decode projections built in the call shape of llm/engine-q8-resident.ts
+// (uniformOf :492-497, buildProjection :521-538, buildFfnProjection :553-582,
+// buildResidualProjection :594-612, pipelineFor :1059-1067, lm_head chunks
+// :1220-1230) and run as the decode step's dispatch list (:1840-1881).  The
+// engine's other kernels (rmsnorm, rope, attention) are not part of this
+// build; device copies stand in for them so the data stays on the device.
+// Every op's output is checked against the ECMAScript oracle on the inputs
+// the op saw (read back from the device).
+import { test, gpuTest, assert, assertMatvecAgrees, assertResidualAgrees, assertFfnAgrees } from "./harness.mjs";
+import { Q8, Q8_FFN, Q8_RESIDUAL, MATMUL_Q8, RMSNORM_LIKE, kernel } from "./wgsl_interfaces.mjs";
+import { createResidentQ8Device, params, UnsupportedPipelineError } from "../../web-xpu-ops_amd/harness/resident.js";
+import { recognise, parseBindings } from "../../web-xpu-ops_amd/harness/wgsl-interface.js";
+import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
+import * as oracle from "../../oracle/q8_oracle.mjs";
+
+const F = "resident.test.mjs";
+
+// ------------------------------------------------------------------ no GPU needed
+
+test(F, "pipelineFor's WGSL recognition: the four interfaces, by binding declarations", () => {
+  assert.strictEqual(recognise(Q8).op, "matvecQ8");
+  assert.strictEqual(recognise(Q8_FFN).op, "matvecQ8Ffn");
+  assert.strictEqual(recognise(Q8_RESIDUAL).op, "matvecQ8Residual");
+  assert.strictEqual(recognise(MATMUL_Q8).op, "matmulQ8");
+  assert.deepStrictEqual(parseBindings(Q8).map((b) => b.name), ["weight", "scale", "vector", "output", "params"]);
+});
+
+test(F, "pipelineFor's WGSL recognition refuses other kernels and near misses with a named error", () => {
+  const refuses = (code, entry) => assert.throws(() => recognise(code, entry),
+    (e) => e instanceof UnsupportedPipelineError && e.name === "UnsupportedPipelineError");
+  refuses(RMSNORM_LIKE);
+  refuses(Q8, "q8");  // no such entry point
+  // bindings in another order, an output declared read-only, f32 weights, a
+  // uniform with other fields: each is a different kernel
+  refuses(Q8.replace("binding(0) var<storage, read> weight", "binding(0) var<storage, read> scale_x")
+    .replace("binding(1) var<storage, read> scale", "binding(1) var<storage, read> weight"));
+  refuses(Q8.replace("var<storage, read_write> output", "var<storage, read> output"));
+  refuses(Q8.replace("weight: array<u32>", "weight: array<f32>"));
+  refuses(Q8.replace("  K: u32,", "  K: f32,"));
+  refuses(Q8.replace("@compute @workgroup_size(256)", "@workgroup_size(256)"));
+  // a binding only inside a comment does not count
+  refuses(Q8.replace("@group(0) @binding(4) var<uniform> params: Params;", "// @group(0) @binding(4) var<uniform> params: Params;"));
+  assert.throws(() => recognise(42), TypeError);
+});
+
+test(F, "params(): the reference's uniform layout (4 bytes per field, little-endian, at least 16)", () => {
+  const b = params([["u32", 11008], ["u32", 4096]]);
+  assert.strictEqual(b.byteLength, 16);
+  const v = new DataView(b);
+  assert.strictEqual(v.getUint32(0, true), 11008);
+  assert.strictEqual(v.getUint32(4, true), 4096);
+  const c = params([["u32", 1], ["i32", -2], ["f32", 0.5], ["u32", 7], ["u32", 9]]);
+  assert.strictEqual(c.byteLength, 20);
+  assert.strictEqual(new DataView(c).getInt32(4, true), -2);
+  assert.strictEqual(new DataView(c).getFloat32(8, true), 0.5);
+});
+
+// ------------------------------------------------------------------ GPU
+
+function rng(seed) {
+  let s = BigInt.asUintN(64, BigInt(seed) * 0x9E3779B97F4A7C15n + 1n);
+  return () => {
+    s = BigInt.asUintN(64, s + 0x9E3779B97F4A7C15n);
+    let z = s;
+    z = BigInt.asUintN(64, (z ^ (z >> 30n)) * 0xBF58476D1CE4E5B9n);
+    z = BigInt.asUintN(64, (z ^ (z >> 27n)) * 0x94D049BB133111EBn);
+    z ^= z >> 31n;
+    return Number(z >> 11n) / 2 ** 53;
+  };
+}
+
+/** A QuantizedLinear ({ codes: Int8Array [N*K], scale: Float32Array [N] }) with full-range codes. */
+function linear(N, K, seed, scaleMag = 0.01) {
+  const r = rng(seed);
+  const codes = new Int8Array(N * K);
+  for (let i = 0; i < codes.length; i += 1) codes[i] = Math.floor(r() * 256) - 128;
+  const scale = Float32Array.from({ length: N }, () => Math.fround(scaleMag * (0.5 + r())));
+  return { codes, scale };
+}
+
+function vec(n, seed) {
+  const r = rng(seed);
+  return Float32Array.from({ length: n }, () => Math.fround(2 * r() - 1));
+}
+
+// llm/engine-q8-resident.ts:492-497
+function uniformOf(device, fields) {
+  const data = params(fields);
+  const buffer = device.createUniformBuffer(data.byteLength);
+  device.upload(buffer, 0, new Uint8Array(data));
+  return buffer;
+}
+
+// :521-538
+async function buildProjection(device, pipeline, lin, N, K, uniform, vectorBuf, outBuf) {
+  const packed = packInt8Rows(lin.codes, N, K);
+  const weightBuf = device.createStorageBuffer(packed.byteLength);
+  device.upload(weightBuf, 0, packed);
+  const scaleBuf = device.createStorageBuffer(lin.scale.byteLength);
+  device.upload(scaleBuf, 0, lin.scale);
+  const bindGroup = await device.bindGroup(pipeline, [weightBuf, scaleBuf, vectorBuf, outBuf, uniform]);
+  return { bindGroup, weight: { weightBuf, scaleBuf }, packed };
+}
+
+// :553-582
+async function buildFfnProjection(device, pipeline, gate, up, N, K, uniform, vectorBuf, outBuf) {
+  const packedGate = packInt8Rows(gate.codes, N, K);
+  const weightGateBuf = device.createStorageBuffer(packedGate.byteLength);
+  device.upload(weightGateBuf, 0, packedGate);
+  const scaleGateBuf = device.createStorageBuffer(gate.scale.byteLength);
+  device.upload(scaleGateBuf, 0, gate.scale);
+  const packedUp = packInt8Rows(up.codes, N, K);
+  const weightUpBuf = device.createStorageBuffer(packedUp.byteLength);
+  device.upload(weightUpBuf, 0, packedUp);
+  const scaleUpBuf = device.createStorageBuffer(up.scale.byteLength);
+  device.upload(scaleUpBuf, 0, up.scale);
+  const bindGroup = await device.bindGroup(pipeline, [weightGateBuf, scaleGateBuf, weightUpBuf, scaleUpBuf, vectorBuf, outBuf, uniform]);
+  return { bindGroup, packedGate, packedUp };
+}
+
+// :594-612
+async function buildResidualProjection(device, pipeline, lin, N, K, uniform, vectorBuf, residualBuf, outBuf) {
+  const packed = packInt8Rows(lin.codes, N, K);
+  const weightBuf = device.createStorageBuffer(packed.byteLength);
+  device.upload(weightBuf, 0, packed);
+  const scaleBuf = device.createStorageBuffer(lin.scale.byteLength);
+  device.upload(scaleBuf, 0, lin.scale);
+  const bindGroup = await device.bindGroup(pipeline, [weightBuf, scaleBuf, vectorBuf, residualBuf, outBuf, uniform]);
+  return { bindGroup, packed };
+}
+
+// A two-layer decoder of ragged sizes (rows of 2 chunks, one partial) with a
+// two-chunk lm_head; every layer has its own activation buffers so each op's
+// inputs can be read back after the batch.
+const CFG = { numLayers: 2, hiddenSize: 1152, qDim: 1152, kvDim: 384, ffnHidden: 3072, vocabSize: 5000, chunk: 3000 };
+
+async function buildEngine(device) {
+  const { numLayers, hiddenSize, qDim, kvDim, ffnHidden, vocabSize, chunk } = CFG;
+  // :1059-1067 (the decode projections' three pipelines)
+  const [matvecPipeline, matvecFfnPipeline, matvecResidualPipeline] = await Promise.all([
+    device.pipelineFor(Q8), device.pipelineFor(Q8_FFN), device.pipelineFor(Q8_RESIDUAL)]);
+  const qUniform = uniformOf(device, [["u32", qDim], ["u32", hiddenSize]]);
+  const kvUniform = uniformOf(device, [["u32", kvDim], ["u32", hiddenSize]]);
+  const oUniform = uniformOf(device, [["u32", hiddenSize], ["u32", qDim]]);
+  const gateUniform = uniformOf(device, [["u32", ffnHidden], ["u32", hiddenSize]]);
+  const downUniform = uniformOf(device, [["u32", hiddenSize], ["u32", ffnHidden]]);
+  const buf = (floats) => device.createStorageBuffer(floats * 4);
+  const hidden = [buf(hiddenSize)];
+  const layers = [];
+  for (let l = 0; l < numLayers; l += 1) {
+    const w = {
+      wq: linear(qDim, hiddenSize, 100 * l + 1), wk: linear(kvDim, hiddenSize, 100 * l + 2),
+      wv: linear(kvDim, hiddenSize, 100 * l + 3), wo: linear(hiddenSize, qDim, 100 * l + 4),
+      gate: linear(ffnHidden, hiddenSize, 100 * l + 5), up: linear(ffnHidden, hiddenSize, 100 * l + 6),
+      down: linear(hiddenSize, ffnHidden, 100 * l + 7, 0.002),
+    };
+    const b = { normed: buf(hiddenSize), q: buf(qDim), k: buf(kvDim), v: buf(kvDim), attnOut: buf(qDim),
+      hiddenB: buf(hiddenSize), normed2: buf(hiddenSize), gated: buf(ffnHidden) };
+    hidden.push(buf(hiddenSize));
+    const wq = await buildProjection(device, matvecPipeline, w.wq, qDim, hiddenSize, qUniform, b.normed, b.q);
+    const wk = await buildProjection(device, matvecPipeline, w.wk, kvDim, hiddenSize, kvUniform, b.normed, b.k);
+    const wv = await buildProjection(device, matvecPipeline, w.wv, kvDim, hiddenSize, kvUniform, b.normed, b.v);
+    const wo = await buildResidualProjection(device, matvecResidualPipeline, w.wo, hiddenSize, qDim, oUniform,
+      b.attnOut, hidden[l], b.hiddenB);
+    const ffn = await buildFfnProjection(device, matvecFfnPipeline, w.gate, w.up, ffnHidden, hiddenSize, gateUniform,
+      b.normed2, b.gated);
+    const down = await buildResidualProjection(device, matvecResidualPipeline, w.down, hiddenSize, ffnHidden,
+      downUniform, b.gated, b.hiddenB, hidden[l + 1]);
+    layers.push({ w, b, wq, wk, wv, wo, ffn, down });
+  }
+  const finalNormedBuf = buf(hiddenSize);
+  const lmHead = linear(vocabSize, hiddenSize, 999);
+  const lmHeadChunks = [];
+  // :1220-1230
+  for (let rowStart = 0; rowStart < vocabSize; rowStart += chunk) {
+    const rowCount = Math.min(chunk, vocabSize - rowStart);
+    const chunkUniform = uniformOf(device, [["u32", rowCount], ["u32", hiddenSize]]);
+    const outBuf = device.createStorageBuffer(rowCount * 4);
+    const staging = device.createStorageBuffer(rowCount * 4, GPUBufferUsage.COPY_DST | GPUBufferUsage.MAP_READ);
+    const slice = { codes: lmHead.codes.subarray(rowStart * hiddenSize, (rowStart + rowCount) * hiddenSize),
+      scale: lmHead.scale.subarray(rowStart, rowStart + rowCount) };
+    const { bindGroup: group, packed } = await buildProjection(device, matvecPipeline, slice, rowCount, hiddenSize,
+      chunkUniform, finalNormedBuf, outBuf);
+    lmHeadChunks.push({ rowCount, group, outBuf, staging, packed, scale: slice.scale });
+  }
+  return { matvecPipeline, matvecFfnPipeline, matvecResidualPipeline, hidden, layers, finalNormedBuf, lmHeadChunks };
+}
+
+/** The decode step's op list (:1840-1881) with device copies standing in for rmsnorm / rope / attention. */
+function decodeOps(e, labels) {
+  const { qDim, kvDim, hiddenSize, ffnHidden } = CFG;
+  const ops = [];
+  const dispatch = (pipeline, bindGroup, workgroups, label) => {
+    ops.push({ kind: "dispatch", pipeline, bindGroup, workgroups });
+    if (labels) labels.push(label);
+  };
+  const copy = (src, dst, floats) => {
+    ops.push({ kind: "copy", src, srcOffset: 0, dst, dstOffset: 0, size: floats * 4 });
+    if (labels) labels.push(null);
+  };
+  e.layers.forEach((L, l) => {
+    copy(e.hidden[l], L.b.normed, hiddenSize);  // stands in for rmsnorm_attn
+    dispatch(e.matvecPipeline, L.wq.bindGroup, [qDim], `L${l}:matvecQ8_wq`);
+    dispatch(e.matvecPipeline, L.wk.bindGroup, [kvDim], `L${l}:matvecQ8_wk`);
+    dispatch(e.matvecPipeline, L.wv.bindGroup, [kvDim], `L${l}:matvecQ8_wv`);
+    copy(L.b.q, L.b.attnOut, qDim);  // stands in for rope + attention
+    dispatch(e.matvecResidualPipeline, L.wo.bindGroup, [hiddenSize], `L${l}:matvecQ8Residual_wo`);
+    copy(L.b.hiddenB, L.b.normed2, hiddenSize);  // stands in for rmsnorm_ffn
+    dispatch(e.matvecFfnPipeline, L.ffn.bindGroup, [ffnHidden], `L${l}:matvecQ8Ffn`);
+    dispatch(e.matvecResidualPipeline, L.down.bindGroup, [hiddenSize], `L${l}:matvecQ8Residual_down`);
+  });
+  copy(e.hidden[e.layers.length], e.finalNormedBuf, hiddenSize);  // stands in for final_norm
+  e.lmHeadChunks.forEach((chunk, i) => dispatch(e.matvecPipeline, chunk.group, [chunk.rowCount], `lm_head_chunk${i}`));
+  return ops;
+}
+
+/** Reads back every activation, then checks each op against the oracle on the inputs it saw. */
+async function checkStep(device, e, logits, what) {
+  const { qDim, kvDim, hiddenSize, ffnHidden } = CFG;
+  const rb = [];
+  const want = (buffer, length) => { rb.push({ source: buffer, sourceOffset: 0, length, type: "f32" }); return rb.length - 1; };
+  const idx = e.layers.map((L, l) => ({
+    hA: want(e.hidden[l], hiddenSize), normed: want(L.b.normed, hiddenSize), q: want(L.b.q, qDim),
+    k: want(L.b.k, kvDim), v: want(L.b.v, kvDim), attnOut: want(L.b.attnOut, qDim), hB: want(L.b.hiddenB, hiddenSize),
+    normed2: want(L.b.normed2, hiddenSize), gated: want(L.b.gated, ffnHidden), out: want(e.hidden[l + 1], hiddenSize),
+  }));
+  const fin = want(e.finalNormedBuf, hiddenSize);
+  const got = await device.batch([], rb);
+  e.layers.forEach((L, l) => {
+    const g = (k) => got[idx[l][k]];
+    const mv = (lin, packed, N, K, vector) => ({ weight: packed, scale: lin.scale, vector, N, K });
+    const aq = mv(L.w.wq, L.wq.packed, qDim, hiddenSize, g("normed"));
+    assertMatvecAgrees(g("q"), oracle.matvecQ8(aq), aq, `${what} L${l} wq`);
+    const ak = mv(L.w.wk, L.wk.packed, kvDim, hiddenSize, g("normed"));
+    assertMatvecAgrees(g("k"), oracle.matvecQ8(ak), ak, `${what} L${l} wk`);
+    const av = mv(L.w.wv, L.wv.packed, kvDim, hiddenSize, g("normed"));
+    assertMatvecAgrees(g("v"), oracle.matvecQ8(av), av, `${what} L${l} wv`);
+    const ao = mv(L.w.wo, L.wo.packed, hiddenSize, qDim, g("attnOut"));
+    assertResidualAgrees(g("hB"), oracle.matvecQ8Residual({ ...ao, residual: g("hA") }), ao, `${what} L${l} wo residual`);
+    const agate = mv(L.w.gate, L.ffn.packedGate, ffnHidden, hiddenSize, g("normed2"));
+    const aup = mv(L.w.up, L.ffn.packedUp, ffnHidden, hiddenSize, g("normed2"));
+    assertFfnAgrees(g("gated"), oracle.matvecQ8(agate), oracle.matvecQ8(aup), oracle.silu, agate, aup, `${what} L${l} ffn`);
+    const ad = mv(L.w.down, L.down.packed, hiddenSize, ffnHidden, g("gated"));
+    assertResidualAgrees(g("out"), oracle.matvecQ8Residual({ ...ad, residual: g("hB") }), ad, `${what} L${l} down residual`);
+  });
+  e.lmHeadChunks.forEach((c, i) => {
+    const a = { weight: c.packed, scale: c.scale, vector: got[fin], N: c.rowCount, K: hiddenSize };
+    assertMatvecAgrees(logits[i], oracle.matvecQ8(a), a, `${what} lm_head chunk ${i}`);
+  });
+}
+
+gpuTest(F, "engine-shaped decode: pipelineFor / bindGroup / uniforms / dispatch + copy ops, per-op parity, no allocation in the loop", async () => {
+  const device = await createResidentQ8Device();
+  assert.ok(device);
+  const e = await buildEngine(device);
+  assert.strictEqual(device.stats.pipelinesCreated, 3);
+  const buffers = device.stats.buffersCreated, pipelines = device.stats.pipelinesCreated;
+  for (let step = 0; step < 3; step += 1) {
+    device.upload(e.hidden[0], 0, vec(CFG.hiddenSize, 7000 + step));  // the token's embedding row
+    const submits = device.stats.submits, launches = device.stats.launches;
+    const ops = decodeOps(e);
+    const logits = await device.batch(ops, e.lmHeadChunks.map((c) => ({
+      staging: c.staging, source: c.outBuf, sourceOffset: 0, length: c.rowCount, type: "f32" })));
+    assert.strictEqual(device.stats.submits, submits + 1);
+    // wq/wk/wv share their vector (one launch per layer), as do the lm_head chunks
+    assert.strictEqual(device.stats.launches - launches, ops.length - 2 * CFG.numLayers - (e.lmHeadChunks.length - 1));
+    assert.deepStrictEqual(logits.map((r) => r.length), e.lmHeadChunks.map((c) => c.rowCount));
+    await checkStep(device, e, logits, `step ${step}`);
+    // pipelines are created once; repeated pipelineFor returns the cached one
+    assert.strictEqual(await device.pipelineFor(Q8), e.matvecPipeline);
+  }
+  assert.strictEqual(device.stats.buffersCreated, buffers);
+  assert.strictEqual(device.stats.pipelinesCreated, pipelines);
+  device.destroy();
+});
+
+gpuTest(F, "BatchProfile: per-dispatch GPU times for labelled ops, submitToDoneMs and readbackMs; same results", async () => {
+  const device = await createResidentQ8Device();
+  const e = await buildEngine(device);
+  device.upload(e.hidden[0], 0, vec(CFG.hiddenSize, 42));
+  const rb = e.lmHeadChunks.map((c) => ({ source: c.outBuf, sourceOffset: 0, length: c.rowCount, type: "f32" }));
+  const plain = await device.batch(decodeOps(e), rb);
+  const labels = [];
+  const ops = decodeOps(e, labels);
+  const sink = { submitToDoneMs: null, readbackMs: null, gpuEntries: [] };
+  const launches = device.stats.launches;
+  const profiled = await device.batch(ops, rb, { labels, sink });
+  assert.strictEqual(device.timestampsSupported, true);
+  assert.ok(sink.submitToDoneMs >= 0 && sink.readbackMs >= 0);
+  const named = labels.filter((x) => x != null);
+  assert.deepStrictEqual(sink.gpuEntries.map((x) => x.label), named);
+  for (const x of sink.gpuEntries) assert.ok(x.seconds > 0 && x.seconds < 0.1, `${x.label}: ${x.seconds}`);
+  // a profiled batch runs every op on its own
+  assert.strictEqual(device.stats.launches - launches, ops.length);
+  profiled.forEach((r, i) => assert.deepStrictEqual(Array.from(r), Array.from(plain[i]), `chunk ${i}`));
+  // a profile without labels reports the CPU-side times only
+  const sink2 = { submitToDoneMs: null, readbackMs: null, gpuEntries: [] };
+  await device.batch(decodeOps(e), rb, { sink: sink2 });
+  assert.ok(sink2.submitToDoneMs >= 0 && sink2.readbackMs >= 0 && sink2.gpuEntries.length === 0);
+  device.destroy();
+});
+
+gpuTest(F, "validation: bad pipelines, bind groups, dispatches and buffers throw before anything runs", async () => {
+  const device = await createResidentQ8Device();
+  await assert.rejects(device.pipelineFor(RMSNORM_LIKE), (err) => err.name === "UnsupportedPipelineError");
+  const pipes = [];
+  for (const code of [Q8, Q8_RESIDUAL]) pipes.push(await device.pipelineFor(code));
+  const [p, pr] = pipes;
+  assert.strictEqual(await device.pipelineFor(Q8, "main"), p);
+  const N = 40, K = 100;
+  const lin = linear(N, K, 5);
+  const packed = packInt8Rows(lin.codes, N, K);
+  const w = device.createStorageBuffer(packed.byteLength);
+  device.upload(w, 0, packed);
+  const s = device.createStorageBuffer(N * 4);
+  device.upload(s, 0, lin.scale);
+  const x = device.createStorageBuffer(K * 4);
+  const x0 = vec(K, 9);
+  device.upload(x, 0, x0);
+  const y = device.createStorageBuffer(N * 4);
+  const u = device.createUniformBuffer(8);
+  device.upload(u, 0, new Uint8Array(params([["u32", N], ["u32", K]])));
+  await assert.rejects(device.bindGroup(p, [w, s, x, y]), /binds 5 buffers/);
+  await assert.rejects(device.bindGroup(p, [w, s, x, y, x]), /needs a uniform buffer/);
+  await assert.rejects(device.bindGroup(p, [w, s, u, y, u]), /needs a storage buffer/);
+  await assert.rejects(device.bindGroup(p, [w, s, x, x, u]), /aliases its vector/);
+  await assert.rejects(device.bindGroup({ op: "matvecQ8" }, [w, s, x, y, u]), TypeError);
+  const group = await device.bindGroup(p, [w, s, x, y, u]);
+  // the residual stream in place is allowed (output over residual)
+  await device.bindGroup(pr, [w, s, x, y, y, u]);
+  const sentinel = new Float32Array(N).fill(-7);
+  device.upload(y, 0, sentinel);
+  const before = device.stats.launches;
+  // the second op reads past the weight: refused before the first one runs
+  await assert.rejects(device.batch([
+    { kind: "dispatch", pipeline: p, bindGroup: group, workgroups: [N] },
+    { kind: "dispatch", pipeline: p, bindGroup: group, workgroups: [N + 1] }]), RangeError);
+  await assert.rejects(device.batch([{ kind: "dispatch", pipeline: pr, bindGroup: group, workgroups: [N] }]),
+    /bind group was made for the matvecQ8 pipeline/);
+  await assert.rejects(device.batch([{ kind: "dispatch", pipeline: p, bindGroup: group, workgroups: [1.5] }]), TypeError);
+  await assert.rejects(device.batch([{ kind: "copy", src: x, srcOffset: 0, dst: u, dstOffset: 0, size: 16 }]), TypeError);
+  await assert.rejects(device.batch([{ kind: "copy", src: x, srcOffset: 2, dst: y, dstOffset: 0, size: 16 }]), RangeError);
+  await assert.rejects(device.batch([], [{ source: u, sourceOffset: 0, length: 2, type: "f32" }]), TypeError);
+  assert.strictEqual(device.stats.launches, before);
+  const [still] = await device.batch([], [{ source: y, sourceOffset: 0, length: N, type: "f32" }]);
+  assert.deepStrictEqual(Array.from(still), Array.from(sentinel));
+  // a dispatch of fewer workgroups than rows computes that many rows, as the WGSL kernel does
+  const [part] = await device.batch([{ kind: "dispatch", pipeline: p, bindGroup: group, workgroups: [N - 8] }],
+    [{ source: y, sourceOffset: 0, length: N, type: "f32" }]);
+  const a = { weight: packed, scale: lin.scale, vector: x0, N: N - 8, K };
+  assertMatvecAgrees(part.subarray(0, N - 8), oracle.matvecQ8(a), a, "partial dispatch");
+  assert.deepStrictEqual(Array.from(part.subarray(N - 8)), Array.from(sentinel.subarray(N - 8)));
+  device.destroy();
+});
+
+gpuTest(F, "matmulQ8 dispatch (prefill) through the resident device, against the oracle", async () => {
+  const device = await createResidentQ8Device();
+  const pipeline = await device.pipelineFor(MATMUL_Q8);
+  const N = 48, M = 200, K = 1030;  // tokens, weight rows, columns
+  const lin = linear(M, K, 77);
+  const packed = packInt8Rows(lin.codes, M, K);
+  const a = vec(N * K, 78);
+  const aBuf = device.createStorageBuffer(a.byteLength);
+  device.upload(aBuf, 0, a);
+  const w = device.createStorageBuffer(packed.byteLength);
+  device.upload(w, 0, packed);
+  const s = device.createStorageBuffer(M * 4);
+  device.upload(s, 0, lin.scale);
+  const out = device.createStorageBuffer(N * M * 4);
+  const u = device.createUniformBuffer(12);
+  device.upload(u, 0, new Uint8Array(params([["u32", N], ["u32", M], ["u32", K]])));
+  const group = await device.bindGroup(pipeline, [aBuf, w, s, out, u]);
+  await assert.rejects(device.batch([{ kind: "dispatch", pipeline, bindGroup: group, workgroups: [Math.ceil(M / 16) - 1, Math.ceil(N / 16)] }]),
+    /covers part of/);
+  const [got] = await device.batch([{ kind: "dispatch", pipeline, bindGroup: group, workgroups: [Math.ceil(M / 16), Math.ceil(N / 16)] }],
+    [{ source: out, sourceOffset: 0, length: N * M, type: "f32" }]);
+  const want = oracle.matmulQ8({ a, weight: packed, scale: lin.scale, N, M, K });
+  // matmulQ8 bar: 1e-5 * sum_k |a * fround(q * s)| + 1e-7 per element
+  const W = Math.ceil(K / 4);
+  for (let n = 0; n < N; n += 1) {
+    for (let m = 0; m < M; m += 1) {
+      let bound = 0;
+      for (let k = 0; k < K; k += 1) {
+        const byte = (packed[m * W + (k >> 2)] >>> ((k & 3) * 8)) & 0xff;
+        bound += Math.abs(a[n * K + k] * Math.fround((byte >= 128 ? byte - 256 : byte) * lin.scale[m]));
+      }
+      const err = Math.abs(got[n * M + m] - want[n * M + m]);
+      if (!(err <= 1e-5 * bound + 1e-7)) assert.fail(`[${n}, ${m}] got ${got[n * M + m]} want ${want[n * M + m]}`);
+    }
+  }
+  device.destroy();
+});
+
+void kernel;

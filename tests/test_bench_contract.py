@@ -60,5 +60,29 @@ def test_json_line_contract():
     assert abs(rl["frac"] - rl["achieved"] / rl["peak"]) < 1e-3
     assert 0.3 < rl["frac"] < 1.0
     assert rl["traffic"] is None or rl["traffic"] >= r["config"]["bytes_per_call"] * 0.99
+    assert abs(rl["launch_us_events"] - r["ms_per_step"] * 1e3) < 1e-2
+    assert "profiles/" in rl["traffic_source"]
+    # the kernel instance that ran is named
+    assert r["config"]["variant"].startswith("matvec_q8_m1 ") and "waves=4" in r["config"]["variant"]
     cb = r["cpu_baseline"]
     assert cb is not None and cb["kind"] in ("port", "reference") and cb["cores"] >= 1 and cb["value"] > 0
+
+
+@pytest.mark.gpu
+def test_short_and_long_runs_agree():
+    """The driver's short run (20 steps after 5 warmups) and a 2000-step run
+    measure the same per-call time: no first touches, no host launch latency
+    and no event fences inside the timed region.  Each bench process places
+    its buffers anew, which moves a run by up to about 1 %, so the medians of
+    three runs of each length are compared."""
+    res = {}
+    for steps, warmup in ((20, 5), (2000, 200)):
+        runs = []
+        for _ in range(3):
+            print(f"bench.py --steps {steps} --warmup {warmup} --no-cpu-baseline", flush=True)
+            p = run_bench("--steps", str(steps), "--warmup", str(warmup), "--no-cpu-baseline")
+            assert p.returncode == 0, p.stderr[-2000:]
+            runs.append(json.loads(p.stdout.strip().splitlines()[-1])["ms_per_step"])
+            print(f"  ms_per_step {runs[-1]}", flush=True)
+        res[steps] = sorted(runs)[1]
+    assert abs(res[20] - res[2000]) <= 0.01 * res[2000], res

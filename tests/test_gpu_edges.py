@@ -1,0 +1,230 @@
+"""Edges the other GPU suites do not reach, through the C ABI:
+
+  * quantize / quantize+pack into device buffers with sentinel tails after the
+    codes, the packed words and the scales (the kernels store a row's last
+    partial word as a full 16-byte store clamped by the row's buffer
+    resource: a store past the row or the buffer would change a sentinel);
+  * rows whose absmax is normal but tiny (the f32 fast path's inverse stays
+    finite) with subnormal elements, so the fast path meets subnormal operands;
+  * the batched LM head (cfg5) checked against the oracle on every row;
+  * which kernel instance ran (wxo_last_variant), per thread.
+
+Bars as everywhere: codes, packed words and scales bit-exact;
+matvecQ8 |y - y_ref| <= 1e-5 * sum_k |s q x| + 1e-7 per row.
+"""
+import threading
+
+import numpy as np
+import pytest
+
+import oracle
+import wxo_q8
+import wxo_workloads as wl
+from test_gpu_parity import assert_bits_equal, assert_matvec
+
+pytestmark = pytest.mark.gpu
+
+SENT_I32 = np.int32(0x5A5A5A5A)
+SENT_U32 = np.uint32(0xA5A5A5A5)
+SENT_F32 = np.float32(-12345.5)
+TAIL = 80  # elements of slack after each output
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    wxo_q8.init()
+
+
+def edge_matrix(rng, N, D):
+    x = (rng.standard_normal((N, D)) * 0.02).astype(np.float32)
+    x[1 % N, D - 1] = 3.0  # absmax in the row's last element (the partial word)
+    if N > 2:
+        x[2, :] = 0.0
+    if N > 3:
+        x[3, D // 2] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("D", [5, 1027, 4099])
+def test_quantize_and_pack_device_sentinel_tails(D):
+    rng = np.random.default_rng(D)
+    N = 7
+    W = (D + 3) // 4
+    x = edge_matrix(rng, N, D)
+    want_codes, want_scales = oracle.quantize(x, N, D)
+    want_packed = oracle.pack_q8(want_codes, N, D)
+    # input followed by huge values: reading past the last row would change its scale
+    src = wxo_q8.DeviceBuffer.from_array(np.concatenate([x.reshape(-1), np.full(TAIL, 1e30, np.float32)]))
+    codes = wxo_q8.DeviceBuffer.from_array(np.full(N * D + TAIL, SENT_I32, np.int32))
+    scales = wxo_q8.DeviceBuffer.from_array(np.full(N + TAIL, SENT_F32, np.float32))
+    packed = wxo_q8.DeviceBuffer.from_array(np.full(N * W + TAIL, SENT_U32, np.uint32))
+    scales2 = wxo_q8.DeviceBuffer.from_array(np.full(N + TAIL, SENT_F32, np.float32))
+    print(f"quantize D={D}: {wxo_q8.last_variant()}", flush=True)
+    wxo_q8.quantize_device(src, N, D, codes, scales)
+    print(f"  {wxo_q8.last_variant()}", flush=True)
+    wxo_q8.quantize_pack_q8_device(src, N, D, packed, scales2)
+    print(f"  {wxo_q8.last_variant()}", flush=True)
+    wxo_q8.synchronize()
+    c = codes.download(np.int32, N * D + TAIL)
+    s = scales.download(np.float32, N + TAIL)
+    p = packed.download(np.uint32, N * W + TAIL)
+    s2 = scales2.download(np.float32, N + TAIL)
+    assert_bits_equal(c[:N * D], want_codes, f"codes D={D}")
+    assert_bits_equal(s[:N], want_scales, f"scales D={D}")
+    assert_bits_equal(p[:N * W], want_packed, f"packed D={D}")
+    assert_bits_equal(s2[:N], want_scales, f"fused scales D={D}")
+    assert np.all(c[N * D:] == SENT_I32), "codes: wrote past the output"
+    assert np.all(s[N:].view(np.uint32) == SENT_F32.view(np.uint32)), "scales: wrote past the output"
+    assert np.all(p[N * W:] == SENT_U32), "packed: wrote past the output"
+    assert np.all(s2[N:].view(np.uint32) == SENT_F32.view(np.uint32)), "fused scales: wrote past the output"
+    for b in (src, codes, scales, packed, scales2):
+        b.free()
+
+
+@pytest.mark.parametrize("D", [5, 1027, 4099])
+def test_quantize_pack_multi_device_sentinel_gaps(D):
+    """Several matrices of one K in one launch, their outputs laid out in one
+    allocation with sentinel gaps between them."""
+    rng = np.random.default_rng(100 + D)
+    W = (D + 3) // 4
+    Ns = [3, 9, 5]
+    xs = [edge_matrix(rng, n, D) for n in Ns]
+    gap = 32
+    words = sum(n * W + gap for n in Ns)
+    pk = wxo_q8.DeviceBuffer.from_array(np.full(words, SENT_U32, np.uint32))
+    sc = wxo_q8.DeviceBuffer.from_array(np.full(sum(n + gap for n in Ns), SENT_F32, np.float32))
+    srcs = [wxo_q8.DeviceBuffer.from_array(x) for x in xs]
+    mats, po, so = [], 0, 0
+    offsets = []
+    for n, src in zip(Ns, srcs):
+        mats.append((src.ptr, n, pk.ptr + 4 * po, sc.ptr + 4 * so))
+        offsets.append((po, so))
+        po += n * W + gap
+        so += n + gap
+    wxo_q8.quantize_pack_q8_multi_device(mats, D)
+    print(f"quantize_pack_multi D={D}: {wxo_q8.last_variant()}", flush=True)
+    wxo_q8.synchronize()
+    p = pk.download(np.uint32, words)
+    s = sc.download(np.float32, so)
+    for (n, x), (po, so) in zip(zip(Ns, xs), offsets):
+        wc, ws = oracle.quantize(x, n, D)
+        assert_bits_equal(p[po:po + n * W], oracle.pack_q8(wc, n, D), f"packed n={n}")
+        assert_bits_equal(s[so:so + n], ws, f"scales n={n}")
+        assert np.all(p[po + n * W:po + n * W + gap] == SENT_U32), "packed gap overwritten"
+        assert np.all(s[so + n:so + n + gap].view(np.uint32) == SENT_F32.view(np.uint32)), "scales gap overwritten"
+    for b in (pk, sc, *srcs):
+        b.free()
+
+
+def tiny_absmax_rows(rng, N, D):
+    """Rows with a normal absmax in [4e-37, 1e-35] (127/absmax finite in f32)
+    and subnormal elements: random subnormals, exact multiples of the smallest
+    subnormal, values near absmax * (k + 1/2) / 127 (near-ties) and signs mixed."""
+    x = np.zeros((N, D), np.float32)
+    tiny = np.float32(1.4e-45)
+    for r in range(N):
+        amax = np.float32(np.exp(rng.uniform(np.log(4e-37), np.log(1e-35))))
+        sub = (rng.integers(-(2 ** 23) + 1, 2 ** 23, D).astype(np.float64) * float(tiny)).astype(np.float32)
+        x[r] = sub
+        k = rng.integers(0, 127, D // 4 + 1)
+        near = (amax.astype(np.float64) * (k + 0.5) / 127.0).astype(np.float32)
+        near = np.where(np.abs(near) < np.float32(1.17549435e-38), near, sub[: near.size])
+        x[r, : near.size] = near * np.where(rng.random(near.size) < 0.5, -1, 1).astype(np.float32)
+        x[r, rng.integers(0, D)] = amax * (1 if r % 2 else -1)
+    return x
+
+
+@pytest.mark.parametrize("D", [7, 256, 1031, 4096])
+def test_quantize_fast_path_meets_subnormal_elements(D):
+    rng = np.random.default_rng(7 * D)
+    N = 16
+    x = tiny_absmax_rows(rng, N, D)
+    absmax = np.abs(x).max(axis=1)
+    assert np.all(absmax >= 3.9e-37) and np.all(absmax <= 1e-35)
+    assert np.all(np.isfinite(np.float32(127.0) / absmax))
+    assert np.mean((np.abs(x) < 1.17549435e-38) & (x != 0)) > 0.5, "mostly subnormal elements"
+    want_codes, want_scales = oracle.quantize(x, N, D)
+    assert np.any(want_codes != 0), "the subnormal elements must reach non-zero codes"
+    codes, scales = wxo_q8.quantize(input=x, N=N, D=D)
+    assert_bits_equal(codes, want_codes, f"codes D={D}")
+    assert_bits_equal(scales, want_scales, f"scales D={D}")
+    packed, s2 = wxo_q8.quantizePackQ8(input=x, N=N, K=D)
+    assert_bits_equal(packed, oracle.pack_q8(want_codes, N, D), f"packed D={D}")
+    assert_bits_equal(s2, want_scales, f"fused scales D={D}")
+
+
+@pytest.mark.parametrize("M", [4, 8, 16])
+def test_batched_lm_head_every_row(M):
+    c = wl.make_config("cfg5", M=M)
+    N, K = c["N"], c["K"]
+    codes, scales = oracle.quantize(c["w"], N, K)
+    w = oracle.pack_q8(codes, N, K)
+    xs = c["x"].reshape(M, K)
+    print(f"cfg5 M={M}: every row", flush=True)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=scales, vectors=xs, N=N, K=K, M=M)
+    print(f"  {wxo_q8.last_variant()}", flush=True)
+    for m in range(M):
+        assert_matvec(ys[m], w, scales, xs[m], N, K)
+
+
+def parse_variant(v):
+    head, *rest = v.split(" ")
+    kv = {}
+    form = None
+    for t in rest:
+        if "=" in t:
+            k, val = t.split("=", 1)
+            kv[k] = val
+        else:
+            form = t
+    return head, form, kv
+
+
+@pytest.mark.parametrize("cfg,M", [("cfg1", 1), ("cfg2", 1), ("cfg3", 1), ("cfg5", 16)])
+def test_variant_names_the_instance_that_ran(cfg, M):
+    c = wl.CONFIGS[cfg]
+    N, K = c["N"], c["K"]
+    W = (K + 3) // 4
+    rng = np.random.default_rng(1)
+    w = wxo_q8.DeviceBuffer.from_array(rng.integers(0, 2 ** 32, N * W, dtype=np.uint64).astype(np.uint32))
+    s = wxo_q8.DeviceBuffer.from_array(np.full(N, 0.01, np.float32))
+    x = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(M * K).astype(np.float32))
+    y = wxo_q8.DeviceBuffer(4 * M * N)
+    wxo_q8.matvec_q8_device(w, s, x, y, N, K, M)
+    wxo_q8.synchronize()
+    v = wxo_q8.last_variant()
+    print(f"{cfg} M={M}: {v}", flush=True)
+    head, form, kv = parse_variant(v)
+    grid = [int(t) for t in kv["grid"].split("x")]
+    if M == 1:
+        chunks = (W + 255) // 256
+        assert head == "matvec_q8_m1"
+        assert int(kv["waves"]) == chunks  # one wave per 1 KiB chunk of a row
+        rows = int(kv["rows"])
+        assert grid[0] * rows >= N > (grid[0] - 1) * rows
+        assert form == ("xreg.masked" if W % 256 else "xreg")
+    else:
+        assert head.startswith("matvec_q8_mfma")
+        assert int(kv["vectors"]) == M and grid[1] == 1
+    # describe() carries the same variant
+    assert f'last="{v}"' in wxo_q8.describe()
+    # thread-local: another thread's calls do not change this thread's variant
+    seen = {}
+
+    def other():
+        seen["before"] = wxo_q8.last_variant()
+        wxo_q8.matvec_q8_device(w, s, x, y, 16, 64, 1)
+        seen["after"] = wxo_q8.last_variant()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["before"] == "" and seen["after"].startswith("matvec_q8_m1 ")
+    assert wxo_q8.last_variant() == v
+    # a refused call leaves the last variant as it was
+    with pytest.raises(wxo_q8.WxoError):
+        wxo_q8.matvec_q8_device(w, s, x, y, N, K, 0)
+    assert wxo_q8.last_variant() == v
+    wxo_q8.synchronize()
+    for b in (w, s, x, y):
+        b.free()

@@ -28,6 +28,7 @@ def test_node_suite_cpu():
 
 
 @pytest.mark.gpu
+@pytest.mark.timeout(400)
 @pytest.mark.skipif(NODE is None, reason="node not on PATH")
 def test_node_suite_gpu():
     proc = run("gpu")

@@ -44,12 +44,32 @@ struct M1Params {
 
 enum : int { kEpiPlain = 0, kEpiResidual = 1, kEpiFfn = 2 };
 
-// `variant` (optional) receives a static string naming the kernel chosen.
+// The kernel instance a launcher chose, for callers that report it
+// (wxo_last_variant): the kernel template, the form selected within it and
+// the parameters that pick the instance.  Fields a kernel has no use for
+// stay 0.
+struct Variant {
+    const char* kernel = "";  // kernel template name
+    const char* form = "";    // selected form within it
+    int waves = 0;            // waves per workgroup
+    int rows = 0;             // rows (or weight-tile rows) per workgroup
+    int slots = 0;            // per-lane unit count: chunk slots whose vector slices stay in
+                              // VGPRs (matvec; 0 = streamed), packed words per lane (quantize)
+    int vectors = 0;          // vectors per pass (batched forms)
+    uint32_t grid_x = 0, grid_y = 0;
+};
+
+inline void set_variant(Variant* v, const char* kernel, const char* form, int waves, int rows, int slots,
+                        int vectors, uint32_t grid_x, uint32_t grid_y = 1) {
+    if (v) *v = Variant{kernel, form, waves, rows, slots, vectors, grid_x, grid_y};
+}
+
+// `variant` (optional) receives the kernel instance chosen.
 hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream,
-                            const char** variant);
+                            Variant* variant);
 // matvecQ8Residual (epi = kEpiResidual) or matvecQ8Ffn (kEpiFfn), M = 1.
 hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo& dev, hipStream_t stream,
-                                  const char** variant);
+                                  Variant* variant);
 // Several single-vector projections of one vector x [K]: output_p =
 // matvecQ8(weight_p, scale_p, x, N_p, K), count <= kMaxProjections, in one
 // launch.  Outputs must be disjoint from each other and from x.
@@ -61,13 +81,13 @@ struct Projection {
     uint32_t N;
 };
 hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count, const float* x, uint32_t K,
-                                  const DeviceInfo& dev, hipStream_t stream, const char** variant);
+                                  const DeviceInfo& dev, hipStream_t stream, Variant* variant);
 hipError_t launch_fused_zero(const MatvecArgs& a, int epi, hipStream_t stream);
 hipError_t launch_fill_scaled_zero(const float* scale, float* y, uint32_t N, uint32_t M, hipStream_t stream);
 
 // quantize (codes != nullptr) and/or packQ8 (packed != nullptr) of f32 rows.
 hipError_t launch_quantize_rows(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed,
-                                float* scales, const DeviceInfo& dev, hipStream_t stream, const char** variant);
+                                float* scales, const DeviceInfo& dev, hipStream_t stream, Variant* variant);
 // quantize + packQ8 of several matrices with the same K (count <= 8), one
 // launch for rows of more than 128 words.
 constexpr uint32_t kMaxQuantizeMatrices = 8;
@@ -82,7 +102,7 @@ hipError_t launch_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, ui
 // matmulQ8 (matmul_q8.hip): a f32 [N, K] x packed weight [M, ceil(K/4)] ->
 // out f32 [N, M].  K <= 2^22.
 hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
-                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, const char** variant);
+                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant);
 
 // dequant_q8.hip
 hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K,

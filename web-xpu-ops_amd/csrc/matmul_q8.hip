@@ -451,14 +451,14 @@ hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale,
 }  // namespace
 
 hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
-                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     if (N == 0 || M == 0) return hipSuccess;
     if (K == 0) {
         // matmul over an empty K: every sum is 0 (ops/matmul/reference.ts:17-18)
         const size_t n = (size_t)N * M;
         const uint32_t grid = (uint32_t)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
         hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, stream, out, n);
-        if (variant) *variant = "matmul.zero";
+        set_variant(variant, "fill_zero", "matmul.k0", 4, 0, 0, 0, grid);
         return hipGetLastError();
     }
     // Up to 32 tokens: the batched single-vector path, one token per vector
@@ -470,7 +470,7 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
     if (N <= 32u) {
         MatvecArgs mv{weight, scale, a, out, M, K, N, (uint32_t)(((uint64_t)K + 3) / 4)};
         const hipError_t e = launch_matvec_q8(mv, dev, stream, variant);
-        if (variant) *variant = "matmul.batched_matvec";
+        if (variant) variant->form = "matmul.tokens_as_vectors";
         return e;
     }
     // 128 weight rows per workgroup when that still gives every CU a tile,
@@ -485,11 +485,13 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
     const uint64_t ntiles = (N + kBN - 1u) / kBN;
     const uint64_t t4 = (uint64_t)((M + 127u) / 128u) * ntiles, t2 = (uint64_t)((M + 63u) / 64u) * ntiles;
     if (t4 >= cus) {
-        if (variant) *variant = t4 <= cus ? "matmul.mfma128.ksplit" : "matmul.mfma128";
+        set_variant(variant, "matmul_q8", t4 <= cus ? "FB4.ksplit2" : "FB4", t4 <= cus ? 16 : 8, 128, 0, (int)kBN,
+                    (uint32_t)((t4 + 7u) / 8u * 8u));
         return t4 <= cus ? launch_fb<4, 8, 64, 2, 2>(a, weight, scale, out, N, M, K, stream)
                          : launch_fb<4, 8, 64, 2, 1>(a, weight, scale, out, N, M, K, stream);
     }
-    if (variant) *variant = t2 <= cus ? "matmul.mfma64.ksplit" : "matmul.mfma64";
+    set_variant(variant, "matmul_q8", t2 <= cus ? "FB2.PD4.ksplit2" : "FB2.PD4", t2 <= cus ? 16 : 8, 64, 0, (int)kBN,
+                (uint32_t)((t2 + 7u) / 8u * 8u));
     return t2 <= cus ? launch_fb<2, 8, 64, 4, 2>(a, weight, scale, out, N, M, K, stream)
                      : launch_fb<2, 8, 64, 4, 1>(a, weight, scale, out, N, M, K, stream);
 }

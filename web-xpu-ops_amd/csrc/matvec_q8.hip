@@ -815,12 +815,13 @@ __global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
 namespace {
 
 template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
-hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** variant) {
+hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, Variant* variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
     const float* aux = EPI == kEpiFfn ? a.scale2 : EPI == kEpiResidual ? a.residual : nullptr;
     hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI, MASK>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
                        a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.weight2, aux);
-    if (variant) *variant = CPW > 0 ? "m1.xreg" : "m1.xstream";
+    set_variant(variant, EPI == kEpiFfn ? "matvec_q8_m1.ffn" : EPI == kEpiResidual ? "matvec_q8_m1.residual" : "matvec_q8_m1",
+                CPW > 0 ? (MASK ? "xreg.masked" : "xreg") : "xstream", WAVES, R, CPW, 1, nblocks);
     return hipGetLastError();
 }
 
@@ -830,7 +831,7 @@ hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, const char** varia
 // takes at most a quarter of the rows (4 rows of each weight per block:
 // 3-4 % faster than 8 at 5632 x 2048 and 11008 x 4096).
 template <int WAVES, int CPW, int RMAX, int EPI>
-hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = EPI == kEpiFfn ? RMAX / 4 : RMAX;
     const uint32_t want = 2u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     if constexpr (RM >= 16) {
@@ -850,7 +851,7 @@ hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
 // its first (6-10 % faster from K = 4099 to 8192, same-process timings).
 // Rows per block: the largest R that still gives 6 waves per CU.
 template <int WAVES, int RMAX, int EPI, bool MASK>
-hipError_t dispatch_m1_wide_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_m1_wide_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = EPI == kEpiFfn ? RMAX / 2 : RMAX;
     const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
@@ -867,7 +868,7 @@ hipError_t dispatch_m1_wide_rows(const MatvecArgs& a, const DeviceInfo& dev, hip
 }
 
 template <int WAVES, int RMAX, int EPI>
-hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     if (a.W % kChunkWords != 0u) return dispatch_m1_wide_rows<WAVES, RMAX, EPI, true>(a, dev, stream, variant);
     return dispatch_m1_wide_rows<WAVES, RMAX, EPI, false>(a, dev, stream, variant);
 }
@@ -877,7 +878,7 @@ hipError_t dispatch_m1_wide(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
 // faster than 4 waves of 4 chunk slots each, same-process timings from
 // K = 9000 to 16384).
 template <int WAVES, int EPI>
-hipError_t dispatch_m1_wider(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_m1_wider(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = EPI == kEpiFfn ? 4 : 8;
     const uint32_t want = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     if constexpr (RM >= 8) {
@@ -888,7 +889,7 @@ hipError_t dispatch_m1_wider(const MatvecArgs& a, const DeviceInfo& dev, hipStre
 }
 
 template <int EPI>
-hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
     if (C == 1) return dispatch_m1_rows<1, 1, 16, EPI>(a, dev, stream, variant);
     if (C == 2) return dispatch_m1_rows<2, 1, 16, EPI>(a, dev, stream, variant);
@@ -913,7 +914,7 @@ hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t s
 }
 
 template <int WAVES, int CPW, int R, int MV>
-hipError_t launch_mv(const MatvecArgs& a, hipStream_t stream, const char** variant) {
+hipError_t launch_mv(const MatvecArgs& a, hipStream_t stream, Variant* variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
     // groups of MV vectors on grid y, at most 65535 per launch
     const uint32_t groups = (a.M + MV - 1) / MV;
@@ -926,14 +927,14 @@ hipError_t launch_mv(const MatvecArgs& a, hipStream_t stream, const char** varia
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    if (variant) *variant = "mb.valu";
+    set_variant(variant, "matvec_q8_mv", "valu", WAVES, R, CPW, MV, nblocks, groups);
     return hipSuccess;
 }
 
 // Rows per workgroup: the largest R (up to RMAX) that still gives every SIMD
 // a wave; fewer, fatter blocks load each vector slice fewer times.
 template <int WAVES, int CPW, int RMAX, int MV>
-hipError_t dispatch_mv_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_mv_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     const uint64_t want = 4u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
     if constexpr (RMAX >= 16) {
@@ -949,7 +950,7 @@ hipError_t dispatch_mv_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
 // row, as for one vector; slices stay in VGPRs while they take at most 128
 // per lane (CPW * MV * 16), otherwise each slot loads its own.
 template <int MV>
-hipError_t dispatch_mv(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+hipError_t dispatch_mv(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = MV >= 8 ? 8 : 16;
     const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
     if (C == 1) return dispatch_mv_rows<1, 1, RM, MV>(a, dev, stream, variant);
@@ -969,7 +970,7 @@ hipError_t dispatch_mv(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t s
 }  // namespace
 
 hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream,
-                            const char** variant) {
+                            Variant* variant) {
     if (a.N == 0 || a.M == 0) return hipSuccess;
     if (a.K == 0) {
         // No terms: y = 0 * s (NaN for a non-finite scale), as the reference.
@@ -1014,7 +1015,8 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
                     else
                         hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<2, kDmaStages>), g2, dim3(256), (size_t)ldsd, stream,
                                            a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
-                    if (variant) *variant = "mb.mfma_dma";
+                    set_variant(variant, "matvec_q8_mfma_dma", two ? "T2.4waves.256" : "T1.4waves.256", 4, 16 * (two ? 2 : 1),
+                                0, (int)MC, g2.x, g2.y);
                     return hipGetLastError();
                 }
                 // 13 to 16 vectors: two tiles per step no longer fit beside the
@@ -1028,7 +1030,7 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
                     const dim3 g8(min((ntiles + 3u) / 4u, cus), (a.M + 15u) / 16u);
                     hipLaunchKernelGGL((matvec_q8_mfma_dma_kernel<1, kDmaStages, 8, 128>), g8, dim3(512), (size_t)lds8,
                                        stream, a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
-                    if (variant) *variant = "mb.mfma_dma8";
+                    set_variant(variant, "matvec_q8_mfma_dma", "T1.8waves.128", 8, 16, 0, (int)MC, g8.x, g8.y);
                     return hipGetLastError();
                 }
             }
@@ -1038,7 +1040,8 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
             else
                 hipLaunchKernelGGL((matvec_q8_mfma_kernel<1, 3>), g, dim3(256), (size_t)lds, stream, a.weight, a.scale,
                                    a.vector, a.output, a.N, a.K, a.W, a.M, Kp);
-            if (variant) *variant = "mb.mfma";
+            set_variant(variant, "matvec_q8_mfma", MC >= 12u ? "T2.D2" : "T1.D3", 4, MC >= 12u ? 32 : 16, 0, (int)MC, g.x,
+                        g.y);
             return hipGetLastError();
         }
     }
@@ -1048,7 +1051,7 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
 }
 
 hipError_t launch_matvec_q8_fused(const MatvecArgs& a, int epi, const DeviceInfo& dev, hipStream_t stream,
-                                  const char** variant) {
+                                  Variant* variant) {
     if (a.N == 0) return hipSuccess;
     if (a.M != 1 || (epi != kEpiResidual && epi != kEpiFfn)) return hipErrorInvalidValue;
     if (a.K == 0) return launch_fused_zero(a, epi, stream);
@@ -1060,7 +1063,7 @@ namespace {
 
 template <int WAVES, int CPW, int R>
 hipError_t launch_multi(const Projection* p, uint32_t count, const float* x, uint32_t K, hipStream_t stream,
-                        const char** variant) {
+                        Variant* variant) {
     Projection q[kMaxProjections] = {};
     uint32_t start[kMaxProjections + 1];
     start[0] = 0;
@@ -1074,13 +1077,13 @@ hipError_t launch_multi(const Projection* p, uint32_t count, const float* x, uin
                        (K + 3) / 4, start[1], start[2], start[3], q[0].weight, q[0].scale, q[0].output, q[0].N,
                        q[1].weight, q[1].scale, q[1].output, q[1].N, q[2].weight, q[2].scale, q[2].output, q[2].N,
                        q[3].weight, q[3].scale, q[3].output, q[3].N);
-    if (variant) *variant = CPW > 0 ? "multi.xreg" : "multi.xstream";
+    set_variant(variant, "matvec_q8_multi", CPW > 0 ? "xreg" : "xstream", WAVES, R, CPW, 1, nblocks);
     return hipGetLastError();
 }
 
 template <int WAVES, int CPW, int RMAX>
 hipError_t dispatch_multi_rows(const Projection* p, uint32_t count, const float* x, uint32_t K,
-                               const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+                               const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     // The rows-per-block rule of the single-vector kernel, over the
     // projections' blocks together.
     const uint64_t want = 2u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
@@ -1104,7 +1107,7 @@ hipError_t dispatch_multi_rows(const Projection* p, uint32_t count, const float*
 // 5 to 8 chunks: one wave per chunk, as for a single projection.
 template <int WAVES>
 hipError_t dispatch_multi_wide(const Projection* p, uint32_t count, const float* x, uint32_t K,
-                               const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+                               const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto waves = [&](uint32_t R) {
         uint64_t b = 0;
@@ -1120,7 +1123,7 @@ hipError_t dispatch_multi_wide(const Projection* p, uint32_t count, const float*
 // 9 to 16 chunks: one wave per chunk, as for a single projection.
 template <int WAVES>
 hipError_t dispatch_multi_wider(const Projection* p, uint32_t count, const float* x, uint32_t K,
-                                const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+                                const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     const uint64_t want = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto blocks = [&](uint32_t R) {
         uint64_t b = 0;
@@ -1135,7 +1138,7 @@ hipError_t dispatch_multi_wider(const Projection* p, uint32_t count, const float
 }  // namespace
 
 hipError_t launch_matvec_q8_multi(const Projection* projections, uint32_t count, const float* x, uint32_t K,
-                                  const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+                                  const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     Projection p[kMaxProjections];
     uint32_t n = 0;
     uint64_t rows = 0;

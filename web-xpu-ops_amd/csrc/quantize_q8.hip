@@ -315,20 +315,25 @@ hipError_t launch_qwg(const float* input, uint32_t N, uint32_t K, int32_t* codes
 
 template <bool CODES, bool PACK>
 hipError_t dispatch_q(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed, float* scales,
-                      hipStream_t stream, const char** variant) {
+                      hipStream_t stream, Variant* variant) {
     const uint32_t W = (K + 3u) / 4u;
-    if (variant) *variant = "row.wg";
+    const char* form = CODES ? (PACK ? "codes+pack" : "codes") : "pack";
     // Short rows: one wave per row (a workgroup per row would leave most of
     // its lanes without a word).
-    if (W <= 64u) return launch_q<1, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (W <= 128u) return launch_q<2, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    if (W <= 128u) {
+        set_variant(variant, "quantize_rows", form, 4, 4, W <= 64u ? 1 : 2, 0, (N + 3u) / 4u);
+        if (W <= 64u) return launch_q<1, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+        return launch_q<2, CODES, PACK>(input, N, K, codes, packed, scales, stream);
+    }
     const uint32_t wpt = (W + 255u) / 256u;
+    set_variant(variant, "quantize_row_wg", form, 4, 1, wpt <= 8 ? (int)(wpt <= 2 ? wpt : wpt <= 4 ? 4 : wpt <= 6 ? 6 : 8) : 0,
+                0, N);
     if (wpt <= 1) return launch_qwg<1, CODES, PACK>(input, N, K, codes, packed, scales, stream);
     if (wpt <= 2) return launch_qwg<2, CODES, PACK>(input, N, K, codes, packed, scales, stream);
     if (wpt <= 4) return launch_qwg<4, CODES, PACK>(input, N, K, codes, packed, scales, stream);
     if (wpt <= 6) return launch_qwg<6, CODES, PACK>(input, N, K, codes, packed, scales, stream);
     if (wpt <= 8) return launch_qwg<8, CODES, PACK>(input, N, K, codes, packed, scales, stream);
-    if (variant) *variant = "row.wg.twopass";
+    if (variant) variant->form = CODES ? (PACK ? "codes+pack.twopass" : "codes.twopass") : "pack.twopass";
     return launch_qwg<0, CODES, PACK>(input, N, K, codes, packed, scales, stream);
 }
 
@@ -390,7 +395,7 @@ hipError_t launch_quantize_pack_multi(const float* const* inputs, const uint32_t
 }
 
 hipError_t launch_quantize_rows(const float* input, uint32_t N, uint32_t K, int32_t* codes, uint32_t* packed,
-                                float* scales, const DeviceInfo& dev, hipStream_t stream, const char** variant) {
+                                float* scales, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     (void)dev;
     if (N == 0) return hipSuccess;
     if (codes && packed) return dispatch_q<true, true>(input, N, K, codes, packed, scales, stream, variant);

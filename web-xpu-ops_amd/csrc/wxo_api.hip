@@ -21,6 +21,9 @@
 namespace {
 
 thread_local char g_error[512] = {0};
+// The kernel instance the calling thread's last successful op launched.
+thread_local wxo::Variant g_variant;
+thread_local char g_variant_text[256] = {0};
 
 int fail(int status, const char* fmt, ...) {
     va_list ap;
@@ -149,6 +152,17 @@ int validate_gather(const int8_t* codes, const float* s, const int64_t* idx, con
 
 hipStream_t as_hip(wxo_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Result of a launch: on success the chosen instance becomes this thread's
+// last variant; an op that launched nothing (no rows) records "none".
+int launched(hipError_t e, const wxo::Variant& v, const char* what) {
+    if (e != hipSuccess) return hip_fail(e, what);
+    g_variant = v;
+    if (!g_variant.kernel || !g_variant.kernel[0]) g_variant = wxo::Variant{"none", "empty", 0, 0, 0, 0, 0, 0};
+    return ok();
+}
+
+wxo::Variant named(const char* kernel, const char* form = "") { return wxo::Variant{kernel, form, 0, 0, 0, 0, 0, 0}; }
+
 // RAII device buffer for the *_host entry points.
 struct DevBuf {
     void* p = nullptr;
@@ -184,6 +198,25 @@ int wxo_abi_version(void) { return WXO_ABI_VERSION; }
 
 const char* wxo_last_error(void) { return g_error; }
 
+const char* wxo_last_variant(void) {
+    const wxo::Variant& v = g_variant;
+    char* b = g_variant_text;
+    const size_t cap = sizeof g_variant_text;
+    b[0] = '\0';
+    if (!v.kernel || !v.kernel[0]) return b;
+    size_t n = (size_t)snprintf(b, cap, "%s", v.kernel);
+    auto add = [&](const char* fmt, auto... xs) {
+        if (n < cap) n += (size_t)snprintf(b + n, cap - n, fmt, xs...);
+    };
+    if (v.form && v.form[0]) add(" %s", v.form);
+    if (v.waves) add(" waves=%d", v.waves);
+    if (v.rows) add(" rows=%d", v.rows);
+    if (v.slots) add(" slots=%d", v.slots);
+    if (v.vectors) add(" vectors=%d", v.vectors);
+    if (v.grid_x) add(" grid=%ux%u", v.grid_x, v.grid_y ? v.grid_y : 1u);
+    return b;
+}
+
 int wxo_init(void) {
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
@@ -200,9 +233,9 @@ const char* wxo_describe(void) {
     snprintf(g_describe, sizeof g_describe,
              "wxo_q8 abi=%d build=%s device=%d name=\"%s\" arch=%s cus=%d hbm_gib=%.1f kernels=matvec_q8_m1(plain|"
              "residual|ffn),matvec_q8_multi,matvec_q8_mv(valu),matvec_q8_mfma(bf16x3),quantize_rows(reg|twopass),pack_q8,"
-             "pack_int8_rows,matmul_q8(bf16x3),dequantize_packed,dequant_transpose,gather_dequant_rows",
+             "pack_int8_rows,matmul_q8(bf16x3),dequantize_packed,dequant_transpose,gather_dequant_rows last=\"%s\"",
              WXO_ABI_VERSION, WXO_BUILD_ID, d->ordinal, d->name, d->arch, d->cu_count,
-             (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0));
+             (double)d->hbm_bytes / (1024.0 * 1024.0 * 1024.0), wxo_last_variant());
     return g_describe;
 }
 
@@ -299,6 +332,15 @@ int wxo_event_create(wxo_event_t* event) {
     return ok();
 }
 
+int wxo_event_create_timer(wxo_event_t* event) {
+    if (!event) return fail(WXO_ERR_INVALID, "event is NULL");
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableSystemFence);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags");
+    *event = reinterpret_cast<wxo_event_t>(ev);
+    return ok();
+}
+
 int wxo_event_destroy(wxo_event_t event) {
     if (!event) return ok();
     hipError_t e = hipEventDestroy(reinterpret_cast<hipEvent_t>(event));
@@ -329,8 +371,9 @@ int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vecto
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     wxo::MatvecArgs a{weight, scale, vector, output, N, K, M, (uint32_t)(((uint64_t)K + 3) / 4)};
-    hipError_t e = wxo::launch_matvec_q8(a, *d, as_hip(stream), nullptr);
-    return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8 launch");
+    wxo::Variant v = N == 0 ? wxo::Variant{} : named("fill_scaled_zero", "K=0");
+    hipError_t e = wxo::launch_matvec_q8(a, *d, as_hip(stream), &v);
+    return launched(e, v, "matvec_q8 launch");
 }
 
 int wxo_matvec_q8_multi(const uint32_t* const* weights, const float* const* scales, float* const* outputs,
@@ -370,8 +413,9 @@ int wxo_matvec_q8_multi(const uint32_t* const* weights, const float* const* scal
         wxo::Projection p[wxo::kMaxProjections];
         const uint32_t n = count - g < wxo::kMaxProjections ? count - g : wxo::kMaxProjections;
         for (uint32_t i = 0; i < n; ++i) p[i] = {weights[g + i], scales[g + i], outputs[g + i], Ns[g + i]};
-        hipError_t e = wxo::launch_matvec_q8_multi(p, n, vector, K, *d, as_hip(stream), nullptr);
-        if (e != hipSuccess) return hip_fail(e, "matvec_q8_multi launch");
+        wxo::Variant v = named("fill_scaled_zero", "K=0");
+        hipError_t e = wxo::launch_matvec_q8_multi(p, n, vector, K, *d, as_hip(stream), &v);
+        WXO_TRY(launched(e, v, "matvec_q8_multi launch"));
     }
     return ok();
 }
@@ -384,8 +428,9 @@ int wxo_matvec_q8_residual(const uint32_t* weight, const float* scale, const flo
     WXO_TRY(current_device(&d));
     wxo::MatvecArgs a{weight, scale, vector, output, N, K, 1, (uint32_t)(((uint64_t)K + 3) / 4)};
     a.residual = residual;
-    hipError_t e = wxo::launch_matvec_q8_fused(a, wxo::kEpiResidual, *d, as_hip(stream), nullptr);
-    return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8_residual launch");
+    wxo::Variant v = N == 0 ? wxo::Variant{} : named("fused_zero", "residual.K=0");
+    hipError_t e = wxo::launch_matvec_q8_fused(a, wxo::kEpiResidual, *d, as_hip(stream), &v);
+    return launched(e, v, "matvec_q8_residual launch");
 }
 
 int wxo_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, const uint32_t* weight_up,
@@ -399,8 +444,9 @@ int wxo_matvec_q8_ffn(const uint32_t* weight_gate, const float* scale_gate, cons
     wxo::MatvecArgs a{weight_gate, scale_gate, vector, output, N, K, 1, (uint32_t)(((uint64_t)K + 3) / 4)};
     a.weight2 = weight_up;
     a.scale2 = scale_up;
-    hipError_t e = wxo::launch_matvec_q8_fused(a, wxo::kEpiFfn, *d, as_hip(stream), nullptr);
-    return e == hipSuccess ? ok() : hip_fail(e, "matvec_q8_ffn launch");
+    wxo::Variant v = N == 0 ? wxo::Variant{} : named("fused_zero", "ffn.K=0");
+    hipError_t e = wxo::launch_matvec_q8_fused(a, wxo::kEpiFfn, *d, as_hip(stream), &v);
+    return launched(e, v, "matvec_q8_ffn launch");
 }
 
 int wxo_quantize(const float* input, uint32_t N, uint32_t D, int32_t* output, float* scales, wxo_stream_t stream) {
@@ -409,8 +455,9 @@ int wxo_quantize(const float* input, uint32_t N, uint32_t D, int32_t* output, fl
     WXO_TRY(check_ptr(scales, N, "scales"));
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
-    hipError_t e = wxo::launch_quantize_rows(input, N, D, output, nullptr, scales, *d, as_hip(stream), nullptr);
-    return e == hipSuccess ? ok() : hip_fail(e, "quantize launch");
+    wxo::Variant v;
+    hipError_t e = wxo::launch_quantize_rows(input, N, D, output, nullptr, scales, *d, as_hip(stream), &v);
+    return launched(e, v, "quantize launch");
 }
 
 int wxo_pack_q8(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed, wxo_stream_t stream) {
@@ -419,7 +466,7 @@ int wxo_pack_q8(const int32_t* codes, uint32_t N, uint32_t K, uint32_t* packed, 
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     hipError_t e = wxo::launch_pack_q8(codes, N, K, packed, *d, as_hip(stream));
-    return e == hipSuccess ? ok() : hip_fail(e, "pack_q8 launch");
+    return launched(e, N && K ? named("pack_q8") : wxo::Variant{}, "pack_q8 launch");
 }
 
 int wxo_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* packed, wxo_stream_t stream) {
@@ -428,7 +475,7 @@ int wxo_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, uint32_t* pa
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     hipError_t e = wxo::launch_pack_int8_rows(codes, N, K, packed, *d, as_hip(stream));
-    return e == hipSuccess ? ok() : hip_fail(e, "pack_int8_rows launch");
+    return launched(e, N && K ? named("pack_int8_rows") : wxo::Variant{}, "pack_int8_rows launch");
 }
 
 int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* packed, float* scales,
@@ -438,8 +485,9 @@ int wxo_quantize_pack_q8(const float* input, uint32_t N, uint32_t K, uint32_t* p
     WXO_TRY(check_ptr(scales, N, "scales"));
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
-    hipError_t e = wxo::launch_quantize_rows(input, N, K, nullptr, packed, scales, *d, as_hip(stream), nullptr);
-    return e == hipSuccess ? ok() : hip_fail(e, "quantize_pack_q8 launch");
+    wxo::Variant v;
+    hipError_t e = wxo::launch_quantize_rows(input, N, K, nullptr, packed, scales, *d, as_hip(stream), &v);
+    return launched(e, v, "quantize_pack_q8 launch");
 }
 
 int wxo_quantize_pack_q8_multi(const float* const* inputs, const uint32_t* Ns, uint32_t* const* packed,
@@ -483,7 +531,7 @@ int wxo_quantize_pack_q8_multi(const float* const* inputs, const uint32_t* Ns, u
         const uint32_t n = count - g < wxo::kMaxQuantizeMatrices ? count - g : wxo::kMaxQuantizeMatrices;
         hipError_t e = wxo::launch_quantize_pack_multi(inputs + g, Ns + g, packed + g, scales + g, n, K, *d,
                                                        as_hip(stream));
-        if (e != hipSuccess) return hip_fail(e, "quantize_pack_q8_multi launch");
+        WXO_TRY(launched(e, named("quantize_pack_multi"), "quantize_pack_q8_multi launch"));
     }
     return ok();
 }
@@ -493,8 +541,9 @@ int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, fl
     WXO_TRY(validate_matmul(a, weight, scale, output, N, M, K));
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
-    hipError_t e = wxo::launch_matmul_q8(a, weight, scale, output, N, M, K, *d, as_hip(stream), nullptr);
-    return e == hipSuccess ? ok() : hip_fail(e, "matmul_q8 launch");
+    wxo::Variant v;
+    hipError_t e = wxo::launch_matmul_q8(a, weight, scale, output, N, M, K, *d, as_hip(stream), &v);
+    return launched(e, v, "matmul_q8 launch");
 }
 
 int wxo_dequantize_packed_q8(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K, float* output,
@@ -503,7 +552,7 @@ int wxo_dequantize_packed_q8(const uint32_t* weight, const float* scale, uint32_
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     hipError_t e = wxo::launch_dequantize_packed(weight, scale, N, K, output, *d, as_hip(stream));
-    return e == hipSuccess ? ok() : hip_fail(e, "dequantize_packed_q8 launch");
+    return launched(e, N && K ? named("dequantize_packed") : wxo::Variant{}, "dequantize_packed_q8 launch");
 }
 
 int wxo_dequant_transpose(const uint32_t* weight, const float* scale, uint32_t out_features, uint32_t in_features,
@@ -512,7 +561,8 @@ int wxo_dequant_transpose(const uint32_t* weight, const float* scale, uint32_t o
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     hipError_t e = wxo::launch_dequant_transpose(weight, scale, out_features, in_features, output, as_hip(stream));
-    return e == hipSuccess ? ok() : hip_fail(e, "dequant_transpose launch");
+    return launched(e, out_features && in_features ? named("dequant_transpose") : wxo::Variant{},
+                    "dequant_transpose launch");
 }
 
 int wxo_gather_dequant_rows(const int8_t* codes, const float* scale, uint32_t rows, uint32_t D,
@@ -521,7 +571,7 @@ int wxo_gather_dequant_rows(const int8_t* codes, const float* scale, uint32_t ro
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     hipError_t e = wxo::launch_gather_dequant_rows(codes, scale, rows, D, indices, count, output, *d, as_hip(stream));
-    return e == hipSuccess ? ok() : hip_fail(e, "gather_dequant_rows launch");
+    return launched(e, count && D ? named("gather_dequant_rows") : wxo::Variant{}, "gather_dequant_rows launch");
 }
 
 // ---- host-array forms ----------------------------------------------------------

@@ -1,8 +1,28 @@
+// Declarations of harness/resident.js: the reference's ResidentDevice
+// (harness/resident.ts:28-145) for the ops this build runs, plus native op kinds.
 export interface ResidentBuffer {
-  readonly ptr: bigint;
+  /** Device address (storage buffers) or null (uniform and MAP_READ staging buffers, held in host memory). */
+  readonly ptr: bigint | null;
   readonly size: number;
+  readonly usage: number;
+  readonly kind: "storage" | "uniform" | "staging";
 }
-export type ResidentQ8Op =
+export declare class UnsupportedPipelineError extends Error {
+  readonly name: "UnsupportedPipelineError";
+}
+export interface ResidentPipeline {
+  /** The MI355X op the WGSL interface was recognised as. */
+  readonly op: "matvecQ8" | "matvecQ8Ffn" | "matvecQ8Residual" | "matmulQ8";
+  readonly entry: string;
+}
+export interface ResidentBindGroup {
+  readonly pipeline: ResidentPipeline;
+  readonly buffers: readonly ResidentBuffer[];
+}
+/** harness/resident.ts:28-39 ResidentOp, plus this device's native op kinds. */
+export type ResidentOp =
+  | { kind: "dispatch"; pipeline: ResidentPipeline; bindGroup: ResidentBindGroup; workgroups: [number] | [number, number] | [number, number, number] }
+  | { kind: "copy"; src: ResidentBuffer; srcOffset: number; dst: ResidentBuffer; dstOffset: number; size: number }
   | { kind: "matvecQ8"; weight: ResidentBuffer; scale: ResidentBuffer; vector: ResidentBuffer; output: ResidentBuffer; N: number; K: number; M?: number }
   | { kind: "matvecQ8Ffn"; weightGate: ResidentBuffer; scaleGate: ResidentBuffer; weightUp: ResidentBuffer; scaleUp: ResidentBuffer; vector: ResidentBuffer; output: ResidentBuffer; N: number; K: number }
   | { kind: "matvecQ8Residual"; weight: ResidentBuffer; scale: ResidentBuffer; vector: ResidentBuffer; residual: ResidentBuffer; output: ResidentBuffer; N: number; K: number }
@@ -10,24 +30,46 @@ export type ResidentQ8Op =
   | { kind: "quantizePackQ8"; input: ResidentBuffer; N: number; K: number; packed: ResidentBuffer; scales: ResidentBuffer }
   | { kind: "matmulQ8"; a: ResidentBuffer; weight: ResidentBuffer; scale: ResidentBuffer; output: ResidentBuffer; N: number; M: number; K: number }
   | { kind: "dequantTranspose"; weight: ResidentBuffer; scale: ResidentBuffer; outFeatures: number; inFeatures: number; output: ResidentBuffer }
-  | { kind: "gatherDequantRows"; codes: ResidentBuffer; scale: ResidentBuffer; rows: number; D: number; indices: ResidentBuffer; count: number; output: ResidentBuffer }
-  | { kind: "copy"; src: ResidentBuffer; srcOffset: number; dst: ResidentBuffer; dstOffset: number; size: number };
-export interface ResidentQ8Readback {
+  | { kind: "gatherDequantRows"; codes: ResidentBuffer; scale: ResidentBuffer; rows: number; D: number; indices: ResidentBuffer; count: number; output: ResidentBuffer };
+/** harness/resident.ts:41-48; `staging` is accepted and not needed. */
+export interface ResidentReadback {
+  staging?: ResidentBuffer;
   source: ResidentBuffer;
   sourceOffset: number;
   length: number;
   type: "f32" | "i32" | "u32";
 }
+/** harness/resident.ts:75-96. */
+export interface BatchProfileSink {
+  submitToDoneMs: number | null;
+  readbackMs: number | null;
+  gpuEntries: { label: string; seconds: number }[];
+}
+export interface BatchProfile {
+  labels?: (string | null | undefined)[];
+  sink: BatchProfileSink;
+}
 export interface ResidentQ8Options {
   /** Run consecutive same-vector matvecQ8 ops as one launch (default true). */
   coalesce?: boolean;
 }
+export declare const BufferUsage: {
+  readonly MAP_READ: number; readonly MAP_WRITE: number; readonly COPY_SRC: number; readonly COPY_DST: number;
+  readonly INDEX: number; readonly VERTEX: number; readonly UNIFORM: number; readonly STORAGE: number;
+  readonly INDIRECT: number; readonly QUERY_RESOLVE: number;
+};
 export declare class ResidentQ8Device {
   constructor(options?: ResidentQ8Options);
-  readonly stats: { buffersCreated: number; submits: number; launches: number };
-  createStorageBuffer(bytes: number): ResidentBuffer;
+  readonly stats: { buffersCreated: number; pipelinesCreated: number; submits: number; launches: number };
+  readonly timestampsSupported: boolean;
+  createStorageBuffer(bytes: number, usage?: number): ResidentBuffer;
+  createUniformBuffer(bytes: number): ResidentBuffer;
   upload(buffer: ResidentBuffer, offset: number, data: ArrayBufferView): void;
-  batch(ops: ResidentQ8Op[], readback?: ResidentQ8Readback[]): Promise<(Float32Array | Int32Array | Uint32Array)[]>;
+  pipelineFor(code: string, entry?: string): Promise<ResidentPipeline>;
+  bindGroup(pipeline: ResidentPipeline, buffers: ResidentBuffer[]): Promise<ResidentBindGroup>;
+  batch(ops: ResidentOp[], readback?: ResidentReadback[], profile?: BatchProfile): Promise<(Float32Array | Int32Array | Uint32Array)[]>;
   destroy(): void;
 }
 export declare function createResidentQ8Device(options?: ResidentQ8Options): Promise<ResidentQ8Device | null>;
+/** harness/wgsl.ts:324-333 params(): a uniform's bytes, 4 per field, at least 16. */
+export declare function params(fields: ["u32" | "i32" | "f32", number][]): ArrayBuffer;

@@ -1,180 +1,414 @@
 // harness/resident: device-resident buffers and one-sync batches for a decode
-// engine, the MI355X counterpart of the reference's ResidentDevice
-// (harness/resident.ts:98-145, createResidentDevice :148, batch :231-382)
-// restricted to what the matvecQ8 path needs: storage buffers, uploads,
-// matvecQ8 (plain, fused FFN, fused residual) / quantize+packQ8 ops, the
-// prefill-side matmulQ8 / dequantTranspose / gatherDequantRows ops and device
-// copies recorded into one batch,
-// one synchronisation per batch, selective readback.
+// engine -- the MI355X counterpart of the reference's ResidentDevice
+// (harness/resident.ts:98-145, createResidentDevice :148, batch :231-382).
 //
-// Buffers are HBM allocations (hipMalloc) owned by the device object and freed
-// by destroy(); ops are enqueued in order on the device's stream as batch()
-// walks them, so nothing is allocated inside a decode loop's steady state
-// (`stats.buffersCreated` stays flat, as the reference's test checks).
+// It takes the reference's own calls for the ops this build runs:
+//   createStorageBuffer(bytes, usage?), createUniformBuffer(bytes),
+//   upload(buffer, offset, data), pipelineFor(code, entry?),
+//   bindGroup(pipeline, buffers), batch(ops, readback, profile?), destroy(),
+//   stats { buffersCreated, pipelinesCreated, submits }, timestampsSupported
+// with ops { kind: "dispatch", pipeline, bindGroup, workgroups } and
+// { kind: "copy", src, srcOffset, dst, dstOffset, size }, so the engine's
+// decode projections (llm/engine-q8-resident.ts:521-538 buildProjection,
+// :1059-1067 pipelineFor, :1840-1881 the dispatch list) are built and run
+// with the same calls.  pipelineFor recognises the reference WGSL of
+// matvecQ8 (q8), matvecQ8Ffn (q8_ffn), matvecQ8Residual (q8_residual) and
+// matmulQ8 by their binding declarations (./wgsl-interface.js) and throws
+// UnsupportedPipelineError for any other kernel (rmsnorm, rope, attention ...
+// are not part of this build).  A dispatch runs the MI355X kernel on the
+// bound buffers:
+//   q8, q8_ffn, q8_residual  rows = workgroups[0] (the WGSL kernels run one
+//                            workgroup per output row, row = workgroup_id.x),
+//                            K from the bound {N, K} uniform
+//   matmulQ8                 N, M, K from the uniform; the dispatch must cover
+//                            the whole [N, M] output (16 x 16 tiles: x over M,
+//                            y over N), as the engine's dispatches do
+// Buffer sizes are checked before anything is enqueued: where WebGPU's robust
+// access would clamp a short buffer, this device throws a RangeError.
 //
-// Consecutive single-vector matvecQ8 ops on the same vector (the engine's
-// wq/wk/wv projections, llm/engine-q8-resident.ts:1843-1845, and its lm_head
-// chunks, :1869) run as one launch of matvecQ8MultiDevice when nothing in the
-// run depends on another op of the run: outputs disjoint from each other, from
-// the vector and from the run's weights and scales.  Consecutive
-// quantizePackQ8 ops with one K run as one quantizePackQ8MultiDevice launch
-// under the same condition.  The results are those of the separate ops; only
-// the launch count changes (`stats.launches`).  Pass `{ coalesce: false }` to
-// the constructor to issue every op on its own.
+// It also keeps its native op kinds (matvecQ8 / matvecQ8Ffn /
+// matvecQ8Residual / packInt8Rows / quantizePackQ8 / matmulQ8 /
+// dequantTranspose / gatherDequantRows with named buffer fields), which the
+// loader and the prefill side use.
+//
+// Buffers: storage buffers are HBM allocations owned by the device and freed
+// by destroy(); uniform buffers and MAP_READ staging buffers live in host
+// memory (the kernels take their sizes as arguments, and readback needs no
+// staging copy), and still count in stats.buffersCreated.  Ops are enqueued in
+// order on the device's stream; batch() synchronises once and reads back only
+// `readback`, so nothing is allocated in a decode loop's steady state.
+//
+// Consecutive single-vector matvecQ8 ops (dispatch or native) on the same
+// vector and K run as one launch when no op of the run reads what another
+// writes (the engine's wq/wk/wv, :1843-1845, and lm_head chunks, :1869).
+// Consecutive quantizePackQ8 ops with one K likewise.  Results are those of
+// the separate ops; only stats.launches changes.  { coalesce: false } turns
+// it off; a batch with profile labels runs every op on its own, as the
+// reference gives every dispatch its own pass when timing.
 import { native } from "../native/index.js";
+import { recognise, UnsupportedPipelineError, params } from "./wgsl-interface.js";
+
+export { UnsupportedPipelineError, params };
 
 const TYPED = { f32: Float32Array, i32: Int32Array, u32: Uint32Array };
+
+/** WebGPU's GPUBufferUsage bit values (the spec's), for callers without a WebGPU global. */
+export const BufferUsage = Object.freeze({
+  MAP_READ: 0x0001, MAP_WRITE: 0x0002, COPY_SRC: 0x0004, COPY_DST: 0x0008, INDEX: 0x0010, VERTEX: 0x0020,
+  UNIFORM: 0x0040, STORAGE: 0x0080, INDIRECT: 0x0100, QUERY_RESOLVE: 0x0200,
+});
+
+const DEFAULT_USAGE = BufferUsage.STORAGE | BufferUsage.COPY_DST | BufferUsage.COPY_SRC;
 
 export class ResidentQ8Device {
   constructor(options = {}) {
     this.addon = native();
     this.addon.init();
     this.coalesce = options.coalesce !== false;
-    this.stats = { buffersCreated: 0, submits: 0, launches: 0 };
+    this.stats = { buffersCreated: 0, pipelinesCreated: 0, submits: 0, launches: 0 };
+    /** HIP events on the device's stream time every labelled op (BatchProfile). */
+    this.timestampsSupported = true;
     this.buffers = new Set();
+    this.pipelines = new Map();
+    this.pipelineSet = new WeakSet();
+    this.groupSet = new WeakSet();
+    this.events = [];
   }
 
-  /** A device buffer of `bytes` bytes: `{ ptr: bigint, size: number }`. */
-  createStorageBuffer(bytes) {
-    const ptr = this.addon.malloc(bytes);
-    const buffer = { ptr, size: bytes };
+  /**
+   * A buffer of max(4, bytes) bytes.  With the default usage (or any usage
+   * without MAP_READ) an HBM allocation `{ ptr: bigint, size }`; a MAP_READ
+   * staging buffer (harness/resident.ts:41-48) is host memory, since readback
+   * copies straight to a fresh typed array.
+   */
+  createStorageBuffer(bytes, usage = DEFAULT_USAGE) {
+    const size = Math.max(4, bytes);
+    let buffer;
+    if (usage & BufferUsage.MAP_READ) {
+      buffer = { ptr: null, host: new Uint8Array(size), size, usage, kind: "staging" };
+    } else {
+      buffer = { ptr: this.addon.malloc(size), size, usage, kind: "storage" };
+    }
     this.buffers.add(buffer);
     this.stats.buffersCreated += 1;
     return buffer;
   }
 
-  /** Host-to-device copy of `data` into `buffer` at byte `offset` (synchronous). */
+  /** A uniform buffer of max(16, bytes) bytes, held in host memory (read when a dispatch is enqueued). */
+  createUniformBuffer(bytes) {
+    const size = Math.max(16, bytes);
+    const buffer = { ptr: null, host: new Uint8Array(size), size, usage: BufferUsage.UNIFORM | BufferUsage.COPY_DST,
+      kind: "uniform" };
+    this.buffers.add(buffer);
+    this.stats.buffersCreated += 1;
+    return buffer;
+  }
+
+  /** `data` into `buffer` at byte `offset`: a host-to-device copy, or into a host-held buffer. */
   upload(buffer, offset, data) {
+    if (!this.buffers.has(buffer)) throw new TypeError("upload: buffer was not created by this device");
     if (offset < 0 || offset + data.byteLength > buffer.size) {
       throw new RangeError(`upload of ${data.byteLength} B at ${offset} overflows a ${buffer.size} B buffer`);
     }
-    this.addon.upload(buffer.ptr + BigInt(offset), data);
+    if (buffer.ptr === null) {
+      buffer.host.set(new Uint8Array(data.buffer, data.byteOffset, data.byteLength), offset);
+    } else {
+      this.addon.upload(buffer.ptr + BigInt(offset), data);
+    }
   }
 
   /**
-   * Enqueues every op in order, waits once, then reads back only `readback`.
-   * ops: { kind: "matvecQ8", weight, scale, vector, output, N, K, M? }
-   *      { kind: "matvecQ8Ffn", weightGate, scaleGate, weightUp, scaleUp, vector, output, N, K }
-   *      { kind: "matvecQ8Residual", weight, scale, vector, residual, output, N, K }
-   *        (output may be the residual buffer: the residual stream updated in place)
-   *      { kind: "packInt8Rows", codes, N, K, packed }   (int8 codes -> packed words)
-   *      { kind: "quantizePackQ8", input, N, K, packed, scales }
-   *      { kind: "matmulQ8", a, weight, scale, output, N, M, K }   (prefill GEMM, output [N, M])
-   *      { kind: "dequantTranspose", weight, scale, outFeatures, inFeatures, output }
-   *      { kind: "gatherDequantRows", codes, scale, rows, D, indices, count, output }
-   *        (indices: an int64 buffer of `count` row ids)
-   *      { kind: "copy", src, srcOffset, dst, dstOffset, size }
-   * readback: { source, sourceOffset, length, type: "f32" | "i32" | "u32" }
+   * The pipeline for WGSL `code` + `entry` (cached, as harness/resident.ts
+   * pipelineFor): one of the interfaces ./wgsl-interface.js recognises, or an
+   * UnsupportedPipelineError.
    */
-  async batch(ops, readback = []) {
-    const a = this.addon;
-    for (let i = 0; i < ops.length; i += 1) {
-      const op = ops[i];
-      this.stats.launches += 1;
-      switch (op.kind) {
-        case "matvecQ8": {
-          const M = op.M === undefined ? 1 : op.M;
-          checkMatvec(op, M);
-          const run = this.coalesce && M === 1 ? sameVectorRun(ops, i) : 1;
-          if (run > 1) {
-            const group = ops.slice(i, i + run);
-            a.matvecQ8MultiDevice(group.map((g) => [g.weight.ptr, g.scale.ptr, g.output.ptr, g.N]), op.vector.ptr,
-                                  op.K);
-            i += run - 1;
-          } else {
-            a.matvecQ8Device(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.output.ptr, op.N, op.K, M);
-          }
-          break;
-        }
-        case "matvecQ8Ffn": {
-          const bytes = op.N * Math.ceil(op.K / 4) * 4;
-          need(op.weightGate, bytes, "weightGate");
-          need(op.scaleGate, op.N * 4, "scaleGate");
-          need(op.weightUp, bytes, "weightUp");
-          need(op.scaleUp, op.N * 4, "scaleUp");
-          need(op.vector, op.K * 4, "vector");
-          need(op.output, op.N * 4, "output");
-          a.matvecQ8FfnDevice(op.weightGate.ptr, op.scaleGate.ptr, op.weightUp.ptr, op.scaleUp.ptr, op.vector.ptr,
-                              op.output.ptr, op.N, op.K);
-          break;
-        }
-        case "matvecQ8Residual": {
-          need(op.weight, op.N * Math.ceil(op.K / 4) * 4, "weight");
-          need(op.scale, op.N * 4, "scale");
-          need(op.vector, op.K * 4, "vector");
-          need(op.residual, op.N * 4, "residual");
-          need(op.output, op.N * 4, "output");
-          a.matvecQ8ResidualDevice(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.residual.ptr, op.output.ptr, op.N,
-                                   op.K);
-          break;
-        }
-        case "packInt8Rows": {
-          need(op.codes, op.N * op.K, "codes");
-          need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
-          a.packInt8RowsDevice(op.codes.ptr, op.N, op.K, op.packed.ptr);
-          break;
-        }
-        case "quantizePackQ8": {
-          checkQuantize(op);
-          const run = this.coalesce ? quantizeRun(ops, i) : 1;
-          if (run > 1) {
-            const group = ops.slice(i, i + run);
-            a.quantizePackQ8MultiDevice(group.map((g) => [g.input.ptr, g.N, g.packed.ptr, g.scales.ptr]), op.K);
-            i += run - 1;
-          } else {
-            a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
-          }
-          break;
-        }
-        case "matmulQ8": {
-          need(op.a, op.N * op.K * 4, "a");
-          need(op.weight, op.M * Math.ceil(op.K / 4) * 4, "weight");
-          need(op.scale, op.M * 4, "scale");
-          need(op.output, op.N * op.M * 4, "output");
-          a.matmulQ8Device(op.a.ptr, op.weight.ptr, op.scale.ptr, op.output.ptr, op.N, op.M, op.K);
-          break;
-        }
-        case "dequantTranspose": {
-          need(op.weight, op.outFeatures * Math.ceil(op.inFeatures / 4) * 4, "weight");
-          need(op.scale, op.outFeatures * 4, "scale");
-          need(op.output, op.outFeatures * op.inFeatures * 4, "output");
-          a.dequantTransposeDevice(op.weight.ptr, op.scale.ptr, op.outFeatures, op.inFeatures, op.output.ptr);
-          break;
-        }
-        case "gatherDequantRows": {
-          need(op.codes, op.rows * op.D, "codes");
-          need(op.scale, op.rows * 4, "scale");
-          need(op.indices, op.count * 8, "indices");
-          need(op.output, op.count * op.D * 4, "output");
-          a.gatherDequantRowsDevice(op.codes.ptr, op.scale.ptr, op.rows, op.D, op.indices.ptr, op.count, op.output.ptr);
-          break;
-        }
-        case "copy": {
-          if (op.srcOffset + op.size > op.src.size || op.dstOffset + op.size > op.dst.size) {
-            throw new RangeError("copy range outside its buffers");
-          }
-          a.copy(op.dst.ptr + BigInt(op.dstOffset), op.src.ptr + BigInt(op.srcOffset), op.size);
-          break;
-        }
-        default:
-          throw new TypeError(`unknown resident op kind ${op.kind}`);
-      }
-    }
-    a.synchronize();
-    this.stats.submits += 1;
-    return readback.map((r) => {
-      const T = TYPED[r.type];
-      if (!T) throw new TypeError(`unknown readback type ${r.type}`);
-      if (r.sourceOffset + r.length * 4 > r.source.size) throw new RangeError("readback outside its buffer");
-      return a.download(r.source.ptr + BigInt(r.sourceOffset), new T(r.length));
-    });
+  async pipelineFor(code, entry = "main") {
+    const key = `${entry} ${code}`;
+    const cached = this.pipelines.get(key);
+    if (cached) return cached;
+    const iface = recognise(code, entry);
+    const pipeline = Object.freeze({ op: iface.op, entry, interface: iface });
+    this.pipelines.set(key, pipeline);
+    this.pipelineSet.add(pipeline);
+    this.stats.pipelinesCreated += 1;
+    return pipeline;
   }
 
-  /** Frees every buffer this device created. */
-  destroy() {
-    for (const b of this.buffers) this.addon.free(b.ptr);
-    this.buffers.clear();
+  /**
+   * A bind group of whole buffers in the pipeline's binding order
+   * (harness/resident.ts bindGroup): storage bindings take this device's
+   * storage buffers, the uniform binding a uniform buffer.  An output that
+   * aliases an input is refused (WebGPU refuses writable aliasing too), except
+   * matvecQ8Residual's output over its residual: the in-place residual stream.
+   */
+  async bindGroup(pipeline, buffers) {
+    if (!this.pipelineSet.has(pipeline)) {
+      throw new TypeError("resident bind group is not valid: pipeline was not created by this device's pipelineFor");
+    }
+    const layout = pipeline.interface.bindings;
+    if (!Array.isArray(buffers) || buffers.length !== layout.length) {
+      throw new Error(`resident bind group is not valid: ${pipeline.op} binds ${layout.length} buffers ` +
+        `(${layout.map((b) => b[0]).join(", ")}), got ${Array.isArray(buffers) ? buffers.length : typeof buffers}`);
+    }
+    layout.forEach(([name, space], i) => {
+      const b = buffers[i];
+      if (!this.buffers.has(b)) throw new TypeError(`resident bind group is not valid: binding ${i} (${name}) is not a buffer of this device`);
+      if (space === "uniform" && b.kind !== "uniform") {
+        throw new TypeError(`resident bind group is not valid: binding ${i} (${name}) needs a uniform buffer`);
+      }
+      if (space === "storage" && b.kind !== "storage") {
+        throw new TypeError(`resident bind group is not valid: binding ${i} (${name}) needs a storage buffer`);
+      }
+    });
+    const out = layout.findIndex((b) => b[2] === "read_write");
+    layout.forEach(([name, space], i) => {
+      if (i === out || space !== "storage") return;
+      if (buffers[i] === buffers[out] && !(pipeline.op === "matvecQ8Residual" && name === "residual")) {
+        throw new Error(`resident bind group is not valid: ${pipeline.op} output aliases its ${name} binding`);
+      }
+    });
+    const group = Object.freeze({ pipeline, buffers: Object.freeze(buffers.slice()) });
+    this.groupSet.add(group);
+    return group;
   }
+
+  /**
+   * Enqueues every op in order, synchronises once, then reads back only
+   * `readback` ({ staging?, source, sourceOffset, length, type }; a staging
+   * buffer, when given, is not needed and not touched).  Every op is checked
+   * before the first is enqueued.  `profile` ({ labels?, sink }) as
+   * harness/resident.ts:75-96: sink.submitToDoneMs (enqueue end to
+   * completion), sink.readbackMs, and with labels sink.gpuEntries
+   * [{ label, seconds }] for each labelled non-copy op, from HIP events
+   * around its launch.
+   */
+  async batch(ops, readback = [], profile = undefined) {
+    const calls = ops.map((op, i) => this.resolve(op, i));
+    const reads = readback.map((r) => checkReadback(r, this.buffers));
+    const labels = profile && profile.labels ? profile.labels : null;
+    const coalesce = this.coalesce && !labels;
+    const a = this.addon;
+    const timed = [];
+    for (let i = 0; i < calls.length; i += 1) {
+      const label = labels && labels[i] != null && calls[i].kind !== "copy" ? labels[i] : null;
+      let events = null;
+      if (label !== null) {
+        events = this.eventPair(timed.length);
+        a.eventRecord(events[0]);
+      }
+      i += this.run(calls, i, coalesce) - 1;
+      if (events) {
+        a.eventRecord(events[1]);
+        timed.push({ label, events });
+      }
+    }
+    const t0 = profile ? performanceNow() : 0;
+    a.synchronize();
+    this.stats.submits += 1;
+    if (profile) profile.sink.submitToDoneMs = performanceNow() - t0;
+    const t1 = profile ? performanceNow() : 0;
+    const results = reads.map((r) => a.download(r.source.ptr + BigInt(r.sourceOffset), new TYPED[r.type](r.length)));
+    if (profile) {
+      profile.sink.readbackMs = performanceNow() - t1;
+      if (labels) {
+        const entries = [];
+        for (const t of timed) {
+          const ms = a.eventElapsedMs(t.events[0], t.events[1]);
+          if (ms > 0) entries.push({ label: t.label, seconds: ms / 1e3 });
+        }
+        profile.sink.gpuEntries = entries;
+      }
+    }
+    return results;
+  }
+
+  /** Frees every buffer and event this device created. */
+  destroy() {
+    for (const b of this.buffers) if (b.ptr !== null) this.addon.free(b.ptr);
+    this.buffers.clear();
+    for (const [s, e] of this.events) {
+      this.addon.eventDestroy(s);
+      this.addon.eventDestroy(e);
+    }
+    this.events = [];
+  }
+
+  eventPair(k) {
+    while (this.events.length <= k) this.events.push([this.addon.eventCreate(), this.addon.eventCreate()]);
+    return this.events[k];
+  }
+
+  /** A checked native call for op `i`: { kind, ...operands } (throws before anything is enqueued). */
+  resolve(op, i) {
+    if (!op || typeof op !== "object") throw new TypeError(`op ${i} is not an object`);
+    switch (op.kind) {
+      case "dispatch":
+        return this.resolveDispatch(op, i);
+      case "copy": {
+        for (const [b, name] of [[op.src, "src"], [op.dst, "dst"]]) {
+          if (!this.buffers.has(b) || b.kind !== "storage") throw new TypeError(`op ${i}: copy ${name} must be a storage buffer of this device`);
+        }
+        if (op.srcOffset % 4 || op.dstOffset % 4 || op.size % 4) {
+          throw new RangeError(`op ${i}: copy offsets and size must be multiples of 4 bytes`);
+        }
+        if (op.srcOffset < 0 || op.dstOffset < 0 || op.size < 0 || op.srcOffset + op.size > op.src.size ||
+            op.dstOffset + op.size > op.dst.size) {
+          throw new RangeError(`op ${i}: copy range outside its buffers`);
+        }
+        return op;
+      }
+      case "matvecQ8":
+        checkMatvec(op, op.M === undefined ? 1 : op.M);
+        return op;
+      case "matvecQ8Ffn":
+        checkFfn(op);
+        return op;
+      case "matvecQ8Residual":
+        checkResidual(op);
+        return op;
+      case "packInt8Rows":
+        need(op.codes, op.N * op.K, "codes");
+        need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
+        return op;
+      case "quantizePackQ8":
+        checkQuantize(op);
+        return op;
+      case "matmulQ8":
+        checkMatmul(op);
+        return op;
+      case "dequantTranspose":
+        need(op.weight, op.outFeatures * Math.ceil(op.inFeatures / 4) * 4, "weight");
+        need(op.scale, op.outFeatures * 4, "scale");
+        need(op.output, op.outFeatures * op.inFeatures * 4, "output");
+        return op;
+      case "gatherDequantRows":
+        need(op.codes, op.rows * op.D, "codes");
+        need(op.scale, op.rows * 4, "scale");
+        need(op.indices, op.count * 8, "indices");
+        need(op.output, op.count * op.D * 4, "output");
+        return op;
+      default:
+        throw new TypeError(`unknown resident op kind ${op.kind}`);
+    }
+  }
+
+  resolveDispatch(op, i) {
+    const group = op.bindGroup;
+    if (!this.groupSet.has(group)) throw new TypeError(`op ${i}: bindGroup was not created by this device's bindGroup`);
+    if (group.pipeline !== op.pipeline) {
+      throw new Error(`op ${i}: bind group was made for the ${group.pipeline.op} pipeline, dispatched with ${op.pipeline && op.pipeline.op}`);
+    }
+    const wg = op.workgroups;
+    if (!Array.isArray(wg) || wg.length < 1 || wg.length > 3 || !wg.every((n) => Number.isInteger(n) && n >= 0)) {
+      throw new TypeError(`op ${i}: workgroups must be [x], [x, y] or [x, y, z] of non-negative integers`);
+    }
+    const [x, y = 1, z = 1] = wg;
+    const b = group.buffers;
+    const u = new DataView(b[b.length - 1].host.buffer);
+    const empty = x === 0 || y === 0 || z === 0;
+    switch (op.pipeline.op) {
+      case "matvecQ8": {
+        const call = { kind: "matvecQ8", weight: b[0], scale: b[1], vector: b[2], output: b[3], N: empty ? 0 : x,
+          K: u.getUint32(4, true), M: 1 };
+        checkMatvec(call, 1);
+        return call;
+      }
+      case "matvecQ8Ffn": {
+        const call = { kind: "matvecQ8Ffn", weightGate: b[0], scaleGate: b[1], weightUp: b[2], scaleUp: b[3],
+          vector: b[4], output: b[5], N: empty ? 0 : x, K: u.getUint32(4, true) };
+        checkFfn(call);
+        return call;
+      }
+      case "matvecQ8Residual": {
+        const call = { kind: "matvecQ8Residual", weight: b[0], scale: b[1], vector: b[2], residual: b[3],
+          output: b[4], N: empty ? 0 : x, K: u.getUint32(4, true) };
+        checkResidual(call);
+        return call;
+      }
+      case "matmulQ8": {
+        const N = u.getUint32(0, true), M = u.getUint32(4, true), K = u.getUint32(8, true);
+        if (!empty && (x * 16 < M || y * 16 < N)) {
+          throw new RangeError(`op ${i}: matmulQ8 dispatch [${wg}] covers part of the ${N} x ${M} output; ` +
+            `this device runs whole outputs ([${Math.ceil(M / 16)}, ${Math.ceil(N / 16)}] workgroups or more)`);
+        }
+        const call = { kind: "matmulQ8", a: b[0], weight: b[1], scale: b[2], output: b[3], N: empty ? 0 : N, M, K };
+        checkMatmul(call);
+        return call;
+      }
+      default:
+        throw new UnsupportedPipelineError(`op ${i}: no MI355X kernel for pipeline ${op.pipeline.op}`);
+    }
+  }
+
+  /** Enqueues call `i` (and any run coalesced with it); returns how many calls it consumed. */
+  run(calls, i, coalesce) {
+    const a = this.addon;
+    const op = calls[i];
+    this.stats.launches += 1;
+    switch (op.kind) {
+      case "matvecQ8": {
+        const M = op.M === undefined ? 1 : op.M;
+        const n = coalesce && M === 1 ? sameVectorRun(calls, i) : 1;
+        if (n > 1) {
+          const group = calls.slice(i, i + n);
+          a.matvecQ8MultiDevice(group.map((g) => [g.weight.ptr, g.scale.ptr, g.output.ptr, g.N]), op.vector.ptr, op.K);
+          return n;
+        }
+        a.matvecQ8Device(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.output.ptr, op.N, op.K, M);
+        return 1;
+      }
+      case "matvecQ8Ffn":
+        a.matvecQ8FfnDevice(op.weightGate.ptr, op.scaleGate.ptr, op.weightUp.ptr, op.scaleUp.ptr, op.vector.ptr,
+                            op.output.ptr, op.N, op.K);
+        return 1;
+      case "matvecQ8Residual":
+        a.matvecQ8ResidualDevice(op.weight.ptr, op.scale.ptr, op.vector.ptr, op.residual.ptr, op.output.ptr, op.N,
+                                 op.K);
+        return 1;
+      case "packInt8Rows":
+        a.packInt8RowsDevice(op.codes.ptr, op.N, op.K, op.packed.ptr);
+        return 1;
+      case "quantizePackQ8": {
+        const n = coalesce ? quantizeRun(calls, i) : 1;
+        if (n > 1) {
+          const group = calls.slice(i, i + n);
+          a.quantizePackQ8MultiDevice(group.map((g) => [g.input.ptr, g.N, g.packed.ptr, g.scales.ptr]), op.K);
+          return n;
+        }
+        a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
+        return 1;
+      }
+      case "matmulQ8":
+        a.matmulQ8Device(op.a.ptr, op.weight.ptr, op.scale.ptr, op.output.ptr, op.N, op.M, op.K);
+        return 1;
+      case "dequantTranspose":
+        a.dequantTransposeDevice(op.weight.ptr, op.scale.ptr, op.outFeatures, op.inFeatures, op.output.ptr);
+        return 1;
+      case "gatherDequantRows":
+        a.gatherDequantRowsDevice(op.codes.ptr, op.scale.ptr, op.rows, op.D, op.indices.ptr, op.count, op.output.ptr);
+        return 1;
+      case "copy":
+        if (op.size > 0) a.copy(op.dst.ptr + BigInt(op.dstOffset), op.src.ptr + BigInt(op.srcOffset), op.size);
+        return 1;
+      default:
+        throw new TypeError(`unknown resident op kind ${op.kind}`);
+    }
+  }
+}
+
+function performanceNow() {
+  const [s, ns] = process.hrtime();
+  return s * 1e3 + ns / 1e6;
+}
+
+function checkReadback(r, owned) {
+  const T = TYPED[r.type];
+  if (!T) throw new TypeError(`unknown readback type ${r.type}`);
+  if (!owned.has(r.source) || r.source.kind !== "storage") throw new TypeError("readback source must be a storage buffer of this device");
+  if (r.sourceOffset % 4 || r.sourceOffset < 0 || r.sourceOffset + r.length * 4 > r.source.size) {
+    throw new RangeError("readback outside its buffer");
+  }
+  return r;
 }
 
 function checkMatvec(op, M) {
@@ -185,26 +419,49 @@ function checkMatvec(op, M) {
   need(op.output, M * op.N * 4, "output");
 }
 
+function checkFfn(op) {
+  const bytes = op.N * Math.ceil(op.K / 4) * 4;
+  need(op.weightGate, bytes, "weightGate");
+  need(op.scaleGate, op.N * 4, "scaleGate");
+  need(op.weightUp, bytes, "weightUp");
+  need(op.scaleUp, op.N * 4, "scaleUp");
+  need(op.vector, op.K * 4, "vector");
+  need(op.output, op.N * 4, "output");
+}
+
+function checkResidual(op) {
+  need(op.weight, op.N * Math.ceil(op.K / 4) * 4, "weight");
+  need(op.scale, op.N * 4, "scale");
+  need(op.vector, op.K * 4, "vector");
+  need(op.residual, op.N * 4, "residual");
+  need(op.output, op.N * 4, "output");
+}
+
 function checkQuantize(op) {
   need(op.input, op.N * op.K * 4, "input");
   need(op.packed, op.N * Math.ceil(op.K / 4) * 4, "packed");
   need(op.scales, op.N * 4, "scales");
 }
 
+function checkMatmul(op) {
+  need(op.a, op.N * op.K * 4, "a");
+  need(op.weight, op.M * Math.ceil(op.K / 4) * 4, "weight");
+  need(op.scale, op.M * 4, "scale");
+  need(op.output, op.N * op.M * 4, "output");
+}
+
 /**
- * How many ops from `start` on (at least 1) form a run of quantizePackQ8 ops
- * with the same K, none writing what another of the run reads or writes.
+ * How many calls from `start` on (at least 1) form a run of quantizePackQ8
+ * calls with the same K, none writing what another of the run reads or writes.
  */
-function quantizeRun(ops, start) {
-  const K = ops[start].K;
+function quantizeRun(calls, start) {
+  const K = calls[start].K;
   const ins = [];
   const outs = [];
   let n = 0;
-  for (let j = start; j < ops.length; j += 1) {
-    const op = ops[j];
-    if (op.kind !== "quantizePackQ8") break;
-    if (j > start) checkQuantize(op);
-    if (op.K !== K) break;
+  for (let j = start; j < calls.length; j += 1) {
+    const op = calls[j];
+    if (op.kind !== "quantizePackQ8" || op.K !== K) break;
     const input = span(op.input, op.N * op.K * 4);
     const own = [span(op.packed, op.N * Math.ceil(op.K / 4) * 4), span(op.scales, op.N * 4)];
     if (overlaps(own[0], own[1]) || own.some((o) => overlaps(o, input) || ins.some((r) => overlaps(o, r)) ||
@@ -228,21 +485,20 @@ function overlaps(x, y) {
 }
 
 /**
- * How many ops from `start` on (at least 1) form a run of single-vector
- * matvecQ8 ops on the same vector and K with no op of the run reading what
- * another writes, so that one launch gives what the ops in order would.
+ * How many calls from `start` on (at least 1) form a run of single-vector
+ * matvecQ8 calls on the same vector and K with no call of the run reading
+ * what another writes, so that one launch gives what the calls in order would.
  */
-function sameVectorRun(ops, start) {
-  const first = ops[start];
+function sameVectorRun(calls, start) {
+  const first = calls[start];
   const vec = span(first.vector, first.K * 4);
   const outs = [];
   const ins = [];
   let n = 0;
-  for (let j = start; j < ops.length; j += 1) {
-    const op = ops[j];
+  for (let j = start; j < calls.length; j += 1) {
+    const op = calls[j];
     if (op.kind !== "matvecQ8" || (op.M !== undefined && op.M !== 1)) break;
-    if (j > start) checkMatvec(op, 1);
-    if (op.K !== first.K || op.vector.ptr !== first.vector.ptr) break;
+    if (op.K !== first.K || op.vector.ptr !== first.vector.ptr || op.N === 0) break;
     const out = span(op.output, op.N * 4);
     const reads = [span(op.weight, op.N * Math.ceil(op.K / 4) * 4), span(op.scale, op.N * 4)];
     if (overlaps(out, vec) || outs.some((o) => overlaps(o, out)) ||
@@ -257,13 +513,21 @@ function sameVectorRun(ops, start) {
 }
 
 function need(buffer, bytes, name) {
-  if (!buffer || typeof buffer.ptr !== "bigint") throw new TypeError(`${name} must be a resident buffer`);
+  if (!buffer || typeof buffer.ptr !== "bigint") throw new TypeError(`${name} must be a resident storage buffer`);
   if (bytes > buffer.size) throw new RangeError(`${name} buffer holds ${buffer.size} B, ${bytes} B needed`);
 }
 
-/** Resolves to null when no gfx950 device is visible (as harness/resident.ts:148 does without an adapter). */
+/**
+ * Resolves to null when no gfx950 device is visible (as harness/resident.ts:148
+ * does without an adapter).  Installs `GPUBufferUsage` (the spec's bit
+ * values) on globalThis when no WebGPU global provides it, as the reference's
+ * createResidentDevice installs the webgpu package's globals, so callers that
+ * create staging buffers with `GPUBufferUsage.COPY_DST | GPUBufferUsage.MAP_READ`
+ * run unchanged.
+ */
 export async function createResidentQ8Device(options = {}) {
   const a = native();
   if (a.deviceCount() === 0) return null;
+  if (typeof globalThis.GPUBufferUsage === "undefined") globalThis.GPUBufferUsage = BufferUsage;
   return new ResidentQ8Device(options);
 }

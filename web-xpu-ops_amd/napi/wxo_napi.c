@@ -28,6 +28,8 @@
  *   quantizePackQ8Device(in, N, K, packed, scales), matmulQ8Device(a, w, s, y, N, M, K),
  *   dequantizePackedQ8Device(w, s, N, K, y), dequantTransposeDevice(w, s, outF, inF, y),
  *   gatherDequantRowsDevice(codes, s, rows, D, indices, count, y)
+ *   lastVariant() -> string (wxo_last_variant: the kernel instance of the last op)
+ *   eventCreate() -> bigint, eventRecord(ev), eventElapsedMs(start, stop), eventDestroy(ev)
  * Device functions are stream-ordered on the null stream; synchronize()
  * (or any download) waits for them.
  * Errors: a TypeError/RangeError for bad arguments, an Error carrying
@@ -198,6 +200,65 @@ static napi_value js_synchronize(napi_env env, napi_callback_info info) {
     int st = wxo_synchronize();
     if (st != WXO_OK) return throw_status(env, st, "synchronize");
     return NULL;
+}
+
+static napi_value js_last_variant(napi_env env, napi_callback_info info) {
+    (void)info;
+    napi_value r;
+    napi_create_string_utf8(env, wxo_last_variant(), NAPI_AUTO_LENGTH, &r);
+    return r;
+}
+
+/* ---------------------------------------------------------------- events
+ * GPU timestamps on the null stream, for per-op timing inside a resident
+ * batch: eventCreate() -> bigint (a timing-only event, wxo_event_create_timer),
+ * eventRecord(ev), eventElapsedMs(start, stop) (waits for `stop`),
+ * eventDestroy(ev). */
+
+static napi_value js_event_create(napi_env env, napi_callback_info info) {
+    (void)info;
+    wxo_event_t ev = NULL;
+    int st = wxo_event_create_timer(&ev);
+    if (st != WXO_OK) return throw_status(env, st, "eventCreate");
+    napi_value r;
+    napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)ev, &r);
+    return r;
+}
+
+static napi_value js_event_destroy(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint64_t ev;
+    if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &ev, "event")) return NULL;
+    int st = wxo_event_destroy((wxo_event_t)(uintptr_t)ev);
+    if (st != WXO_OK) return throw_status(env, st, "eventDestroy");
+    return NULL;
+}
+
+static napi_value js_event_record(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint64_t ev;
+    if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &ev, "event")) return NULL;
+    int st = wxo_event_record((wxo_event_t)(uintptr_t)ev, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "eventRecord");
+    return NULL;
+}
+
+static napi_value js_event_elapsed_ms(napi_env env, napi_callback_info info) {
+    size_t argc = 2;
+    napi_value argv[2];
+    uint64_t a, b;
+    if (!get_args(env, info, 2, &argc, argv) || !get_ptr(env, argv[0], &a, "start") ||
+        !get_ptr(env, argv[1], &b, "stop"))
+        return NULL;
+    int st = wxo_event_synchronize((wxo_event_t)(uintptr_t)b);
+    float ms = 0.0f;
+    if (st == WXO_OK) st = wxo_event_elapsed_ms(&ms, (wxo_event_t)(uintptr_t)a, (wxo_event_t)(uintptr_t)b);
+    if (st != WXO_OK) return throw_status(env, st, "eventElapsedMs");
+    napi_value r;
+    napi_create_double(env, (double)ms, &r);
+    return r;
 }
 
 /* ---------------------------------------------------------------- host-array ops */
@@ -873,6 +934,11 @@ static napi_value init_module(napi_env env, napi_value exports) {
     napi_property_descriptor props[] = {
         {"abiVersion", NULL, js_abi_version, NULL, NULL, NULL, napi_enumerable, NULL},
         {"describe", NULL, js_describe, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"lastVariant", NULL, js_last_variant, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"eventCreate", NULL, js_event_create, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"eventDestroy", NULL, js_event_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"eventRecord", NULL, js_event_record, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"eventElapsedMs", NULL, js_event_elapsed_ms, NULL, NULL, NULL, napi_enumerable, NULL},
         {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
         {"init", NULL, js_init, NULL, NULL, NULL, napi_enumerable, NULL},
         {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},

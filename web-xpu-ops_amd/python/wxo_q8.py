@@ -44,6 +44,7 @@ _P, _U32, _SZ, _I = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_
 SIGNATURES = {
     "wxo_abi_version": ([], _I),
     "wxo_last_error": ([], ctypes.c_char_p),
+    "wxo_last_variant": ([], ctypes.c_char_p),
     "wxo_init": ([], _I),
     "wxo_describe": ([], ctypes.c_char_p),
     "wxo_device_count": ([ctypes.POINTER(_I)], _I),
@@ -58,6 +59,7 @@ SIGNATURES = {
     "wxo_stream_destroy": ([_P], _I),
     "wxo_stream_synchronize": ([_P], _I),
     "wxo_event_create": ([ctypes.POINTER(_P)], _I),
+    "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
     "wxo_event_destroy": ([_P], _I),
     "wxo_event_record": ([_P, _P], _I),
     "wxo_event_synchronize": ([_P], _I),
@@ -121,6 +123,11 @@ def _check(status: int) -> None:
 
 def describe() -> str:
     return lib().wxo_describe().decode()
+
+
+def last_variant() -> str:
+    """The kernel instance this thread's last successful op launched."""
+    return lib().wxo_last_variant().decode()
 
 
 def device_count() -> int:
@@ -197,9 +204,10 @@ class Stream:
 
 
 class Event:
-    def __init__(self):
+    def __init__(self, timer: bool = False):
+        """timer=True: a timing-only event (wxo_event_create_timer, no fence)."""
         p = ctypes.c_void_p(0)
-        _check(lib().wxo_event_create(ctypes.byref(p)))
+        _check((lib().wxo_event_create_timer if timer else lib().wxo_event_create)(ctypes.byref(p)))
         self.handle = p.value
 
     def record(self, stream=None) -> None:
