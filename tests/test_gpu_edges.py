@@ -228,3 +228,41 @@ def test_variant_names_the_instance_that_ran(cfg, M):
     wxo_q8.synchronize()
     for b in (w, s, x, y):
         b.free()
+
+
+@pytest.mark.parametrize("K", list(range(1, 20)) + [31, 63, 64, 65, 255, 256, 257, 1023, 1025, 2049, 4096, 4099, 5001])
+@pytest.mark.parametrize("N", [1, 3, 50])
+@pytest.mark.parametrize("offset", [0, 3])
+def test_pack_int8_rows_any_alignment_sentinel_tail(K, N, offset):
+    """packInt8Rows (llm/weights-q8.ts:137-139) bit-exact for row lengths on both
+    sides of the streaming kernel's 4W >= 16 switch, codes starting at any byte
+    (a row slice of a larger buffer) and a sentinel tail after the output."""
+    rng = np.random.default_rng(K * 131 + N * 7 + offset)
+    W = (K + 3) // 4
+    codes = rng.integers(-128, 128, N * K).astype(np.int8)
+    src = wxo_q8.DeviceBuffer.from_array(np.concatenate([rng.integers(-128, 128, offset).astype(np.int8), codes,
+                                                         np.full(8, 0x55, np.int8)]))
+    dst = wxo_q8.DeviceBuffer.from_array(np.full(N * W + TAIL, SENT_U32, np.uint32))
+    wxo_q8.pack_int8_rows_device(src.ptr + offset, N, K, dst)
+    wxo_q8.synchronize()
+    got = dst.download(np.uint32, N * W + TAIL)
+    assert_bits_equal(got[:N * W], oracle.pack_int8_rows(codes, N, K), f"packInt8Rows N={N} K={K} +{offset}")
+    assert np.all(got[N * W:] == SENT_U32), "wrote past the output"
+    for b in (src, dst):
+        b.free()
+
+
+def test_pack_int8_rows_exact_size_input_ends_the_buffer():
+    """The input is an exactly sized allocation whose byte count is not a
+    multiple of 4: the last row's last codes come from a partial dword."""
+    for N, K in ((3, 4099), (1, 13), (5, 1021), (4096, 4099)):
+        rng = np.random.default_rng(N + K)
+        codes = rng.integers(-128, 128, N * K).astype(np.int8)
+        src = wxo_q8.DeviceBuffer.from_array(codes)
+        W = (K + 3) // 4
+        dst = wxo_q8.DeviceBuffer(N * W * 4)
+        wxo_q8.pack_int8_rows_device(src, N, K, dst)
+        wxo_q8.synchronize()
+        assert_bits_equal(dst.download(np.uint32, N * W), oracle.pack_int8_rows(codes, N, K), f"N={N} K={K}")
+        src.free()
+        dst.free()
