@@ -57,8 +57,8 @@ PEAK_FP32_FMA_TFLOPS = 157.3 / 2
 PEAK_BF16_MFMA_TFLOPS = 2500.0
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "matvec_q8_cfg2_traffic.txt")
 TRAFFIC_NOTE = ("HBM bytes per launch from the committed rocprofv3 --pmc summary "
-                "profiles/matvec_q8_cfg2_traffic.txt (not measured in this run: counters need their own "
-                "profiler process)")
+                "profiles/matvec_q8_cfg2_traffic.txt: TCC_EA0 read and write requests x request size, taken "
+                "in its own profiler run (counters need their own process), not in this one")
 
 
 def log(msg: str) -> None:
@@ -619,10 +619,13 @@ def main() -> int:
     log(f"timed region {total_ms:.3f} ms / {args.steps} calls = {launch_us:.3f} us/call ({variant})")
 
     if args.calibrate_copy:
-        # A plain device copy of the packed weight (rocclr's copyBuffer kernel):
-        # the known-size reference that scales FETCH_SIZE / WRITE_SIZE.
+        # Plain device copies of one weight copy into another (rocclr's
+        # copyBuffer kernel), source and destination rotating through the
+        # copies like the timed calls, so neither is cache-resident: the
+        # known-size reference for the traffic counters.
         for i in range(args.calibrate_copy):
-            wxo_q8.lib().wxo_memcpy_dtod(rot.ptr + ((i + 1) % copies) * row_bytes, packed0.ptr, row_bytes, sp)
+            src, dst = (2 * i) % copies, (2 * i + 1) % copies
+            wxo_q8.lib().wxo_memcpy_dtod(rot.ptr + dst * row_bytes, rot.ptr + src * row_bytes, row_bytes, sp)
         stream.synchronize()
         log(f"calibration: {args.calibrate_copy} device copies of {row_bytes} B")
 
