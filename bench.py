@@ -126,6 +126,77 @@ def time_loop(stream, launch, steps, warmup):
     return e0.elapsed_ms(e1) * 1e3 / steps
 
 
+ROT_TARGET = 600 * 1024 * 1024  # > 2x the 256 MB Infinity Cache
+
+
+def _check(st):
+    if st != 0:
+        raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
+
+
+def prepare_weights(stream, w_f32, N, K, copies):
+    """Quantize+pack `w_f32` on the GPU into `copies` consecutive copies (rotation)."""
+    L = wxo_q8.lib()
+    W = (K + 3) // 4
+    src = wxo_q8.DeviceBuffer.from_array(w_f32, stream)
+    packed = wxo_q8.DeviceBuffer(N * W * 4 * copies)
+    scale = wxo_q8.DeviceBuffer(N * 4)
+    wxo_q8.quantize_pack_q8_device(src, N, K, packed, scale, stream)
+    for i in range(1, copies):
+        _check(L.wxo_memcpy_dtod(packed.ptr + i * N * W * 4, packed.ptr, N * W * 4, stream.handle))
+    stream.synchronize()
+    src.free()
+    return packed, scale
+
+
+def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup):
+    """One matvecQ8 configuration on rotated weights: us per call, algorithmic
+    GB/s, the bound (HBM, or the compute rate of the path that runs: one-wide
+    FP32 FMA for one vector, bf16 matrix cores at three products per code for
+    batched vectors) and the kernel instance."""
+    L = wxo_q8.lib()
+    sp = stream.handle
+    W = (K + 3) // 4
+    nbytes = wl.matvec_bytes(N, K, M)
+    copies = max(1, -(-ROT_TARGET // (N * W * 4)))
+    packed, scale = prepare_weights(stream, w_f32, N, K, copies)
+    vec = wxo_q8.DeviceBuffer.from_array(x, stream)
+    out = wxo_q8.DeviceBuffer(N * M * 4)
+    ptrs = [packed.ptr + i * N * W * 4 for i in range(copies)]
+    for i in range(copies):  # every copy read once before timing
+        _check(L.wxo_matvec_q8(ptrs[i], scale.ptr, vec.ptr, out.ptr, N, K, M, sp))
+    us = time_loop(stream, lambda i: _check(L.wxo_matvec_q8(ptrs[i % copies], scale.ptr, vec.ptr, out.ptr,
+                                                            N, K, M, sp)), steps, warmup)
+    variant = wxo_q8.last_variant()
+    gbs = nbytes / (us * 1e-6) / 1e9
+    flops = 2.0 * N * K * M
+    tflops = flops / (us * 1e-6) / 1e12
+    hbm_us = nbytes / (PEAK_HBM_GBS * 1e9) * 1e6
+    if M == 1:  # one FMA per code on the VALU
+        comp_us, comp_name = flops / (PEAK_FP32_FMA_TFLOPS * 1e12) * 1e6, "valu_fp32"
+    else:  # matrix cores: three bf16 products per code, 16 vectors per tile
+        mflops = 3.0 * 2.0 * N * K * 16 * (-(-M // 16))
+        comp_us, comp_name = mflops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6, "mfma_bf16"
+    bound = "hbm" if hbm_us >= comp_us else comp_name
+    log(f"{name}: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM  bound={bound}  [{variant}]")
+    for b in (packed, scale, vec, out):
+        b.free()
+    return {"case": name, "N": N, "K": K, "M": M, "us": round(us, 3), "GB/s": round(gbs, 1),
+            "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "TFLOP/s": round(tflops, 2),
+            "bound": bound, "pct_of_bound": round(100 * max(hbm_us, comp_us) / us, 1),
+            "weight_copies": copies, "variant": variant}
+
+
+def run_case(stream, spec, steps, warmup):
+    """`--case cfgN[:M]`: one BASELINE matvecQ8 configuration alone (M vectors)."""
+    name, _, m = spec.partition(":")
+    M = int(m) if m else 1
+    if name not in wl.CONFIGS:
+        raise SystemExit(f"--case: unknown configuration {name!r} (one of {', '.join(wl.CONFIGS)})")
+    c = wl.make_config(name, M=M)
+    return measure_matvec(stream, f"{name} matvecQ8 M={M}", c["N"], c["K"], M, c["w"], c["x"], steps, warmup)
+
+
 def run_suite(stream, steps, warmup):
     """Every BASELINE configuration on one GPU: us/step, algorithmic GB/s and
     the fraction of the bound that applies (HBM, or the compute rate of the
@@ -134,52 +205,15 @@ def run_suite(stream, steps, warmup):
     L = wxo_q8.lib()
     sp = stream.handle
     results = []
-    rot_target = 600 * 1024 * 1024  # > 2x the 256 MB Infinity Cache
-
-    def check(st):
-        if st != 0:
-            raise wxo_q8.WxoError(st, L.wxo_last_error().decode())
+    rot_target = ROT_TARGET
+    check = _check
 
     def prepare(w_f32, N, K, copies):
-        W = (K + 3) // 4
-        src = wxo_q8.DeviceBuffer.from_array(w_f32, stream)
-        packed = wxo_q8.DeviceBuffer(N * W * 4 * copies)
-        scale = wxo_q8.DeviceBuffer(N * 4)
-        wxo_q8.quantize_pack_q8_device(src, N, K, packed, scale, stream)
-        for i in range(1, copies):
-            check(L.wxo_memcpy_dtod(packed.ptr + i * N * W * 4, packed.ptr, N * W * 4, sp))
-        stream.synchronize()
-        src.free()
-        return packed, scale
+        return prepare_weights(stream, w_f32, N, K, copies)
 
     def matvec_case(name, N, K, M, w_f32, x):
-        W = (K + 3) // 4
-        nbytes = wl.matvec_bytes(N, K, M)
-        copies = max(1, -(-rot_target // (N * W * 4)))
-        packed, scale = prepare(w_f32, N, K, copies)
-        vec = wxo_q8.DeviceBuffer.from_array(x, stream)
-        out = wxo_q8.DeviceBuffer(N * M * 4)
-        ptrs = [packed.ptr + i * N * W * 4 for i in range(copies)]
-        us = time_loop(stream, lambda i: check(L.wxo_matvec_q8(ptrs[i % copies], scale.ptr, vec.ptr, out.ptr,
-                                                               N, K, M, sp)), steps, warmup)
-        gbs = nbytes / (us * 1e-6) / 1e9
-        flops = 2.0 * N * K * M
-        tflops = flops / (us * 1e-6) / 1e12
-        hbm_us = nbytes / (PEAK_HBM_GBS * 1e9) * 1e6
-        if M == 1:  # one FMA per code on the VALU
-            comp_us, comp_name = flops / (PEAK_FP32_FMA_TFLOPS * 1e12) * 1e6, "valu_fp32"
-        else:  # matrix cores: three bf16 products per code, 16 vectors per tile
-            mflops = 3.0 * 2.0 * N * K * 16 * (-(-M // 16))
-            comp_us, comp_name = mflops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6, "mfma_bf16"
-        valu_us = comp_us
-        bound = "hbm" if hbm_us >= comp_us else comp_name
-        results.append({"case": name, "N": N, "K": K, "M": M, "us": round(us, 3), "GB/s": round(gbs, 1),
-                        "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "TFLOP/s": round(tflops, 2),
-                        "bound": bound, "pct_of_bound": round(100 * max(hbm_us, valu_us) / us, 1),
-                        "weight_copies": copies})
-        log(f"suite {name}: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM  bound={bound}")
-        for b in (packed, scale, vec, out):
-            b.free()
+        results.append(measure_matvec(stream, "suite " + name, N, K, M, w_f32, x, steps, warmup))
+        results[-1]["case"] = name
 
     c1 = wl.make_config("cfg1")
     matvec_case("cfg1 matvecQ8", c1["N"], c1["K"], 1, c1["w"], c1["x"])
@@ -524,6 +558,9 @@ def main() -> int:
                     help="also measure every BASELINE configuration and write the table (JSON) to PATH")
     ap.add_argument("--prefill-suite", metavar="PATH", default=None,
                     help="measure only the prefill-side ops (matmulQ8, dequant, gather) and write them to PATH")
+    ap.add_argument("--case", metavar="CFG[:M]", default=None,
+                    help="measure one BASELINE configuration alone (e.g. cfg5:16) and print its line (diagnostics, "
+                         "profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="after timing, run this many device copies of the packed weight (counter calibration)")
     args = ap.parse_args()
@@ -537,6 +574,9 @@ def main() -> int:
 
     wxo_q8.init()
     log(wxo_q8.describe())
+    if args.case:
+        print(json.dumps(run_case(wxo_q8.Stream(), args.case, args.steps, args.warmup)), flush=True)
+        return 0
     if args.prefill_suite:
         stream = wxo_q8.Stream()
         table = []
