@@ -204,8 +204,9 @@ def test_variant_names_the_instance_that_ran(cfg, M):
         assert grid[0] * rows >= N > (grid[0] - 1) * rows
         assert form == ("xreg.masked" if W % 256 else "xreg")
     else:
-        assert head.startswith("matvec_q8_mfma")
-        assert int(kv["vectors"]) == M and grid[1] == 1
+        # cfg5 (K = 1024): the k-split kernel, 128 codes per wave, 16 vectors per tile
+        assert head == "matvec_q8_ksplit" and form == "x16"
+        assert int(kv["vectors"]) == M and grid[1] == 1 and int(kv["slots"]) == 1 and int(kv["waves"]) == 8
     # describe() carries the same variant
     assert f'last="{v}"' in wxo_q8.describe()
     # thread-local: another thread's calls do not change this thread's variant

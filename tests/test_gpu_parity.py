@@ -267,15 +267,18 @@ def test_batched_same_sign_long_k(M, K):
 
 
 @pytest.mark.parametrize("M,K", [(5, 1030), (8, 64), (12, 2048), (13, 4099), (16, 1024), (17, 1500), (32, 520),
-                                 (6, 3000), (14, 1000), (16, 768), (13, 1536), (20, 1024), (33, 1000)])
+                                 (6, 3000), (14, 1000), (16, 768), (13, 1536), (20, 1024), (33, 1000),
+                                 (5, 769), (5, 2047), (6, 897), (7, 1024), (8, 1025), (8, 2048), (9, 1100),
+                                 (16, 2048), (16, 2047), (18, 900), (21, 1999)])
 def test_batched_matrix_core_shapes(M, K):
-    # From 16384 rows and 5 vectors the batched call runs on the matrix cores
-    # (when the tile's x parts fit in LDS); smaller shapes take the VALU path,
-    # which the other batched tests cover.  Ragged row tail (N % 16 != 0),
-    # ragged K, vector tiles past 16, full-range codes (-128 included).  16
-    # vectors with K <= 1024 and 13 with 1024 < K <= 1536 take the 8-wave
-    # kernel with 128-code steps, as do 20 and 33 vectors at K <= 1024 (groups
-    # of 16 on grid y, the last one partial).
+    # From 16384 rows and 5 vectors the batched call runs on the matrix cores;
+    # smaller shapes take the VALU path, which the other batched tests cover.
+    # Ragged row tail (N % 16 != 0), ragged K, vector tiles past 16,
+    # full-range codes (-128 included).  768 < K <= 2048 runs the k-split
+    # kernel: 128 codes per wave (K <= 1024) or 256, vectors packed 5 (h|m|l
+    # in one operand), 8 (h|m, l) or 16 per tile (groups on grid y, the last
+    # one partial at 18, 21 and 33); K = 769 and 897 leave waves with no codes
+    # or a partial slice.  Other K run the x-parts-in-LDS kernels.
     rng = np.random.default_rng(M * 1009 + K)
     N = 16397
     w = random_weights(rng, N, K, full_range=True)
@@ -286,7 +289,7 @@ def test_batched_matrix_core_shapes(M, K):
         assert_matvec(ys[m], w, s, xs[m], N, K)
 
 
-@pytest.mark.parametrize("M,K", [(5, 5376), (16, 1536), (16, 1024), (13, 1536)])
+@pytest.mark.parametrize("M,K", [(5, 5376), (16, 1536), (16, 1024), (13, 1536), (16, 2048), (8, 2048), (5, 2048)])
 def test_batched_matrix_core_same_sign_long_k(M, K):
     # The longest K whose x parts still fit in LDS for the tile, all terms
     # positive: the matrix cores' longest accumulation chains.
@@ -303,7 +306,8 @@ def test_batched_matrix_core_same_sign_long_k(M, K):
 
 @pytest.mark.parametrize("M,K,N", [(M, K, 37) for M in (2, 4, 8, 12, 16) for K in (1030, 4096)]
                          + [(M, 1030, 16397) for M in (5, 8, 12, 16)] + [(6, 4096, 16397), (16, 1000, 16397),
-                                                                         (13, 1500, 16397)])
+                                                                         (13, 1500, 16397), (5, 1000, 16397),
+                                                                         (8, 1000, 16397), (4, 1000, 32771)])
 def test_batched_nonfinite_vectors(M, K, N):
     # Inf and NaN entries reach every row as the reference's f64 sum has them
     # (q * Inf = +-Inf, 0 * Inf = NaN), including NaNs whose payload sits only
@@ -325,6 +329,20 @@ def test_batched_nonfinite_vectors(M, K, N):
     for m in range(M):
         assert_matvec(ys[m], w, s, xs[m], N, K)
     assert np.isnan(ys[0]).all()  # every row meets a NaN in vector 0
+
+
+@pytest.mark.parametrize("M,K", [(4, 1024), (4, 1500), (3, 1024), (4, 512)])
+def test_batched_four_vectors_large_n(M, K):
+    # 4 vectors from 32768 rows run on the k-split kernel (5 vectors per tile,
+    # one filled with zeros); 3 vectors and K = 512 stay on the VALU path.
+    rng = np.random.default_rng(M * 31 + K)
+    N = 32771
+    w = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
 
 
 @pytest.mark.parametrize("M", [1, 4, 8, 16])

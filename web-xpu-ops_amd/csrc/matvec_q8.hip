@@ -411,6 +411,21 @@ __device__ __forceinline__ bf16x8 codes_to_bf16(uint32_t w0, uint32_t w1) {
 // output.
 constexpr uint32_t kTileSlotFloats = 16u * 17u;  // one 16 x 16 block, rows skewed by a float
 
+// The bf16 parts of one vector entry as f32 bit patterns (low 16 bits zero):
+// x = h + m + l exactly for finite x.  A NaN whose payload sits in the low 16
+// bits would truncate to an infinity: it becomes the canonical quiet NaN
+// instead; a non-finite x is all h.
+__device__ __forceinline__ void split_x_parts(float xe, uint32_t& hb, uint32_t& mb, uint32_t& lb) {
+    hb = __builtin_isnan(xe) ? 0x7fc00000u : __float_as_uint(xe) & 0xffff0000u;
+    mb = 0u;
+    lb = 0u;
+    if (isfinite(xe)) {
+        const float r1 = xe - __uint_as_float(hb);  // exact
+        mb = __float_as_uint(r1) & 0xffff0000u;
+        lb = __float_as_uint(r1 - __uint_as_float(mb)) & 0xffff0000u;  // exact, <= 8 significant bits
+    }
+}
+
 // Splits the four vector entries k .. k+3 of column m (v; entries past K count
 // as 0) into bf16 parts h, m, l and stores them in B-operand order:
 // [part][32-code block][lane group][column] x 8 bf16.  Code k sits in block
@@ -423,15 +438,8 @@ __device__ __forceinline__ void store_x_parts(uint16_t* xparts, uint32_t MC, uin
     for (int e = 0; e < 4; ++e) {
         // entries past K belong to the next vector (or read 0): zero them
         const float xe = (k + (uint32_t)e < K) ? __uint_as_float(v[e]) : 0.0f;
-        // a NaN whose payload sits in the low 16 bits would truncate to an
-        // infinity: it becomes the canonical quiet NaN instead
-        const uint32_t hb = __builtin_isnan(xe) ? 0x7fc00000u : __float_as_uint(xe) & 0xffff0000u;
-        uint32_t mb = 0u, lb = 0u;
-        if (isfinite(xe)) {
-            const float r1 = xe - __uint_as_float(hb);  // exact
-            mb = __float_as_uint(r1) & 0xffff0000u;
-            lb = __float_as_uint(r1 - __uint_as_float(mb));  // exact, <= 8 significant bits
-        }
+        uint32_t hb, mb, lb;
+        split_x_parts(xe, hb, mb, lb);
         hh[e] = (uint16_t)(hb >> 16);
         mm[e] = (uint16_t)(mb >> 16);
         ll[e] = (uint16_t)(lb >> 16);
@@ -810,6 +818,291 @@ __global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Batched, K up to 2048: the row's codes split across the workgroup's 8 waves
+// (wave w owns codes 128 (w + 8 s) .. +127 of step s = 0 .. SW - 1), so each
+// wave's share of the x parts fits in its VGPRs (12 bf16x8 registers per
+// step and B operand set) and is never read again from LDS; only the weight
+// tiles pass through LDS.  A workgroup walks a contiguous range of 16-row
+// tiles; for each (tile, step) pair a wave fetches its 16 rows x 128 codes
+// (2 KiB, two DMA instructions of 8 rows x 128 bytes, whole lines) into one of
+// kKsStages private LDS stages, kKsStages - 1 pairs ahead of the one it
+// converts and multiplies.  The 8 partial 16 x 16 blocks of a tile meet in
+// LDS: every kKsGroup tiles the waves pass one barrier, and tile t's partials
+// are summed (in wave order) by wave t mod 8, which scales and stores them.
+// The partial sums of a tile are written after the next pair's matrix work is
+// issued, so the write does not hold the next pair's loads back.
+//
+// PACK sets how the x parts fill a B operand's 16 columns:
+//   1: 16 vectors, one part each: h, m, l in three operands (3 matrix ops per
+//      32-code block)
+//   2: up to 8 vectors: h | m side by side, then l | 0 (2 ops); the m column
+//      sums move to the h lanes with a DPP row rotation
+//   3: up to 5 vectors: h | m | l in one operand (1 op)
+// A column's parts are summed as h + (m + l), the order PACK 1 uses too.
+//
+// Measured on MI355X (same-process, rotating weight copies), against the
+// matrix-core kernels above: LM head N = 151936, K = 1024: 16 vectors
+// 38-39 us (45-47), 8 vectors 34-35 (41), 5 vectors 32-33 (41); K = 2048:
+// 16 vectors 71 us (240); N = 32768, K = 2048, 16 vectors 18.5-20 us (58).
+// Of the 16-vector time at K = 1024: the weight stream alone (loads, no
+// matrix work) 29.8 us; the shader clock runs at 1.8-2.1 GHz while the
+// matrix cores work against 2.3-2.4 GHz for the loads alone.
+constexpr int kKsGroup = 2;   // tiles per barrier
+constexpr int kKsStages = 4;  // LDS stages per wave (3 pairs in flight)
+constexpr uint32_t kKsWaves = 8;
+
+template <int CTRL>
+__device__ __forceinline__ f32x4 dpp_f32x4(f32x4 v) {
+    f32x4 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        r[q] = __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v[q]), CTRL, 0xf, 0xf, false));
+    return r;
+}
+
+constexpr int ks_gcd(int a, int b) { return b == 0 ? a : ks_gcd(b, a % b); }
+
+template <int PACK>
+constexpr uint32_t ks_vectors() { return PACK == 1 ? 16u : PACK == 2 ? 8u : 5u; }
+
+template <int SW, int PACK>
+__global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
+    const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
+    float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t ks_lds[];
+    constexpr int G = kKsGroup, D = kKsStages;
+    constexpr uint32_t SC = 128, TBY = 16u * SC;
+    constexpr int GP = G * SW;                          // pairs per group
+    constexpr int PER = GP / ks_gcd(GP, D) * D;         // pairs per unrolled loop body
+    constexpr int NB = PACK == 1 ? 3 : PACK == 2 ? 2 : 1;
+    constexpr uint32_t VPB = ks_vectors<PACK>();
+    static_assert(8 % G == 0, "the reducing wave is the tile index mod 8");
+    const uint32_t m0 = blockIdx.y * VPB;
+    const uint32_t MC = min(VPB, M - m0);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    // B column j carries part `sel` of vector `vj`
+    const uint32_t sel = PACK == 1 ? 0u : PACK == 2 ? j / 8u : j / 5u;
+    const uint32_t vj = PACK == 1 ? j : PACK == 2 ? j % 8u : j % 5u;
+    const bool col_ok = vj < MC && sel < (uint32_t)PACK;
+    uint8_t* wst = ks_lds + wv * ((uint32_t)D * TBY);
+    float* red = reinterpret_cast<float*>(ks_lds + kKsWaves * (uint32_t)D * TBY);  // [2][G][8 waves][64][4]
+    const uint32_t rowbytes = W * 4u;
+    const uint32_t ntiles = (N + 15u) / 16u;
+    const uint32_t b0 = (uint32_t)((uint64_t)blockIdx.x * ntiles / gridDim.x);
+    const uint32_t b1 = (uint32_t)((uint64_t)(blockIdx.x + 1u) * ntiles / gridDim.x);
+    const uint32_t ngroups = (b1 - b0 + G - 1) / G;
+    // The pair count rounded up to whole loop bodies; the loop stops at the
+    // first group past the range.  Tiles past the range within the last group
+    // are empty (zero-length resources) but run, so every wave passes the
+    // same barriers.
+    const uint32_t total = ((ngroups * (uint32_t)GP + PER - 1) / PER) * PER;
+
+    // DMA instruction ii of a pair: lane -> row 8 ii + lane / 8, stored at
+    // position lane % 8, which holds piece (lane % 8) ^ (row % 8)
+    int voff[2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+        const uint32_t row = 8u * (uint32_t)ii + lane / 8u;
+        voff[ii] = (int)(row * rowbytes + (((lane % 8u) ^ (row % 8u)) * 16u));
+    }
+
+    // Memory operations per pair: two DMA instructions, plus the scale load
+    // on a tile's last step (`i % SW` folds to a constant in the unrolled loop,
+    // so the count is fixed per position and the waits below are exact).
+    auto issue = [&](uint32_t i, u32x4v& sc) {
+        const uint32_t ti = i / SW, s = i % SW;
+        const uint32_t c0 = 128u * (wv + kKsWaves * s);
+        const bool ok = b0 + ti < b1 && c0 < K;
+        const uint32_t tile = ok ? b0 + ti : 0u;
+        const uint32_t rows = ok ? min(16u, N - tile * 16u) : 0u;
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)tile * 16u * W, rows * rowbytes);
+        uint8_t* sb = wst + (i % (uint32_t)D) * TBY;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wrs, (__attribute__((address_space(3))) void*)(sb + (uint32_t)ii * 1024u), 16, voff[ii], (int)c0, 0,
+                kCachePolicyNT);
+        if (s == SW - 1u) {
+            const bool mine = b0 + ti < b1 && (ti & 7u) == wv;  // this wave sums and stores the tile
+            const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + (size_t)(mine ? b0 + ti : 0u) * 16u,
+                                                         mine ? min(16u, N - (b0 + ti) * 16u) * 4u : 0u);
+            sc = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(g * 16u), 0, 0);
+        }
+    };
+
+    // This wave's x parts: lane (j, g), step s, block (u, e) holds codes
+    // c0 + 64u + 16g + 8e + 0..7 of vector m0 + vj: the k order in which the
+    // lane reads its A operand (piece 4u + g of row j).  Entries past K are 0
+    // (they would belong to the next vector).
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x + (size_t)m0 * K, MC * K * 4u);
+    u32x4v xl[SW][2][4];
+#pragma unroll
+    for (int s = 0; s < SW; ++s)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t c = 128u * (wv + kKsWaves * (uint32_t)s) + 64u * (uint32_t)u + 16u * g + 4u * (uint32_t)q;
+                const int off = (col_ok && c < K) ? (int)((vj * K + c) * 4u) : (int)0x7ffffff0;
+                xl[s][u][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+            }
+    u32x4v sbuf[D];
+#pragma unroll
+    for (int q = 0; q < D - 1; ++q) issue((uint32_t)q, sbuf[q]);
+
+    bf16x8 bx[SW][2][2][NB];
+#pragma unroll
+    for (int s = 0; s < SW; ++s)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                u32x4v pv[3];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t hw[2], mw[2], lw[2];
+#pragma unroll
+                    for (int z = 0; z < 2; ++z) {
+                        const int idx = 8 * e + 2 * p + z;
+                        const uint32_t c = 128u * (wv + kKsWaves * (uint32_t)s) + 64u * (uint32_t)u + 16u * g + (uint32_t)idx;
+                        const float xe = c < K ? __uint_as_float(xl[s][u][idx / 4][idx % 4]) : 0.0f;
+                        split_x_parts(xe, hw[z], mw[z], lw[z]);
+                    }
+                    pv[0][p] = (hw[0] >> 16) | hw[1];
+                    pv[1][p] = (mw[0] >> 16) | mw[1];
+                    pv[2][p] = (lw[0] >> 16) | lw[1];
+                }
+                const u32x4v zero = {0u, 0u, 0u, 0u};
+                if constexpr (PACK == 1) {
+#pragma unroll
+                    for (int b = 0; b < 3; ++b) bx[s][u][e][b] = __builtin_bit_cast(bf16x8, pv[b]);
+                } else if constexpr (PACK == 2) {
+                    bx[s][u][e][0] = __builtin_bit_cast(bf16x8, sel == 0u ? pv[0] : pv[1]);
+                    bx[s][u][e][1] = __builtin_bit_cast(bf16x8, sel == 0u ? pv[2] : zero);
+                } else {
+                    bx[s][u][e][0] = __builtin_bit_cast(bf16x8, sel == 0u ? pv[0] : sel == 1u ? pv[1] : pv[2]);
+                }
+            }
+
+    f32x4 acc[NB], pacc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = pacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4v rsc = {0u, 0u, 0u, 0u};
+    const uint32_t arow = j * SC;
+
+    auto compute = [&](uint32_t i, int s) {
+        const uint8_t* sb = wst + (i % (uint32_t)D) * TBY;
+        u32x4v a[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            a[u] = *reinterpret_cast<const u32x4v*>(sb + arow + (((4u * (uint32_t)u + g) ^ (j & 7u)) * 16u));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const bf16x8 av = codes_to_bf16(a[u][2 * e], a[u][2 * e + 1]);
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[s][u][e][b], acc[b], 0, 0, 0);
+            }
+    };
+    // A lane's 4 sums (rows 4g .. 4g+3 of column j): valid where sel == 0.
+    // DPP row_ror:n hands lane i the value of lane (i - n) mod 16 of its row.
+    auto combine = [&](const f32x4 (&c)[NB]) -> f32x4 {
+        if constexpr (PACK == 1) return c[0] + (c[1] + c[2]);
+        else if constexpr (PACK == 2) return c[0] + (dpp_f32x4<0x128>(c[0]) + c[1]);
+        else return c[0] + (dpp_f32x4<0x12B>(c[0]) + dpp_f32x4<0x126>(c[0]));
+    };
+    auto red_write = [&](uint32_t ti, const f32x4 (&c)[NB]) {
+        const uint32_t grp = ti / G, t = ti % G;
+        *reinterpret_cast<f32x4*>(red + ((((grp & 1u) * G + t) * kKsWaves + wv) * 64u + lane) * 4u) = combine(c);
+    };
+    auto finish = [&](uint32_t i, int s, bool defer, const u32x4v& sc) {
+        if (s != SW - 1) return;
+        const uint32_t ti = i / SW;
+        if (defer) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) pacc[b] = acc[b];
+        } else {
+            red_write(ti, acc);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if ((ti & 7u) == wv) rsc = sc;
+    };
+    auto reduce = [&](uint32_t grp) {
+        const uint32_t t = (wv - grp * G) & 7u;
+        if (t >= (uint32_t)G) return;
+        const uint32_t ti = grp * G + t;
+        const float* rp = red + ((((grp & 1u) * G + t) * kKsWaves) * 64u + lane) * 4u;
+        f32x4 sum = *reinterpret_cast<const f32x4*>(rp);
+#pragma unroll
+        for (int w = 1; w < (int)kKsWaves; ++w) sum += *reinterpret_cast<const f32x4*>(rp + (uint32_t)w * 256u);
+        const uint32_t tile = b0 + ti;
+        if (tile < b1 && col_ok && sel == 0u) {
+            const uint32_t row = tile * 16u + 4u * g;
+            float* yo = y + (size_t)(m0 + vj) * N + row;
+            if (row + 3u < N) {
+                f32x4 o;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = sum[q] * __uint_as_float(rsc[q]);
+                *reinterpret_cast<f32x4_a4*>(yo) = o;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (row + (uint32_t)q < N) yo[q] = sum[q] * __uint_as_float(rsc[q]);
+            }
+        }
+    };
+
+    // vmcnt for pair i: the memory operations of the D - 1 pairs issued after
+    // it (y stores issued in between only make the wait longer)
+    auto after = [](int par) {
+        int n = 0;
+        for (int r = 1; r < D; ++r) n += 2 + (((par + r) % SW) == SW - 1 ? 1 : 0);
+        return n;
+    };
+    constexpr int kA0 = after(0), kA1 = SW > 1 ? after(1) : after(0);
+    static_assert(kA0 < 64 && kA1 < 64, "vmcnt holds at most 63");
+    constexpr int kVmWait0 = 0x0f70 | (kA0 & 15) | ((kA0 >> 4) << 14);
+    constexpr int kVmWait1 = 0x0f70 | (kA1 & 15) | ((kA1 >> 4) << 14);
+    for (uint32_t i = 0; i < total; i += (uint32_t)PER) {
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            // groups past the range (the loop body is PER pairs long): stop at
+            // the first, the same for every wave of the workgroup
+            if (q % GP == 0 && i + (uint32_t)q >= ngroups * (uint32_t)GP) break;
+            // the stage refilled next was read by the previous pair
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_sched_barrier(0);
+            issue(i + (uint32_t)(q + D - 1), sbuf[(q + D - 1) % D]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q % SW == 0) __builtin_amdgcn_s_waitcnt(kVmWait0);
+            else __builtin_amdgcn_s_waitcnt(kVmWait1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(i + (uint32_t)q, q % SW);
+            if ((q % GP) != 0 && ((q - 1) % SW) == SW - 1) red_write((i + (uint32_t)q - 1u) / SW, pacc);
+            finish(i + (uint32_t)q, q % SW, ((q + 1) % GP) != 0, sbuf[q % D]);
+            if ((q + 1) % GP == 0) {
+                // the group's partials are in LDS: meet, then its tiles' waves
+                // sum them (the other half of the double buffer is written next)
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                reduce((i + (uint32_t)q) / GP);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // no fetch into LDS outlives the workgroup
+}
+
+constexpr uint32_t kKsLdsBytes = kKsWaves * kKsStages * 16u * 128u + 2u * kKsGroup * kKsWaves * 1024u;
+
+// ---------------------------------------------------------------------------
 // Host-side dispatch.
 
 namespace {
@@ -931,6 +1224,22 @@ hipError_t launch_mv(const MatvecArgs& a, hipStream_t stream, Variant* variant) 
     return hipSuccess;
 }
 
+// One workgroup per CU (the LDS stages and partial sums take 128 KiB), each
+// with a contiguous range of 16-row tiles; vector groups of ks_vectors<PACK>()
+// on grid y.
+template <int SW, int PACK>
+hipError_t launch_ksplit(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
+    constexpr uint32_t VPB = ks_vectors<PACK>();
+    const uint32_t ntiles = (a.N + 15u) / 16u;
+    const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    const dim3 grid(ntiles < cus ? ntiles : cus, (a.M + VPB - 1u) / VPB);
+    hipLaunchKernelGGL((matvec_q8_ksplit_kernel<SW, PACK>), grid, dim3(64 * kKsWaves), (size_t)kKsLdsBytes, stream,
+                       a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M);
+    set_variant(variant, "matvec_q8_ksplit", PACK == 1 ? "x16" : PACK == 2 ? "x8" : "x5", (int)kKsWaves, 16, SW,
+                (int)(a.M < VPB ? a.M : VPB), grid.x, grid.y);
+    return hipGetLastError();
+}
+
 // Rows per workgroup: the largest R (up to RMAX) that still gives every SIMD
 // a wave; fewer, fatter blocks load each vector slice fewer times.
 template <int WAVES, int CPW, int RMAX, int MV>
@@ -977,6 +1286,23 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
         return launch_fill_scaled_zero(a.scale, a.output, a.N, a.M, stream);
     }
     if (a.M == 1) return dispatch_m1<kEpiPlain>(a, dev, stream, variant);
+    // Batched, 768 < K <= 2048 on large weights: codes split across a
+    // workgroup's waves, x parts in VGPRs (every wave busy from K > 896; at
+    // K = 512 half of them would idle and the kernels below win).  Against
+    // the kernels below (same-process, MI355X): 1.1-1.5x from 5 vectors at
+    // 16384 <= N <= 151936, 2.6-3.4x at K = 2048 with 16 vectors; with 4
+    // vectors it wins from N = 32768, and the VALU path keeps 2 and 3.
+    if (a.K > 768u && a.K <= 2048u && a.N >= kMfmaMinRows && (a.M >= 5u || (a.M == 4u && a.N >= 32768u)) &&
+        (a.M + 15u) / 16u <= 65535u) {
+        if (a.K <= 1024u) {
+            if (a.M <= 5u) return launch_ksplit<1, 3>(a, dev, stream, variant);
+            if (a.M <= 8u) return launch_ksplit<1, 2>(a, dev, stream, variant);
+            return launch_ksplit<1, 1>(a, dev, stream, variant);
+        }
+        if (a.M <= 5u) return launch_ksplit<2, 3>(a, dev, stream, variant);
+        if (a.M <= 8u) return launch_ksplit<2, 2>(a, dev, stream, variant);
+        return launch_ksplit<2, 1>(a, dev, stream, variant);
+    }
     // Batched.  The matrix-core kernels pay a per-workgroup prologue (the x
     // parts of the whole K for their 16-vector tile, written to LDS) and a
     // 64-byte-per-row load pattern; they win only on large weights with at
