@@ -197,12 +197,16 @@ def test_variant_names_the_instance_that_ran(cfg, M):
     head, form, kv = parse_variant(v)
     grid = [int(t) for t in kv["grid"].split("x")]
     if M == 1:
-        chunks = (W + 255) // 256
+        full, tail = divmod(W, 256)
         assert head == "matvec_q8_m1"
-        assert int(kv["waves"]) == chunks  # one wave per 1 KiB chunk of a row
         rows = int(kv["rows"])
         assert grid[0] * rows >= N > (grid[0] - 1) * rows
-        assert form == ("xreg.masked" if W % 256 else "xreg")
+        if 1 <= tail <= 4 and 1 <= full <= 8:
+            # cfg3 (K = 4099): one wave per whole 1 KiB chunk, the last word rides with wave 0
+            assert form == "xreg.tail" and int(kv["waves"]) == full
+        else:
+            assert int(kv["waves"]) == (W + 255) // 256  # one wave per 1 KiB chunk of a row
+            assert form == ("xreg.masked" if tail else "xreg")
     else:
         # cfg5 (K = 1024): the k-split kernel, 128 codes per wave, 16 vectors per tile
         assert head == "matvec_q8_ksplit" and form == "x16"

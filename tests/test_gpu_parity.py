@@ -146,6 +146,22 @@ def test_matvec_k_sweep(N, K):
     assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
 
 
+@pytest.mark.parametrize("K", [1025, 1028, 1040, 2049, 3076, 4097, 4099, 4100, 4112, 4113, 5121, 6150, 7180, 8193,
+                               8200, 8208, 8209])
+@pytest.mark.parametrize("N", [1, 15, 100, 4097])
+def test_matvec_tail_words(N, K):
+    # Rows of 1 to 8 whole 1024-code chunks plus 1 to 4 words run without a
+    # wave for the partial chunk: wave 0's lanes take the tail words (their
+    # 16-byte loads run into the next row, whose codes meet x entries past K).
+    # K = 4113 and 8209 (5 tail words) keep the masked partial-chunk wave.
+    # Every byte value, pad codes included; row tails at N = 15 and 4097.
+    rng = np.random.default_rng(N * 7919 + K)
+    w = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
+
+
 @pytest.mark.parametrize("K", [4100, 5000, 5632, 7000, 8192, 9000, 11008, 12288, 16384])
 @pytest.mark.parametrize("N", [100, 1000, 4097, 11008])
 def test_matvec_one_wave_per_chunk(N, K):
@@ -398,7 +414,7 @@ def test_residual_kat(case):
 
 FUSED_SHAPES = [(1, 1), (1, 4), (3, 7), (37, 64), (100, 1024), (9, 1030), (70, 2048), (21, 4099), (513, 4096),
                 (5, 8200), (3, 20000), (2000, 300), (4097, 1000), (2048, 5632), (700, 7000), (4097, 8192), (4096, 11008),
-                (300, 16384)]
+                (300, 16384), (100, 1028), (4097, 4100), (33, 8208)]
 
 
 @pytest.mark.parametrize("N,K", FUSED_SHAPES)

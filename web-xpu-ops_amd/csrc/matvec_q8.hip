@@ -121,7 +121,15 @@ __device__ __forceinline__ float residual_epilogue(float r, float projected) {
 // request, instead of reading the next row's words (then multiplied by zero x).
 // Same results; cfg3 (4096 x 4099) 5.02 -> 4.90 us, 4096 x 4352 4.95 -> 4.84;
 // left off for whole chunks, where the extra compare costs ~2 %.
-template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
+//
+// TAIL (rows of WAVES whole chunks plus 1 to 4 words, e.g. K = 4097 .. 4112):
+// no wave for the partial chunk.  Wave 0's lane r also loads row r's last 16
+// bytes (the tail words, then the next row's first words, whose codes meet x
+// entries past K, i.e. 0) and the 16 x entries from 1024 WAVES; the product
+// joins the lane's sum for row r before the wave reduction.  Same-process,
+// against a masked wave for the partial chunk: 4096 x 4099 4.55 us (4.92),
+// 4096 x 8200 7.13 (7.83 on 9 waves), 11008 x 8200 15.8 (18.2).
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
 __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight, const float* __restrict__ scale,
                                              const float* __restrict__ x, float* y, uint32_t N, uint32_t K,
                                              uint32_t W, const uint32_t* __restrict__ weight2, const float* aux,
@@ -130,9 +138,10 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     constexpr int V = R * NWT;                     // dot products per block
     constexpr int SHIFT = 6 - ilog2(V);
     constexpr int XS = CPW > 0 ? CPW : 1;
+    static_assert(!TAIL || (CPW == 1 && !MASK && R <= 64), "the tail form has one whole chunk per wave");
     const int lane = (int)(threadIdx.x & 63u);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t C = (W + kChunkWords - 1) / kChunkWords;
+    const uint32_t C = TAIL ? (uint32_t)WAVES : (W + kChunkWords - 1) / kChunkWords;
     const uint32_t row0 = block * (uint32_t)R;
     const uint32_t rows = min((uint32_t)R, N - row0);  // >= 1
     const uint32_t rowbytes = W * 4u;
@@ -145,6 +154,16 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     if constexpr (CPW > 0) {
 #pragma unroll
         for (int j = 0; j < CPW; ++j) load_x16_rsrc(xrs, wave + (uint32_t)j * WAVES, lane, xr[j]);
+    }
+    u32x4v tw[NWT];
+    float tx[16];
+    if constexpr (TAIL) {
+        if (wave == 0u) {  // wave-uniform
+            const int toff = (uint32_t)lane < rows ? (int)((uint32_t)lane * rowbytes + (uint32_t)WAVES * 1024u) : 0x40000000;
+            tw[0] = load_nt_b128(wrs, toff, 0);
+            if constexpr (NWT == 2) tw[1] = load_nt_b128(wrs2, toff, 0);
+            load_x16_rsrc(xrs, (uint32_t)WAVES, 0, tx);
+        }
     }
     // Keep the issue order as written: the scheduler would otherwise trickle
     // the weight loads in between FMAs to save VGPRs, throttling the bytes in
@@ -187,6 +206,19 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
             acc[r] = a;
         }
     }
+    if constexpr (TAIL) {
+        if (wave == 0u) {
+#pragma unroll
+            for (int n = 0; n < NWT; ++n) {
+                float t = fma_word(tw[n].x, tx[0], tx[1], tx[2], tx[3], 0.0f);
+                t = fma_word(tw[n].y, tx[4], tx[5], tx[6], tx[7], t);
+                t = fma_word(tw[n].z, tx[8], tx[9], tx[10], tx[11], t);
+                t = fma_word(tw[n].w, tx[12], tx[13], tx[14], tx[15], t);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[n * R + r] += lane == r ? t : 0.0f;
+            }
+        }
+    }
 
     wave_reduce_rows<V>(acc, lane);
     const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
@@ -216,11 +248,11 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     }
 }
 
-template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
 __global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
     float* y, uint32_t N, uint32_t K, uint32_t W, const uint32_t* __restrict__ weight2, const float* aux) {
-    m1_row_block<WAVES, CPW, R, EPI, MASK>(weight, scale, x, y, N, K, W, weight2, aux, blockIdx.x);
+    m1_row_block<WAVES, CPW, R, EPI, MASK, TAIL>(weight, scale, x, y, N, K, W, weight2, aux, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -1107,57 +1139,59 @@ constexpr uint32_t kKsLdsBytes = kKsWaves * kKsStages * 16u * 128u + 2u * kKsGro
 
 namespace {
 
-template <int WAVES, int CPW, int R, int EPI, bool MASK = false>
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
 hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, Variant* variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
     const float* aux = EPI == kEpiFfn ? a.scale2 : EPI == kEpiResidual ? a.residual : nullptr;
-    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI, MASK>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
+    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI, MASK, TAIL>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
                        a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.weight2, aux);
     set_variant(variant, EPI == kEpiFfn ? "matvec_q8_m1.ffn" : EPI == kEpiResidual ? "matvec_q8_m1.residual" : "matvec_q8_m1",
-                CPW > 0 ? (MASK ? "xreg.masked" : "xreg") : "xstream", WAVES, R, CPW, 1, nblocks);
+                CPW > 0 ? (TAIL ? "xreg.tail" : MASK ? "xreg.masked" : "xreg") : "xstream", WAVES, R, CPW, 1, nblocks);
     return hipGetLastError();
 }
 
 // Rows per workgroup: the largest R whose grid still gives every CU at least
 // two workgroups (fewer, fatter blocks amortise the per-workgroup vector
-// fetch; too few leave CUs idle).  The fused FFN streams two weights and
+// fetch; too few leave CUs idle), one workgroup for the tail form (cfg3,
+// 4096 x 4099: 16 rows 4.55 us against 8 rows 4.92; 2048 x 4099: 8 rows 3.46
+// against 4 rows 3.60; same-process).  The fused FFN streams two weights and
 // takes at most a quarter of the rows (4 rows of each weight per block:
 // 3-4 % faster than 8 at 5632 x 2048 and 11008 x 4096).
-template <int WAVES, int CPW, int RMAX, int EPI>
+template <int WAVES, int CPW, int RMAX, int EPI, bool TAIL = false>
 hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = EPI == kEpiFfn ? RMAX / 4 : RMAX;
-    const uint32_t want = 2u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    const uint32_t want = (TAIL ? 1u : 2u) * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     if constexpr (RM >= 16) {
-        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16, EPI>(a, stream, variant);
+        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16, EPI, false, TAIL>(a, stream, variant);
     }
     if constexpr (RM >= 8) {
-        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8, EPI>(a, stream, variant);
+        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8, EPI, false, TAIL>(a, stream, variant);
     }
     if constexpr (RM >= 4) {
-        if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4, EPI>(a, stream, variant);
+        if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4, EPI, false, TAIL>(a, stream, variant);
     }
-    return launch_m1<WAVES, CPW, 2, EPI>(a, stream, variant);
+    return launch_m1<WAVES, CPW, 2, EPI, false, TAIL>(a, stream, variant);
 }
 
 // One wave per chunk for 5 to 8 chunks (rows of 4097 .. 8192 codes): the
 // chunks load side by side instead of one wave walking a second slot after
 // its first (6-10 % faster from K = 4099 to 8192, same-process timings).
 // Rows per block: the largest R that still gives 6 waves per CU.
-template <int WAVES, int RMAX, int EPI, bool MASK>
+template <int WAVES, int RMAX, int EPI, bool MASK, bool TAIL = false>
 hipError_t dispatch_m1_wide_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = EPI == kEpiFfn ? RMAX / 2 : RMAX;
     const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
     if constexpr (RM >= 16) {
-        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI, MASK>(a, stream, variant);
+        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI, MASK, TAIL>(a, stream, variant);
     }
     if constexpr (RM >= 8) {
-        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI, MASK>(a, stream, variant);
+        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI, MASK, TAIL>(a, stream, variant);
     }
     if constexpr (RM >= 4) {
-        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI, MASK>(a, stream, variant);
+        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI, MASK, TAIL>(a, stream, variant);
     }
-    return launch_m1<WAVES, 1, 2, EPI, MASK>(a, stream, variant);
+    return launch_m1<WAVES, 1, 2, EPI, MASK, TAIL>(a, stream, variant);
 }
 
 template <int WAVES, int RMAX, int EPI>
@@ -1183,6 +1217,21 @@ hipError_t dispatch_m1_wider(const MatvecArgs& a, const DeviceInfo& dev, hipStre
 
 template <int EPI>
 hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
+    // 1 to 8 whole chunks and 1 to 4 more words: no wave for the partial
+    // chunk; its words ride with wave 0 (the tail form of m1_row_block)
+    if (a.W % kChunkWords >= 1u && a.W % kChunkWords <= 4u) {
+        switch (a.W / kChunkWords) {
+            case 1: return dispatch_m1_rows<1, 1, 16, EPI, true>(a, dev, stream, variant);
+            case 2: return dispatch_m1_rows<2, 1, 16, EPI, true>(a, dev, stream, variant);
+            case 3: return dispatch_m1_rows<3, 1, 16, EPI, true>(a, dev, stream, variant);
+            case 4: return dispatch_m1_rows<4, 1, 16, EPI, true>(a, dev, stream, variant);
+            case 5: return dispatch_m1_wide_rows<5, 16, EPI, false, true>(a, dev, stream, variant);
+            case 6: return dispatch_m1_wide_rows<6, 16, EPI, false, true>(a, dev, stream, variant);
+            case 7: return dispatch_m1_wide_rows<7, 16, EPI, false, true>(a, dev, stream, variant);
+            case 8: return dispatch_m1_wide_rows<8, 16, EPI, false, true>(a, dev, stream, variant);
+            default: break;
+        }
+    }
     const uint32_t C = (a.W + kChunkWords - 1) / kChunkWords;
     if (C == 1) return dispatch_m1_rows<1, 1, 16, EPI>(a, dev, stream, variant);
     if (C == 2) return dispatch_m1_rows<2, 1, 16, EPI>(a, dev, stream, variant);
