@@ -860,7 +860,8 @@ __global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
 // kKsStages private LDS stages, kKsStages - 1 pairs ahead of the one it
 // converts and multiplies.  The 8 partial 16 x 16 blocks of a tile meet in
 // LDS: every kKsGroup tiles the waves pass one barrier, and tile t's partials
-// are summed (in wave order) by wave t mod 8, which scales and stores them.
+// are summed (in wave order) by wave t mod 8, which scales and stores them
+// during the next group's first pair.
 // The partial sums of a tile are written after the next pair's matrix work is
 // issued, so the write does not hold the next pair's loads back.
 //
@@ -1069,9 +1070,15 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
         if (t >= (uint32_t)G) return;
         const uint32_t ti = grp * G + t;
         const float* rp = red + ((((grp & 1u) * G + t) * kKsWaves) * 64u + lane) * 4u;
-        f32x4 sum = *reinterpret_cast<const f32x4*>(rp);
+        // all 8 partials in flight at once (left to itself the compiler keeps
+        // two, and the other waves then wait for this one at the next barrier)
+        f32x4 part[kKsWaves];
 #pragma unroll
-        for (int w = 1; w < (int)kKsWaves; ++w) sum += *reinterpret_cast<const f32x4*>(rp + (uint32_t)w * 256u);
+        for (int w = 0; w < (int)kKsWaves; ++w) part[w] = *reinterpret_cast<const f32x4*>(rp + (uint32_t)w * 256u);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 sum = part[0];
+#pragma unroll
+        for (int w = 1; w < (int)kKsWaves; ++w) sum += part[w];
         const uint32_t tile = b0 + ti;
         if (tile < b1 && col_ok && sel == 0u) {
             const uint32_t row = tile * 16u + 4u * g;
@@ -1100,15 +1107,22 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
     static_assert(kA0 < 64 && kA1 < 64, "vmcnt holds at most 63");
     constexpr int kVmWait0 = 0x0f70 | (kA0 & 15) | ((kA0 >> 4) << 14);
     constexpr int kVmWait1 = 0x0f70 | (kA1 & 15) | ((kA1 >> 4) << 14);
+    uint32_t pending = ~0u;  // a group whose partials are written but not yet summed (wave-uniform)
     for (uint32_t i = 0; i < total; i += (uint32_t)PER) {
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             // groups past the range (the loop body is PER pairs long): stop at
             // the first, the same for every wave of the workgroup
             if (q % GP == 0 && i + (uint32_t)q >= ngroups * (uint32_t)GP) break;
-            // the stage refilled next was read by the previous pair
+            // the stage refilled next was read by the previous pair; if that
+            // iteration ended with a deferred partial-sum write (its last LDS
+            // operation), the write may still be in flight: LDS operations
+            // complete in order, so lgkmcnt(1) already covers the reads
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            if (q > 0 && ((q - 1) % GP) != 0 && ((q - 2 + GP) % SW) == SW - 1 && (q % GP) != 0)
+                __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00 | 0x0100);  // lgkmcnt(1)
+            else
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
             __builtin_amdgcn_sched_barrier(0);
             issue(i + (uint32_t)(q + D - 1), sbuf[(q + D - 1) % D]);
             __builtin_amdgcn_sched_barrier(0);
@@ -1116,19 +1130,29 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
             else __builtin_amdgcn_s_waitcnt(kVmWait1);
             __builtin_amdgcn_sched_barrier(0);
             compute(i + (uint32_t)q, q % SW);
+            // the deferred write stays behind this pair's A reads (the wait above relies on it)
+            __builtin_amdgcn_sched_barrier(0);
             if ((q % GP) != 0 && ((q - 1) % SW) == SW - 1) red_write((i + (uint32_t)q - 1u) / SW, pacc);
             finish(i + (uint32_t)q, q % SW, ((q + 1) % GP) != 0, sbuf[q % D]);
+            if (q % GP == 0 && pending != ~0u) {
+                // the previous group's sums, behind this pair's matrix work
+                // (its partials sit in the half of the double buffer that the
+                // next barrier protects)
+                reduce(pending);
+                pending = ~0u;
+            }
             if ((q + 1) % GP == 0) {
-                // the group's partials are in LDS: meet, then its tiles' waves
-                // sum them (the other half of the double buffer is written next)
+                // the group's partials are in LDS: meet; its tiles' waves sum
+                // them during the next group's first pair
                 __builtin_amdgcn_sched_barrier(0);
                 __builtin_amdgcn_s_waitcnt(0xc07f);
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                reduce((i + (uint32_t)q) / GP);
+                pending = (i + (uint32_t)q) / GP;
             }
         }
     }
+    if (pending != ~0u) reduce(pending);
     __builtin_amdgcn_s_waitcnt(0);  // no fetch into LDS outlives the workgroup
 }
 
