@@ -180,6 +180,27 @@ def parse_variant(v):
     return head, form, kv
 
 
+@pytest.mark.parametrize("N,K,form,extra", [
+    (4096, 4099, "xreg.tailwave", 1),   # 256 blocks: one per CU, the tail words on a wave of their own
+    (2048, 4099, "xreg.tailwave", 1),   # 256 blocks of 8 rows
+    (100, 8200, "xreg.tailwave", 1),
+    (4097, 4099, "xreg.tail", 0),       # 257 blocks: the tail words ride with wave 0
+    (11008, 8200, "xreg.tail", 0),      # 688 blocks of 9 waves would share CUs
+])
+def test_tail_form_choice(N, K, form, extra):
+    """Rows of whole chunks plus 1-4 words: the extra tail wave runs only while
+    the grid is at most one workgroup per CU; either form matches the oracle."""
+    W = (K + 3) // 4
+    rng = np.random.default_rng(N + K)
+    w = rng.integers(0, 2 ** 32, N * W, dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    got = wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K)
+    head, got_form, kv = parse_variant(wxo_q8.last_variant())
+    assert head == "matvec_q8_m1" and got_form == form and int(kv["waves"]) == W // 256 + extra
+    assert_matvec(got, w, s, x, N, K)
+
+
 @pytest.mark.parametrize("cfg,M", [("cfg1", 1), ("cfg2", 1), ("cfg3", 1), ("cfg5", 16)])
 def test_variant_names_the_instance_that_ran(cfg, M):
     c = wl.CONFIGS[cfg]
@@ -202,8 +223,9 @@ def test_variant_names_the_instance_that_ran(cfg, M):
         rows = int(kv["rows"])
         assert grid[0] * rows >= N > (grid[0] - 1) * rows
         if 1 <= tail <= 4 and 1 <= full <= 8:
-            # cfg3 (K = 4099): one wave per whole 1 KiB chunk, the last word rides with wave 0
-            assert form == "xreg.tail" and int(kv["waves"]) == full
+            # cfg3 (K = 4099, 256 blocks of 16 rows, one per CU): one wave per
+            # whole 1 KiB chunk and one more for the rows' last words
+            assert form == "xreg.tailwave" and int(kv["waves"]) == full + 1 and grid[0] <= 256
         else:
             assert int(kv["waves"]) == (W + 255) // 256  # one wave per 1 KiB chunk of a row
             assert form == ("xreg.masked" if tail else "xreg")

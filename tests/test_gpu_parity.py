@@ -151,8 +151,9 @@ def test_matvec_k_sweep(N, K):
 @pytest.mark.parametrize("N", [1, 15, 100, 4097])
 def test_matvec_tail_words(N, K):
     # Rows of 1 to 8 whole 1024-code chunks plus 1 to 4 words run without a
-    # wave for the partial chunk: wave 0's lanes take the tail words (their
-    # 16-byte loads run into the next row, whose codes meet x entries past K).
+    # wave streaming the partial chunk: one extra wave's lanes take the tail
+    # words (their 16-byte loads run into the next row, whose codes meet x
+    # entries past K).
     # K = 4113 and 8209 (5 tail words) keep the masked partial-chunk wave.
     # Every byte value, pad codes included; row tails at N = 15 and 4097.
     rng = np.random.default_rng(N * 7919 + K)

@@ -123,13 +123,26 @@ __device__ __forceinline__ float residual_epilogue(float r, float projected) {
 // left off for whole chunks, where the extra compare costs ~2 %.
 //
 // TAIL (rows of WAVES whole chunks plus 1 to 4 words, e.g. K = 4097 .. 4112):
-// no wave for the partial chunk.  Wave 0's lane r also loads row r's last 16
-// bytes (the tail words, then the next row's first words, whose codes meet x
-// entries past K, i.e. 0) and the 16 x entries from 1024 WAVES; the product
-// joins the lane's sum for row r before the wave reduction.  Same-process,
-// against a masked wave for the partial chunk: 4096 x 4099 4.55 us (4.92),
-// 4096 x 8200 7.13 (7.83 on 9 waves), 11008 x 8200 15.8 (18.2).
-template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
+// no wave streams the partial chunk.  A lane r loads row r's last 16 bytes
+// (the tail words, then the next row's first words, whose codes meet x
+// entries past K, i.e. 0) and the 16 x entries from 1024 WAVES.
+//   kTailWave0 (1): wave 0 does it and adds the product to its row's sum
+//     before the wave reduction.
+//   kTailExtraWave (2): one more wave (wave WAVES) issues that single load and
+//     leaves the sums in LDS for the block's combine.  A wave's loads return
+//     in issue order, so a 17th load on a streaming wave holds back that
+//     wave's whole block; a wave of its own costs a wave slot instead, which
+//     is free while every CU holds one workgroup.
+// Same-process (us), wave 0 -> extra wave: 4096 x 4099 (one workgroup per CU)
+// 4.86 -> 4.67, 2048 x 4099 3.76 -> 3.51, 4096 x 4112 4.91 -> 4.77, 4096 x
+// 8200 7.34 -> 7.30, 11008 x 4100 9.25 -> 9.23, but 11008 x 8200 (688
+// workgroups of 9 waves) 16.1 -> 17.1; no tail at all (wrong results) 4.59 at
+// 4096 x 4099.  Against a masked wave streaming the partial chunk, the wave-0
+// tail had taken 4096 x 4099 from 4.92 us, 4096 x 8200 from 7.83 and 11008 x
+// 8200 from 18.2.
+constexpr int kTailWave0 = 1;
+constexpr int kTailExtraWave = 2;
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, int TAIL = 0>
 __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight, const float* __restrict__ scale,
                                              const float* __restrict__ x, float* y, uint32_t N, uint32_t K,
                                              uint32_t W, const uint32_t* __restrict__ weight2, const float* aux,
@@ -138,7 +151,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     constexpr int V = R * NWT;                     // dot products per block
     constexpr int SHIFT = 6 - ilog2(V);
     constexpr int XS = CPW > 0 ? CPW : 1;
-    static_assert(!TAIL || (CPW == 1 && !MASK && R <= 64), "the tail form has one whole chunk per wave");
+    static_assert(TAIL == 0 || (CPW == 1 && !MASK && R <= 64), "the tail forms have one whole chunk per wave");
     const int lane = (int)(threadIdx.x & 63u);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t C = TAIL ? (uint32_t)WAVES : (W + kChunkWords - 1) / kChunkWords;
@@ -150,6 +163,29 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
         NWT == 2 ? make_rsrc(weight2 + (size_t)row0 * W, rows * rowbytes) : wrs;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, K * 4u);
 
+    // The tail wave's per-row sums (one per streamed weight).
+    __shared__ float tpart[TAIL == kTailExtraWave ? NWT : 1][TAIL == kTailExtraWave ? R : 1];
+    if constexpr (TAIL == kTailExtraWave) {
+        if (wave == (uint32_t)WAVES) {  // wave-uniform: the tail wave
+            const int toff = (uint32_t)lane < rows ? (int)((uint32_t)lane * rowbytes + (uint32_t)WAVES * 1024u) : 0x40000000;
+            u32x4v tw[NWT];
+            float tx[16];
+            tw[0] = load_nt_b128(wrs, toff, 0);
+            if constexpr (NWT == 2) tw[1] = load_nt_b128(wrs2, toff, 0);
+            load_x16_rsrc(xrs, (uint32_t)WAVES, 0, tx);
+#pragma unroll
+            for (int n = 0; n < NWT; ++n) {
+                float t = fma_word(tw[n].x, tx[0], tx[1], tx[2], tx[3], 0.0f);
+                t = fma_word(tw[n].y, tx[4], tx[5], tx[6], tx[7], t);
+                t = fma_word(tw[n].z, tx[8], tx[9], tx[10], tx[11], t);
+                t = fma_word(tw[n].w, tx[12], tx[13], tx[14], tx[15], t);
+                if (lane < R) tpart[n][lane] = t;
+            }
+            __syncthreads();  // the block's one barrier, met by every wave
+            return;
+        }
+    }
+
     float xr[XS][16];
     if constexpr (CPW > 0) {
 #pragma unroll
@@ -157,7 +193,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     }
     u32x4v tw[NWT];
     float tx[16];
-    if constexpr (TAIL) {
+    if constexpr (TAIL == kTailWave0) {
         if (wave == 0u) {  // wave-uniform
             const int toff = (uint32_t)lane < rows ? (int)((uint32_t)lane * rowbytes + (uint32_t)WAVES * 1024u) : 0x40000000;
             tw[0] = load_nt_b128(wrs, toff, 0);
@@ -206,7 +242,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
             acc[r] = a;
         }
     }
-    if constexpr (TAIL) {
+    if constexpr (TAIL == kTailWave0) {
         if (wave == 0u) {
 #pragma unroll
             for (int n = 0; n < NWT; ++n) {
@@ -223,7 +259,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     wave_reduce_rows<V>(acc, lane);
     const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
     const uint32_t rr = (uint32_t)lane >> SHIFT;
-    if constexpr (WAVES == 1 && EPI == kEpiPlain) {
+    if constexpr (WAVES == 1 && EPI == kEpiPlain && TAIL != kTailExtraWave) {
         if (leader && rr < rows) y[row0 + rr] = acc[0] * scale[row0 + rr];
     } else {
         __shared__ float part[WAVES][V];
@@ -234,6 +270,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
             float d = part[0][t];
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) d += part[w][t];
+            if constexpr (TAIL == kTailExtraWave) d += tpart[0][t];
             if constexpr (EPI == kEpiPlain) {
                 y[row] = d * scale[row];
             } else if constexpr (EPI == kEpiResidual) {
@@ -242,14 +279,15 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
                 float du = part[0][R + t];
 #pragma unroll
                 for (int w = 1; w < WAVES; ++w) du += part[w][R + t];
+                if constexpr (TAIL == kTailExtraWave) du += tpart[NWT - 1][t];
                 y[row] = ffn_epilogue(__fmul_rn(d, scale[row]), __fmul_rn(du, aux[row]));
             }
         }
     }
 }
 
-template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
-__global__ __launch_bounds__(WAVES * 64) void matvec_q8_m1_kernel(
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, int TAIL = 0>
+__global__ __launch_bounds__((WAVES + (TAIL == kTailExtraWave ? 1 : 0)) * 64) void matvec_q8_m1_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
     float* y, uint32_t N, uint32_t K, uint32_t W, const uint32_t* __restrict__ weight2, const float* aux) {
     m1_row_block<WAVES, CPW, R, EPI, MASK, TAIL>(weight, scale, x, y, N, K, W, weight2, aux, blockIdx.x);
@@ -1163,15 +1201,32 @@ constexpr uint32_t kKsLdsBytes = kKsWaves * kKsStages * 16u * 128u + 2u * kKsGro
 
 namespace {
 
-template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
-hipError_t launch_m1(const MatvecArgs& a, hipStream_t stream, Variant* variant) {
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, int TAIL = 0>
+hipError_t launch_m1_form(const MatvecArgs& a, hipStream_t stream, Variant* variant) {
     const uint32_t nblocks = (a.N + R - 1) / R;
     const float* aux = EPI == kEpiFfn ? a.scale2 : EPI == kEpiResidual ? a.residual : nullptr;
-    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI, MASK, TAIL>), dim3(nblocks), dim3(WAVES * 64), 0, stream,
+    constexpr int NW = WAVES + (TAIL == kTailExtraWave ? 1 : 0);
+    hipLaunchKernelGGL((matvec_q8_m1_kernel<WAVES, CPW, R, EPI, MASK, TAIL>), dim3(nblocks), dim3(NW * 64), 0, stream,
                        a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.weight2, aux);
     set_variant(variant, EPI == kEpiFfn ? "matvec_q8_m1.ffn" : EPI == kEpiResidual ? "matvec_q8_m1.residual" : "matvec_q8_m1",
-                CPW > 0 ? (TAIL ? "xreg.tail" : MASK ? "xreg.masked" : "xreg") : "xstream", WAVES, R, CPW, 1, nblocks);
+                CPW > 0 ? (TAIL == kTailExtraWave ? "xreg.tailwave" : TAIL ? "xreg.tail" : MASK ? "xreg.masked" : "xreg")
+                        : "xstream",
+                NW, R, CPW, 1, nblocks);
     return hipGetLastError();
+}
+
+// TAIL (bool): rows of whole chunks plus 1 to 4 words.  The extra tail wave
+// when the grid is at most one workgroup per CU (it then takes no CU's wave
+// slots from another workgroup), else the tail words on wave 0.
+template <int WAVES, int CPW, int R, int EPI, bool MASK = false, bool TAIL = false>
+hipError_t launch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
+    if constexpr (TAIL) {
+        const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+        if ((a.N + R - 1) / R <= cus) return launch_m1_form<WAVES, CPW, R, EPI, MASK, kTailExtraWave>(a, stream, variant);
+        return launch_m1_form<WAVES, CPW, R, EPI, MASK, kTailWave0>(a, stream, variant);
+    } else {
+        return launch_m1_form<WAVES, CPW, R, EPI, MASK, 0>(a, stream, variant);
+    }
 }
 
 // Rows per workgroup: the largest R whose grid still gives every CU at least
@@ -1186,15 +1241,15 @@ hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
     constexpr int RM = EPI == kEpiFfn ? RMAX / 4 : RMAX;
     const uint32_t want = (TAIL ? 1u : 2u) * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     if constexpr (RM >= 16) {
-        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16, EPI, false, TAIL>(a, stream, variant);
+        if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16, EPI, false, TAIL>(a, dev, stream, variant);
     }
     if constexpr (RM >= 8) {
-        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8, EPI, false, TAIL>(a, stream, variant);
+        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, CPW, 8, EPI, false, TAIL>(a, dev, stream, variant);
     }
     if constexpr (RM >= 4) {
-        if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4, EPI, false, TAIL>(a, stream, variant);
+        if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, CPW, 4, EPI, false, TAIL>(a, dev, stream, variant);
     }
-    return launch_m1<WAVES, CPW, 2, EPI, false, TAIL>(a, stream, variant);
+    return launch_m1<WAVES, CPW, 2, EPI, false, TAIL>(a, dev, stream, variant);
 }
 
 // One wave per chunk for 5 to 8 chunks (rows of 4097 .. 8192 codes): the
@@ -1207,15 +1262,15 @@ hipError_t dispatch_m1_wide_rows(const MatvecArgs& a, const DeviceInfo& dev, hip
     const uint64_t want = 6u * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     auto waves = [&](uint32_t R) { return (uint64_t)((a.N + R - 1) / R) * WAVES; };
     if constexpr (RM >= 16) {
-        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI, MASK, TAIL>(a, stream, variant);
+        if (waves(16) >= want) return launch_m1<WAVES, 1, 16, EPI, MASK, TAIL>(a, dev, stream, variant);
     }
     if constexpr (RM >= 8) {
-        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI, MASK, TAIL>(a, stream, variant);
+        if (waves(8) >= want) return launch_m1<WAVES, 1, 8, EPI, MASK, TAIL>(a, dev, stream, variant);
     }
     if constexpr (RM >= 4) {
-        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI, MASK, TAIL>(a, stream, variant);
+        if (waves(4) >= want) return launch_m1<WAVES, 1, 4, EPI, MASK, TAIL>(a, dev, stream, variant);
     }
-    return launch_m1<WAVES, 1, 2, EPI, MASK, TAIL>(a, stream, variant);
+    return launch_m1<WAVES, 1, 2, EPI, MASK, TAIL>(a, dev, stream, variant);
 }
 
 template <int WAVES, int RMAX, int EPI>
@@ -1233,16 +1288,16 @@ hipError_t dispatch_m1_wider(const MatvecArgs& a, const DeviceInfo& dev, hipStre
     constexpr int RM = EPI == kEpiFfn ? 4 : 8;
     const uint32_t want = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     if constexpr (RM >= 8) {
-        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, 1, 8, EPI>(a, stream, variant);
+        if ((a.N + 7) / 8 >= want) return launch_m1<WAVES, 1, 8, EPI>(a, dev, stream, variant);
     }
-    if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, 1, 4, EPI>(a, stream, variant);
-    return launch_m1<WAVES, 1, 2, EPI>(a, stream, variant);
+    if ((a.N + 3) / 4 >= want) return launch_m1<WAVES, 1, 4, EPI>(a, dev, stream, variant);
+    return launch_m1<WAVES, 1, 2, EPI>(a, dev, stream, variant);
 }
 
 template <int EPI>
 hipError_t dispatch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
-    // 1 to 8 whole chunks and 1 to 4 more words: no wave for the partial
-    // chunk; its words ride with wave 0 (the tail form of m1_row_block)
+    // 1 to 8 whole chunks and 1 to 4 more words: no wave streams the partial
+    // chunk; one extra wave loads its words (the tail form of m1_row_block)
     if (a.W % kChunkWords >= 1u && a.W % kChunkWords <= 4u) {
         switch (a.W / kChunkWords) {
             case 1: return dispatch_m1_rows<1, 1, 16, EPI, true>(a, dev, stream, variant);
