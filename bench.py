@@ -126,6 +126,59 @@ def time_loop(stream, launch, steps, warmup):
     return e0.elapsed_ms(e1) * 1e3 / steps
 
 
+# Host-issued time_loop measures what a caller issuing one call at a time
+# sees: for a kernel shorter than the host's issue cost per call (~3 us from
+# Python through ctypes, ~2.8 us from C) that is the host's rate, not the
+# GPU's.  time_loop_queued puts a fixed-length spin kernel ahead of the timed
+# launches, so the host has queued them all before the GPU reaches the first:
+# the events then bracket back-to-back execution on the GPU alone.
+
+
+def _spin(stream, us):
+    """A spin kernel of `us` microseconds (the GPU's 100 MHz clock) on `stream`."""
+    _check(wxo_q8.lib().wxo_spin(int(us), stream.handle))
+
+
+def time_loop_queued(stream, launch, steps):
+    """GPU-side mean us per step: `steps` launches queued behind a spin kernel
+    long enough for the host to issue them all, between timing-only events.
+    Returns None if the host did not finish issuing inside the spin."""
+    stream.synchronize()
+    t0 = time.perf_counter()
+    for i in range(5):  # the host's issue time per step, to size the spin
+        launch(i)
+    per_step_us = (time.perf_counter() - t0) * 1e6 / 5
+    stream.synchronize()
+    e0, e1 = wxo_q8.Event(timer=True), wxo_q8.Event(timer=True)
+    spin_us = min(900000.0, 2.0 * per_step_us * steps + 1000.0)
+    _spin(stream, spin_us)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        launch(i)
+    e1.record(stream)
+    host_us = (time.perf_counter() - t0) * 1e6
+    e1.synchronize()
+    if host_us > 0.8 * spin_us:
+        log(f"queued timing: the host took {host_us:.0f} us to issue {steps} steps (spin {spin_us:.0f} us); dropped")
+        return None
+    return e0.elapsed_ms(e1) * 1e3 / steps
+
+
+def time_both(stream, launch, steps, warmup):
+    """(host-issued us per step, GPU-side queued us per step or None)."""
+    us = time_loop(stream, launch, steps, warmup)
+    return us, time_loop_queued(stream, launch, steps)
+
+
+def _q(usq):
+    return None if usq is None else round(usq, 3)
+
+
+def _qs(usq):
+    return "" if usq is None else f"  (queued: {usq:.2f} us)"
+
+
 ROT_TARGET = 600 * 1024 * 1024  # > 2x the 256 MB Infinity Cache
 
 
@@ -149,7 +202,7 @@ def prepare_weights(stream, w_f32, N, K, copies):
     return packed, scale
 
 
-def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup):
+def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup, queued=False):
     """One matvecQ8 configuration on rotated weights: us per call, algorithmic
     GB/s, the bound (HBM, or the compute rate of the path that runs: one-wide
     FP32 FMA for one vector, bf16 matrix cores at three products per code for
@@ -165,8 +218,10 @@ def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup):
     ptrs = [packed.ptr + i * N * W * 4 for i in range(copies)]
     for i in range(copies):  # every copy read once before timing
         _check(L.wxo_matvec_q8(ptrs[i], scale.ptr, vec.ptr, out.ptr, N, K, M, sp))
-    us = time_loop(stream, lambda i: _check(L.wxo_matvec_q8(ptrs[i % copies], scale.ptr, vec.ptr, out.ptr,
-                                                            N, K, M, sp)), steps, warmup)
+    def call(i):
+        _check(L.wxo_matvec_q8(ptrs[i % copies], scale.ptr, vec.ptr, out.ptr, N, K, M, sp))
+    us = time_loop(stream, call, steps, warmup)
+    usq = time_loop_queued(stream, call, steps) if queued else None
     variant = wxo_q8.last_variant()
     gbs = nbytes / (us * 1e-6) / 1e9
     flops = 2.0 * N * K * M
@@ -178,13 +233,16 @@ def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup):
         mflops = 3.0 * 2.0 * N * K * 16 * (-(-M // 16))
         comp_us, comp_name = mflops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6, "mfma_bf16"
     bound = "hbm" if hbm_us >= comp_us else comp_name
-    log(f"{name}: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM  bound={bound}  [{variant}]")
+    log(f"{name}: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM  bound={bound}  [{variant}]{_qs(usq)}")
     for b in (packed, scale, vec, out):
         b.free()
-    return {"case": name, "N": N, "K": K, "M": M, "us": round(us, 3), "GB/s": round(gbs, 1),
-            "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "TFLOP/s": round(tflops, 2),
-            "bound": bound, "pct_of_bound": round(100 * max(hbm_us, comp_us) / us, 1),
-            "weight_copies": copies, "variant": variant}
+    r = {"case": name, "N": N, "K": K, "M": M, "us": round(us, 3), "GB/s": round(gbs, 1),
+         "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "TFLOP/s": round(tflops, 2),
+         "bound": bound, "pct_of_bound": round(100 * max(hbm_us, comp_us) / us, 1),
+         "weight_copies": copies, "variant": variant}
+    if queued:
+        r["us_queued"] = _q(usq)
+    return r
 
 
 def run_case(stream, spec, steps, warmup):
@@ -212,7 +270,7 @@ def run_suite(stream, steps, warmup):
         return prepare_weights(stream, w_f32, N, K, copies)
 
     def matvec_case(name, N, K, M, w_f32, x):
-        results.append(measure_matvec(stream, "suite " + name, N, K, M, w_f32, x, steps, warmup))
+        results.append(measure_matvec(stream, "suite " + name, N, K, M, w_f32, x, steps, warmup, queued=True))
         results[-1]["case"] = name
 
     c1 = wl.make_config("cfg1")
@@ -239,11 +297,12 @@ def run_suite(stream, steps, warmup):
             W = (K + 3) // 4
             check(L.wxo_matvec_q8(packed.ptr + li * N * W * 4, scale.ptr, (vf if K == 5632 else vh).ptr, outb.ptr,
                                   N, K, 1, sp))
-    us = time_loop(stream, layer_step, max(1, steps // 7), max(1, warmup // 7))
+    us, usq = time_both(stream, layer_step, max(1, steps // 7), max(1, warmup // 7))
     gbs = layer_bytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 decoder layer: 7 matvecQ8 calls", "bytes": layer_bytes, "us": round(us, 3),
-                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
-    log(f"suite cfg4 layer: {us:.2f} us/layer  {gbs:.0f} GB/s")
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers,
+                    "us_queued": _q(usq)})
+    log(f"suite cfg4 layer: {us:.2f} us/layer  {gbs:.0f} GB/s{_qs(usq)}")
 
     # The same layer as the resident engine runs its decode projections
     # (llm/engine-q8-resident.ts:1843-1869): q/k/v plain, o_proj and down_proj
@@ -270,12 +329,12 @@ def run_suite(stream, steps, warmup):
         check(L.wxo_matvec_q8_ffn(wg, sg, wu, su, vh.ptr, hidden.ptr, 5632, 2048, sp))
         w, sc = wp("wDown")
         check(L.wxo_matvec_q8_residual(w, sc, vf.ptr, resid.ptr, resid.ptr, 2048, 5632, sp))
-    us = time_loop(stream, fused_step, max(1, steps // 7), max(1, warmup // 7))
+    us, usq = time_both(stream, fused_step, max(1, steps // 7), max(1, warmup // 7))
     gbs = layer_bytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 decoder layer as the resident engine runs it: 3 matvecQ8 + 2 matvecQ8Residual "
                             "+ 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3), "GB/s": round(gbs, 1),
-                    "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
-    log(f"suite cfg4 layer fused: {us:.2f} us/layer  {gbs:.0f} GB/s")
+                    "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers, "us_queued": _q(usq)})
+    log(f"suite cfg4 layer fused: {us:.2f} us/layer  {gbs:.0f} GB/s{_qs(usq)}")
 
     # The same again as the resident batch issues it: the three same-vector
     # projections wq/wk/wv coalesced into one wxo_matvec_q8_multi launch.
@@ -300,12 +359,13 @@ def run_suite(stream, steps, warmup):
         check(L.wxo_matvec_q8_ffn(wg, sg, wu, su, vh.ptr, hidden.ptr, 5632, 2048, sp))
         w, sc = wp("wDown")
         check(L.wxo_matvec_q8_residual(w, sc, vf.ptr, resid.ptr, resid.ptr, 2048, 5632, sp))
-    us = time_loop(stream, coalesced_step, max(1, steps // 7), max(1, warmup // 7))
+    us, usq = time_both(stream, coalesced_step, max(1, steps // 7), max(1, warmup // 7))
     gbs = layer_bytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 decoder layer as the resident batch issues it: wq/wk/wv in one matvecQ8 multi "
                             "launch + 2 matvecQ8Residual + 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3),
-                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers})
-    log(f"suite cfg4 layer coalesced: {us:.2f} us/layer  {gbs:.0f} GB/s")
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers,
+                    "us_queued": _q(usq)})
+    log(f"suite cfg4 layer coalesced: {us:.2f} us/layer  {gbs:.0f} GB/s{_qs(usq)}")
     qkv_out.free()
     resid.free()
     hidden.free()
@@ -321,11 +381,11 @@ def run_suite(stream, steps, warmup):
     def quant_step(i):
         for (N, K, src), (packed, scale) in zip(srcs, outs):
             wxo_q8.quantize_pack_q8_device(src, N, K, packed, scale, stream)
-    us = time_loop(stream, quant_step, max(1, steps // 20), 2)
+    us, usq = time_both(stream, quant_step, max(1, steps // 20), 2)
     gbs = qbytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 quantize+packQ8 (fused) of the 7 matrices", "bytes": qbytes, "us": round(us, 3),
-                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
-    log(f"suite cfg4 quantize+pack: {us:.2f} us  {gbs:.0f} GB/s")
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "us_queued": _q(usq)})
+    log(f"suite cfg4 quantize+pack: {us:.2f} us  {gbs:.0f} GB/s{_qs(usq)}")
 
     # The same seven as the resident batch issues them: matrices with one K
     # in one wxo_quantize_pack_q8_multi launch (K = 2048 x 6, K = 5632 x 1).
@@ -336,12 +396,12 @@ def run_suite(stream, steps, warmup):
     def quant_multi_step(i):
         for K, group in by_k.items():
             wxo_q8.quantize_pack_q8_multi_device(group, K, stream)
-    us = time_loop(stream, quant_multi_step, max(1, steps // 20), 2)
+    us, usq = time_both(stream, quant_multi_step, max(1, steps // 20), 2)
     gbs = qbytes / (us * 1e-6) / 1e9
     results.append({"case": f"cfg4 quantize+packQ8 of the 7 matrices as the resident batch issues them "
                             f"({len(by_k)} launches, one per K)", "bytes": qbytes, "us": round(us, 3),
-                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
-    log(f"suite cfg4 quantize+pack coalesced: {us:.2f} us  {gbs:.0f} GB/s")
+                    "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "us_queued": _q(usq)})
+    log(f"suite cfg4 quantize+pack coalesced: {us:.2f} us  {gbs:.0f} GB/s{_qs(usq)}")
     for (_, _, src), (packed, scale) in zip(srcs, outs):
         src.free()
         packed.free()
@@ -383,14 +443,15 @@ def run_suite(stream, steps, warmup):
     src3 = wxo_q8.DeviceBuffer.from_array(np.random.default_rng(3).integers(-127, 128, N3 * K3 * copies3)
                                           .astype(np.int8), stream)
     dst3 = wxo_q8.DeviceBuffer(N3 * W3 * 4 * copies3)
-    us = time_loop(stream, lambda i: check(L.wxo_pack_int8_rows(src3.ptr + (i % copies3) * N3 * K3, N3, K3,
-                                                                dst3.ptr + (i % copies3) * N3 * W3 * 4, sp)),
-                   max(1, steps // 4), max(1, warmup // 4))
+    us, usq = time_both(stream, lambda i: check(L.wxo_pack_int8_rows(src3.ptr + (i % copies3) * N3 * K3, N3, K3,
+                                                                     dst3.ptr + (i % copies3) * N3 * W3 * 4, sp)),
+                        max(1, steps // 4), max(1, warmup // 4))
     pbytes = N3 * K3 + N3 * W3 * 4
     gbs = pbytes / (us * 1e-6) / 1e9
     results.append({"case": "packInt8Rows on the GPU, device-resident codes, N=4096 K=4099 (ragged)", "bytes": pbytes,
-                    "us": round(us, 3), "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
-    log(f"suite packInt8Rows ragged 4096x4099: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM")
+                    "us": round(us, 3), "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1),
+                    "us_queued": _q(usq)})
+    log(f"suite packInt8Rows ragged 4096x4099: {us:.2f} us  {gbs:.0f} GB/s  {100*gbs/PEAK_HBM_GBS:.1f}% HBM{_qs(usq)}")
     src3.free()
     dst3.free()
     del mats, host_codes
@@ -495,7 +556,7 @@ def run_prefill_suite(stream, steps, warmup, results, check):
     for name, N, K, packed, scale in prepared:
         a = a_f if K == 5632 else a_h
         us = time_loop(stream, lambda i: check(L.wxo_matmul_q8(a.ptr, packed.ptr, scale.ptr, out.ptr, T, N, K, sp)),
-                       max(1, steps // 20), max(1, warmup // 20))
+                       max(1, steps // 20), max(1, warmup // 20))  # 25+ us per call: never host-bound
         flops = 2.0 * T * N * K
         bound_us = 3.0 * flops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6
         total_flops += flops
@@ -521,24 +582,24 @@ def run_prefill_suite(stream, steps, warmup, results, check):
                      ("dequantTranspose", lambda i: check(L.wxo_dequant_transpose(packed.ptr, scale.ptr, N, K,
                                                                                     out2.ptr, sp)))):
         out2 = wxo_q8.DeviceBuffer(N * K * 4)
-        us = time_loop(stream, fn, max(1, steps // 20), max(1, warmup // 20))
+        us, usq = time_both(stream, fn, max(1, steps // 20), max(1, warmup // 20))
         gbs = dq_bytes / (us * 1e-6) / 1e9
         results.append({"case": f"{case} N={N} K={K}", "bytes": dq_bytes, "us": round(us, 3), "GB/s": round(gbs, 1),
-                        "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1)})
-        log(f"suite {case} {N}x{K}: {us:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% HBM")
+                        "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "us_queued": _q(usq)})
+        log(f"suite {case} {N}x{K}: {us:.2f} us  {gbs:.0f} GB/s  {100 * gbs / PEAK_HBM_GBS:.1f}% HBM{_qs(usq)}")
         out2.free()
     rows, D = 32000, 2048
     table = wxo_q8.DeviceBuffer.from_array(rng.integers(-127, 128, rows * D).astype(np.int8), stream)
     tscale = wxo_q8.DeviceBuffer.from_array(rng.uniform(0.001, 0.02, rows).astype(np.float32), stream)
     idx = wxo_q8.DeviceBuffer.from_array(rng.integers(0, rows, T).astype(np.int64), stream)
     g_bytes = T * (D + 4 + 8 + 4 * D)
-    us = time_loop(stream, lambda i: check(L.wxo_gather_dequant_rows(table.ptr, tscale.ptr, rows, D, idx.ptr, T,
-                                                                     out.ptr, sp)),
-                   max(1, steps // 20), max(1, warmup // 20))
+    us, usq = time_both(stream, lambda i: check(L.wxo_gather_dequant_rows(table.ptr, tscale.ptr, rows, D, idx.ptr, T,
+                                                                          out.ptr, sp)),
+                        max(1, steps // 20), max(1, warmup // 20))
     gbs = g_bytes / (us * 1e-6) / 1e9
     results.append({"case": f"gatherDequantRows {T} rows of a {rows}x{D} table", "bytes": g_bytes, "us": round(us, 3),
-                    "GB/s": round(gbs, 1)})
-    log(f"suite gatherDequantRows {T} of {rows}x{D}: {us:.2f} us  {gbs:.0f} GB/s")
+                    "GB/s": round(gbs, 1), "us_queued": _q(usq)})
+    log(f"suite gatherDequantRows {T} of {rows}x{D}: {us:.2f} us  {gbs:.0f} GB/s{_qs(usq)}")
     for b in (a_h, a_f, out, table, tscale, idx):
         b.free()
     for _, _, _, packed, scale in prepared:

@@ -130,6 +130,12 @@ int wxo_event_destroy(wxo_event_t event);
 int wxo_event_record(wxo_event_t event, wxo_stream_t stream);
 int wxo_event_synchronize(wxo_event_t event);
 int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
+/* A one-wave kernel on `stream` that returns after `us` microseconds of the
+ * GPU's constant 100 MHz clock (us <= 1,000,000, else WXO_ERR_INVALID).  A
+ * measurement aid with no counterpart in the reference: launches enqueued
+ * behind it are all queued by the time the GPU reaches them, so events around
+ * them time back-to-back execution rather than the host's issue rate. */
+int wxo_spin(uint32_t us, wxo_stream_t stream);
 
 /* ---- ops on device pointers (asynchronous on `stream`) --------------------- */
 

@@ -68,6 +68,9 @@ def test_validation_happens_before_device_access():
     assert L.wxo_pack_q8(None, 3, 5, None, None) == wxo_q8.WXO_ERR_INVALID
     assert L.wxo_pack_int8_rows(None, 3, 5, None, None) == wxo_q8.WXO_ERR_INVALID
     assert L.wxo_quantize_pack_q8(None, 3, 5, None, None, None) == wxo_q8.WXO_ERR_INVALID
+    # the measurement spin refuses more than a second before touching a device
+    assert L.wxo_spin(1000001, None) == wxo_q8.WXO_ERR_INVALID
+    assert "spin longer than 1 s" in L.wxo_last_error().decode()
     # multi-projection: arrays, per-projection sizes, overlapping outputs
     assert L.wxo_matvec_q8_multi(None, None, None, None, 0, None, 8, None) == wxo_q8.WXO_OK
     assert L.wxo_matvec_q8_multi(None, None, None, None, 2, None, 8, None) == wxo_q8.WXO_ERR_INVALID

@@ -293,3 +293,28 @@ def test_pack_int8_rows_exact_size_input_ends_the_buffer():
         assert_bits_equal(dst.download(np.uint32, N * W), oracle.pack_int8_rows(codes, N, K), f"N={N} K={K}")
         src.free()
         dst.free()
+
+
+def test_spin_holds_the_stream():
+    """wxo_spin: the stream's next work starts after the requested time of the
+    100 MHz clock, and launches queued behind it run back to back."""
+    L = wxo_q8.lib()
+    st = wxo_q8.Stream()
+    e0, e1, e2 = (wxo_q8.Event(timer=True) for _ in range(3))
+    e0.record(st)
+    assert L.wxo_spin(300, st.handle) == wxo_q8.WXO_OK
+    e1.record(st)
+    w = wxo_q8.DeviceBuffer.from_array(np.zeros(64 * 4, np.uint32))
+    s = wxo_q8.DeviceBuffer.from_array(np.ones(64, np.float32))
+    x = wxo_q8.DeviceBuffer.from_array(np.ones(16, np.float32))
+    y = wxo_q8.DeviceBuffer(64 * 4)
+    for _ in range(20):
+        wxo_q8.matvec_q8_device(w, s, x, y, 64, 16, 1, st)
+    e2.record(st)
+    e2.synchronize()
+    spun = e0.elapsed_ms(e1) * 1e3
+    assert 290.0 <= spun < 5000.0, spun
+    assert e1.elapsed_ms(e2) * 1e3 < 20 * 50.0  # 20 small launches, queued: well under 50 us each
+    assert np.all(y.download(np.float32, 64) == 0.0)
+    st.destroy()
+

@@ -363,6 +363,24 @@ int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop) {
     return e == hipSuccess ? ok() : hip_fail(e, "hipEventElapsedTime");
 }
 
+namespace {
+// Waits `ticks` of the 100 MHz real-time counter; every lane leaves once the
+// counter has moved that far, whatever the shader clock does meanwhile.
+__global__ __launch_bounds__(64) void spin_kernel(uint64_t ticks) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+}  // namespace
+
+int wxo_spin(uint32_t us, wxo_stream_t stream) {
+    if (us > 1000000u) return fail(WXO_ERR_INVALID, "spin longer than 1 s");
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipLaunchKernelGGL(spin_kernel, dim3(1), dim3(64), 0, as_hip(stream), (uint64_t)us * 100u);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ok() : hip_fail(e, "spin launch");
+}
+
 // ---- ops on device pointers ------------------------------------------------
 
 int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output, uint32_t N,

@@ -60,6 +60,7 @@ SIGNATURES = {
     "wxo_stream_synchronize": ([_P], _I),
     "wxo_event_create": ([ctypes.POINTER(_P)], _I),
     "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
+    "wxo_spin": ([ctypes.c_uint32, _P], _I),
     "wxo_event_destroy": ([_P], _I),
     "wxo_event_record": ([_P, _P], _I),
     "wxo_event_synchronize": ([_P], _I),
