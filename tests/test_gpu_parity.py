@@ -208,12 +208,17 @@ def test_matvec_nonfinite_scale_and_vector():
     assert np.isnan(y[3])
 
 
-def test_matvec_row_chunks_equal_whole():
+@pytest.mark.parametrize("N,K,chunks", [
+    (1000, 1030, ((0, 333), (333, 1), (334, 666))),  # tail words: extra wave (333, 1) and wave 0 (1000, 666)
+    (4096, 4099, ((0, 2500), (2500, 1596))),         # whole: extra wave; chunks: tail words on wave 0
+    (5632, 2048, ((0, 2048), (2048, 3584))),         # whole chunks: rows per block 2 (whole), 8 and 2
+    (11008, 4096, ((0, 4096), (4096, 6912))),        # rows per block 16, 16 and 16 on different grids
+])
+def test_matvec_row_chunks_equal_whole(N, K, chunks):
     # llm/engine-q8-resident.ts:1214-1230 / llm/kernels.ts:140-151: a caller may
     # run a projection as row chunks on sub-buffers; each chunk must give the
-    # same rows as one whole call.
+    # same rows as one whole call, whatever grid and form each call picks.
     rng = np.random.default_rng(9)
-    N, K = 1000, 1030
     W = (K + 3) // 4
     w = random_weights(rng, N, K)
     s = rng.uniform(0.01, 0.02, N).astype(np.float32)
@@ -222,12 +227,31 @@ def test_matvec_row_chunks_equal_whole():
     whole = wxo_q8.DeviceBuffer(4 * N)
     wxo_q8.matvec_q8_device(bw, bs, bx, whole, N, K)
     parts = wxo_q8.DeviceBuffer(4 * N)
-    for start, count in ((0, 333), (333, 1), (334, 666)):
+    for start, count in chunks:
         wxo_q8.matvec_q8_device(bw.ptr + 4 * W * start, bs.ptr + 4 * start, bx, parts.ptr + 4 * start, count, K)
     a = whole.download(np.float32, N)
     b = parts.download(np.float32, N)
     assert_matvec(a, w, s, x, N, K)
     assert_bits_equal(b, a, "chunked vs whole")
+
+
+@pytest.mark.parametrize("N,K,chunks", [(5632, 2048, ((0, 2048), (2048, 3584))),
+                                        (4096, 4100, ((0, 1000), (1000, 3096)))])
+def test_ffn_row_chunks_equal_whole(N, K, chunks):
+    """The fused FFN form, chunked over rows, gives the whole call's bits."""
+    rng = np.random.default_rng(11)
+    W = (K + 3) // 4
+    wg, wu = random_weights(rng, N, K), random_weights(rng, N, K)
+    sg, su = (rng.uniform(0.01, 0.02, N).astype(np.float32) for _ in range(2))
+    x = rng.standard_normal(K).astype(np.float32)
+    b_wg, b_sg, b_wu, b_su, bx = (wxo_q8.DeviceBuffer.from_array(a) for a in (wg, sg, wu, su, x))
+    whole = wxo_q8.DeviceBuffer(4 * N)
+    wxo_q8.matvec_q8_ffn_device(b_wg, b_sg, b_wu, b_su, bx, whole, N, K)
+    parts = wxo_q8.DeviceBuffer(4 * N)
+    for start, count in chunks:
+        wxo_q8.matvec_q8_ffn_device(b_wg.ptr + 4 * W * start, b_sg.ptr + 4 * start, b_wu.ptr + 4 * W * start,
+                                    b_su.ptr + 4 * start, bx, parts.ptr + 4 * start, count, K)
+    assert_bits_equal(parts.download(np.float32, N), whole.download(np.float32, N), "FFN chunked vs whole")
 
 
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])

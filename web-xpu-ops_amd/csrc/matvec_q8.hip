@@ -126,10 +126,13 @@ __device__ __forceinline__ float residual_epilogue(float r, float projected) {
 // no wave streams the partial chunk.  A lane r loads row r's last 16 bytes
 // (the tail words, then the next row's first words, whose codes meet x
 // entries past K, i.e. 0) and the 16 x entries from 1024 WAVES.
-//   kTailWave0 (1): wave 0 does it and adds the product to its row's sum
-//     before the wave reduction.
-//   kTailExtraWave (2): one more wave (wave WAVES) issues that single load and
-//     leaves the sums in LDS for the block's combine.  A wave's loads return
+//   kTailWave0 (1): wave 0 does it, after its own chunk.
+//   kTailExtraWave (2): one more wave (wave WAVES) issues that single load.
+// Either way the tail sums wait in LDS and join each row's total after the
+// chunk waves' partials, so both forms give the same bits, and a projection
+// run as row chunks gives the same rows as one call, whichever form each
+// call picks (the wave reduction sums every row in the same lane order for
+// any R, since each pairwise add is commutative).  A wave's loads return
 //     in issue order, so a 17th load on a streaming wave holds back that
 //     wave's whole block; a wave of its own costs a wave slot instead, which
 //     is free while every CU holds one workgroup.
@@ -163,8 +166,8 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
         NWT == 2 ? make_rsrc(weight2 + (size_t)row0 * W, rows * rowbytes) : wrs;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, K * 4u);
 
-    // The tail wave's per-row sums (one per streamed weight).
-    __shared__ float tpart[TAIL == kTailExtraWave ? NWT : 1][TAIL == kTailExtraWave ? R : 1];
+    // The tail words' per-row sums (one per streamed weight).
+    __shared__ float tpart[TAIL ? NWT : 1][TAIL ? R : 1];
     if constexpr (TAIL == kTailExtraWave) {
         if (wave == (uint32_t)WAVES) {  // wave-uniform: the tail wave
             const int toff = (uint32_t)lane < rows ? (int)((uint32_t)lane * rowbytes + (uint32_t)WAVES * 1024u) : 0x40000000;
@@ -250,8 +253,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
                 t = fma_word(tw[n].y, tx[4], tx[5], tx[6], tx[7], t);
                 t = fma_word(tw[n].z, tx[8], tx[9], tx[10], tx[11], t);
                 t = fma_word(tw[n].w, tx[12], tx[13], tx[14], tx[15], t);
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[n * R + r] += lane == r ? t : 0.0f;
+                if (lane < R) tpart[n][lane] = t;
             }
         }
     }
@@ -259,7 +261,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
     wave_reduce_rows<V>(acc, lane);
     const bool leader = (lane & ((1 << SHIFT) - 1)) == 0;
     const uint32_t rr = (uint32_t)lane >> SHIFT;
-    if constexpr (WAVES == 1 && EPI == kEpiPlain && TAIL != kTailExtraWave) {
+    if constexpr (WAVES == 1 && EPI == kEpiPlain && TAIL == 0) {
         if (leader && rr < rows) y[row0 + rr] = acc[0] * scale[row0 + rr];
     } else {
         __shared__ float part[WAVES][V];
@@ -270,7 +272,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
             float d = part[0][t];
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) d += part[w][t];
-            if constexpr (TAIL == kTailExtraWave) d += tpart[0][t];
+            if constexpr (TAIL) d += tpart[0][t];
             if constexpr (EPI == kEpiPlain) {
                 y[row] = d * scale[row];
             } else if constexpr (EPI == kEpiResidual) {
@@ -279,7 +281,7 @@ __device__ __forceinline__ void m1_row_block(const uint32_t* __restrict__ weight
                 float du = part[0][R + t];
 #pragma unroll
                 for (int w = 1; w < WAVES; ++w) du += part[w][R + t];
-                if constexpr (TAIL == kTailExtraWave) du += tpart[NWT - 1][t];
+                if constexpr (TAIL) du += tpart[NWT - 1][t];
                 y[row] = ffn_epilogue(__fmul_rn(d, scale[row]), __fmul_rn(du, aux[row]));
             }
         }
@@ -1229,9 +1231,11 @@ hipError_t launch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t str
     }
 }
 
-// Rows per workgroup: the largest R whose grid still gives every CU at least
-// two workgroups (fewer, fatter blocks amortise the per-workgroup vector
-// fetch; too few leave CUs idle), one workgroup for the tail form (cfg3,
+// Rows per workgroup: for whole chunks, an R whose grid is a whole multiple
+// of the CU count when there is one (below); otherwise the largest R whose
+// grid still gives every CU at least two workgroups (fewer, fatter blocks
+// amortise the per-workgroup vector fetch; too few leave CUs idle), one
+// workgroup for the tail form (cfg3,
 // 4096 x 4099: 16 rows 4.55 us against 8 rows 4.92; 2048 x 4099: 8 rows 3.46
 // against 4 rows 3.60; same-process).  The fused FFN streams two weights and
 // takes at most a quarter of the rows (4 rows of each weight per block:
@@ -1239,7 +1243,31 @@ hipError_t launch_m1(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t str
 template <int WAVES, int CPW, int RMAX, int EPI, bool TAIL = false>
 hipError_t dispatch_m1_rows(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr int RM = EPI == kEpiFfn ? RMAX / 4 : RMAX;
-    const uint32_t want = (TAIL ? 1u : 2u) * (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    if constexpr (!TAIL && CPW == 1 && (WAVES == 2 || WAVES == 4)) {
+        // First choice for rows of 2 or 4 chunks: the largest R whose grid is
+        // a whole multiple of the CU count, so that every CU streams the same
+        // bytes; at most 8 rows per block with 2 waves, whose 16-row chain is
+        // too long.  Same-process, launches queued (us): 2048 x 2048 R=8 (256
+        // blocks) 2.83-2.86 against R=4 2.99-3.01; 1024 x 2048 R=4 2.52
+        // against R=2 2.63; 4096 x 4096 R=16 4.70-4.72 against R=8 4.83;
+        // 5632 x 2048 R=2 (2816 blocks) 4.12-4.13 against R=8 (704) 4.24,
+        // its FFN form 5.93-5.95 against 6.07; 4096 x 2048 keeps R=8 (3.83;
+        // R=16 3.74, R=4 3.57).  11008 x 4096 has no such R and keeps R=16.
+        constexpr int RW = WAVES == 2 ? (RM < 8 ? RM : 8) : RM;
+        auto whole = [&](uint32_t R) { const uint32_t nb = (a.N + R - 1) / R; return nb >= cus && nb % cus == 0u; };
+        if constexpr (RW >= 16) {
+            if (whole(16)) return launch_m1<WAVES, CPW, 16, EPI, false, TAIL>(a, dev, stream, variant);
+        }
+        if constexpr (RW >= 8) {
+            if (whole(8)) return launch_m1<WAVES, CPW, 8, EPI, false, TAIL>(a, dev, stream, variant);
+        }
+        if constexpr (RW >= 4) {
+            if (whole(4)) return launch_m1<WAVES, CPW, 4, EPI, false, TAIL>(a, dev, stream, variant);
+        }
+        if (whole(2)) return launch_m1<WAVES, CPW, 2, EPI, false, TAIL>(a, dev, stream, variant);
+    }
+    const uint32_t want = (TAIL ? 1u : 2u) * cus;
     if constexpr (RM >= 16) {
         if ((a.N + 15) / 16 >= want) return launch_m1<WAVES, CPW, 16, EPI, false, TAIL>(a, dev, stream, variant);
     }
