@@ -109,12 +109,20 @@ async function main() {
   await dev.batch(ops);
   const launches = dev.stats.launches - launches0;
   const steps = Math.max(20, Math.floor(calls / 4));
-  us = await timeLoop(steps, () => dev.batch(ops));
   const layerBytes = 4 * (H * (H / 4) * 4) + 2 * (F * (H / 4) * 4) + H * (F / 4) * 4;
-  results.push({ case: `N-API end to end: one decode step, ${L} layers of cfg4 shapes as one resident batch ` +
-                       `(${ops.length} ops, ${launches} launches, one synchronisation)`,
-                 us: +us.toFixed(1), us_per_layer: +(us / L).toFixed(2),
-                 "GB/s": +(L * layerBytes / us / 1e3).toFixed(1) });
+  // op by op (every launch issued each step), then as the device runs a
+  // repeating step list by default: captured once, one graph launch per step
+  for (const graphs of [false, true]) {
+    dev.graphs = graphs;
+    const g0 = dev.stats.graphLaunches;
+    us = await timeLoop(steps, () => dev.batch(ops));
+    const replayed = dev.stats.graphLaunches - g0;
+    results.push({ case: `N-API end to end: one decode step, ${L} layers of cfg4 shapes as one resident batch ` +
+                         `(${ops.length} ops, ${launches} launches, one synchronisation), ` +
+                         (graphs ? "replayed as one captured graph" : "launched op by op"),
+                   us: +us.toFixed(1), us_per_layer: +(us / L).toFixed(2),
+                   "GB/s": +(L * layerBytes / us / 1e3).toFixed(1), graph_launches: replayed });
+  }
   dev.destroy();
   console.log(JSON.stringify({ node: process.version, results }));
 }

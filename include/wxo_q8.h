@@ -87,6 +87,7 @@ typedef enum wxo_status {
 
 typedef struct wxo_stream_opaque* wxo_stream_t; /* hipStream_t */
 typedef struct wxo_event_opaque* wxo_event_t;   /* hipEvent_t */
+typedef struct wxo_graph_opaque* wxo_graph_t;   /* hipGraphExec_t */
 
 /* ---- library / device ---------------------------------------------------- */
 int wxo_abi_version(void);
@@ -136,6 +137,26 @@ int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
  * behind it are all queued by the time the GPU reaches them, so events around
  * them time back-to-back execution rather than the host's issue rate. */
 int wxo_spin(uint32_t us, wxo_stream_t stream);
+
+/* ---- captured batches ------------------------------------------------------
+ * The reference encodes a resident batch's passes into one command encoder
+ * and submits it once (harness/resident.ts:231-382, one submit per decode
+ * step).  Here the same batch is captured once as a HIP graph and replayed:
+ * one launch call per step instead of one per op.
+ *
+ * wxo_graph_capture_begin: from now on, the calling thread's work on `stream`
+ *   (not NULL) is recorded, not run.  Thread-local capture mode: a call of
+ *   this thread that cannot be recorded fails instead of running early.
+ * wxo_graph_capture_end: ends the capture and instantiates it into *graph.  On
+ *   any failure the capture is closed anyway and *graph is NULL.
+ * wxo_graph_launch: runs the graph on `stream` (the kernels read their buffers
+ *   when they run, so buffers keep their addresses and may change contents).
+ * wxo_graph_destroy: frees it (NULL is a no-op).
+ * No op of this library records a memset node. */
+int wxo_graph_capture_begin(wxo_stream_t stream);
+int wxo_graph_capture_end(wxo_stream_t stream, wxo_graph_t* graph);
+int wxo_graph_launch(wxo_graph_t graph, wxo_stream_t stream);
+int wxo_graph_destroy(wxo_graph_t graph);
 
 /* ---- ops on device pointers (asynchronous on `stream`) --------------------- */
 

@@ -274,7 +274,53 @@ gpuTest(F, "engine-shaped decode: pipelineFor / bindGroup / uniforms / dispatch 
   }
   assert.strictEqual(device.stats.buffersCreated, buffers);
   assert.strictEqual(device.stats.pipelinesCreated, pipelines);
+  // the step's op list runs op by op once, is captured at its first repeat and replayed after
+  assert.strictEqual(device.stats.graphsCaptured, 1);
+  assert.strictEqual(device.stats.graphLaunches, 2);
   device.destroy();
+});
+
+gpuTest(F, "captured batches: every replay gives the bits of the same batch issued op by op; a changed op list is captured at its repeat", async () => {
+  const replaying = await createResidentQ8Device();
+  const eager = await createResidentQ8Device({ graphs: false });
+  const [er, ee] = [await buildEngine(replaying), await buildEngine(eager)];
+  const rb = (e) => e.lmHeadChunks.map((c) => ({ source: c.outBuf, sourceOffset: 0, length: c.rowCount, type: "f32" }));
+  const same = (a, b, what) => a.forEach((r, i) => assert.deepStrictEqual(Array.from(r), Array.from(b[i]), `${what} chunk ${i}`));
+  for (let step = 0; step < 5; step += 1) {
+    for (const [d, e] of [[replaying, er], [eager, ee]]) d.upload(e.hidden[0], 0, vec(CFG.hiddenSize, 500 + step));
+    const got = await replaying.batch(decodeOps(er), rb(er));
+    const want = await eager.batch(decodeOps(ee), rb(ee));
+    same(got, want, `step ${step}`);
+    // eager work between replays: a readback-only batch and an upload into a buffer the graph reads
+    const mid = await replaying.batch([], [{ source: er.layers[0].b.q, sourceOffset: 0, length: CFG.qDim, type: "f32" }]);
+    assert.strictEqual(mid[0].length, CFG.qDim);
+  }
+  // step 0 op by op, step 1 captured and launched, steps 2-4 replayed
+  assert.strictEqual(replaying.stats.graphsCaptured, 1);
+  assert.strictEqual(replaying.stats.graphLaunches, 4);
+  assert.strictEqual(eager.stats.graphLaunches, 0);
+  assert.strictEqual(replaying.stats.launches, eager.stats.launches);
+  // a different op list (the last lm_head chunk computes half its rows): op by op the first time,
+  // captured at its repeat; the same bits every time
+  const partial = (e) => {
+    const ops = decodeOps(e);
+    const last = ops[ops.length - 1];
+    ops[ops.length - 1] = { ...last, workgroups: [Math.floor(last.workgroups[0] / 2)] };
+    return ops;
+  };
+  for (let rep = 0; rep < 2; rep += 1) {
+    for (const [d, e] of [[replaying, er], [eager, ee]]) d.upload(e.hidden[0], 0, vec(CFG.hiddenSize, 900 + rep));
+    same(await replaying.batch(partial(er), rb(er)), await eager.batch(partial(ee), rb(ee)), `partial dispatch ${rep}`);
+    assert.strictEqual(replaying.stats.graphsCaptured, 1 + rep);
+  }
+  // and back to the decode list: op by op, then captured again
+  for (let rep = 0; rep < 2; rep += 1) {
+    same(await replaying.batch(decodeOps(er), rb(er)), await eager.batch(decodeOps(ee), rb(ee)), `decode again ${rep}`);
+    assert.strictEqual(replaying.stats.graphsCaptured, 2 + rep);
+  }
+  assert.strictEqual(replaying.stats.graphLaunches, 6);
+  replaying.destroy();
+  eager.destroy();
 });
 
 gpuTest(F, "BatchProfile: per-dispatch GPU times for labelled ops, submitToDoneMs and readbackMs; same results", async () => {

@@ -71,6 +71,11 @@ def test_validation_happens_before_device_access():
     # the measurement spin refuses more than a second before touching a device
     assert L.wxo_spin(1000001, None) == wxo_q8.WXO_ERR_INVALID
     assert "spin longer than 1 s" in L.wxo_last_error().decode()
+    # graph capture needs a stream of its own
+    assert L.wxo_graph_capture_begin(None) == wxo_q8.WXO_ERR_INVALID
+    assert "not the null stream" in L.wxo_last_error().decode()
+    assert L.wxo_graph_launch(None, None) == wxo_q8.WXO_ERR_INVALID
+    assert L.wxo_graph_destroy(None) == wxo_q8.WXO_OK
     # multi-projection: arrays, per-projection sizes, overlapping outputs
     assert L.wxo_matvec_q8_multi(None, None, None, None, 0, None, 8, None) == wxo_q8.WXO_OK
     assert L.wxo_matvec_q8_multi(None, None, None, None, 2, None, 8, None) == wxo_q8.WXO_ERR_INVALID

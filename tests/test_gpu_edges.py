@@ -300,14 +300,16 @@ def test_spin_holds_the_stream():
     100 MHz clock, and launches queued behind it run back to back."""
     L = wxo_q8.lib()
     st = wxo_q8.Stream()
-    e0, e1, e2 = (wxo_q8.Event(timer=True) for _ in range(3))
-    e0.record(st)
-    assert L.wxo_spin(300, st.handle) == wxo_q8.WXO_OK
-    e1.record(st)
     w = wxo_q8.DeviceBuffer.from_array(np.zeros(64 * 4, np.uint32))
     s = wxo_q8.DeviceBuffer.from_array(np.ones(64, np.float32))
     x = wxo_q8.DeviceBuffer.from_array(np.ones(16, np.float32))
     y = wxo_q8.DeviceBuffer(64 * 4)
+    wxo_q8.matvec_q8_device(w, s, x, y, 64, 16, 1, st)  # the kernel's first launch (code object load) untimed
+    st.synchronize()
+    e0, e1, e2 = (wxo_q8.Event(timer=True) for _ in range(3))
+    e0.record(st)
+    assert L.wxo_spin(300, st.handle) == wxo_q8.WXO_OK
+    e1.record(st)
     for _ in range(20):
         wxo_q8.matvec_q8_device(w, s, x, y, 64, 16, 1, st)
     e2.record(st)
@@ -317,4 +319,54 @@ def test_spin_holds_the_stream():
     assert e1.elapsed_ms(e2) * 1e3 < 20 * 50.0  # 20 small launches, queued: well under 50 us each
     assert np.all(y.download(np.float32, 64) == 0.0)
     st.destroy()
+
+
+def test_graph_replays_match_eager_issue():
+    """A captured sequence (three same-vector projections in one launch, a
+    residual projection into the residual stream, a device copy) replayed
+    several times, with eager uploads, eager launches and synchronisations
+    between the replays: every replay equals the same ops issued directly."""
+    rng = np.random.default_rng(21)
+    N, K = 2048, 2048
+    W = (K + 3) // 4
+    ws = [wxo_q8.DeviceBuffer.from_array(rng.integers(0, 2 ** 32, N * W, dtype=np.uint64).astype(np.uint32))
+          for _ in range(4)]
+    sc = wxo_q8.DeviceBuffer.from_array(rng.uniform(0.001, 0.01, N).astype(np.float32))
+    x = wxo_q8.DeviceBuffer(4 * K)
+    qkv = wxo_q8.DeviceBuffer(3 * 4 * N)
+    resid = wxo_q8.DeviceBuffer(4 * N)
+    copy = wxo_q8.DeviceBuffer(4 * N)
+    st = wxo_q8.Stream()
+
+    def ops(stream):
+        wxo_q8.matvec_q8_multi_device([(ws[i].ptr, sc.ptr, qkv.ptr + 4 * N * i, N) for i in range(3)], x.ptr, K,
+                                      stream)
+        wxo_q8.matvec_q8_residual_device(ws[3], sc, qkv, resid, resid, N, K, stream)
+        wxo_q8._check(wxo_q8.lib().wxo_memcpy_dtod(copy.ptr, resid.ptr, 4 * N, stream.handle))
+
+    g = wxo_q8.Graph.capture(st, lambda: ops(st))
+    try:
+        for step in range(4):
+            xv = rng.standard_normal(K).astype(np.float32)
+            r0 = rng.standard_normal(N).astype(np.float32)
+            x.upload(xv)
+            resid.upload(r0)
+            wxo_q8.synchronize()
+            g.launch(st)
+            st.synchronize()
+            got = (qkv.download(np.float32, 3 * N), resid.download(np.float32, N), copy.download(np.float32, N))
+            # the same ops issued directly on the same inputs
+            resid.upload(r0)
+            wxo_q8.synchronize()
+            ops(st)
+            st.synchronize()
+            want = (qkv.download(np.float32, 3 * N), resid.download(np.float32, N), copy.download(np.float32, N))
+            for a, b, what in zip(got, want, ("qkv", "residual", "copy")):
+                assert_bits_equal(a, b, f"step {step} {what}")
+            # eager work of another shape between replays
+            wxo_q8.matvec_q8_device(ws[0], sc, x, copy, 1000, K, 1, st)
+            st.synchronize()
+    finally:
+        g.destroy()
+        st.destroy()
 

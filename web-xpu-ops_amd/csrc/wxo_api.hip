@@ -372,6 +372,44 @@ __global__ __launch_bounds__(64) void spin_kernel(uint64_t ticks) {
 }
 }  // namespace
 
+int wxo_graph_capture_begin(wxo_stream_t stream) {
+    if (!stream) return fail(WXO_ERR_INVALID, "graph capture needs a stream of its own, not the null stream");
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    hipError_t e = hipStreamBeginCapture(as_hip(stream), hipStreamCaptureModeThreadLocal);
+    return e == hipSuccess ? ok() : hip_fail(e, "hipStreamBeginCapture");
+}
+
+int wxo_graph_capture_end(wxo_stream_t stream, wxo_graph_t* graph) {
+    if (!graph) return fail(WXO_ERR_INVALID, "graph is NULL");
+    *graph = nullptr;
+    if (!stream) return fail(WXO_ERR_INVALID, "graph capture needs a stream of its own, not the null stream");
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(as_hip(stream), &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return hip_fail(e, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph = reinterpret_cast<wxo_graph_t>(exec);
+    return ok();
+}
+
+int wxo_graph_launch(wxo_graph_t graph, wxo_stream_t stream) {
+    if (!graph) return fail(WXO_ERR_INVALID, "graph is NULL");
+    hipError_t e = hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipGraphLaunch");
+}
+
+int wxo_graph_destroy(wxo_graph_t graph) {
+    if (!graph) return ok();
+    hipError_t e = hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph));
+    return e == hipSuccess ? ok() : hip_fail(e, "hipGraphExecDestroy");
+}
+
 int wxo_spin(uint32_t us, wxo_stream_t stream) {
     if (us > 1000000u) return fail(WXO_ERR_INVALID, "spin longer than 1 s");
     const wxo::DeviceInfo* d = nullptr;

@@ -52,6 +52,8 @@ export interface BatchProfile {
 export interface ResidentQ8Options {
   /** Run consecutive same-vector matvecQ8 ops as one launch (default true). */
   coalesce?: boolean;
+  /** Capture a batch that repeats its predecessor as a HIP graph and replay it (default true). */
+  graphs?: boolean;
 }
 export declare const BufferUsage: {
   readonly MAP_READ: number; readonly MAP_WRITE: number; readonly COPY_SRC: number; readonly COPY_DST: number;
@@ -60,7 +62,10 @@ export declare const BufferUsage: {
 };
 export declare class ResidentQ8Device {
   constructor(options?: ResidentQ8Options);
-  readonly stats: { buffersCreated: number; pipelinesCreated: number; submits: number; launches: number };
+  readonly stats: { buffersCreated: number; pipelinesCreated: number; submits: number; launches: number;
+    graphsCaptured: number; graphLaunches: number };
+  /** Whether repeating batches are captured and replayed (the `graphs` option). */
+  graphs: boolean;
   readonly timestampsSupported: boolean;
   createStorageBuffer(bytes: number, usage?: number): ResidentBuffer;
   createUniformBuffer(bytes: number): ResidentBuffer;

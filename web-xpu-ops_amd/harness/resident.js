@@ -45,6 +45,18 @@
 // the separate ops; only stats.launches changes.  { coalesce: false } turns
 // it off; a batch with profile labels runs every op on its own, as the
 // reference gives every dispatch its own pass when timing.
+//
+// One launch per step: the reference records a batch into one command
+// encoder and submits it once (harness/resident.ts:231-382).  Here a batch of
+// two or more ops that resolves to the same calls as the batch before it
+// (same kinds, buffers, sizes and K: a decode loop's steps, new contents in
+// the same buffers) is captured as a HIP graph, and replayed for as long as
+// the batches keep resolving to those calls; a batch that matches neither
+// the graph nor its predecessor runs op by op (a one-off list is never
+// captured).  The kernels read their buffers when they run, so uploads
+// between steps are seen.  stats.graphsCaptured / stats.graphLaunches count
+// them; { graphs: false } issues every launch each time, and a profiled batch
+// always does (its events time each op).
 import { native } from "../native/index.js";
 import { recognise, UnsupportedPipelineError, params } from "./wgsl-interface.js";
 
@@ -65,7 +77,11 @@ export class ResidentQ8Device {
     this.addon = native();
     this.addon.init();
     this.coalesce = options.coalesce !== false;
-    this.stats = { buffersCreated: 0, pipelinesCreated: 0, submits: 0, launches: 0 };
+    this.graphs = options.graphs !== false;
+    this.stats = { buffersCreated: 0, pipelinesCreated: 0, submits: 0, launches: 0, graphsCaptured: 0,
+      graphLaunches: 0 };
+    this.graph = null;        // the last captured batch: { handle, key, launches }
+    this.lastKey = null;      // the previous batch's calls (callKey)
     /** HIP events on the device's stream time every labelled op (BatchProfile). */
     this.timestampsSupported = true;
     this.buffers = new Set();
@@ -189,18 +205,8 @@ export class ResidentQ8Device {
     const coalesce = this.coalesce && !labels;
     const a = this.addon;
     const timed = [];
-    for (let i = 0; i < calls.length; i += 1) {
-      const label = labels && labels[i] != null && calls[i].kind !== "copy" ? labels[i] : null;
-      let events = null;
-      if (label !== null) {
-        events = this.eventPair(timed.length);
-        a.eventRecord(events[0]);
-      }
-      i += this.run(calls, i, coalesce) - 1;
-      if (events) {
-        a.eventRecord(events[1]);
-        timed.push({ label, events });
-      }
+    if (!(this.graphs && !labels && calls.length > 1 && this.replay(calls, coalesce))) {
+      this.enqueue(calls, coalesce, labels, timed);
     }
     const t0 = profile ? performanceNow() : 0;
     a.synchronize();
@@ -222,8 +228,62 @@ export class ResidentQ8Device {
     return results;
   }
 
+  /** Enqueues every call (coalesced runs as one launch), with events around labelled ones. */
+  enqueue(calls, coalesce, labels, timed) {
+    const a = this.addon;
+    for (let i = 0; i < calls.length; i += 1) {
+      const label = labels && labels[i] != null && calls[i].kind !== "copy" ? labels[i] : null;
+      let events = null;
+      if (label !== null) {
+        events = this.eventPair(timed.length);
+        a.eventRecord(events[0]);
+      }
+      i += this.run(calls, i, coalesce) - 1;
+      if (events) {
+        a.eventRecord(events[1]);
+        timed.push({ label, events });
+      }
+    }
+  }
+
+  /**
+   * One graph launch for `calls` if they match the captured graph, or the
+   * previous batch (then captured now); false (nothing enqueued) otherwise.
+   */
+  replay(calls, coalesce) {
+    const a = this.addon;
+    const key = callKey(calls, coalesce);
+    const g = this.graph;
+    const last = this.lastKey;
+    this.lastKey = key;
+    if (g === null || !sameKey(g.key, key)) {
+      if (last === null || !sameKey(last, key)) return false;
+      if (g !== null) a.graphDestroy(g.handle);
+      this.graph = null;
+      const before = this.stats.launches;
+      a.graphBegin();
+      let handle = null;
+      try {
+        this.enqueue(calls, coalesce, null, null);
+      } finally {
+        handle = a.graphEnd();
+      }
+      this.graph = { handle, key, launches: this.stats.launches - before };
+      this.stats.graphsCaptured += 1;
+    } else {
+      this.stats.launches += g.launches;
+    }
+    a.graphLaunch(this.graph.handle);
+    this.stats.graphLaunches += 1;
+    return true;
+  }
+
   /** Frees every buffer and event this device created. */
   destroy() {
+    if (this.graph !== null) {
+      this.addon.graphDestroy(this.graph.handle);
+      this.graph = null;
+    }
     for (const b of this.buffers) if (b.ptr !== null) this.addon.free(b.ptr);
     this.buffers.clear();
     for (const [s, e] of this.events) {
@@ -394,6 +454,29 @@ export class ResidentQ8Device {
         throw new TypeError(`unknown resident op kind ${op.kind}`);
     }
   }
+}
+
+/**
+ * The values that decide what a batch enqueues: every call's kind, its
+ * buffers' addresses and its numbers (sizes, K, offsets), in order.
+ */
+function callKey(calls, coalesce) {
+  const key = [coalesce];
+  for (const c of calls) {
+    for (const k in c) {
+      const v = c[k];
+      if (typeof v === "number" || typeof v === "string") key.push(v);
+      else if (v !== null && typeof v === "object" && typeof v.ptr === "bigint") key.push(v.ptr);
+    }
+    key.push(null);
+  }
+  return key;
+}
+
+function sameKey(a, b) {
+  if (a.length !== b.length) return false;
+  for (let i = 0; i < a.length; i += 1) if (a[i] !== b[i]) return false;
+  return true;
 }
 
 function performanceNow() {

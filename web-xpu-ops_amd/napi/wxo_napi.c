@@ -30,8 +30,10 @@
  *   gatherDequantRowsDevice(codes, s, rows, D, indices, count, y)
  *   lastVariant() -> string (wxo_last_variant: the kernel instance of the last op)
  *   eventCreate() -> bigint, eventRecord(ev), eventElapsedMs(start, stop), eventDestroy(ev)
- * Device functions are stream-ordered on the null stream; synchronize()
- * (or any download) waits for them.
+ *   graphBegin(), graphEnd() -> bigint, graphLaunch(graph), graphDestroy(graph)
+ * Device functions are stream-ordered on the null stream (on the capture
+ * stream while a capture is open); synchronize() (or any download) waits for
+ * them.
  * Errors: a TypeError/RangeError for bad arguments, an Error carrying
  * wxo_last_error() (and a numeric `status` property) for a failed call.
  */
@@ -202,6 +204,70 @@ static napi_value js_synchronize(napi_env env, napi_callback_info info) {
     return NULL;
 }
 
+/* ---------------------------------------------------------------- streams and captured batches
+ * Device-pointer ops enqueue on g_stream: the null stream, except while a
+ * batch is being captured (graphBegin .. graphEnd), when it is the addon's
+ * capture stream.  graphBegin() starts recording; graphEnd() -> bigint closes
+ * the capture and instantiates it (wxo_graph_capture_end); graphLaunch(g)
+ * replays it on the capture stream; graphDestroy(g) frees it.  synchronize()
+ * waits for every stream.  upload/download stay synchronous on the null
+ * stream. */
+static wxo_stream_t g_stream = NULL;
+static wxo_stream_t g_capture = NULL;
+
+static napi_value js_graph_begin(napi_env env, napi_callback_info info) {
+    (void)info;
+    if (g_stream != NULL) {
+        napi_throw_error(env, "WXO_NAPI", "graphBegin: a capture is already open");
+        return NULL;
+    }
+    int st = WXO_OK;
+    if (g_capture == NULL) st = wxo_stream_create(&g_capture);
+    if (st == WXO_OK) st = wxo_graph_capture_begin(g_capture);
+    if (st != WXO_OK) return throw_status(env, st, "graphBegin");
+    g_stream = g_capture;
+    return NULL;
+}
+
+static napi_value js_graph_end(napi_env env, napi_callback_info info) {
+    (void)info;
+    if (g_stream == NULL) {
+        napi_throw_error(env, "WXO_NAPI", "graphEnd: no capture is open");
+        return NULL;
+    }
+    wxo_graph_t g = NULL;
+    int st = wxo_graph_capture_end(g_capture, &g);
+    g_stream = NULL;
+    if (st != WXO_OK) return throw_status(env, st, "graphEnd");
+    napi_value r;
+    napi_create_bigint_uint64(env, (uint64_t)(uintptr_t)g, &r);
+    return r;
+}
+
+static napi_value js_graph_launch(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint64_t g;
+    if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &g, "graph")) return NULL;
+    if (g_stream != NULL) {
+        napi_throw_error(env, "WXO_NAPI", "graphLaunch: a capture is open");
+        return NULL;
+    }
+    int st = wxo_graph_launch((wxo_graph_t)(uintptr_t)g, g_capture);
+    if (st != WXO_OK) return throw_status(env, st, "graphLaunch");
+    return NULL;
+}
+
+static napi_value js_graph_destroy(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint64_t g;
+    if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &g, "graph")) return NULL;
+    int st = wxo_graph_destroy((wxo_graph_t)(uintptr_t)g);
+    if (st != WXO_OK) return throw_status(env, st, "graphDestroy");
+    return NULL;
+}
+
 static napi_value js_last_variant(napi_env env, napi_callback_info info) {
     (void)info;
     napi_value r;
@@ -240,7 +306,7 @@ static napi_value js_event_record(napi_env env, napi_callback_info info) {
     napi_value argv[1];
     uint64_t ev;
     if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &ev, "event")) return NULL;
-    int st = wxo_event_record((wxo_event_t)(uintptr_t)ev, NULL);
+    int st = wxo_event_record((wxo_event_t)(uintptr_t)ev, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "eventRecord");
     return NULL;
 }
@@ -663,7 +729,7 @@ static napi_value js_copy(napi_env env, napi_callback_info info) {
         napi_throw_type_error(env, NULL, "bytes must be a non-negative integer");
         return NULL;
     }
-    int st = wxo_memcpy_dtod((void*)(uintptr_t)dst, (const void*)(uintptr_t)src, (size_t)d, NULL);
+    int st = wxo_memcpy_dtod((void*)(uintptr_t)dst, (const void*)(uintptr_t)src, (size_t)d, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "copy");
     return NULL;
 }
@@ -681,7 +747,7 @@ static napi_value js_matvec_q8_device(napi_env env, napi_callback_info info) {
         return NULL;
     if (argc > 6 && !get_u32(env, argv[6], &M, "M")) return NULL;
     int st = wxo_matvec_q8((const uint32_t*)(uintptr_t)w, (const float*)(uintptr_t)s, (const float*)(uintptr_t)x,
-                           (float*)(uintptr_t)y, N, K, M, NULL);
+                           (float*)(uintptr_t)y, N, K, M, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "matvecQ8Device");
     return NULL;
 }
@@ -727,7 +793,7 @@ static napi_value js_matvec_q8_multi_device(napi_env env, napi_callback_info inf
         ys[i] = (float*)(uintptr_t)y;
     }
     if (okay) {
-        int st = wxo_matvec_q8_multi(ws, ss, ys, ns, count, (const float*)(uintptr_t)x, K, NULL);
+        int st = wxo_matvec_q8_multi(ws, ss, ys, ns, count, (const float*)(uintptr_t)x, K, g_stream);
         if (st != WXO_OK) throw_status(env, st, "matvecQ8MultiDevice");
     }
     free(ws);
@@ -776,7 +842,7 @@ static napi_value js_quantize_pack_q8_multi_device(napi_env env, napi_callback_i
         ss[i] = (float*)(uintptr_t)sc;
     }
     if (okay) {
-        int st = wxo_quantize_pack_q8_multi(ins, ns, ps, ss, count, K, NULL);
+        int st = wxo_quantize_pack_q8_multi(ins, ns, ps, ss, count, K, g_stream);
         if (st != WXO_OK) throw_status(env, st, "quantizePackQ8MultiDevice");
     }
     free(ins);
@@ -799,7 +865,7 @@ static napi_value js_matvec_q8_residual_device(napi_env env, napi_callback_info 
         return NULL;
     int st = wxo_matvec_q8_residual((const uint32_t*)(uintptr_t)w, (const float*)(uintptr_t)s,
                                     (const float*)(uintptr_t)x, (const float*)(uintptr_t)r, (float*)(uintptr_t)y, N,
-                                    K, NULL);
+                                    K, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "matvecQ8ResidualDevice");
     return NULL;
 }
@@ -817,7 +883,7 @@ static napi_value js_matvec_q8_ffn_device(napi_env env, napi_callback_info info)
         return NULL;
     int st = wxo_matvec_q8_ffn((const uint32_t*)(uintptr_t)wg, (const float*)(uintptr_t)sg,
                                (const uint32_t*)(uintptr_t)wu, (const float*)(uintptr_t)su,
-                               (const float*)(uintptr_t)x, (float*)(uintptr_t)y, N, K, NULL);
+                               (const float*)(uintptr_t)x, (float*)(uintptr_t)y, N, K, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "matvecQ8FfnDevice");
     return NULL;
 }
@@ -831,7 +897,7 @@ static napi_value js_quantize_device(napi_env env, napi_callback_info info) {
         !get_u32(env, argv[1], &N, "N") || !get_u32(env, argv[2], &D, "D") || !get_ptr(env, argv[3], &out, "output") ||
         !get_ptr(env, argv[4], &sc, "scales"))
         return NULL;
-    int st = wxo_quantize((const float*)(uintptr_t)in, N, D, (int32_t*)(uintptr_t)out, (float*)(uintptr_t)sc, NULL);
+    int st = wxo_quantize((const float*)(uintptr_t)in, N, D, (int32_t*)(uintptr_t)out, (float*)(uintptr_t)sc, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "quantizeDevice");
     return NULL;
 }
@@ -845,7 +911,7 @@ static napi_value pack_device_common(napi_env env, napi_callback_info info, int 
         !get_u32(env, argv[1], &N, "N") || !get_u32(env, argv[2], &K, "K") || !get_ptr(env, argv[3], &packed, "packed"))
         return NULL;
     int st = int8 ? wxo_pack_int8_rows((const int8_t*)(uintptr_t)codes, N, K, (uint32_t*)(uintptr_t)packed, NULL)
-                  : wxo_pack_q8((const int32_t*)(uintptr_t)codes, N, K, (uint32_t*)(uintptr_t)packed, NULL);
+                  : wxo_pack_q8((const int32_t*)(uintptr_t)codes, N, K, (uint32_t*)(uintptr_t)packed, g_stream);
     if (st != WXO_OK) return throw_status(env, st, int8 ? "packInt8RowsDevice" : "packQ8Device");
     return NULL;
 }
@@ -865,7 +931,7 @@ static napi_value js_quantize_pack_q8_device(napi_env env, napi_callback_info in
         !get_ptr(env, argv[3], &packed, "packed") || !get_ptr(env, argv[4], &sc, "scales"))
         return NULL;
     int st = wxo_quantize_pack_q8((const float*)(uintptr_t)in, N, K, (uint32_t*)(uintptr_t)packed,
-                                  (float*)(uintptr_t)sc, NULL);
+                                  (float*)(uintptr_t)sc, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "quantizePackQ8Device");
     return NULL;
 }
@@ -882,7 +948,7 @@ static napi_value js_matmul_q8_device(napi_env env, napi_callback_info info) {
         !get_u32(env, argv[6], &K, "K"))
         return NULL;
     int st = wxo_matmul_q8((const float*)(uintptr_t)a, (const uint32_t*)(uintptr_t)w, (const float*)(uintptr_t)s,
-                           (float*)(uintptr_t)y, N, M, K, NULL);
+                           (float*)(uintptr_t)y, N, M, K, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "matmulQ8Device");
     return NULL;
 }
@@ -900,7 +966,7 @@ static napi_value dequant_device_common(napi_env env, napi_callback_info info, i
     const uint32_t* wp = (const uint32_t*)(uintptr_t)w;
     const float* sp = (const float*)(uintptr_t)s;
     int st = transpose ? wxo_dequant_transpose(wp, sp, N, K, (float*)(uintptr_t)y, NULL)
-                       : wxo_dequantize_packed_q8(wp, sp, N, K, (float*)(uintptr_t)y, NULL);
+                       : wxo_dequantize_packed_q8(wp, sp, N, K, (float*)(uintptr_t)y, g_stream);
     if (st != WXO_OK) return throw_status(env, st, transpose ? "dequantTransposeDevice" : "dequantizePackedQ8Device");
     return NULL;
 }
@@ -923,7 +989,7 @@ static napi_value js_gather_dequant_rows_device(napi_env env, napi_callback_info
         !get_ptr(env, argv[6], &y, "output"))
         return NULL;
     int st = wxo_gather_dequant_rows((const int8_t*)(uintptr_t)c, (const float*)(uintptr_t)s, rows, D,
-                                     (const int64_t*)(uintptr_t)ix, count, (float*)(uintptr_t)y, NULL);
+                                     (const int64_t*)(uintptr_t)ix, count, (float*)(uintptr_t)y, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "gatherDequantRowsDevice");
     return NULL;
 }
@@ -935,6 +1001,10 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"abiVersion", NULL, js_abi_version, NULL, NULL, NULL, napi_enumerable, NULL},
         {"describe", NULL, js_describe, NULL, NULL, NULL, napi_enumerable, NULL},
         {"lastVariant", NULL, js_last_variant, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"graphBegin", NULL, js_graph_begin, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"graphEnd", NULL, js_graph_end, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"graphLaunch", NULL, js_graph_launch, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"graphDestroy", NULL, js_graph_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
         {"eventCreate", NULL, js_event_create, NULL, NULL, NULL, napi_enumerable, NULL},
         {"eventDestroy", NULL, js_event_destroy, NULL, NULL, NULL, napi_enumerable, NULL},
         {"eventRecord", NULL, js_event_record, NULL, NULL, NULL, napi_enumerable, NULL},

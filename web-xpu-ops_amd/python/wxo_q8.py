@@ -61,6 +61,10 @@ SIGNATURES = {
     "wxo_event_create": ([ctypes.POINTER(_P)], _I),
     "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
     "wxo_spin": ([ctypes.c_uint32, _P], _I),
+    "wxo_graph_capture_begin": ([_P], _I),
+    "wxo_graph_capture_end": ([_P, ctypes.POINTER(_P)], _I),
+    "wxo_graph_launch": ([_P, _P], _I),
+    "wxo_graph_destroy": ([_P], _I),
     "wxo_event_destroy": ([_P], _I),
     "wxo_event_record": ([_P, _P], _I),
     "wxo_event_synchronize": ([_P], _I),
@@ -201,6 +205,35 @@ class Stream:
     def destroy(self) -> None:
         if self.handle:
             _check(lib().wxo_stream_destroy(self.handle))
+            self.handle = None
+
+
+class Graph:
+    """Ops of this library captured once on a stream and replayed
+    (wxo_graph_capture_begin/_end, wxo_graph_launch)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @staticmethod
+    def capture(stream: "Stream", record) -> "Graph":
+        """Runs `record()` with `stream` capturing, and returns the graph; the
+        capture is closed whatever `record` does."""
+        _check(lib().wxo_graph_capture_begin(stream.handle))
+        p = ctypes.c_void_p(0)
+        try:
+            record()
+        finally:
+            st = lib().wxo_graph_capture_end(stream.handle, ctypes.byref(p))
+        _check(st)
+        return Graph(p.value)
+
+    def launch(self, stream: "Stream") -> None:
+        _check(lib().wxo_graph_launch(self.handle, stream.handle))
+
+    def destroy(self) -> None:
+        if self.handle:
+            _check(lib().wxo_graph_destroy(self.handle))
             self.handle = None
 
 
