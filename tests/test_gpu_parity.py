@@ -307,6 +307,28 @@ def test_batched_same_sign_long_k(M, K):
         assert_matvec(ys[m], w, s, xs[m], N, K)
 
 
+@pytest.mark.parametrize("N,K,M,kernel", [
+    (11008, 2048, 5, "matvec_q8_ksplit"), (11003, 2048, 16, "matvec_q8_ksplit"), (5632, 2048, 12, "matvec_q8_ksplit"),
+    (8191, 1900, 24, "matvec_q8_ksplit"), (2048, 2048, 32, "matvec_q8_ksplit"), (2047, 1500, 32, "matvec_q8_ksplit"),
+    (8192, 1024, 5, "matvec_q8_ksplit"), (5632, 1000, 8, "matvec_q8_ksplit"), (4096, 1024, 16, "matvec_q8_ksplit"),
+    (4100, 800, 12, "matvec_q8_ksplit"),
+    (4096, 2048, 16, "matvec_q8_mv"), (11008, 2048, 4, "matvec_q8_mv"), (2048, 2048, 16, "matvec_q8_mv"),
+    (4096, 2048, 32, "matvec_q8_mv"), (4096, 1024, 24, "matvec_q8_mv"), (5632, 768, 16, "matvec_q8_mv"),
+])
+def test_batched_decoder_sized_weights(N, K, M, kernel):
+    # Below 16384 rows the k-split kernel runs where it beats the VALU path
+    # (enough rows times vectors for its fixed pass, or 32 vectors in one
+    # round of workgroups); ragged rows and K, full-range codes.
+    rng = np.random.default_rng(N * 31 + K + M)
+    w = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(0.001, 0.05, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    ys = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs, N=N, K=K, M=M)
+    assert wxo_q8.last_variant().split(" ")[0] == kernel, wxo_q8.last_variant()
+    for m in range(M):
+        assert_matvec(ys[m], w, s, xs[m], N, K)
+
+
 @pytest.mark.parametrize("M,K", [(5, 1030), (8, 64), (12, 2048), (13, 4099), (16, 1024), (17, 1500), (32, 520),
                                  (6, 3000), (14, 1000), (16, 768), (13, 1536), (20, 1024), (33, 1000),
                                  (5, 769), (5, 2047), (6, 897), (7, 1024), (8, 1025), (8, 2048), (9, 1100),

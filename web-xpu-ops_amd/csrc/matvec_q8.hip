@@ -1448,8 +1448,26 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
     // the kernels below (same-process, MI355X): 1.1-1.5x from 5 vectors at
     // 16384 <= N <= 151936, 2.6-3.4x at K = 2048 with 16 vectors; with 4
     // vectors it wins from N = 32768, and the VALU path keeps 2 and 3.
-    if (a.K > 768u && a.K <= 2048u && a.N >= kMfmaMinRows && (a.M >= 5u || (a.M == 4u && a.N >= 32768u)) &&
-        (a.M + 15u) / 16u <= 65535u) {
+    // Below 16384 rows (decoder-sized weights) it wins where the VALU path's
+    // M + 1 operations per code outgrow the k-split kernel's cost, about one
+    // fixed pass (~10 us at K = 2048, ~6 us at K = 1024) per round of one
+    // workgroup per CU.  Same-process, launches queued, VALU -> k-split (us):
+    // K = 2048: 11008 rows x 5 / 16 vectors 14.4 -> 10.9 / 23.9 -> 12.8,
+    // 5632 x 12 / 16 15.4 -> 9.9 / 16.2 -> 10.9, 2048 x 32 12.6 -> 10.5;
+    // K = 1024: 8192 x 5 6.7 -> 6.3, 5632 x 8 6.7 -> 6.2, 4096 x 16 7.5 ->
+    // 6.6.  The VALU path keeps 4096 rows at K = 2048 (9.7 against 10.7 at 16
+    // vectors), 4 vectors, and two or more rounds at 4096 rows or fewer.
+    const auto ksplit_small = [&]() {
+        const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+        const uint32_t ntiles = (a.N + 15u) / 16u;
+        const bool one_round = (uint64_t)(ntiles < cus ? ntiles : cus) * ((a.M + 15u) / 16u) <= cus;
+        if (a.M >= 32u && one_round) return true;
+        if (a.K > 1024u) return (a.N >= 11008u && a.M >= 5u) || (a.N >= 5632u && a.M >= 12u);
+        return (a.N >= 8192u && a.M >= 5u) || (a.N >= 5632u && a.M >= 8u) ||
+               (a.N >= 4096u && a.M >= 12u && a.M <= 16u);
+    };
+    if (a.K > 768u && a.K <= 2048u && (a.M + 15u) / 16u <= 65535u &&
+        (a.N >= kMfmaMinRows ? (a.M >= 5u || (a.M == 4u && a.N >= 32768u)) : ksplit_small())) {
         if (a.K <= 1024u) {
             if (a.M <= 5u) return launch_ksplit<1, 3>(a, dev, stream, variant);
             if (a.M <= 8u) return launch_ksplit<1, 2>(a, dev, stream, variant);
