@@ -572,6 +572,31 @@ def run_prefill_suite(stream, steps, warmup, results, check):
                     "pct_of_bound": round(100 * bound_us / total_us, 1)})
     log(f"suite prefill layer: {total_us:.1f} us  {total_flops / (total_us * 1e-6) / 1e12:.1f} TFLOP/s")
 
+    # The same layer as the resident batch issues it: projections of the same
+    # activations (q, k, v; gate, up) in one wxo_matmul_q8_multi launch each.
+    by = {name: (N, K, packed, scale) for name, N, K, packed, scale in prepared}
+    outs = {name: wxo_q8.DeviceBuffer(T * N * 4) for name, N, _, _, _ in prepared}
+    groups = [(a_h, ("wq", "wk", "wv")), (a_h, ("wo",)), (a_h, ("wGate", "wUp")), (a_f, ("wDown",))]
+    layer_us = 0.0
+    for act, names in groups:
+        K = by[names[0]][1]
+        projs = [(by[n][2].ptr, by[n][3].ptr, outs[n].ptr, by[n][0]) for n in names]
+        us = time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, T, K, stream),
+                       max(1, steps // 20), max(1, warmup // 20))
+        flops = sum(2.0 * T * by[n][0] * K for n in names)
+        layer_us += us
+        results.append({"case": f"prefill matmulQ8 {'+'.join(names)} in one launch: tokens={T} K={K}",
+                        "us": round(us, 3), "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
+                        "variant": wxo_q8.last_variant()})
+        log(f"suite prefill {'+'.join(names)} one launch: {us:.2f} us  {flops / (us * 1e-6) / 1e12:.1f} TFLOP/s")
+    results.append({"case": f"prefill matmulQ8: one decoder layer, {T} tokens, as the resident batch issues it "
+                            f"(q/k/v and gate/up each in one launch: 4 launches)", "us": round(layer_us, 3),
+                    "TFLOP/s": round(total_flops / (layer_us * 1e-6) / 1e12, 1),
+                    "pct_of_bound": round(100 * bound_us / layer_us, 1)})
+    log(f"suite prefill layer, coalesced: {layer_us:.1f} us  {total_flops / (layer_us * 1e-6) / 1e12:.1f} TFLOP/s")
+    for b in outs.values():
+        b.free()
+
     # dequantizePackedQ8 and dequantTranspose of the gate projection, gather of
     # the prompt's rows from a 32000 x 2048 int8 embedding table
     _, N, K, packed, scale = prepared[4]

@@ -226,6 +226,17 @@ int wxo_quantize_pack_q8_multi(const float* const* inputs, const uint32_t* Ns, u
  * sum of per-term dequantized products.  K = 0 gives zeros.  K <= 2^22. */
 int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* output, uint32_t N,
                   uint32_t M, uint32_t K, wxo_stream_t stream);
+/* matmulQ8 of several weights on the same activations a [N, K]: outputs[p]
+ * f32 [N, Ms[p]] = wxo_matmul_q8(a, weights[p], scales[p], N, Ms[p], K), in one
+ * launch per 4 projections (their tiles shared out together: a prompt's q, k, v
+ * or gate and up).  The reference issues one matmulQ8 dispatch per
+ * projection (ops/matmul/reference.ts:124-137 per call); results are within the
+ * same bound of it, not bit-equal to the single calls (the tile shape follows
+ * the launch's total work).  The arrays are host memory; outputs must not
+ * overlap a, each other, or any weight or scale. */
+int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const float* const* scales,
+                        float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                        wxo_stream_t stream);
 
 /* dequantizePackedQ8: output f32 [N, K], output[n*K + k] = q[n, k] * scale[n] rounded to
  * f32 once (bit-exact to the reference). */

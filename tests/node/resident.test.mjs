@@ -402,6 +402,54 @@ gpuTest(F, "validation: bad pipelines, bind groups, dispatches and buffers throw
   device.destroy();
 });
 
+gpuTest(F, "consecutive matmulQ8 dispatches on one activation buffer (a prompt's q, k, v) run as one launch, against the oracle", async () => {
+  const device = await createResidentQ8Device({ graphs: false });
+  const pipeline = await device.pipelineFor(MATMUL_Q8);
+  const N = 40, K = 520, rows = [96, 32, 32];  // tokens, columns, rows of q, k, v
+  const a = vec(N * K, 91);
+  const aBuf = device.createStorageBuffer(a.byteLength);
+  device.upload(aBuf, 0, a);
+  const proj = [];
+  for (const [i, M] of rows.entries()) {
+    const lin = linear(M, K, 92 + i);
+    const packed = packInt8Rows(lin.codes, M, K);
+    const w = device.createStorageBuffer(packed.byteLength);
+    device.upload(w, 0, packed);
+    const s = device.createStorageBuffer(M * 4);
+    device.upload(s, 0, lin.scale);
+    const out = device.createStorageBuffer(N * M * 4);
+    const u = device.createUniformBuffer(12);
+    device.upload(u, 0, new Uint8Array(params([["u32", N], ["u32", M], ["u32", K]])));
+    proj.push({ M, packed, scale: lin.scale, out, group: await device.bindGroup(pipeline, [aBuf, w, s, out, u]) });
+  }
+  const ops = proj.map((p) => ({ kind: "dispatch", pipeline, bindGroup: p.group, workgroups: [Math.ceil(p.M / 16), Math.ceil(N / 16)] }));
+  const rb = proj.map((p) => ({ source: p.out, sourceOffset: 0, length: N * p.M, type: "f32" }));
+  const launches = device.stats.launches;
+  const got = await device.batch(ops, rb);
+  assert.strictEqual(device.stats.launches - launches, 1);
+  proj.forEach((p, i) => {
+    const want = oracle.matmulQ8({ a, weight: p.packed, scale: p.scale, N, M: p.M, K });
+    const W = Math.ceil(K / 4);
+    for (let n = 0; n < N; n += 1) {
+      for (let m = 0; m < p.M; m += 1) {
+        let bound = 0;
+        for (let k = 0; k < K; k += 1) {
+          const byte = (p.packed[m * W + (k >> 2)] >>> ((k & 3) * 8)) & 0xff;
+          bound += Math.abs(a[n * K + k] * Math.fround((byte >= 128 ? byte - 256 : byte) * p.scale[m]));
+        }
+        const err = Math.abs(got[i][n * p.M + m] - want[n * p.M + m]);
+        if (!(err <= 1e-5 * bound + 1e-7)) assert.fail(`projection ${i} [${n}, ${m}] got ${got[i][n * p.M + m]} want ${want[n * p.M + m]}`);
+      }
+    }
+  });
+  // an op between them that writes the activations ends the run
+  const copy = { kind: "copy", src: proj[0].out, srcOffset: 0, dst: aBuf, dstOffset: 0, size: 64 };
+  const before = device.stats.launches;
+  await device.batch([ops[0], copy, ops[1], ops[2]]);
+  assert.strictEqual(device.stats.launches - before, 3);
+  device.destroy();
+});
+
 gpuTest(F, "matmulQ8 dispatch (prefill) through the resident device, against the oracle", async () => {
   const device = await createResidentQ8Device();
   const pipeline = await device.pipelineFor(MATMUL_Q8);

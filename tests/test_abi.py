@@ -86,6 +86,12 @@ def test_validation_happens_before_device_access():
                                       0x30000, 8)
     with pytest.raises(wxo_q8.WxoError, match="projection 0: output overlaps the vector"):
         wxo_q8.matvec_q8_multi_device([(16, 16, 0x3001c, 4)], 0x30000, 8)
+    # multi-projection matmul: outputs disjoint from the activations and each other
+    assert L.wxo_matmul_q8_multi(None, None, None, None, None, 0, 4, 8, None) == wxo_q8.WXO_OK
+    with pytest.raises(wxo_q8.WxoError, match="outputs of projections 0 and 1 overlap"):
+        wxo_q8.matmul_q8_multi_device(0x30000, [(0x10000, 0x20000, 0x40000, 4), (0x11000, 0x21000, 0x40010, 4)], 2, 8)
+    with pytest.raises(wxo_q8.WxoError, match="projection 0: output overlaps the activations"):
+        wxo_q8.matmul_q8_multi_device(0x30000, [(0x10000, 0x20000, 0x30010, 4)], 2, 8)
     with pytest.raises(wxo_q8.WxoError, match="projection 1: output overlaps the weight or scale of projection 0"):
         wxo_q8.matvec_q8_multi_device([(0x50000, 0x60000, 0x10000, 4), (16, 16, 0x50004, 4)], 0x30000, 8)
     assert L.wxo_quantize_pack_q8_multi(None, None, None, None, 0, 8, None) == wxo_q8.WXO_OK

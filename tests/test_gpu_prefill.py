@@ -229,6 +229,42 @@ def test_matmul_prefill_layer_projection(M, K):
     assert_matmul(y, a, w, s, N, M, K, rows=[0, 1, 63, 64, 200, 511])
 
 
+@pytest.mark.parametrize("N,K,Ms", [
+    (512, 2048, (2048, 2048, 2048)),       # a prompt's q, k, v: one launch
+    (512, 2048, (5632, 5632)),             # gate and up
+    (100, 2048, (2048, 256, 256)),         # grouped-query k and v
+    (33, 1000, (1000, 37, 3000)),          # ragged rows per projection, ragged K
+    (70, 4099, (130, 64, 1, 200, 65)),     # five projections: two launches
+    (64, 64, (64, 0, 16)),                 # an empty projection is skipped
+    (8, 520, (300, 20000)),                # up to 32 tokens: the batched path per projection
+])
+def test_matmul_multi_projection(N, K, Ms):
+    """Several weights on the same activations in one launch: every output
+    within the matmulQ8 bound of the oracle, nothing written outside them."""
+    rng = np.random.default_rng(N + K + len(Ms))
+    a = rng.standard_normal(N * K).astype(np.float32)
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    W = (K + 3) // 4
+    host, bufs = [], []
+    for M in Ms:
+        codes = rng.integers(-128, 128, (M, K)).astype(np.int32)
+        w = oracle.pack_q8(codes.reshape(-1), M, K) if M else np.zeros(1, np.uint32)
+        s = rng.uniform(0.001, 0.05, max(M, 1)).astype(np.float32)
+        out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        out.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), out, M))
+    wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
+    wxo_q8.synchronize()
+    if N > 32 and 1 < sum(1 for M in Ms if M) <= 4:  # one launch over all of them
+        assert wxo_q8.last_variant().startswith("matmul_q8.multi "), wxo_q8.last_variant()
+    for (w, s, M), (_, _, out, _) in zip(host, bufs):
+        got = out.download(np.float32, N * M + 64)
+        assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        if M:
+            assert_matmul(got[:N * M], a, w, s[:M], N, M, K)
+
+
 def test_matmul_invalid_sizes_raise():
     with pytest.raises(wxo_q8.WxoError):
         wxo_q8.matmulQ8(a=np.zeros(4, np.float32), weight=np.zeros(1, np.uint32), scale=np.zeros(1, np.float32),

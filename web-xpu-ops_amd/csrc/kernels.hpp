@@ -103,6 +103,18 @@ hipError_t launch_pack_int8_rows(const int8_t* codes, uint32_t N, uint32_t K, ui
 // out f32 [N, M].  K <= 2^22.
 hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
                             uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant);
+// Several projections of the same activations a [N, K]: output_p [N, M_p] =
+// matmulQ8(a, weight_p, scale_p), count <= kMaxMatmulProjectionsPerLaunch in
+// one launch.  Outputs must be disjoint from each other and from a.
+constexpr uint32_t kMaxMatmulProjectionsPerLaunch = 4;
+struct MatmulProjection {
+    const uint32_t* weight;
+    const float* scale;
+    float* output;
+    uint32_t M;
+};
+hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projections, uint32_t count, uint32_t N,
+                                  uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant);
 
 // dequant_q8.hip
 hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K,

@@ -61,6 +61,18 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kBN = 64;            // tokens per workgroup
 constexpr uint32_t kFoldCodes = 1024;   // fold the accumulator every 1024 codes
+constexpr uint32_t kMaxMatmulProjections = 4;
+
+// Up to four projections of the same activations in one launch: projection p
+// owns weight-row tiles [mt0[p], mt0[p + 1]) of the launch's tile sequence
+// (mt0[p] = 0xffffffff past the last one).
+struct MatmulProjections {
+    const uint32_t* weight[kMaxMatmulProjections];
+    const float* scale[kMaxMatmulProjections];
+    float* out[kMaxMatmulProjections];
+    uint32_t M[kMaxMatmulProjections];
+    uint32_t mt0[kMaxMatmulProjections];
+};
 
 
 
@@ -110,11 +122,9 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
 }
 
 template <int FB, int NW, int BK, int PD, int KS>
-__global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a,
-                                                        const uint32_t* __restrict__ weight,
-                                                        const float* __restrict__ scale, float* __restrict__ out,
-                                                        uint32_t N, uint32_t M, uint32_t K, uint32_t W,
-                                                        uint32_t mtiles, uint32_t ntiles) {
+__global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a, MatmulProjections P,
+                                                        uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
+                                                        uint32_t ntiles) {
     constexpr uint32_t BM = 32u * FB;                 // weight rows per workgroup
     constexpr uint32_t kBK = (uint32_t)BK;            // codes per K step
     constexpr uint32_t kRowBytes = kBK * 2u;          // one LDS row: BK bf16
@@ -144,7 +154,13 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     const uint32_t lin = xcd * per + slot;
     if (lin >= total) return;  // whole workgroup: no barrier is skipped by part of it
     const uint32_t nt = lin / mtiles, mt = lin - nt * mtiles;
-    const uint32_t m0 = mt * BM, n0 = nt * kBN;
+    // the projection that owns weight-row tile mt (wave-uniform)
+    const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
+    const uint32_t* __restrict__ weight = P.weight[pj];
+    const float* __restrict__ scale = P.scale[pj];
+    float* __restrict__ out = P.out[pj];
+    const uint32_t M = P.M[pj];
+    const uint32_t m0 = (mt - P.mt0[pj]) * BM, n0 = nt * kBN;
 
     // KS groups of NW waves share the tile and split its K steps in halves;
     // their sums meet in LDS at the end.
@@ -433,45 +449,76 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
+// One launch over `count` (1 to 4) projections of the same activations.
 template <int FB, int NW, int BK, int PD, int KS = 1>
-hipError_t launch_fb(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N, uint32_t M,
-                     uint32_t K, hipStream_t stream) {
+hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
+                     hipStream_t stream) {
     constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
     constexpr uint32_t BM = 32u * FB;
     const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
-    const uint32_t mtiles = (M + BM - 1u) / BM, ntiles = (N + kBN - 1u) / kBN;
+    MatmulProjections P = {};
+    uint32_t mtiles = 0;
+    for (uint32_t i = 0; i < kMaxMatmulProjections; ++i) {
+        if (i < count) {
+            P.weight[i] = p[i].weight;
+            P.scale[i] = p[i].scale;
+            P.out[i] = p[i].output;
+            P.M[i] = p[i].M;
+            P.mt0[i] = mtiles;
+            mtiles += (p[i].M + BM - 1u) / BM;
+        } else {
+            P.mt0[i] = 0xffffffffu;
+        }
+    }
+    const uint32_t ntiles = (N + kBN - 1u) / kBN;
     const uint32_t total = mtiles * ntiles;
     const uint32_t grid = ((total + 7u) / 8u) * 8u;
     const size_t lds = (size_t)KS * (2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes);
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS>), dim3(grid), dim3(64 * NW * KS), lds, stream, a, weight, scale, out,
-                       N, M, K, W, mtiles, ntiles);
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS>), dim3(grid), dim3(64 * NW * KS), lds, stream, a, P, N, K,
+                       W, mtiles, ntiles);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
-                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
-    if (N == 0 || M == 0) return hipSuccess;
+hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projections, uint32_t count, uint32_t N,
+                                  uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
+    static_assert(kMaxMatmulProjectionsPerLaunch == kMaxMatmulProjections, "one launch's projection table");
+    MatmulProjection p[kMaxMatmulProjections];
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (projections[i].M == 0) continue;
+        if (n == kMaxMatmulProjections) return hipErrorInvalidValue;
+        p[n++] = projections[i];
+    }
+    if (N == 0 || n == 0) return hipSuccess;
     if (K == 0) {
         // matmul over an empty K: every sum is 0 (ops/matmul/reference.ts:17-18)
-        const size_t n = (size_t)N * M;
-        const uint32_t grid = (uint32_t)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
-        hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, stream, out, n);
-        set_variant(variant, "fill_zero", "matmul.k0", 4, 0, 0, 0, grid);
-        return hipGetLastError();
+        for (uint32_t i = 0; i < n; ++i) {
+            const size_t e = (size_t)N * p[i].M;
+            const uint32_t grid = (uint32_t)((e + 255) / 256 < 65536 ? (e + 255) / 256 : 65536);
+            hipLaunchKernelGGL(fill_zero_kernel, dim3(grid), dim3(256), 0, stream, p[i].output, e);
+            set_variant(variant, "fill_zero", "matmul.k0", 4, 0, 0, 0, grid);
+            const hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
+        }
+        return hipSuccess;
     }
     // Up to 32 tokens: the batched single-vector path, one token per vector
-    // (out[n, m] is y[vector n][row m], the same layout).  The GEMM walks all
-    // of K in a serial chain of steps per workgroup whatever the token count
-    // (20 us for 1 token at 2048 x 2048); the batched path streams the weight
-    // once per 8 or 16 tokens (3.6 us for 1 token, 12 us for 32; the GEMM
-    // wins from about 64 tokens).  Both compute the matvecQ8 form.
+    // (out[n, m] is y[vector n][row m], the same layout), one call per
+    // projection.  The GEMM walks all of K in a serial chain of steps per
+    // workgroup whatever the token count (20 us for 1 token at 2048 x 2048);
+    // the batched path streams the weight once per 8 or 16 tokens (3.6 us
+    // for 1 token, 10.5 us for 32; the GEMM wins from about 64 tokens).
+    // Both compute the matvecQ8 form.
     if (N <= 32u) {
-        MatvecArgs mv{weight, scale, a, out, M, K, N, (uint32_t)(((uint64_t)K + 3) / 4)};
-        const hipError_t e = launch_matvec_q8(mv, dev, stream, variant);
-        if (variant) variant->form = "matmul.tokens_as_vectors";
-        return e;
+        for (uint32_t i = 0; i < n; ++i) {
+            MatvecArgs mv{p[i].weight, p[i].scale, a, p[i].output, p[i].M, K, N, (uint32_t)(((uint64_t)K + 3) / 4)};
+            const hipError_t e = launch_matvec_q8(mv, dev, stream, variant);
+            if (e != hipSuccess) return e;
+            if (variant) variant->form = "matmul.tokens_as_vectors";
+        }
+        return hipSuccess;
     }
     // 128 weight rows per workgroup when that still gives every CU a tile,
     // otherwise 64 rows with four register sets of loads in flight (6-16 %
@@ -480,20 +527,31 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
     // they save).  When the tiles fit in one workgroup per CU, two groups of
     // 8 waves split each tile's K steps (half the serial chain; 8-15 %
     // faster, 512 x 4096 x 11008 in 172 us against 197); with more tiles the
-    // smaller one-group workgroups (two per CU) win.
+    // smaller one-group workgroups (two per CU) win.  Projections in one
+    // launch count their tiles together.
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const uint64_t ntiles = (N + kBN - 1u) / kBN;
-    const uint64_t t4 = (uint64_t)((M + 127u) / 128u) * ntiles, t2 = (uint64_t)((M + 63u) / 64u) * ntiles;
-    if (t4 >= cus) {
-        set_variant(variant, "matmul_q8", t4 <= cus ? "FB4.ksplit2" : "FB4", t4 <= cus ? 16 : 8, 128, 0, (int)kBN,
-                    (uint32_t)((t4 + 7u) / 8u * 8u));
-        return t4 <= cus ? launch_fb<4, 8, 64, 2, 2>(a, weight, scale, out, N, M, K, stream)
-                         : launch_fb<4, 8, 64, 2, 1>(a, weight, scale, out, N, M, K, stream);
+    uint64_t t4 = 0, t2 = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        t4 += (uint64_t)((p[i].M + 127u) / 128u) * ntiles;
+        t2 += (uint64_t)((p[i].M + 63u) / 64u) * ntiles;
     }
-    set_variant(variant, "matmul_q8", t2 <= cus ? "FB2.PD4.ksplit2" : "FB2.PD4", t2 <= cus ? 16 : 8, 64, 0, (int)kBN,
-                (uint32_t)((t2 + 7u) / 8u * 8u));
-    return t2 <= cus ? launch_fb<2, 8, 64, 4, 2>(a, weight, scale, out, N, M, K, stream)
-                     : launch_fb<2, 8, 64, 4, 1>(a, weight, scale, out, N, M, K, stream);
+    if (t4 >= cus) {
+        set_variant(variant, n > 1 ? "matmul_q8.multi" : "matmul_q8", t4 <= cus ? "FB4.ksplit2" : "FB4",
+                    t4 <= cus ? 16 : 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
+        return t4 <= cus ? launch_fb<4, 8, 64, 2, 2>(a, p, n, N, K, stream)
+                         : launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
+    }
+    set_variant(variant, n > 1 ? "matmul_q8.multi" : "matmul_q8", t2 <= cus ? "FB2.PD4.ksplit2" : "FB2.PD4",
+                t2 <= cus ? 16 : 8, 64, 0, (int)kBN, (uint32_t)((t2 + 7u) / 8u * 8u));
+    return t2 <= cus ? launch_fb<2, 8, 64, 4, 2>(a, p, n, N, K, stream)
+                     : launch_fb<2, 8, 64, 4, 1>(a, p, n, N, K, stream);
+}
+
+hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float* scale, float* out, uint32_t N,
+                            uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
+    const MatmulProjection p{weight, scale, out, M};
+    return launch_matmul_q8_multi(a, &p, 1, N, K, dev, stream, variant);
 }
 
 }  // namespace wxo

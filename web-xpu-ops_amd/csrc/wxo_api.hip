@@ -602,6 +602,51 @@ int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, fl
     return launched(e, v, "matmul_q8 launch");
 }
 
+int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const float* const* scales,
+                        float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                        wxo_stream_t stream) {
+    if (count == 0) return ok();
+    if (!weights || !scales || !outputs || !Ms) return fail(WXO_ERR_INVALID, "projection arrays are NULL");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (validate_matmul(a, weights[i], scales[i], outputs[i], N, Ms[i], K) != WXO_OK) {
+            char why[256];
+            snprintf(why, sizeof why, "%s", g_error);
+            return fail(WXO_ERR_INVALID, "projection %u: %s", i, why);
+        }
+    }
+    // The projections run concurrently: an output that overlaps the
+    // activations, another output or any weight or scale would make the
+    // result depend on the schedule.
+    const uint64_t W = ((uint64_t)K + 3) / 4;
+    const auto meet = [](const void* p, uint64_t pb, const void* q, uint64_t qb) {
+        const uintptr_t p0 = (uintptr_t)p, q0 = (uintptr_t)q;
+        return pb > 0 && qb > 0 && p0 < q0 + qb && q0 < p0 + pb;
+    };
+    for (uint32_t i = 0; i < count; ++i) {
+        const uint64_t ob = (uint64_t)N * Ms[i] * 4u;
+        if (meet(outputs[i], ob, a, (uint64_t)N * K * 4u))
+            return fail(WXO_ERR_INVALID, "projection %u: output overlaps the activations", i);
+        for (uint32_t j = 0; j < count; ++j) {
+            if (j < i && meet(outputs[i], ob, outputs[j], (uint64_t)N * Ms[j] * 4u))
+                return fail(WXO_ERR_INVALID, "outputs of projections %u and %u overlap", j, i);
+            if (meet(outputs[i], ob, weights[j], (uint64_t)Ms[j] * W * 4u) ||
+                meet(outputs[i], ob, scales[j], (uint64_t)Ms[j] * 4u))
+                return fail(WXO_ERR_INVALID, "projection %u: output overlaps the weight or scale of projection %u", i, j);
+        }
+    }
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    for (uint32_t g = 0; g < count; g += wxo::kMaxMatmulProjectionsPerLaunch) {
+        wxo::MatmulProjection p[wxo::kMaxMatmulProjectionsPerLaunch];
+        const uint32_t n = count - g < wxo::kMaxMatmulProjectionsPerLaunch ? count - g : wxo::kMaxMatmulProjectionsPerLaunch;
+        for (uint32_t i = 0; i < n; ++i) p[i] = {weights[g + i], scales[g + i], outputs[g + i], Ms[g + i]};
+        wxo::Variant v = named("matmul_q8.multi", "empty");
+        hipError_t e = wxo::launch_matmul_q8_multi(a, p, n, N, K, *d, as_hip(stream), &v);
+        WXO_TRY(launched(e, v, "matmul_q8_multi launch"));
+    }
+    return ok();
+}
+
 int wxo_dequantize_packed_q8(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K, float* output,
                              wxo_stream_t stream) {
     WXO_TRY(validate_dequant(weight, scale, output, N, K));

@@ -41,7 +41,9 @@
 // Consecutive single-vector matvecQ8 ops (dispatch or native) on the same
 // vector and K run as one launch when no op of the run reads what another
 // writes (the engine's wq/wk/wv, :1843-1845, and lm_head chunks, :1869).
-// Consecutive quantizePackQ8 ops with one K likewise.  Results are those of
+// Consecutive quantizePackQ8 ops with one K likewise, and consecutive matmulQ8
+// ops on the same activations (a prompt's q, k, v; gate and up) run as one
+// GEMM launch over their weights.  Results are those of
 // the separate ops; only stats.launches changes.  { coalesce: false } turns
 // it off; a batch with profile labels runs every op on its own, as the
 // reference gives every dispatch its own pass when timing.
@@ -438,9 +440,16 @@ export class ResidentQ8Device {
         a.quantizePackQ8Device(op.input.ptr, op.N, op.K, op.packed.ptr, op.scales.ptr);
         return 1;
       }
-      case "matmulQ8":
+      case "matmulQ8": {
+        const n = coalesce ? sameActivationRun(calls, i) : 1;
+        if (n > 1) {
+          const group = calls.slice(i, i + n);
+          a.matmulQ8MultiDevice(group.map((g) => [g.weight.ptr, g.scale.ptr, g.output.ptr, g.M]), op.a.ptr, op.N, op.K);
+          return n;
+        }
         a.matmulQ8Device(op.a.ptr, op.weight.ptr, op.scale.ptr, op.output.ptr, op.N, op.M, op.K);
         return 1;
+      }
       case "dequantTranspose":
         a.dequantTransposeDevice(op.weight.ptr, op.scale.ptr, op.outFeatures, op.inFeatures, op.output.ptr);
         return 1;
@@ -537,6 +546,34 @@ function checkMatmul(op) {
  * How many calls from `start` on (at least 1) form a run of quantizePackQ8
  * calls with the same K, none writing what another of the run reads or writes.
  */
+/**
+ * How many calls from `start` on (at least 1) form a run of matmulQ8 calls on
+ * the same activations (buffer, N, K), none writing the activations or what
+ * another of the run reads or writes: a prompt's q, k and v, or gate and up.
+ */
+function sameActivationRun(calls, start) {
+  const first = calls[start];
+  const act = span(first.a, first.N * first.K * 4);
+  const outs = [];
+  const ins = [];
+  let n = 0;
+  for (let j = start; j < calls.length; j += 1) {
+    const op = calls[j];
+    if (op.kind !== "matmulQ8" || op.a.ptr !== first.a.ptr || op.N !== first.N || op.K !== first.K) break;
+    if (op.N === 0 || op.M === 0) break;
+    const out = span(op.output, op.N * op.M * 4);
+    const reads = [span(op.weight, op.M * Math.ceil(op.K / 4) * 4), span(op.scale, op.M * 4)];
+    if (overlaps(out, act) || outs.some((o) => overlaps(o, out)) ||
+        reads.some((r) => outs.some((o) => overlaps(o, r))) || ins.some((r) => overlaps(r, out))) {
+      break;
+    }
+    outs.push(out);
+    ins.push(...reads);
+    n += 1;
+  }
+  return Math.max(n, 1);
+}
+
 function quantizeRun(calls, start) {
   const K = calls[start].K;
   const ins = [];

@@ -26,6 +26,7 @@
  *   matvecQ8Device(w, s, x, y, N, K, M), quantizeDevice(in, N, D, out, scales),
  *   packQ8Device(codes, N, K, packed), packInt8RowsDevice(codes, N, K, packed),
  *   quantizePackQ8Device(in, N, K, packed, scales), matmulQ8Device(a, w, s, y, N, M, K),
+ *   matmulQ8MultiDevice([[w, s, y, M], ...], a, N, K),
  *   dequantizePackedQ8Device(w, s, N, K, y), dequantTransposeDevice(w, s, outF, inF, y),
  *   gatherDequantRowsDevice(codes, s, rows, D, indices, count, y)
  *   lastVariant() -> string (wxo_last_variant: the kernel instance of the last op)
@@ -937,6 +938,58 @@ static napi_value js_quantize_pack_q8_device(napi_env env, napi_callback_info in
 }
 
 /* matmulQ8Device(a, weight, scale, output, N, M, K): device addresses */
+/* matmulQ8MultiDevice([[weight, scale, output, M], ...], a, N, K): several
+ * projections of the same activations a [N, K] (device addresses), one launch
+ * per 4. */
+static napi_value js_matmul_q8_multi_device(napi_env env, napi_callback_info info) {
+    size_t argc = 4;
+    napi_value argv[4];
+    uint64_t a;
+    uint32_t N, K, count = 0;
+    bool is_array = false;
+    if (!get_args(env, info, 4, &argc, argv)) return NULL;
+    if (napi_is_array(env, argv[0], &is_array) != napi_ok || !is_array)
+        return type_error(env, "%s must be an array of [weight, scale, output, M]", "projections"), NULL;
+    if (!get_ptr(env, argv[1], &a, "a") || !get_u32(env, argv[2], &N, "N") || !get_u32(env, argv[3], &K, "K"))
+        return NULL;
+    napi_get_array_length(env, argv[0], &count);
+    const size_t n = count > 0 ? count : 1;
+    const uint32_t** ws = (const uint32_t**)calloc(n, sizeof *ws);
+    const float** ss = (const float**)calloc(n, sizeof *ss);
+    float** ys = (float**)calloc(n, sizeof *ys);
+    uint32_t* ms = (uint32_t*)calloc(n, sizeof *ms);
+    int okay = ws && ss && ys && ms;
+    if (!okay) napi_throw_error(env, NULL, "matmulQ8MultiDevice: out of host memory");
+    for (uint32_t i = 0; okay && i < count; ++i) {
+        napi_value e, f[4];
+        uint32_t len = 0;
+        uint64_t w, sc, y;
+        okay = napi_get_element(env, argv[0], i, &e) == napi_ok && napi_is_array(env, e, &is_array) == napi_ok &&
+               is_array && napi_get_array_length(env, e, &len) == napi_ok && len == 4;
+        if (!okay) {
+            char idx[16];
+            snprintf(idx, sizeof idx, "%u", i);
+            type_error(env, "projection %s must be [weight, scale, output, M]", idx);
+            break;
+        }
+        for (uint32_t j = 0; j < 4; ++j) napi_get_element(env, e, j, &f[j]);
+        okay = get_ptr(env, f[0], &w, "weight") && get_ptr(env, f[1], &sc, "scale") &&
+               get_ptr(env, f[2], &y, "output") && get_u32(env, f[3], &ms[i], "M");
+        ws[i] = (const uint32_t*)(uintptr_t)w;
+        ss[i] = (const float*)(uintptr_t)sc;
+        ys[i] = (float*)(uintptr_t)y;
+    }
+    if (okay) {
+        int st = wxo_matmul_q8_multi((const float*)(uintptr_t)a, ws, ss, ys, ms, count, N, K, g_stream);
+        if (st != WXO_OK) throw_status(env, st, "matmulQ8MultiDevice");
+    }
+    free(ws);
+    free(ss);
+    free(ys);
+    free(ms);
+    return NULL;
+}
+
 static napi_value js_matmul_q8_device(napi_env env, napi_callback_info info) {
     size_t argc = 7;
     napi_value argv[7];
@@ -1038,6 +1091,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"dequantTranspose", NULL, js_dequant_transpose, NULL, NULL, NULL, napi_enumerable, NULL},
         {"gatherDequantRows", NULL, js_gather_dequant_rows, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matmulQ8Device", NULL, js_matmul_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matmulQ8MultiDevice", NULL, js_matmul_q8_multi_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"dequantizePackedQ8Device", NULL, js_dequantize_packed_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"dequantTransposeDevice", NULL, js_dequant_transpose_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"gatherDequantRowsDevice", NULL, js_gather_dequant_rows_device, NULL, NULL, NULL, napi_enumerable, NULL},

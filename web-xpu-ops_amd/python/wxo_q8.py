@@ -61,6 +61,7 @@ SIGNATURES = {
     "wxo_event_create": ([ctypes.POINTER(_P)], _I),
     "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
     "wxo_spin": ([ctypes.c_uint32, _P], _I),
+    "wxo_matmul_q8_multi": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
     "wxo_graph_capture_begin": ([_P], _I),
     "wxo_graph_capture_end": ([_P, ctypes.POINTER(_P)], _I),
     "wxo_graph_launch": ([_P, _P], _I),
@@ -282,6 +283,17 @@ def _addr(x) -> int:
 def matvec_q8_device(weight, scale, vector, output, N: int, K: int, M: int = 1, stream=None) -> None:
     _check(lib().wxo_matvec_q8(_addr(weight), _addr(scale), _addr(vector), _addr(output), N, K, M,
                                _stream_ptr(stream)))
+
+
+def matmul_q8_multi_device(a, projections, N: int, K: int, stream=None) -> None:
+    """projections: a sequence of (weight, scale, output, M) on the same
+    activations a [N, K]; one launch per 4."""
+    n = len(projections)
+    ws = (ctypes.c_void_p * max(n, 1))(*[_addr(p[0]) for p in projections])
+    ss = (ctypes.c_void_p * max(n, 1))(*[_addr(p[1]) for p in projections])
+    ys = (ctypes.c_void_p * max(n, 1))(*[_addr(p[2]) for p in projections])
+    ms = (ctypes.c_uint32 * max(n, 1))(*[int(p[3]) for p in projections])
+    _check(lib().wxo_matmul_q8_multi(_addr(a), ws, ss, ys, ms, n, N, K, _stream_ptr(stream)))
 
 
 def matvec_q8_multi_device(projections, vector, K: int, stream=None) -> None:
