@@ -527,20 +527,30 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
     // they save).  When the tiles fit in one workgroup per CU, two groups of
     // 8 waves split each tile's K steps (half the serial chain; 8-15 %
     // faster, 512 x 4096 x 11008 in 172 us against 197); with more tiles the
-    // smaller one-group workgroups (two per CU) win.  Projections in one
-    // launch count their tiles together.
+    // smaller one-group workgroups (two per CU) win.  Short prompts whose
+    // 32-row tiles still fit one workgroup per CU take those: each tile's
+    // steps move less through LDS and twice the CUs work (64 tokens, 2048 x
+    // 2048: 18.5 -> 16.2 us; 2048 x 5632: 44.7 -> 38.3 us; the same sums in
+    // the same order, so the same bits).  Projections in one launch count
+    // their tiles together.
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const uint64_t ntiles = (N + kBN - 1u) / kBN;
-    uint64_t t4 = 0, t2 = 0;
+    uint64_t t4 = 0, t2 = 0, t1 = 0;
     for (uint32_t i = 0; i < n; ++i) {
         t4 += (uint64_t)((p[i].M + 127u) / 128u) * ntiles;
         t2 += (uint64_t)((p[i].M + 63u) / 64u) * ntiles;
+        t1 += (uint64_t)((p[i].M + 31u) / 32u) * ntiles;
     }
     if (t4 >= cus) {
         set_variant(variant, n > 1 ? "matmul_q8.multi" : "matmul_q8", t4 <= cus ? "FB4.ksplit2" : "FB4",
                     t4 <= cus ? 16 : 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
         return t4 <= cus ? launch_fb<4, 8, 64, 2, 2>(a, p, n, N, K, stream)
                          : launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
+    }
+    if (t1 <= cus) {
+        set_variant(variant, n > 1 ? "matmul_q8.multi" : "matmul_q8", "FB1.PD4.ksplit2", 16, 32, 0, (int)kBN,
+                    (uint32_t)((t1 + 7u) / 8u * 8u));
+        return launch_fb<1, 8, 64, 4, 2>(a, p, n, N, K, stream);
     }
     set_variant(variant, n > 1 ? "matmul_q8.multi" : "matmul_q8", t2 <= cus ? "FB2.PD4.ksplit2" : "FB2.PD4",
                 t2 <= cus ? 16 : 8, 64, 0, (int)kBN, (uint32_t)((t2 + 7u) / 8u * 8u));
