@@ -594,6 +594,23 @@ def run_prefill_suite(stream, steps, warmup, results, check):
                     "TFLOP/s": round(total_flops / (layer_us * 1e-6) / 1e12, 1),
                     "pct_of_bound": round(100 * bound_us / layer_us, 1)})
     log(f"suite prefill layer, coalesced: {layer_us:.1f} us  {total_flops / (layer_us * 1e-6) / 1e12:.1f} TFLOP/s")
+    # Short prompts: the same four launches over the first Ts tokens (the
+    # dispatch picks its tile shape from the tile count).
+    for Ts in (64, 128, 256):
+        short_us = 0.0
+        variants = []
+        for act, names in groups:
+            K = by[names[0]][1]
+            projs = [(by[n][2].ptr, by[n][3].ptr, outs[n].ptr, by[n][0]) for n in names]
+            short_us += time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, Ts, K, stream),
+                                  max(1, steps // 20), max(1, warmup // 20))
+            variants.append(wxo_q8.last_variant())
+        short_flops = total_flops * Ts / T
+        results.append({"case": f"prefill matmulQ8: one decoder layer, {Ts} tokens, as the resident batch issues it "
+                                f"(4 launches)", "us": round(short_us, 3),
+                        "TFLOP/s": round(short_flops / (short_us * 1e-6) / 1e12, 1), "variants": variants})
+        log(f"suite prefill layer, {Ts} tokens, coalesced: {short_us:.1f} us  "
+            f"{short_flops / (short_us * 1e-6) / 1e12:.1f} TFLOP/s")
     for b in outs.values():
         b.free()
 
