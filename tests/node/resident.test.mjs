@@ -11,7 +11,7 @@
 // the op saw (read back from the device).
 import { test, gpuTest, assert, assertMatvecAgrees, assertResidualAgrees, assertFfnAgrees } from "./harness.mjs";
 import { Q8, Q8_FFN, Q8_RESIDUAL, MATMUL_Q8, RMSNORM_LIKE, kernel } from "./wgsl_interfaces.mjs";
-import { createResidentQ8Device, params, UnsupportedPipelineError } from "../../web-xpu-ops_amd/harness/resident.js";
+import { createResidentQ8Device, createResidentDevice, runnerFromResident, params, UnsupportedPipelineError } from "../../web-xpu-ops_amd/harness/resident.js";
 import { recognise, parseBindings } from "../../web-xpu-ops_amd/harness/wgsl-interface.js";
 import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
 import * as oracle from "../../oracle/q8_oracle.mjs";
@@ -44,6 +44,11 @@ test(F, "pipelineFor's WGSL recognition refuses other kernels and near misses wi
   // a binding only inside a comment does not count
   refuses(Q8.replace("@group(0) @binding(4) var<uniform> params: Params;", "// @group(0) @binding(4) var<uniform> params: Params;"));
   assert.throws(() => recognise(42), TypeError);
+});
+
+test(F, "createResidentDevice is the reference's name for createResidentQ8Device (harness/resident.ts:148)", () => {
+  assert.strictEqual(createResidentDevice, createResidentQ8Device);
+  assert.strictEqual(typeof runnerFromResident, "function");
 });
 
 test(F, "params(): the reference's uniform layout (4 bytes per field, little-endian, at least 16)", () => {
@@ -487,5 +492,91 @@ gpuTest(F, "matmulQ8 dispatch (prefill) through the resident device, against the
   }
   device.destroy();
 });
+
+gpuTest(F, "runnerFromResident: one dispatch per call on its own buffers, destroyed afterwards, against the oracle", async () => {
+  const device = await createResidentDevice();
+  const run = runnerFromResident(device);
+  const N = 300, K = 1030;
+  const lin = linear(N, K, 61);
+  const packed = packInt8Rows(lin.codes, N, K);
+  const vector = vec(K, 62);
+  const dispatch = (rows) => ({
+    code: Q8,
+    bindings: [
+      { kind: "storage", data: packed },
+      { kind: "storage", data: lin.scale },
+      { kind: "storage", data: vector },
+      { kind: "out", type: "f32", length: N },
+      { kind: "uniform", data: params([["u32", N], ["u32", K]]) },
+    ],
+    workgroups: [rows],
+  });
+  const want = oracle.matvecQ8({ weight: packed, scale: lin.scale, vector, N, K });
+  const live = device.buffers.size;
+  for (let call = 0; call < 2; call += 1) {
+    const before = device.stats.buffersCreated;
+    const [got] = await run(dispatch(N));
+    assertMatvecAgrees(got, want, { weight: packed, scale: lin.scale, vector, N, K }, `call ${call}`);
+    // three inputs, the output, the uniform and the output's staging buffer, all released
+    assert.strictEqual(device.stats.buffersCreated - before, 6);
+    assert.strictEqual(device.buffers.size, live);
+  }
+  // a dispatch the device refuses (one row more than the weight holds) still
+  // releases what the call made
+  await assert.rejects(run(dispatch(N + 1)), /needed/);
+  assert.strictEqual(device.buffers.size, live);
+  device.destroy();
+});
+
+gpuTest(F, "buffer.destroy(): released once, and every later use throws before anything runs", async () => {
+  const device = await createResidentQ8Device();
+  const pipeline = await device.pipelineFor(Q8);
+  const N = 64, K = 256;
+  const lin = linear(N, K, 71);
+  const packed = packInt8Rows(lin.codes, N, K);
+  const w = device.createStorageBuffer(packed.byteLength);
+  device.upload(w, 0, packed);
+  const s = device.createStorageBuffer(N * 4);
+  device.upload(s, 0, lin.scale);
+  const x = device.createStorageBuffer(K * 4);
+  device.upload(x, 0, vec(K, 72));
+  const y = device.createStorageBuffer(N * 4);
+  const u = device.createUniformBuffer(8);
+  device.upload(u, 0, new Uint8Array(params([["u32", N], ["u32", K]])));
+  const group = await device.bindGroup(pipeline, [w, s, x, y, u]);
+  const op = { kind: "dispatch", pipeline, bindGroup: group, workgroups: [N] };
+  const [first] = await device.batch([op], [{ source: y, sourceOffset: 0, length: N, type: "f32" }]);
+  const size = device.buffers.size;
+  x.destroy();
+  x.destroy();  // a second destroy does nothing
+  assert.strictEqual(device.buffers.size, size - 1);
+  assert.strictEqual(x.ptr, null);
+  assert.throws(() => device.upload(x, 0, new Float32Array(4)), TypeError);
+  await assert.rejects(device.batch([op]), /destroyed/);
+  await assert.rejects(device.batch([{ kind: "matvecQ8", weight: w, scale: s, vector: x, output: y, N, K }]), TypeError);
+  await assert.rejects(device.bindGroup(pipeline, [w, s, x, y, u]), /not a buffer of this device/);
+  u.destroy();
+  y.destroy();
+  await assert.rejects(device.batch([], [{ source: y, sourceOffset: 0, length: N, type: "f32" }]), TypeError);
+  // the buffers left still work: a fresh vector and output through a new bind group
+  const x2 = device.createStorageBuffer(K * 4);
+  device.upload(x2, 0, vec(K, 72));
+  const y2 = device.createStorageBuffer(N * 4);
+  const u2 = device.createUniformBuffer(8);
+  device.upload(u2, 0, new Uint8Array(params([["u32", N], ["u32", K]])));
+  const g2 = await device.bindGroup(pipeline, [w, s, x2, y2, u2]);
+  const [again] = await device.batch([{ kind: "dispatch", pipeline, bindGroup: g2, workgroups: [N] }],
+    [{ source: y2, sourceOffset: 0, length: N, type: "f32" }]);
+  assertBitsEqualLocal(again, first);
+  device.destroy();
+  assert.strictEqual(device.buffers.size, 0);
+});
+
+function assertBitsEqualLocal(got, want) {
+  assert.strictEqual(got.length, want.length);
+  const a = new Uint32Array(got.buffer, got.byteOffset, got.length);
+  const b = new Uint32Array(want.buffer, want.byteOffset, want.length);
+  for (let i = 0; i < a.length; i += 1) if (a[i] !== b[i]) assert.fail(`element ${i}: ${got[i]} vs ${want[i]}`);
+}
 
 void kernel;

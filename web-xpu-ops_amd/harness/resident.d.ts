@@ -6,6 +6,8 @@ export interface ResidentBuffer {
   readonly size: number;
   readonly usage: number;
   readonly kind: "storage" | "uniform" | "staging";
+  /** GPUBuffer.destroy(): releases the memory now; later calls do nothing, later uses throw. */
+  destroy(): void;
 }
 export declare class UnsupportedPipelineError extends Error {
   readonly name: "UnsupportedPipelineError";
@@ -76,5 +78,21 @@ export declare class ResidentQ8Device {
   destroy(): void;
 }
 export declare function createResidentQ8Device(options?: ResidentQ8Options): Promise<ResidentQ8Device | null>;
+/** harness/resident.ts:148: the same factory under the reference's name. */
+export declare const createResidentDevice: typeof createResidentQ8Device;
+/** harness/wgsl.ts:12-31 Binding and Dispatch. */
+export type Binding =
+  | { kind: "storage"; data: Float32Array | Int32Array | Uint32Array }
+  | { kind: "out"; type: "f32" | "i32" | "u32"; length: number }
+  | { kind: "scratch"; length: number }
+  | { kind: "uniform"; data: ArrayBuffer };
+export interface Dispatch {
+  code: string;
+  entry?: string;
+  bindings: Binding[];
+  workgroups: [number] | [number, number] | [number, number, number];
+}
+/** harness/resident.ts:429-485: one dispatch per call on its own buffers, destroyed afterwards. */
+export declare function runnerFromResident(device: ResidentQ8Device): (dispatch: Dispatch) => Promise<(Float32Array | Int32Array | Uint32Array)[]>;
 /** harness/wgsl.ts:324-333 params(): a uniform's bytes, 4 per field, at least 16. */
 export declare function params(fields: ["u32" | "i32" | "f32", number][]): ArrayBuffer;

@@ -101,22 +101,35 @@ export class ResidentQ8Device {
    */
   createStorageBuffer(bytes, usage = DEFAULT_USAGE) {
     const size = Math.max(4, bytes);
-    let buffer;
     if (usage & BufferUsage.MAP_READ) {
-      buffer = { ptr: null, host: new Uint8Array(size), size, usage, kind: "staging" };
-    } else {
-      buffer = { ptr: this.addon.malloc(size), size, usage, kind: "storage" };
+      return this.track({ ptr: null, host: new Uint8Array(size), size, usage, kind: "staging" });
     }
-    this.buffers.add(buffer);
-    this.stats.buffersCreated += 1;
-    return buffer;
+    return this.track({ ptr: this.addon.malloc(size), size, usage, kind: "storage" });
   }
 
   /** A uniform buffer of max(16, bytes) bytes, held in host memory (read when a dispatch is enqueued). */
   createUniformBuffer(bytes) {
     const size = Math.max(16, bytes);
-    const buffer = { ptr: null, host: new Uint8Array(size), size, usage: BufferUsage.UNIFORM | BufferUsage.COPY_DST,
-      kind: "uniform" };
+    return this.track({ ptr: null, host: new Uint8Array(size), size, usage: BufferUsage.UNIFORM | BufferUsage.COPY_DST,
+      kind: "uniform" });
+  }
+
+  /**
+   * Registers a new buffer and gives it GPUBuffer's destroy(): the memory is
+   * released at once (a batch has synchronised before it returns, so no
+   * enqueued work still reads it), later calls are no-ops, and any later use
+   * of the buffer (upload, a bind group that holds it, an op, a readback)
+   * throws.  The engine destroys its transient per-prefill buffers this way
+   * (llm/engine-q8-resident.ts:1693), as runnerFromResident does its
+   * per-call ones (harness/resident.ts:480-482).
+   */
+  track(buffer) {
+    buffer.destroy = () => {
+      if (!this.buffers.delete(buffer)) return;
+      if (buffer.ptr !== null) this.addon.free(buffer.ptr);
+      buffer.ptr = null;
+      buffer.host = null;
+    };
     this.buffers.add(buffer);
     this.stats.buffersCreated += 1;
     return buffer;
@@ -286,8 +299,7 @@ export class ResidentQ8Device {
       this.addon.graphDestroy(this.graph.handle);
       this.graph = null;
     }
-    for (const b of this.buffers) if (b.ptr !== null) this.addon.free(b.ptr);
-    this.buffers.clear();
+    for (const b of [...this.buffers]) b.destroy();
     for (const [s, e] of this.events) {
       this.addon.eventDestroy(s);
       this.addon.eventDestroy(e);
@@ -357,6 +369,9 @@ export class ResidentQ8Device {
   resolveDispatch(op, i) {
     const group = op.bindGroup;
     if (!this.groupSet.has(group)) throw new TypeError(`op ${i}: bindGroup was not created by this device's bindGroup`);
+    group.buffers.forEach((b, j) => {
+      if (!this.buffers.has(b)) throw new TypeError(`op ${i}: binding ${j} of the bind group was destroyed`);
+    });
     if (group.pipeline !== op.pipeline) {
       throw new Error(`op ${i}: bind group was made for the ${group.pipeline.op} pipeline, dispatched with ${op.pipeline && op.pipeline.op}`);
     }
@@ -650,4 +665,62 @@ export async function createResidentQ8Device(options = {}) {
   if (a.deviceCount() === 0) return null;
   if (typeof globalThis.GPUBufferUsage === "undefined") globalThis.GPUBufferUsage = BufferUsage;
   return new ResidentQ8Device(options);
+}
+
+/** The reference's name for the same factory (harness/resident.ts:148, re-exported by harness/index.ts:5). */
+export const createResidentDevice = createResidentQ8Device;
+
+/**
+ * harness/resident.ts:429-485: a Runner's run(dispatch) over a resident
+ * device, for one-off dispatches.  Each call makes its own buffers (an
+ * upload per "storage" and "uniform" binding, an empty buffer per "out" and
+ * "scratch" one), binds them in the dispatch's order, runs the one dispatch
+ * with a readback of every "out" binding, and destroys every buffer it made,
+ * results or not.  The pipeline comes from pipelineFor, so the dispatch's
+ * WGSL must be one of the interfaces it recognises.
+ */
+export function runnerFromResident(device) {
+  return async function run(dispatch) {
+    const { code, entry = "main", bindings, workgroups } = dispatch;
+    const pipeline = await device.pipelineFor(code, entry);
+    const made = [];
+    const keep = (b) => {
+      made.push(b);
+      return b;
+    };
+    try {
+      const outs = [];
+      const bound = bindings.map((binding) => {
+        switch (binding.kind) {
+          case "out": {
+            const b = keep(device.createStorageBuffer(binding.length * 4));
+            outs.push({ buffer: b, length: binding.length, type: binding.type });
+            return b;
+          }
+          case "scratch":
+            return keep(device.createStorageBuffer(Math.max(4, binding.length * 4)));
+          case "uniform": {
+            const b = keep(device.createUniformBuffer(binding.data.byteLength));
+            device.upload(b, 0, new Uint8Array(binding.data));
+            return b;
+          }
+          case "storage": {
+            const b = keep(device.createStorageBuffer(binding.data.byteLength));
+            device.upload(b, 0, binding.data);
+            return b;
+          }
+          default:
+            throw new TypeError(`unknown binding kind ${binding.kind}`);
+        }
+      });
+      const bindGroup = await device.bindGroup(pipeline, bound);
+      const readback = outs.map((o) => ({
+        staging: keep(device.createStorageBuffer(o.length * 4, BufferUsage.COPY_DST | BufferUsage.MAP_READ)),
+        source: o.buffer, sourceOffset: 0, length: o.length, type: o.type,
+      }));
+      return await device.batch([{ kind: "dispatch", pipeline, bindGroup, workgroups }], readback);
+    } finally {
+      for (const b of made) b.destroy();
+    }
+  };
 }
