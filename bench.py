@@ -573,15 +573,19 @@ def run_prefill_suite(stream, steps, warmup, results, check):
     log(f"suite prefill layer: {total_us:.1f} us  {total_flops / (total_us * 1e-6) / 1e12:.1f} TFLOP/s")
 
     # The same layer as the resident batch issues it: projections of the same
-    # activations (q, k, v; gate, up) in one wxo_matmul_q8_multi launch each.
+    # activations (q, k, v; gate, up) in one wxo_matmul_q8_multi_ws launch
+    # each, with the device's workspace (short prompts split their tiles' K
+    # steps between workgroups).
     by = {name: (N, K, packed, scale) for name, N, K, packed, scale in prepared}
+    ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
     outs = {name: wxo_q8.DeviceBuffer(T * N * 4) for name, N, _, _, _ in prepared}
     groups = [(a_h, ("wq", "wk", "wv")), (a_h, ("wo",)), (a_h, ("wGate", "wUp")), (a_f, ("wDown",))]
     layer_us = 0.0
     for act, names in groups:
         K = by[names[0]][1]
         projs = [(by[n][2].ptr, by[n][3].ptr, outs[n].ptr, by[n][0]) for n in names]
-        us = time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, T, K, stream),
+        us = time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, T, K, stream, ws, ws_bytes),
                        max(1, steps // 20), max(1, warmup // 20))
         flops = sum(2.0 * T * by[n][0] * K for n in names)
         layer_us += us
@@ -602,7 +606,8 @@ def run_prefill_suite(stream, steps, warmup, results, check):
         for act, names in groups:
             K = by[names[0]][1]
             projs = [(by[n][2].ptr, by[n][3].ptr, outs[n].ptr, by[n][0]) for n in names]
-            short_us += time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, Ts, K, stream),
+            short_us += time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, Ts, K, stream, ws,
+                                                                                  ws_bytes),
                                   max(1, steps // 20), max(1, warmup // 20))
             variants.append(wxo_q8.last_variant())
         short_flops = total_flops * Ts / T
@@ -613,6 +618,7 @@ def run_prefill_suite(stream, steps, warmup, results, check):
             f"{short_flops / (short_us * 1e-6) / 1e12:.1f} TFLOP/s")
     for b in outs.values():
         b.free()
+    ws.free()
 
     # dequantizePackedQ8 and dequantTranspose of the gate projection, gather of
     # the prompt's rows from a 32000 x 2048 int8 embedding table

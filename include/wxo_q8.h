@@ -237,6 +237,20 @@ int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, fl
 int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const float* const* scales,
                         float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
                         wxo_stream_t stream);
+/* wxo_matmul_q8_multi with a caller-owned workspace: device memory of
+ * workspace_bytes (16-byte aligned) that touches no input or output.  No
+ * counterpart in the reference, which has no workspace: a short prompt's few
+ * tiles leave most CUs idle, and with room in the workspace their K steps are
+ * split between 2 or 4 workgroups whose partial sums meet in a second launch
+ * (added in a fixed order: deterministic, and within the same bound of the
+ * reference).  wxo_matmul_q8_workspace_bytes gives the size that allows every
+ * split on the current device; less (or NULL and 0) allows fewer splits or
+ * none, never an error.  The workspace's contents are scratch between calls;
+ * calls that share one workspace must not overlap in time. */
+int wxo_matmul_q8_multi_ws(const float* a, const uint32_t* const* weights, const float* const* scales,
+                           float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                           void* workspace, size_t workspace_bytes, wxo_stream_t stream);
+int wxo_matmul_q8_workspace_bytes(size_t* bytes);
 
 /* dequantizePackedQ8: output f32 [N, K], output[n*K + k] = q[n, k] * scale[n] rounded to
  * f32 once (bit-exact to the reference). */

@@ -94,6 +94,18 @@ def test_validation_happens_before_device_access():
         wxo_q8.matmul_q8_multi_device(0x30000, [(0x10000, 0x20000, 0x30010, 4)], 2, 8)
     with pytest.raises(wxo_q8.WxoError, match="projection 1: output overlaps the weight or scale of projection 0"):
         wxo_q8.matvec_q8_multi_device([(0x50000, 0x60000, 0x10000, 4), (16, 16, 0x50004, 4)], 0x30000, 8)
+    # the matmul workspace touches no input or output, and is what it says it is
+    proj = [(0x10000, 0x20000, 0x40000, 4)]
+    with pytest.raises(wxo_q8.WxoError, match="workspace overlaps projection 0's weight, scale or output"):
+        wxo_q8.matmul_q8_multi_device(0x30000, proj, 2, 8, workspace=0x40010, workspace_bytes=64)
+    with pytest.raises(wxo_q8.WxoError, match="workspace overlaps the activations"):
+        wxo_q8.matmul_q8_multi_device(0x30000, proj, 2, 8, workspace=0x2ff00, workspace_bytes=0x200)
+    with pytest.raises(wxo_q8.WxoError, match="workspace is NULL with 64 bytes"):
+        wxo_q8.matmul_q8_multi_device(0x30000, proj, 2, 8, workspace=0, workspace_bytes=64)
+    with pytest.raises(wxo_q8.WxoError, match="workspace is not 16-byte aligned"):
+        wxo_q8.matmul_q8_multi_device(0x30000, proj, 2, 8, workspace=0x70004, workspace_bytes=64)
+    with pytest.raises(wxo_q8.WxoError):  # bytes = NULL
+        wxo_q8._check(L.wxo_matmul_q8_workspace_bytes(None))
     assert L.wxo_quantize_pack_q8_multi(None, None, None, None, 0, 8, None) == wxo_q8.WXO_OK
     with pytest.raises(wxo_q8.WxoError, match="matrix 1: input is NULL"):
         wxo_q8.quantize_pack_q8_multi_device([(0x10000, 2, 0x20000, 0x30000), (0, 2, 0x40000, 0x50000)], 8)

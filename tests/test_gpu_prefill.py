@@ -284,6 +284,77 @@ def test_matmul_short_prompt_is_deterministic(N, M, K):
     assert_matmul(first, a, w, s, N, M, K)
 
 
+SPLIT_CASES = [
+    # (N, Ms, K, form): tokens, the projections' rows, columns, the expected split
+    (64, [2048], 2048, "wgsplit4"),     # 64 tiles of 32 rows: four workgroups per tile
+    (33, [300], 4099, "wgsplit4"),      # ragged rows and K, a one-token second tile row
+    (200, [256], 2048, "wgsplit4"),
+    (100, [1000], 1030, "wgsplit2"),    # 17 steps: two runs of at least 4 per K group
+    (128, [2048], 5632, "wgsplit2"),    # 128 tiles: two workgroups per tile
+    (64, [512, 256, 256], 2048, "wgsplit4"),  # three projections (q, k, v of a small model)
+    (64, [2048, 2048, 2048], 2048, "ksplit2"),  # 192 tiles: no room to split
+    (40, [96, 32, 32], 520, "ksplit2"),  # 9 steps: too few to split
+]
+
+
+@pytest.mark.parametrize("N,Ms,K,form", SPLIT_CASES)
+def test_matmul_workspace_split(N, Ms, K, form):
+    """wxo_matmul_q8_multi_ws: short prompts split each tile's K steps between
+    workgroups whose parts meet in a second launch, in part order.  Every
+    output within the matmulQ8 bar of the oracle (Inf and NaN activations
+    included), the same bits on every run, nothing written outside the
+    outputs, and the workspace left as scratch."""
+    rng = np.random.default_rng(N * 7 + K + len(Ms))
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[3] = np.inf
+    a[K + 11] = np.nan
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
+    host, bufs = [], []
+    for M in Ms:
+        codes = rng.integers(-128, 128, (M, K)).astype(np.int32)
+        w = oracle.pack_q8(codes.reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        out.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), out, M))
+    runs = []
+    for _ in range(3):
+        wxo_q8.matmul_q8_multi_device(ba, bufs, N, K, workspace=ws, workspace_bytes=ws_bytes)
+        wxo_q8.synchronize()
+        assert wxo_q8.last_variant().split()[1].endswith(form), wxo_q8.last_variant()
+        runs.append([b[2].download(np.float32, N * b[3] + 64) for b in bufs])
+    for r in runs[1:]:
+        for got, first in zip(r, runs[0]):
+            assert_bits_equal(got, first, "repeat")
+    for (w, s, M), got in zip(host, runs[0]):
+        assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        assert_matmul(got[:N * M], a, w, s, N, M, K)
+
+
+def test_matmul_workspace_size_sets_the_split():
+    """A workspace too small for four parts splits in two; one too small for
+    that (or none) does not split; the results agree within the bar either
+    way."""
+    N, M, K = 64, 2048, 2048
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    codes = rng.integers(-128, 128, (M, K)).astype(np.int32)
+    w = oracle.pack_q8(codes.reshape(-1), M, K)
+    s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ba, bw, bs = (wxo_q8.DeviceBuffer.from_array(x) for x in (a, w, s))
+    out = wxo_q8.DeviceBuffer(4 * N * M)
+    ws = wxo_q8.DeviceBuffer(3 * 4 * N * M)
+    for nbytes, form in [(3 * 4 * N * M, "wgsplit4"), (3 * 4 * N * M - 16, "wgsplit2"), (4 * N * M, "wgsplit2"),
+                         (4 * N * M - 16, "ksplit2"), (0, "ksplit2")]:
+        wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, out, M)], N, K, workspace=ws, workspace_bytes=nbytes)
+        wxo_q8.synchronize()
+        assert wxo_q8.last_variant().split()[1].endswith(form), (nbytes, wxo_q8.last_variant())
+        assert_matmul(out.download(np.float32, N * M), a, w, s, N, M, K)
+
+
 def test_matmul_invalid_sizes_raise():
     with pytest.raises(wxo_q8.WxoError):
         wxo_q8.matmulQ8(a=np.zeros(4, np.float32), weight=np.zeros(1, np.uint32), scale=np.zeros(1, np.float32),

@@ -105,7 +105,11 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
                             uint32_t M, uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant);
 // Several projections of the same activations a [N, K]: output_p [N, M_p] =
 // matmulQ8(a, weight_p, scale_p), count <= kMaxMatmulProjectionsPerLaunch in
-// one launch.  Outputs must be disjoint from each other and from a.
+// one launch.  Outputs must be disjoint from each other and from a.  With a
+// workspace (device memory, disjoint from everything else), short prompts
+// split each tile's K steps between workgroups and add the parts in a
+// second launch; it needs (parts - 1) x the outputs' floats, at most
+// kMatmulWorkspaceBytesPerCu per CU.
 constexpr uint32_t kMaxMatmulProjectionsPerLaunch = 4;
 struct MatmulProjection {
     const uint32_t* weight;
@@ -113,8 +117,10 @@ struct MatmulProjection {
     float* output;
     uint32_t M;
 };
+constexpr size_t kMatmulWorkspaceBytesPerCu = 6144;  // 3 extra parts of 32 x 64 outputs per 4 CUs
 hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projections, uint32_t count, uint32_t N,
-                                  uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant);
+                                  uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant,
+                                  float* workspace = nullptr, size_t workspace_bytes = 0);
 
 // dequant_q8.hip
 hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, uint32_t N, uint32_t K,

@@ -602,9 +602,10 @@ int wxo_matmul_q8(const float* a, const uint32_t* weight, const float* scale, fl
     return launched(e, v, "matmul_q8 launch");
 }
 
-int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const float* const* scales,
-                        float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
-                        wxo_stream_t stream) {
+namespace {
+int matmul_multi(const float* a, const uint32_t* const* weights, const float* const* scales, float* const* outputs,
+                 const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K, void* workspace, size_t workspace_bytes,
+                 wxo_stream_t stream) {
     if (count == 0) return ok();
     if (!weights || !scales || !outputs || !Ms) return fail(WXO_ERR_INVALID, "projection arrays are NULL");
     for (uint32_t i = 0; i < count; ++i) {
@@ -634,6 +635,20 @@ int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const fl
                 return fail(WXO_ERR_INVALID, "projection %u: output overlaps the weight or scale of projection %u", i, j);
         }
     }
+    // The workspace is written while every input is read and every output
+    // written: it must touch none of them.
+    if (workspace_bytes > 0 && !workspace) return fail(WXO_ERR_INVALID, "workspace is NULL with %zu bytes", workspace_bytes);
+    if (workspace && ((uintptr_t)workspace & 15u)) return fail(WXO_ERR_INVALID, "workspace is not 16-byte aligned");
+    if (workspace) {
+        if (meet(workspace, workspace_bytes, a, (uint64_t)N * K * 4u))
+            return fail(WXO_ERR_INVALID, "workspace overlaps the activations");
+        for (uint32_t i = 0; i < count; ++i) {
+            if (meet(workspace, workspace_bytes, outputs[i], (uint64_t)N * Ms[i] * 4u) ||
+                meet(workspace, workspace_bytes, weights[i], (uint64_t)Ms[i] * W * 4u) ||
+                meet(workspace, workspace_bytes, scales[i], (uint64_t)Ms[i] * 4u))
+                return fail(WXO_ERR_INVALID, "workspace overlaps projection %u's weight, scale or output", i);
+        }
+    }
     const wxo::DeviceInfo* d = nullptr;
     WXO_TRY(current_device(&d));
     for (uint32_t g = 0; g < count; g += wxo::kMaxMatmulProjectionsPerLaunch) {
@@ -641,9 +656,32 @@ int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const fl
         const uint32_t n = count - g < wxo::kMaxMatmulProjectionsPerLaunch ? count - g : wxo::kMaxMatmulProjectionsPerLaunch;
         for (uint32_t i = 0; i < n; ++i) p[i] = {weights[g + i], scales[g + i], outputs[g + i], Ms[g + i]};
         wxo::Variant v = named("matmul_q8.multi", "empty");
-        hipError_t e = wxo::launch_matmul_q8_multi(a, p, n, N, K, *d, as_hip(stream), &v);
+        hipError_t e = wxo::launch_matmul_q8_multi(a, p, n, N, K, *d, as_hip(stream), &v,
+                                                   static_cast<float*>(workspace), workspace_bytes);
         WXO_TRY(launched(e, v, "matmul_q8_multi launch"));
     }
+    return ok();
+}
+}  // namespace
+
+int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const float* const* scales,
+                        float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                        wxo_stream_t stream) {
+    return matmul_multi(a, weights, scales, outputs, Ms, count, N, K, nullptr, 0, stream);
+}
+
+int wxo_matmul_q8_multi_ws(const float* a, const uint32_t* const* weights, const float* const* scales,
+                           float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                           void* workspace, size_t workspace_bytes, wxo_stream_t stream) {
+    return matmul_multi(a, weights, scales, outputs, Ms, count, N, K, workspace, workspace_bytes, stream);
+}
+
+int wxo_matmul_q8_workspace_bytes(size_t* bytes) {
+    if (!bytes) return fail(WXO_ERR_INVALID, "bytes is NULL");
+    *bytes = 0;
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    *bytes = (size_t)(d->cu_count > 0 ? d->cu_count : 256) * wxo::kMatmulWorkspaceBytesPerCu;
     return ok();
 }
 

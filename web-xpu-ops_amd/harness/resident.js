@@ -78,6 +78,11 @@ export class ResidentQ8Device {
   constructor(options = {}) {
     this.addon = native();
     this.addon.init();
+    // Scratch for matmulQ8 on short prompts, whose tiles' K steps are split
+    // between workgroups (wxo_matmul_q8_multi_ws): one per device, made here
+    // so that no batch allocates.
+    this.workspaceBytes = this.addon.matmulQ8WorkspaceBytes();
+    this.workspace = this.addon.malloc(this.workspaceBytes);
     this.coalesce = options.coalesce !== false;
     this.graphs = options.graphs !== false;
     this.stats = { buffersCreated: 0, pipelinesCreated: 0, submits: 0, launches: 0, graphsCaptured: 0,
@@ -295,6 +300,10 @@ export class ResidentQ8Device {
 
   /** Frees every buffer and event this device created. */
   destroy() {
+    if (this.workspace !== null) {
+      this.addon.free(this.workspace);
+      this.workspace = null;
+    }
     if (this.graph !== null) {
       this.addon.graphDestroy(this.graph.handle);
       this.graph = null;
@@ -457,13 +466,10 @@ export class ResidentQ8Device {
       }
       case "matmulQ8": {
         const n = coalesce ? sameActivationRun(calls, i) : 1;
-        if (n > 1) {
-          const group = calls.slice(i, i + n);
-          a.matmulQ8MultiDevice(group.map((g) => [g.weight.ptr, g.scale.ptr, g.output.ptr, g.M]), op.a.ptr, op.N, op.K);
-          return n;
-        }
-        a.matmulQ8Device(op.a.ptr, op.weight.ptr, op.scale.ptr, op.output.ptr, op.N, op.M, op.K);
-        return 1;
+        const group = calls.slice(i, i + n);
+        a.matmulQ8MultiDevice(group.map((g) => [g.weight.ptr, g.scale.ptr, g.output.ptr, g.M]), op.a.ptr, op.N, op.K,
+          this.workspace, this.workspaceBytes);
+        return n;
       }
       case "dequantTranspose":
         a.dequantTransposeDevice(op.weight.ptr, op.scale.ptr, op.outFeatures, op.inFeatures, op.output.ptr);

@@ -941,17 +941,37 @@ static napi_value js_quantize_pack_q8_device(napi_env env, napi_callback_info in
 /* matmulQ8MultiDevice([[weight, scale, output, M], ...], a, N, K): several
  * projections of the same activations a [N, K] (device addresses), one launch
  * per 4. */
+/* matmulQ8WorkspaceBytes(): the workspace size that allows every split on the current device. */
+static napi_value js_matmul_q8_workspace_bytes(napi_env env, napi_callback_info info) {
+    (void)info;
+    size_t bytes = 0;
+    int st = wxo_matmul_q8_workspace_bytes(&bytes);
+    if (st != WXO_OK) return throw_status(env, st, "matmulQ8WorkspaceBytes"), NULL;
+    napi_value r;
+    napi_create_double(env, (double)bytes, &r);
+    return r;
+}
+
+/* matmulQ8MultiDevice(projections, a, N, K[, workspace, workspaceBytes]):
+ * with a workspace (a device address and its size), wxo_matmul_q8_multi_ws. */
 static napi_value js_matmul_q8_multi_device(napi_env env, napi_callback_info info) {
-    size_t argc = 4;
-    napi_value argv[4];
-    uint64_t a;
-    uint32_t N, K, count = 0;
-    bool is_array = false;
+    size_t argc = 6;
+    napi_value argv[6];
+    uint64_t a, wsp = 0;
+    uint32_t N, K, count = 0, wsb = 0;
+    bool is_array = false, with_ws = false;
     if (!get_args(env, info, 4, &argc, argv)) return NULL;
     if (napi_is_array(env, argv[0], &is_array) != napi_ok || !is_array)
         return type_error(env, "%s must be an array of [weight, scale, output, M]", "projections"), NULL;
     if (!get_ptr(env, argv[1], &a, "a") || !get_u32(env, argv[2], &N, "N") || !get_u32(env, argv[3], &K, "K"))
         return NULL;
+    if (argc >= 6) {
+        napi_valuetype t;
+        napi_typeof(env, argv[4], &t);
+        with_ws = t != napi_undefined && t != napi_null;
+        if (with_ws && (!get_ptr(env, argv[4], &wsp, "workspace") || !get_u32(env, argv[5], &wsb, "workspaceBytes")))
+            return NULL;
+    }
     napi_get_array_length(env, argv[0], &count);
     const size_t n = count > 0 ? count : 1;
     const uint32_t** ws = (const uint32_t**)calloc(n, sizeof *ws);
@@ -980,7 +1000,9 @@ static napi_value js_matmul_q8_multi_device(napi_env env, napi_callback_info inf
         ys[i] = (float*)(uintptr_t)y;
     }
     if (okay) {
-        int st = wxo_matmul_q8_multi((const float*)(uintptr_t)a, ws, ss, ys, ms, count, N, K, g_stream);
+        int st = with_ws ? wxo_matmul_q8_multi_ws((const float*)(uintptr_t)a, ws, ss, ys, ms, count, N, K,
+                                                  (void*)(uintptr_t)wsp, wsb, g_stream)
+                         : wxo_matmul_q8_multi((const float*)(uintptr_t)a, ws, ss, ys, ms, count, N, K, g_stream);
         if (st != WXO_OK) throw_status(env, st, "matmulQ8MultiDevice");
     }
     free(ws);
@@ -1092,6 +1114,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"gatherDequantRows", NULL, js_gather_dequant_rows, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matmulQ8Device", NULL, js_matmul_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matmulQ8MultiDevice", NULL, js_matmul_q8_multi_device, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matmulQ8WorkspaceBytes", NULL, js_matmul_q8_workspace_bytes, NULL, NULL, NULL, napi_enumerable, NULL},
         {"dequantizePackedQ8Device", NULL, js_dequantize_packed_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"dequantTransposeDevice", NULL, js_dequant_transpose_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"gatherDequantRowsDevice", NULL, js_gather_dequant_rows_device, NULL, NULL, NULL, napi_enumerable, NULL},

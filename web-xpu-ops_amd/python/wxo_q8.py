@@ -62,6 +62,8 @@ SIGNATURES = {
     "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
     "wxo_spin": ([ctypes.c_uint32, _P], _I),
     "wxo_matmul_q8_multi": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
+    "wxo_matmul_q8_multi_ws": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _SZ, _P], _I),
+    "wxo_matmul_q8_workspace_bytes": ([ctypes.POINTER(_SZ)], _I),
     "wxo_graph_capture_begin": ([_P], _I),
     "wxo_graph_capture_end": ([_P, ctypes.POINTER(_P)], _I),
     "wxo_graph_launch": ([_P, _P], _I),
@@ -285,15 +287,29 @@ def matvec_q8_device(weight, scale, vector, output, N: int, K: int, M: int = 1, 
                                _stream_ptr(stream)))
 
 
-def matmul_q8_multi_device(a, projections, N: int, K: int, stream=None) -> None:
+def matmul_q8_multi_device(a, projections, N: int, K: int, stream=None, workspace=None,
+                           workspace_bytes: int = 0) -> None:
     """projections: a sequence of (weight, scale, output, M) on the same
-    activations a [N, K]; one launch per 4."""
+    activations a [N, K]; one launch per 4.  With a workspace (a device buffer
+    or address and its size in bytes), short prompts split each tile's K steps
+    between workgroups (wxo_matmul_q8_multi_ws)."""
     n = len(projections)
     ws = (ctypes.c_void_p * max(n, 1))(*[_addr(p[0]) for p in projections])
     ss = (ctypes.c_void_p * max(n, 1))(*[_addr(p[1]) for p in projections])
     ys = (ctypes.c_void_p * max(n, 1))(*[_addr(p[2]) for p in projections])
     ms = (ctypes.c_uint32 * max(n, 1))(*[int(p[3]) for p in projections])
-    _check(lib().wxo_matmul_q8_multi(_addr(a), ws, ss, ys, ms, n, N, K, _stream_ptr(stream)))
+    if workspace is None:
+        _check(lib().wxo_matmul_q8_multi(_addr(a), ws, ss, ys, ms, n, N, K, _stream_ptr(stream)))
+    else:
+        _check(lib().wxo_matmul_q8_multi_ws(_addr(a), ws, ss, ys, ms, n, N, K, _addr(workspace), workspace_bytes,
+                                            _stream_ptr(stream)))
+
+
+def matmul_q8_workspace_bytes() -> int:
+    """The workspace size that allows every split of wxo_matmul_q8_multi_ws on the current device."""
+    b = ctypes.c_size_t(0)
+    _check(lib().wxo_matmul_q8_workspace_bytes(ctypes.byref(b)))
+    return b.value
 
 
 def matvec_q8_multi_device(projections, vector, K: int, stream=None) -> None:
