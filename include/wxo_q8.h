@@ -251,6 +251,20 @@ int wxo_matmul_q8_multi_ws(const float* a, const uint32_t* const* weights, const
                            float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
                            void* workspace, size_t workspace_bytes, wxo_stream_t stream);
 int wxo_matmul_q8_workspace_bytes(size_t* bytes);
+/* wxo_matmul_q8_multi_ws with the library's own workspace instead of one the
+ * caller passes: no counterpart in the reference.  For callers that cannot
+ * allocate device memory at all (code under HIP graph capture, serving loops
+ * or harnesses that forbid hipMalloc): it allocates nothing and calls no
+ * allocating routine.  The workspace is a 1.5 MiB array in the library's code
+ * object (each GPU holds its own from the library's load until the process
+ * ends); a split that would need more runs with fewer parts, so no size is
+ * refused for it.  The array keeps the last call's contents and needs no
+ * clearing (a call reads only what it wrote).  Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (other streams,
+ * other threads) race and give wrong results. */
+int wxo_matmul_q8_multi_static(const float* a, const uint32_t* const* weights, const float* const* scales,
+                               float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                               wxo_stream_t stream);
 
 /* dequantizePackedQ8: output f32 [N, K], output[n*K + k] = q[n, k] * scale[n] rounded to
  * f32 once (bit-exact to the reference). */

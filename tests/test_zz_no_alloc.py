@@ -1,0 +1,67 @@
+"""wxo_matmul_q8_multi_static, the allocation-free matmulQ8 over the library's
+own scratch array, against wxo_matmul_q8_multi_ws with a caller-owned
+workspace of the same size: the same bits (the same split, the same sums in
+the same order), within the matmulQ8 bar of the oracle (|y - y_ref| <= 1e-5 *
+sum_k |a * fround(q * s)| + 1e-7, ops/matmul/reference.ts:124-137), nothing
+written past the outputs, on two calls in a row, the second smaller than the
+first (it must not read what the first left in the array)."""
+import numpy as np
+import pytest
+
+import oracle
+import wxo_q8
+
+pytestmark = pytest.mark.gpu
+
+SCRATCH_BYTES = 256 * 6144  # the library's array: 6 KiB per CU of a 256-CU device
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    wxo_q8.init()
+
+
+def check_matmul(got, a, w, s, N, M, K):
+    want = oracle.matmul_q8(np.asarray(a, np.float32).reshape(N, K), w, s, N, M, K)
+    bound = oracle.matmul_absterm(np.asarray(a, np.float32).reshape(N, K), w, s, N, M, K)
+    ok, msg = oracle.check_matvec(np.asarray(got).reshape(-1), want.reshape(-1), bound.reshape(-1))
+    assert ok, f"N={N} M={M} K={K}: {msg}"
+
+
+def test_no_alloc_matches_the_workspace_entry():
+    rng = np.random.default_rng(2024)
+    ws_bytes = min(wxo_q8.matmul_q8_workspace_bytes(), SCRATCH_BYTES)
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
+    # the first call fills the whole array (four parts of 64 x 2048 outputs);
+    # the second is smaller, over two projections
+    for N, Ms, K, form in [(64, [2048], 2048, "wgsplit4"), (40, [512, 256], 1030, "wgsplit2")]:
+        a = rng.standard_normal(N * K).astype(np.float32)
+        a[1] = np.inf
+        ba = wxo_q8.DeviceBuffer.from_array(a)
+        host, with_ws, without = [], [], []
+        for M in Ms:
+            codes = rng.integers(-128, 128, (M, K)).astype(np.int32)
+            w = oracle.pack_q8(codes.reshape(-1), M, K)
+            s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+            bw, bs = wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s)
+            outs = []
+            for _ in range(2):
+                o = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+                o.upload(np.full(N * M + 64, 7.5, np.float32))
+                outs.append(o)
+            host.append((w, s, M))
+            with_ws.append((bw, bs, outs[0], M))
+            without.append((bw, bs, outs[1], M))
+        wxo_q8.matmul_q8_multi_device(ba, with_ws, N, K, workspace=ws, workspace_bytes=ws_bytes)
+        wxo_q8.synchronize()
+        assert wxo_q8.last_variant().split()[1].endswith(form), wxo_q8.last_variant()
+        wxo_q8.matmul_q8_multi_static_device(ba, without, N, K)
+        wxo_q8.synchronize()
+        assert wxo_q8.last_variant().split()[1].endswith(form), wxo_q8.last_variant()
+        for (w, s, M), p, q in zip(host, with_ws, without):
+            ref = p[2].download(np.float32, N * M + 64)
+            got = q[2].download(np.float32, N * M + 64)
+            assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+            bad = np.flatnonzero(got[:N * M].view(np.uint32) != ref[:N * M].view(np.uint32))
+            assert bad.size == 0, f"N={N} M={M}: {bad.size} outputs differ from the workspace entry's, first {bad[0]}"
+            check_matmul(got[:N * M], a, w, s, N, M, K)

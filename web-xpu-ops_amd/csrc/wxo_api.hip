@@ -51,6 +51,17 @@ wxo::DeviceInfo g_dev[kMaxDevices];
 std::mutex g_dev_mu;
 char g_describe[1024] = {0};
 
+// The workspace of wxo_matmul_q8_multi_static: the largest split workspace
+// wxo_matmul_q8_multi_ws ever uses on a 256-CU device (6 KiB per CU).  Each
+// GPU holds its own copy from the code object's load until the process ends.
+// Host code never passes the array's name to a kernel or a copy (on the host
+// it is only a stand-in for the symbol): it uses g_scratch[device], the
+// device address that hipGetSymbolAddress gives once per device at set-up.
+constexpr size_t kScratchBytes = 256u * wxo::kMatmulWorkspaceBytesPerCu;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+void* g_scratch[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+
 // Device info for the current HIP device, probed once per device.
 int current_device(const wxo::DeviceInfo** out) {
     int count = 0;
@@ -73,6 +84,10 @@ int current_device(const wxo::DeviceInfo** out) {
         d.hbm_bytes = prop.totalGlobalMem;
         snprintf(d.name, sizeof d.name, "%s", prop.name);
         snprintf(d.arch, sizeof d.arch, "%s", prop.gcnArchName);
+        // this device is current: its copy of the scratch array
+        void* p = nullptr;
+        g_scratch_err[ordinal] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch[ordinal] = g_scratch_err[ordinal] == hipSuccess ? p : nullptr;
         d.ordinal = ordinal;
     }
     *out = &d;
@@ -674,6 +689,19 @@ int wxo_matmul_q8_multi_ws(const float* a, const uint32_t* const* weights, const
                            float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
                            void* workspace, size_t workspace_bytes, wxo_stream_t stream) {
     return matmul_multi(a, weights, scales, outputs, Ms, count, N, K, workspace, workspace_bytes, stream);
+}
+
+int wxo_matmul_q8_multi_static(const float* a, const uint32_t* const* weights, const float* const* scales,
+                               float* const* outputs, const uint32_t* Ms, uint32_t count, uint32_t N, uint32_t K,
+                               wxo_stream_t stream) {
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    void* ws = g_scratch[d->ordinal];
+    if (!ws) {
+        return fail(WXO_ERR_DEVICE, "the library's scratch array on device %d is unavailable (hipGetSymbolAddress: %s)",
+                    d->ordinal, hipGetErrorString(g_scratch_err[d->ordinal]));
+    }
+    return matmul_multi(a, weights, scales, outputs, Ms, count, N, K, ws, kScratchBytes, stream);
 }
 
 int wxo_matmul_q8_workspace_bytes(size_t* bytes) {

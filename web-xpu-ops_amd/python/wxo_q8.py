@@ -64,6 +64,7 @@ SIGNATURES = {
     "wxo_matmul_q8_multi": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
     "wxo_matmul_q8_multi_ws": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _SZ, _P], _I),
     "wxo_matmul_q8_workspace_bytes": ([ctypes.POINTER(_SZ)], _I),
+    "wxo_matmul_q8_multi_static": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
     "wxo_graph_capture_begin": ([_P], _I),
     "wxo_graph_capture_end": ([_P, ctypes.POINTER(_P)], _I),
     "wxo_graph_launch": ([_P, _P], _I),
@@ -303,6 +304,18 @@ def matmul_q8_multi_device(a, projections, N: int, K: int, stream=None, workspac
     else:
         _check(lib().wxo_matmul_q8_multi_ws(_addr(a), ws, ss, ys, ms, n, N, K, _addr(workspace), workspace_bytes,
                                             _stream_ptr(stream)))
+
+
+def matmul_q8_multi_static_device(a, projections, N: int, K: int, stream=None) -> None:
+    """matmul_q8_multi_device with the library's own workspace
+    (wxo_matmul_q8_multi_static): allocates nothing; calls that overlap in
+    time on one GPU race."""
+    n = len(projections)
+    ws = (ctypes.c_void_p * max(n, 1))(*[_addr(p[0]) for p in projections])
+    ss = (ctypes.c_void_p * max(n, 1))(*[_addr(p[1]) for p in projections])
+    ys = (ctypes.c_void_p * max(n, 1))(*[_addr(p[2]) for p in projections])
+    ms = (ctypes.c_uint32 * max(n, 1))(*[int(p[3]) for p in projections])
+    _check(lib().wxo_matmul_q8_multi_static(_addr(a), ws, ss, ys, ms, n, N, K, _stream_ptr(stream)))
 
 
 def matmul_q8_workspace_bytes() -> int:
