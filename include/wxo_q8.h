@@ -239,11 +239,12 @@ int wxo_matmul_q8_multi(const float* a, const uint32_t* const* weights, const fl
                         wxo_stream_t stream);
 /* wxo_matmul_q8_multi with a caller-owned workspace: device memory of
  * workspace_bytes (16-byte aligned) that touches no input or output.  No
- * counterpart in the reference, which has no workspace: a short prompt's few
- * tiles leave most CUs idle, and with room in the workspace their K steps are
- * split between 2 or 4 workgroups whose partial sums meet in a second launch
- * (added in a fixed order: deterministic, and within the same bound of the
- * reference).  wxo_matmul_q8_workspace_bytes gives the size that allows every
+ * counterpart in the reference, which has no workspace.  With room in it,
+ * some tiles split their K steps between workgroups whose partial sums meet in
+ * a second launch (added in a fixed order: deterministic, and within the same
+ * bound of the reference): all of a short prompt's tiles, which would leave
+ * most CUs idle, and the last tiles of a prompt whose tiles fill one round of
+ * the CUs unevenly, so that every CU holds the same work.  wxo_matmul_q8_workspace_bytes gives the size that allows every
  * split on the current device; less (or NULL and 0) allows fewer splits or
  * none, never an error.  The workspace's contents are scratch between calls;
  * calls that share one workspace must not overlap in time. */
@@ -255,7 +256,7 @@ int wxo_matmul_q8_workspace_bytes(size_t* bytes);
  * caller passes: no counterpart in the reference.  For callers that cannot
  * allocate device memory at all (code under HIP graph capture, serving loops
  * or harnesses that forbid hipMalloc): it allocates nothing and calls no
- * allocating routine.  The workspace is a 1.5 MiB array in the library's code
+ * allocating routine.  The workspace is an 8 MiB array in the library's code
  * object (each GPU holds its own from the library's load until the process
  * ends); a split that would need more runs with fewer parts, so no size is
  * refused for it.  The array keeps the last call's contents and needs no

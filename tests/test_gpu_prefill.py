@@ -334,6 +334,77 @@ def test_matmul_workspace_split(N, Ms, K, form):
         assert_matmul(got[:N * M], a, w, s, N, M, K)
 
 
+BALANCE_CASES = [
+    # (N, Ms, K): between cus and 2 x cus 128-row tiles
+    (512, [2048, 2048, 2048], 2048),  # a 512-token prompt's q, k, v: 384 tiles, 128 of them split
+    (256, [5632, 5632], 2048),        # a 256-token prompt's gate, up: 352 tiles, 160 split
+    (700, [2048, 1500], 1030),        # ragged tokens, rows and K: 308 tiles, 204 split
+]
+
+
+@pytest.mark.parametrize("N,Ms,K", BALANCE_CASES)
+def test_matmul_workspace_balance(N, Ms, K):
+    """Prompts whose 128-row tiles fill one round of two workgroups per CU
+    unevenly: with a workspace the last tiles split their K steps in two, so
+    every CU holds the same work.  Outputs within the matmulQ8 bar of the oracle (every 5th
+    token, both split and whole tiles among them), Inf and NaN activations
+    included; the same bits on every run; nothing written past the outputs."""
+    rng = np.random.default_rng(N + K + sum(Ms))
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[(N - 1) * K + 2] = np.inf   # the last token row is a split tile's
+    a[3 * K + 9] = np.nan
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
+    host, bufs = [], []
+    for M in Ms:
+        codes = rng.integers(-128, 128, (M, K)).astype(np.int32)
+        w = oracle.pack_q8(codes.reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        out.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), out, M))
+    runs = []
+    for _ in range(2):
+        wxo_q8.matmul_q8_multi_device(ba, bufs, N, K, workspace=ws, workspace_bytes=ws_bytes)
+        wxo_q8.synchronize()
+        assert wxo_q8.last_variant().split()[1] == "FB4.balance2", wxo_q8.last_variant()
+        runs.append([b[2].download(np.float32, N * b[3] + 64) for b in bufs])
+    rows = np.unique(np.concatenate([np.arange(0, N, 5), [3, N - 1]]))
+    for (w, s, M), got, again in zip(host, runs[0], runs[1]):
+        assert_bits_equal(again, got, "repeat")
+        assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)
+    # without the workspace: the unsplit kernel, the same bound
+    for (_, _, out, _) in bufs:
+        out.upload(np.zeros(out.nbytes // 4, np.float32))
+    wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
+    wxo_q8.synchronize()
+    assert wxo_q8.last_variant().split()[1] == "FB4", wxo_q8.last_variant()
+    for (w, s, M), b in zip(host, bufs):
+        assert_matmul(b[2].download(np.float32, N * M), a, w, s, N, M, K, rows=rows)
+
+
+def test_matmul_workspace_leaves_several_rounds_unsplit():
+    """704 tiles (a 512-token gate and up) take several rounds of two
+    workgroups per CU: the dispatch evens the CUs out itself and the split
+    does not pay, so a workspace changes nothing there."""
+    N, M, K = 512, 5632, 2048
+    rng = np.random.default_rng(11)
+    ba = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(N * K).astype(np.float32))
+    bw = wxo_q8.DeviceBuffer.from_array(rng.integers(0, 2 ** 32, M * K // 4, dtype=np.uint64).astype(np.uint32))
+    bs = wxo_q8.DeviceBuffer.from_array(np.full(M, 0.01, np.float32))
+    outs = [wxo_q8.DeviceBuffer(4 * N * M) for _ in range(2)]
+    ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
+    wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, outs[0], M), (bw, bs, outs[1], M)], N, K, workspace=ws,
+                                  workspace_bytes=ws_bytes)
+    wxo_q8.synchronize()
+    assert wxo_q8.last_variant().split()[1] == "FB4", wxo_q8.last_variant()
+    assert_bits_equal(outs[1].download(np.float32, N * M), outs[0].download(np.float32, N * M), "same weight")
+
+
 def test_matmul_workspace_size_sets_the_split():
     """A workspace too small for four parts splits in two; one too small for
     that (or none) does not split; the results agree within the bar either

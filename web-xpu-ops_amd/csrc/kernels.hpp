@@ -106,9 +106,10 @@ hipError_t launch_matmul_q8(const float* a, const uint32_t* weight, const float*
 // Several projections of the same activations a [N, K]: output_p [N, M_p] =
 // matmulQ8(a, weight_p, scale_p), count <= kMaxMatmulProjectionsPerLaunch in
 // one launch.  Outputs must be disjoint from each other and from a.  With a
-// workspace (device memory, disjoint from everything else), short prompts
-// split each tile's K steps between workgroups and add the parts in a
-// second launch; it needs (parts - 1) x the outputs' floats, at most
+// workspace (device memory, disjoint from everything else), some tiles split
+// their K steps between workgroups (all of a short prompt's; the last ones of
+// a prompt whose tiles fill one round unevenly) and a second launch adds them;
+// the workspace holds one tile of floats per extra part, at most
 // kMatmulWorkspaceBytesPerCu per CU.
 constexpr uint32_t kMaxMatmulProjectionsPerLaunch = 4;
 struct MatmulProjection {
@@ -117,7 +118,7 @@ struct MatmulProjection {
     float* output;
     uint32_t M;
 };
-constexpr size_t kMatmulWorkspaceBytesPerCu = 6144;  // 3 extra parts of 32 x 64 outputs per 4 CUs
+constexpr size_t kMatmulWorkspaceBytesPerCu = 32768;  // one 128 x 64-output half per CU
 hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projections, uint32_t count, uint32_t N,
                                   uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant,
                                   float* workspace = nullptr, size_t workspace_bytes = 0);

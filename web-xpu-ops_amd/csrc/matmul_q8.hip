@@ -65,10 +65,12 @@ constexpr uint32_t kMaxMatmulProjections = 4;
 
 // Up to four projections of the same activations in one launch: projection p
 // owns weight-row tiles [mt0[p], mt0[p + 1]) of the launch's tile sequence
-// (mt0[p] = 0xffffffff past the last one).  A launch whose tiles' K steps are
-// split between XS workgroups writes part 0's sums into the outputs and part
-// j's (j >= 1) into part + (j - 1) * partstride + partoff[p], laid out as
-// the outputs are; split_sum_kernel then adds them.
+// (mt0[p] = 0xffffffff past the last one).  A split launch runs its first
+// `whole` tiles whole and splits the other `splits` tiles' K steps into
+// `parts` runs, one workgroup each: part 0 stores its unscaled sums into the
+// output, part j >= 1 into the workspace block (j - 1) * splits + (tile -
+// whole) of BM x kBN floats ([token][row] within the tile), and
+// split_sum_kernel adds the parts in part order and scales them.
 struct MatmulProjections {
     const uint32_t* weight[kMaxMatmulProjections];
     const float* scale[kMaxMatmulProjections];
@@ -76,8 +78,7 @@ struct MatmulProjections {
     uint32_t M[kMaxMatmulProjections];
     uint32_t mt0[kMaxMatmulProjections];
     float* part;
-    uint32_t partoff[kMaxMatmulProjections];
-    uint32_t partstride;
+    uint32_t whole, splits, parts;
 };
 
 
@@ -127,11 +128,12 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
     l = __float_as_uint(r - __uint_as_float(m));
 }
 
-// XS > 1 splits every tile's K steps between XS workgroups as well (short
-// prompts, whose few tiles would leave most CUs idle): part xs takes the
-// xs-th run of the steps, stores its unscaled sums (above), and the sum
-// kernel adds the parts in part order and scales them.
-template <int FB, int NW, int BK, int PD, int KS, int XS = 1>
+// SPLIT instances take the split launch above: whole tiles plus split tiles
+// whose K steps are shared by `parts` workgroups (a short prompt's few tiles,
+// which would leave most CUs idle, or the tiles past the last whole round of
+// a long prompt, which would leave some CUs with one tile more than others).
+// The other instances run every tile whole, with no branch on it.
+template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false>
 __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a, MatmulProjections P,
                                                         uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
                                                         uint32_t ntiles) {
@@ -153,20 +155,37 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     static_assert(PD == 2 || PD == 4, "2 or 4 register sets of loads in flight");
     static_assert(kFoldSteps % (uint32_t)PD == 0u, "a fold group starts on register set 0 and stage 0");
     static_assert(KS == 1 || KS == 2, "K split over 1 or 2 groups of NW waves");
-    static_assert(XS == 1 || XS == 2 || XS == 4, "K split over 1, 2 or 4 workgroups");
-    constexpr uint32_t NP = (uint32_t)(KS * XS);      // parts of a tile's K steps
     // Per K group: [A0 A1 B0 B1]
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
-    // contiguous run of the (token-major) tile sequence.
-    const uint32_t total = mtiles * ntiles * (uint32_t)XS;
-    const uint32_t per = (total + 7u) / 8u;
+    // contiguous run of the (token-major) tile sequence.  A split launch
+    // gives each XCD a run of the whole tiles first and then a run of the
+    // split tiles' parts, so every XCD holds its share of both and the whole
+    // tiles are dispatched first.  Workgroups past the end return whole (no
+    // barrier is skipped by part of one).
     const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    const uint32_t lin = xcd * per + slot;
-    if (lin >= total) return;  // whole workgroup: no barrier is skipped by part of it
-    const uint32_t tile = XS == 1 ? lin : lin / (uint32_t)XS;
-    const uint32_t xs = XS == 1 ? 0u : lin - tile * (uint32_t)XS;  // which run of the K steps
+    uint32_t tile, xs = 0u, np = (uint32_t)KS;  // np: runs of this tile's K steps
+    if constexpr (!SPLIT) {
+        const uint32_t total = mtiles * ntiles;
+        const uint32_t lin = xcd * ((total + 7u) / 8u) + slot;
+        if (lin >= total) return;
+        tile = lin;
+    } else {
+        const uint32_t wpx = (P.whole + 7u) / 8u;
+        if (slot < wpx) {
+            const uint32_t i = xcd * wpx + slot;
+            if (i >= P.whole) return;
+            tile = i;
+        } else {
+            const uint32_t np_all = P.splits * P.parts;
+            const uint32_t q = xcd * ((np_all + 7u) / 8u) + (slot - wpx);
+            if (q >= np_all) return;
+            tile = P.whole + q / P.parts;
+            xs = q % P.parts;
+            np = (uint32_t)KS * P.parts;
+        }
+    }
     const uint32_t nt = tile / mtiles, mt = tile - nt * mtiles;
     // the projection that owns weight-row tile mt (wave-uniform)
     const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
@@ -358,12 +377,13 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     // reads and the loads fall outside the buffer resources (they return 0).
     const uint32_t steps = (K + kBK - 1u) / kBK;
     const bool ragged = (K % kBK) != 0u;
-    // This group's steps: [s0, s0 + gs), run xs * KS + kg of NP; every group
+    // This group's steps: [s0, s0 + gs), run xs * KS + kg of np; every group
     // runs `iters` iterations (the same barriers), skipping the matrix work
     // past its own steps.
-    const uint32_t iters = NP == 1u ? steps : (steps + NP - 1u) / NP;
-    const uint32_t s0 = (xs * (uint32_t)KS + kg) * iters;
-    const uint32_t gs = NP == 1u ? steps : (s0 < steps ? min(iters, steps - s0) : 0u);
+    constexpr bool kOneRun = KS == 1 && !SPLIT;  // every group takes all the steps: no skip
+    const uint32_t iters = kOneRun ? steps : (steps + np - 1u) / np;
+    const uint32_t s0 = kOneRun ? 0u : (xs * (uint32_t)KS + kg) * iters;
+    const uint32_t gs = kOneRun ? steps : (s0 < steps ? min(iters, steps - s0) : 0u);
     auto convert_checked = [&](int s, int st) {
         const float rsum = convert_store(s, st);
         if (__builtin_amdgcn_ballot_w64(__builtin_isnan(rsum)) != 0) nonfinite_fixup(s, st);  // uniform
@@ -380,7 +400,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     auto iter = [&](int q, uint32_t i) {
         const int nx = (q + 1) % PD;
         if (ragged && s0 + i + 2u == steps) mask_b(nx, (s0 + i + 1u) * kBK);  // uniform
-        if (NP == 1u || i < gs) compute(q & 1);                                // uniform
+        if (kOneRun || i < gs) compute(q & 1);                                 // uniform
         convert_checked(nx, (q + 1) & 1);
         issue(nx, (s0 + i + 1u + (uint32_t)PD) * kBK);
         __syncthreads();
@@ -432,29 +452,27 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     }
 
     // Epilogue: lane (j, g) of block (f, b) holds features m0 + wm + 16 f +
-    // 4 g .. +3 of token n0 + wn + 16 b + j.  A split launch stores the
-    // unscaled sums: part 0 into the output, part xs into its part buffer.
-    const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + m0, XS == 1 ? mrows * 4u : 0u);
-    float* const dst = XS == 1 || xs == 0u ? out : P.part + (size_t)(xs - 1u) * P.partstride + P.partoff[pj];
+    // 4 g .. +3 of token n0 + wn + 16 b + j.  A split tile stores unscaled
+    // sums: part 0 into the output, part xs into its workspace block.
+    const bool split = SPLIT && tile >= P.whole;
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + m0, split ? 0u : mrows * 4u);
+    float* const blk = SPLIT && xs > 0u
+        ? P.part + ((size_t)(xs - 1u) * P.splits + (tile - P.whole)) * (size_t)(BM * kBN) : nullptr;
 #pragma unroll
     for (int f = 0; f < FB; ++f) {
         const uint32_t fm = wm + 16u * (uint32_t)f + 4u * g;  // within the tile
-        u32x4v sv = {0x3f800000u, 0x3f800000u, 0x3f800000u, 0x3f800000u};  // 1.0f
-        if constexpr (XS == 1) sv = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
+        const u32x4v sv = split ? u32x4v{0x3f800000u, 0x3f800000u, 0x3f800000u, 0x3f800000u}  // 1.0f
+                                : __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
 #pragma unroll
         for (int b = 0; b < TB; ++b) {
             const uint32_t tok = wn + 16u * (uint32_t)b + j;
             if (tok >= ntok) continue;
             f32x4 y;
-            if constexpr (XS == 1) {
-                y[0] = sum[f][b][0] * __uint_as_float(sv.x);
-                y[1] = sum[f][b][1] * __uint_as_float(sv.y);
-                y[2] = sum[f][b][2] * __uint_as_float(sv.z);
-                y[3] = sum[f][b][3] * __uint_as_float(sv.w);
-            } else {
-                y = sum[f][b];
-            }
-            float* o = dst + (size_t)(n0 + tok) * M + m0 + fm;
+            y[0] = sum[f][b][0] * __uint_as_float(sv.x);
+            y[1] = sum[f][b][1] * __uint_as_float(sv.y);
+            y[2] = sum[f][b][2] * __uint_as_float(sv.z);
+            y[3] = sum[f][b][3] * __uint_as_float(sv.w);
+            float* o = blk ? blk + tok * BM + fm : out + (size_t)(n0 + tok) * M + m0 + fm;
             if (fm + 3u < mrows) {
                 *reinterpret_cast<f32x4_a4*>(o) = f32x4_a4{y[0], y[1], y[2], y[3]};
             } else {
@@ -467,18 +485,43 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
 }
 
 // out = (part 0 + part 1 + ... + part parts-1) * scale, in part order, for
-// every output of a split launch (grid y: projection).
-__global__ __launch_bounds__(256) void split_sum_kernel(MatmulProjections P, uint32_t N, uint32_t parts) {
-    const uint32_t p = blockIdx.y;
-    float* __restrict__ y = P.out[p];
-    const float* __restrict__ sc = P.scale[p];
-    const uint32_t M = P.M[p];
-    const float* part = P.part + P.partoff[p];
-    const uint32_t n = N * M;
-    for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < n; e += gridDim.x * blockDim.x) {
-        float v = y[e];
-        for (uint32_t j = 1; j < parts; ++j) v += part[(size_t)(j - 1u) * P.partstride + e];
-        y[e] = v * sc[e % M];
+// every output of the split tiles of a split launch.  Grid x: split tile;
+// grid y: BM / 16 slices of it; a thread takes 4 consecutive rows of one
+// token (one 16-byte group of every part), all its loads in flight at once.
+template <uint32_t BM>
+__global__ __launch_bounds__(256) void split_sum_kernel(MatmulProjections P, uint32_t N, uint32_t mtiles) {
+    constexpr uint32_t G = BM / 4u;  // 4-row groups per token
+    static_assert(kBN * G == 256u * (BM / 16u), "one group per thread");
+    const uint32_t st = blockIdx.x, tile = P.whole + st;
+    const uint32_t nt = tile / mtiles, mt = tile - nt * mtiles;
+    const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
+    const uint32_t M = P.M[pj];
+    const uint32_t m0 = (mt - P.mt0[pj]) * BM, n0 = nt * kBN;
+    const uint32_t mrows = min(BM, M - m0), ntok = min(kBN, N - n0);
+    const uint32_t e = blockIdx.y * 256u + threadIdx.x;  // group index within the tile
+    const uint32_t t = e / G, r = (e - t * G) * 4u;
+    if (t >= ntok || r >= mrows) return;
+    float* y = P.out[pj] + (size_t)(n0 + t) * M + m0 + r;
+    const float* sc = P.scale[pj] + m0 + r;
+    const uint32_t parts = P.parts;
+    const size_t blk = (size_t)BM * kBN, off = (size_t)st * blk + (size_t)t * BM + r;
+    if (r + 3u < mrows) {
+        f32x4 v = *reinterpret_cast<const f32x4_a4*>(y);
+        const f32x4 s4 = *reinterpret_cast<const f32x4_a4*>(sc);
+        f32x4 q[3];
+#pragma unroll
+        for (uint32_t j = 1; j < 4u; ++j)
+            if (j < parts) q[j - 1u] = *reinterpret_cast<const f32x4*>(P.part + (size_t)(j - 1u) * P.splits * blk + off);
+#pragma unroll
+        for (uint32_t j = 1; j < 4u; ++j)
+            if (j < parts) v += q[j - 1u];
+        *reinterpret_cast<f32x4_a4*>(y) = v * s4;
+    } else {
+        for (uint32_t k = 0; k < mrows - r; ++k) {
+            float v = y[k];
+            for (uint32_t j = 1; j < parts; ++j) v += P.part[(size_t)(j - 1u) * P.splits * blk + off + k];
+            y[k] = v * sc[k];
+        }
     }
 }
 
@@ -488,17 +531,19 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
 }
 
 // One launch over `count` (1 to 4) projections of the same activations.
-// One launch over `count` (1 to 4) projections of the same activations; with
-// XS > 1 a second, the sum of the parts (`part` holds (XS - 1) x the
-// launch's outputs).
-template <int FB, int NW, int BK, int PD, int KS = 1, int XS = 1>
+// One launch over `count` (1 to 4) projections of the same activations.  With
+// splits > 0 (a SPLIT instance) the last `splits` tiles of the sequence have
+// their K steps split into `parts` runs, with the workspace `part` holding
+// (parts - 1) x splits blocks of BM x kBN floats, and a second launch sums
+// them.
+template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false>
 hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
-                     hipStream_t stream, float* part = nullptr) {
+                     hipStream_t stream, float* part = nullptr, uint32_t splits = 0, uint32_t parts = 1) {
     constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
     constexpr uint32_t BM = 32u * FB;
     const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
     MatmulProjections P = {};
-    uint32_t mtiles = 0, outs = 0;
+    uint32_t mtiles = 0;
     for (uint32_t i = 0; i < kMaxMatmulProjections; ++i) {
         if (i < count) {
             P.weight[i] = p[i].weight;
@@ -506,28 +551,26 @@ hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, 
             P.out[i] = p[i].output;
             P.M[i] = p[i].M;
             P.mt0[i] = mtiles;
-            P.partoff[i] = outs;
             mtiles += (p[i].M + BM - 1u) / BM;
-            if constexpr (XS > 1) outs += N * p[i].M;  // a split launch's outputs fit 32 bits (its tiles fit the CUs)
         } else {
             P.mt0[i] = 0xffffffffu;
         }
     }
-    P.part = part;
-    P.partstride = outs;
     const uint32_t ntiles = (N + kBN - 1u) / kBN;
-    const uint32_t total = mtiles * ntiles * (uint32_t)XS;
-    const uint32_t grid = ((total + 7u) / 8u) * 8u;
+    const uint32_t tiles = mtiles * ntiles;
+    P.part = part;
+    P.whole = tiles - splits;
+    P.splits = splits;
+    P.parts = parts;
+    uint32_t grid = ((tiles + 7u) / 8u) * 8u;
+    if constexpr (SPLIT) grid = 8u * ((P.whole + 7u) / 8u + (splits * parts + 7u) / 8u);
     const size_t lds = (size_t)KS * (2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes);
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, XS>), dim3(grid), dim3(64 * NW * KS), lds, stream, a, P, N,
-                       K, W, mtiles, ntiles);
-    if constexpr (XS > 1) {
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
+                       P, N, K, W, mtiles, ntiles);
+    if constexpr (SPLIT) {
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
-        uint32_t most = 0;
-        for (uint32_t i = 0; i < count; ++i) most = most > N * p[i].M ? most : N * p[i].M;
-        const uint32_t gx = (most + 255u) / 256u < 1024u ? (most + 255u) / 256u : 1024u;
-        hipLaunchKernelGGL(split_sum_kernel, dim3(gx, count), dim3(256), 0, stream, P, N, (uint32_t)XS);
+        hipLaunchKernelGGL(split_sum_kernel<BM>, dim3(splits, BM / 16u), dim3(256), 0, stream, P, N, mtiles);
     }
     return hipGetLastError();
 }
@@ -595,27 +638,46 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
         t2 += (uint64_t)((p[i].M + 63u) / 64u) * ntiles;
         t1 += (uint64_t)((p[i].M + 31u) / 32u) * ntiles;
     }
+    const uint32_t steps = (uint32_t)(((uint64_t)K + 63u) / 64u);
+    const char* kname = n > 1 ? "matmul_q8.multi" : "matmul_q8";
     if (t4 >= cus) {
-        set_variant(variant, n > 1 ? "matmul_q8.multi" : "matmul_q8", t4 <= cus ? "FB4.ksplit2" : "FB4",
-                    t4 <= cus ? 16 : 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
-        return t4 <= cus ? launch_fb<4, 8, 64, 2, 2>(a, p, n, N, K, stream)
-                         : launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
+        if (t4 == cus) {
+            set_variant(variant, kname, "FB4.ksplit2", 16, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
+            return launch_fb<4, 8, 64, 2, 2>(a, p, n, N, K, stream);
+        }
+        // Two workgroups per CU.  Between cus and 2 x cus tiles, some CUs
+        // take two tiles and the others one (384 tiles: half and half).  With
+        // a workspace, the last S = 2 x cus - tiles tiles split their K steps
+        // in two, so that whole tiles plus halves fill the 2 x cus slots and
+        // every CU holds the same work (384 tiles -> 256 whole and 256 halves,
+        // one of each per CU).  The halves' sum is a second launch (~5 us
+        // with its launch); with more tiles the dispatch already evens the
+        // CUs out over several rounds and the split no longer pays (704
+        // tiles: the GEMM 90 -> 85 us, plus the sum).  Same process, 512
+        // tokens: q, k, v 54.9 -> 49.3 us; at 256 tokens gate and up 51.6 ->
+        // 47.1.
+        const uint64_t slots = 2ull * cus;
+        const uint64_t S = t4 < slots ? slots - t4 : 0u;
+        const size_t blk = (size_t)128u * kBN * 4u;
+        if (workspace && S > 0 && steps >= 8u && S * blk <= workspace_bytes) {
+            set_variant(variant, kname, "FB4.balance2", 8, 128, 0, (int)kBN, (uint32_t)(t4 + S));
+            return launch_fb<4, 8, 64, 2, 1, true>(a, p, n, N, K, stream, workspace, (uint32_t)S, 2u);
+        }
+        set_variant(variant, kname, "FB4", 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
+        return launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
     }
     if (t1 <= cus) {
-        // With a workspace, tiles that fill at most half (a quarter) of the
-        // CUs also split their K steps between 2 (4) workgroups, each run at
+        // With a workspace, tiles that fill at most a quarter (a half) of the
+        // CUs also split their K steps between 4 (2) workgroups, each run at
         // least 4 steps per K group; the parts' sums meet in a second launch.
-        uint64_t outs = 0;  // the launch's outputs
-        for (uint32_t i = 0; i < n; ++i) outs += (uint64_t)N * p[i].M;
-        const uint32_t steps = (uint32_t)(((uint64_t)K + 63u) / 64u);
-        const char* kname = n > 1 ? "matmul_q8.multi" : "matmul_q8";
-        if (workspace && 4u * t1 <= cus && steps >= 32u && 3u * outs * 4u <= workspace_bytes) {
-            set_variant(variant, kname, "FB1.PD4.ksplit2.wgsplit4", 16, 32, 0, (int)kBN, (uint32_t)((4u * t1 + 7u) / 8u * 8u));
-            return launch_fb<1, 8, 64, 4, 2, 4>(a, p, n, N, K, stream, workspace);
+        const size_t blk = (size_t)32u * kBN * 4u;
+        if (workspace && 4u * t1 <= cus && steps >= 32u && 3u * t1 * blk <= workspace_bytes) {
+            set_variant(variant, kname, "FB1.PD4.ksplit2.wgsplit4", 16, 32, 0, (int)kBN, (uint32_t)(4u * t1));
+            return launch_fb<1, 8, 64, 4, 2, true>(a, p, n, N, K, stream, workspace, (uint32_t)t1, 4u);
         }
-        if (workspace && 2u * t1 <= cus && steps >= 16u && outs * 4u <= workspace_bytes) {
-            set_variant(variant, kname, "FB1.PD4.ksplit2.wgsplit2", 16, 32, 0, (int)kBN, (uint32_t)((2u * t1 + 7u) / 8u * 8u));
-            return launch_fb<1, 8, 64, 4, 2, 2>(a, p, n, N, K, stream, workspace);
+        if (workspace && 2u * t1 <= cus && steps >= 16u && t1 * blk <= workspace_bytes) {
+            set_variant(variant, kname, "FB1.PD4.ksplit2.wgsplit2", 16, 32, 0, (int)kBN, (uint32_t)(2u * t1));
+            return launch_fb<1, 8, 64, 4, 2, true>(a, p, n, N, K, stream, workspace, (uint32_t)t1, 2u);
         }
         set_variant(variant, kname, "FB1.PD4.ksplit2", 16, 32, 0, (int)kBN, (uint32_t)((t1 + 7u) / 8u * 8u));
         return launch_fb<1, 8, 64, 4, 2>(a, p, n, N, K, stream);
