@@ -386,6 +386,52 @@ def test_matmul_workspace_balance(N, Ms, K):
         assert_matmul(b[2].download(np.float32, N * M), a, w, s, N, M, K, rows=rows)
 
 
+FB4_CASES = [
+    # (N, Ms, K, workspace, form): 128-row tiles with two K groups, one per CU
+    (128, [5632, 5632], 2048, False, "FB4.ksplit2"),          # 176 tiles: most of the CUs
+    (256, [2048, 2048, 2048], 2048, True, "FB4.ksplit2"),     # 192 tiles, with a workspace too
+    (512, [2048], 4096, True, "FB4.ksplit2.wgsplit2"),         # 128 tiles x 2 parts
+    (512, [2048], 2048, True, "FB2.PD4.ksplit2"),              # too few steps per part: 64-row tiles
+    (256, [2048], 5632, True, "FB4.ksplit2.wgsplit4"),         # 64 tiles x 4 parts
+    (500, [1900], 3000, True, "FB4.ksplit2.wgsplit2"),         # ragged tokens, rows and K: 120 tiles x 2
+]
+
+
+@pytest.mark.parametrize("N,Ms,K,use_ws,form", FB4_CASES)
+def test_matmul_128_row_tiles(N, Ms, K, use_ws, form):
+    """128-row tiles filling most of the CUs, or all of them with their K
+    steps split between workgroups through the workspace: within the matmulQ8
+    bar of the oracle (every 3rd token), Inf and NaN activations included, the
+    same bits on a second run, nothing written past the outputs."""
+    rng = np.random.default_rng(N * 3 + K + len(Ms))
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[(N - 1) * K + 5] = np.inf
+    a[6 * K + 1] = np.nan
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    ws_bytes = wxo_q8.matmul_q8_workspace_bytes() if use_ws else 0
+    ws = wxo_q8.DeviceBuffer(ws_bytes) if use_ws else None
+    host, bufs = [], []
+    for M in Ms:
+        codes = rng.integers(-128, 128, (M, K)).astype(np.int32)
+        w = oracle.pack_q8(codes.reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        out.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), out, M))
+    runs = []
+    for _ in range(2):
+        wxo_q8.matmul_q8_multi_device(ba, bufs, N, K, workspace=ws, workspace_bytes=ws_bytes)
+        wxo_q8.synchronize()
+        assert wxo_q8.last_variant().split()[1] == form, wxo_q8.last_variant()
+        runs.append([b[2].download(np.float32, N * b[3] + 64) for b in bufs])
+    rows = np.unique(np.concatenate([np.arange(0, N, 3), [6, N - 1]]))
+    for (w, s, M), got, again in zip(host, runs[0], runs[1]):
+        assert_bits_equal(again, got, "repeat")
+        assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)
+
+
 def test_matmul_workspace_leaves_several_rounds_unsplit():
     """704 tiles (a 512-token gate and up) take several rounds of two
     workgroups per CU: the dispatch evens the CUs out itself and the split

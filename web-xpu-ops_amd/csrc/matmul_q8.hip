@@ -666,6 +666,33 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
         set_variant(variant, kname, "FB4", 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
         return launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
     }
+    // 128-row tiles that fill most of the CUs, one per CU with two K groups,
+    // beat smaller tiles that fill them all: a 128-row tile moves ~19 bytes
+    // through LDS per output and step against ~27 for 64 rows and ~45 for
+    // 32.  Same process, µs: 128 tokens gate and up (176 tiles) 38.6 -> 32.0,
+    // 256 tokens q, k, v (192 tiles) 38.9 -> 33.2; with 128 tiles (half the
+    // CUs) they lose (512 tokens o: 29.6 -> 31.4, one box and process).
+    if (5u * t4 >= 3u * cus) {
+        set_variant(variant, kname, "FB4.ksplit2", 16, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
+        return launch_fb<4, 8, 64, 2, 2>(a, p, n, N, K, stream);
+    }
+    // With a workspace, 128-row tiles whose K steps split in 2 or 4 fill
+    // (nearly) every CU, as long as each K group keeps at least 10 steps
+    // (the split's second launch and every part's pipeline start cost a few
+    // us): 512 tokens down 55.8 -> 49.9 us (2 parts, 22 steps per group), 256
+    // tokens down 40.2 -> 31.1 (4 parts, 11 steps).  Fewer workgroups than
+    // 7/8 of the CUs, or shorter runs, lose to the smaller tiles below (512
+    // tokens o in 2 parts of 8 steps per group: 21.9 -> 26.0; 128 tokens q, k,
+    // v in 2 parts on 3/4 of the CUs: 21.8 -> 23.9).
+    for (uint32_t xs : {4u, 2u}) {
+        const size_t blk = (size_t)128u * kBN * 4u;
+        if (workspace && t4 * xs <= cus && 8u * t4 * xs > 7u * cus && steps >= 20u * xs &&
+            (xs - 1u) * t4 * blk <= workspace_bytes) {
+            set_variant(variant, kname, xs == 4u ? "FB4.ksplit2.wgsplit4" : "FB4.ksplit2.wgsplit2", 16, 128, 0, (int)kBN,
+                        (uint32_t)(t4 * xs));
+            return launch_fb<4, 8, 64, 2, 2, true>(a, p, n, N, K, stream, workspace, (uint32_t)t4, xs);
+        }
+    }
     if (t1 <= cus) {
         // With a workspace, tiles that fill at most a quarter (a half) of the
         // CUs also split their K steps between 4 (2) workgroups, each run at
