@@ -528,6 +528,56 @@ gpuTest(F, "runnerFromResident: one dispatch per call on its own buffers, destro
   device.destroy();
 });
 
+gpuTest(F, "captured prefill batches: split matmulQ8 launches (the workspace's two kernels) replay with the bits of op-by-op issue", async () => {
+  const replaying = await createResidentQ8Device();
+  const eager = await createResidentQ8Device({ graphs: false });
+  const N = 64, K = 2048, Kd = 1100, rows = [512, 256, 256], Md = 512;  // q, k, v; a down-like projection
+  const lins = rows.map((M, i) => linear(M, K, 300 + i));
+  const ld = linear(Md, Kd, 310);
+  const setup = (d) => {
+    const buf = (bytes) => d.createStorageBuffer(bytes);
+    const put = (data) => { const b = buf(data.byteLength); d.upload(b, 0, data); return b; };
+    const a = buf(N * K * 4), ad = buf(N * Kd * 4);
+    const proj = lins.map((l, i) => ({ w: put(packInt8Rows(l.codes, rows[i], K)), s: put(l.scale), y: buf(N * rows[i] * 4), M: rows[i] }));
+    const down = { w: put(packInt8Rows(ld.codes, Md, Kd)), s: put(ld.scale), y: buf(N * Md * 4), M: Md };
+    const ops = [...proj.map((p) => ({ kind: "matmulQ8", a, weight: p.w, scale: p.s, output: p.y, N, M: p.M, K })),
+      { kind: "matmulQ8", a: ad, weight: down.w, scale: down.s, output: down.y, N, M: Md, K: Kd }];
+    const rb = [...proj, down].map((p) => ({ source: p.y, sourceOffset: 0, length: N * p.M, type: "f32" }));
+    return { a, ad, ops, rb };
+  };
+  const [r, e] = [setup(replaying), setup(eager)];
+  let last = null;
+  for (let step = 0; step < 4; step += 1) {
+    const x = vec(N * K, 700 + step), xd = vec(N * Kd, 800 + step);
+    for (const [d, t] of [[replaying, r], [eager, e]]) { d.upload(t.a, 0, x); d.upload(t.ad, 0, xd); }
+    const got = await replaying.batch(r.ops, r.rb);
+    const want = await eager.batch(e.ops, e.rb);
+    got.forEach((g, i) => assertBitsEqualLocal(g, want[i]));
+    last = { x, got };
+  }
+  // step 0 op by op, step 1 captured and launched, steps 2-3 replayed; q/k/v shared one launch
+  assert.strictEqual(replaying.stats.graphsCaptured, 1);
+  assert.strictEqual(replaying.stats.graphLaunches, 3);
+  assert.strictEqual(replaying.stats.launches, eager.stats.launches);
+  // the last replay's q against the oracle (matmulQ8 bar)
+  const W = Math.ceil(K / 4);
+  const packed = packInt8Rows(lins[0].codes, rows[0], K);
+  const want = oracle.matmulQ8({ a: last.x, weight: packed, scale: lins[0].scale, N, M: rows[0], K });
+  for (let n = 0; n < N; n += 7) {
+    for (let m = 0; m < rows[0]; m += 5) {
+      let bound = 0;
+      for (let k = 0; k < K; k += 1) {
+        const byte = (packed[m * W + (k >> 2)] >>> ((k & 3) * 8)) & 0xff;
+        bound += Math.abs(last.x[n * K + k] * Math.fround((byte >= 128 ? byte - 256 : byte) * lins[0].scale[m]));
+      }
+      const err = Math.abs(last.got[0][n * rows[0] + m] - want[n * rows[0] + m]);
+      if (!(err <= 1e-5 * bound + 1e-7)) assert.fail(`[${n}, ${m}] got ${last.got[0][n * rows[0] + m]} want ${want[n * rows[0] + m]}`);
+    }
+  }
+  replaying.destroy();
+  eager.destroy();
+});
+
 gpuTest(F, "buffer.destroy(): released once, and every later use throws before anything runs", async () => {
   const device = await createResidentQ8Device();
   const pipeline = await device.pipelineFor(Q8);
