@@ -46,6 +46,14 @@
 // Workgroups are numbered so that the 8 XCDs (which take workgroups
 // round-robin) each hold a contiguous run of tiles that share activation
 // tiles in that XCD's L2.
+//
+// With a caller's workspace, a launch may also split some tiles' K steps
+// between 2 or 4 workgroups (a short prompt's tiles, which would leave most
+// CUs idle; the last tiles of a round that would load the CUs unevenly):
+// part 0 stores its unscaled sums into the output, the other parts into
+// tile-sized workspace blocks, and a second launch adds them in part order
+// and scales them.  The stream order between the two launches is the only
+// synchronisation, so every run gives the same bits.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
