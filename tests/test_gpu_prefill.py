@@ -432,6 +432,63 @@ def test_matmul_128_row_tiles(N, Ms, K, use_ws, form):
         assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)
 
 
+def random_packed(rng, M, K):
+    """Packed weight words with any bytes and zero pad codes past K (the wire format)."""
+    W = (K + 3) // 4
+    w = rng.integers(0, 2 ** 32, (M, W), dtype=np.uint64).astype(np.uint32)
+    if K % 4:
+        w[:, -1] &= np.uint32((1 << (8 * (K % 4))) - 1)
+    return w.reshape(-1)
+
+
+def test_matmul_random_shapes_every_plan():
+    """Seeded random shapes across the dispatch's plans (32-, 64- and 128-row
+    tiles, one or two K groups, splits in 2 or 4 parts, the balanced round,
+    several projections), with and without a workspace: every output row
+    sampled is within the matmulQ8 bar of the oracle, and nothing is written
+    past the outputs."""
+    rng = np.random.default_rng(20261202)
+    forms = set()
+    for case in range(24):
+        N = int(rng.integers(33, 700))
+        Ms = [int(rng.integers(1, 2600)) for _ in range(int(rng.integers(1, 4)))]
+        K = int(rng.integers(64, 5200))
+        a = rng.standard_normal(N * K).astype(np.float32)
+        ba = wxo_q8.DeviceBuffer.from_array(a)
+        host, bufs = [], []
+        for M in Ms:
+            w = random_packed(rng, M, K)
+            s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+            out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+            host.append((w, s, M))
+            bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), out, M))
+        rows = np.unique(np.r_[rng.integers(0, N, 5), N - 1])
+        ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+        ws = wxo_q8.DeviceBuffer(ws_bytes)
+        for use_ws in (False, True):
+            for (_, _, out, M) in bufs:
+                out.upload(np.full(N * M + 64, 7.5, np.float32))
+            if use_ws:
+                wxo_q8.matmul_q8_multi_device(ba, bufs, N, K, workspace=ws, workspace_bytes=ws_bytes)
+            else:
+                wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
+            wxo_q8.synchronize()
+            form = wxo_q8.last_variant().split()[1]
+            forms.add(form)
+            for (w, s, M), (_, _, out, _) in zip(host, bufs):
+                got = out.download(np.float32, N * M + 64)
+                where = f"case {case} N={N} Ms={Ms} K={K} workspace={use_ws} {form}"
+                assert np.all(got[N * M:] == np.float32(7.5)), f"{where}: written past the output"
+                asub = np.ascontiguousarray(a.reshape(N, K)[rows])
+                want = oracle.matmul_q8(asub, w, s, len(rows), M, K)
+                bound = oracle.matmul_absterm(asub, w, s, len(rows), M, K)
+                ok, msg = oracle.check_matvec(got[:N * M].reshape(N, M)[rows].reshape(-1), want.reshape(-1),
+                                              bound.reshape(-1))
+                assert ok, f"{where}: {msg}"
+        ws.free()
+    assert len(forms) >= 5, forms
+
+
 def test_matmul_workspace_leaves_several_rounds_unsplit():
     """704 tiles (a 512-token gate and up) take several rounds of two
     workgroups per CU: the dispatch evens the CUs out itself and the split
