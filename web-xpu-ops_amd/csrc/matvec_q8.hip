@@ -1160,7 +1160,7 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
             // complete in order, so lgkmcnt(1) already covers the reads
             __builtin_amdgcn_sched_barrier(0);
             if (q > 0 && ((q - 1) % GP) != 0 && ((q - 2 + GP) % SW) == SW - 1 && (q % GP) != 0)
-                __builtin_amdgcn_s_waitcnt(0xc07f & ~0x0f00 | 0x0100);  // lgkmcnt(1)
+                __builtin_amdgcn_s_waitcnt((0xc07f & ~0x0f00) | 0x0100);  // lgkmcnt(1)
             else
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
             __builtin_amdgcn_sched_barrier(0);
