@@ -114,6 +114,12 @@ int wxo_malloc(void** ptr, size_t bytes);
 int wxo_free(void* ptr);
 int wxo_memcpy_htod(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
 int wxo_memcpy_dtoh(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
+/* Sets `bytes` bytes at the device address `ptr` to (value & 0xff), on
+ * `stream`, with a fill kernel (so it may be captured into a HIP graph).  No
+ * counterpart in the reference: WebGPU hands out zero-filled buffers, which the
+ * engine relies on (llm/engine-q8-resident.ts:1103-1110, :1424), and the
+ * resident device clears every new storage buffer with this. */
+int wxo_memset(void* ptr, int value, size_t bytes, wxo_stream_t stream);
 int wxo_memcpy_dtod(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
 int wxo_synchronize(void);
 int wxo_stream_create(wxo_stream_t* stream);

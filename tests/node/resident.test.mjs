@@ -578,6 +578,20 @@ gpuTest(F, "captured prefill batches: split matmulQ8 launches (the workspace's t
   eager.destroy();
 });
 
+gpuTest(F, "new storage buffers read as zero, as WebGPU's do (the engine's never-uploaded attention mask)", async () => {
+  const device = await createResidentQ8Device();
+  // fill a buffer with non-zero bytes and release it, so the next allocation can reuse the memory
+  for (const bytes of [4096, 4 * 1000 + 12, 1 << 20]) {
+    const a = device.createStorageBuffer(bytes);
+    device.upload(a, 0, new Uint8Array(bytes).fill(0xa5));
+    a.destroy();
+    const b = device.createStorageBuffer(bytes);
+    const [got] = await device.batch([], [{ source: b, sourceOffset: 0, length: bytes / 4, type: "u32" }]);
+    assert.ok(got.every((x) => x === 0), `${bytes} B: a new buffer holds non-zero bytes`);
+  }
+  device.destroy();
+});
+
 gpuTest(F, "buffer.destroy(): released once, and every later use throws before anything runs", async () => {
   const device = await createResidentQ8Device();
   const pipeline = await device.pipelineFor(Q8);

@@ -75,3 +75,21 @@ def test_read_waits_for_the_stream():
     for b in (weight, scale, out):
         b.free()
     stream.destroy()
+
+
+@pytest.mark.parametrize("offset", [0, 1, 3, 16, 17])
+@pytest.mark.parametrize("length", [0, 1, 15, 16, 17, 1000, 65536 + 5])
+def test_memset_any_offset_and_length(offset, length):
+    """wxo_memset sets exactly [offset, offset + length) and no byte around it."""
+    wxo_q8.init()
+    size = 70000
+    before = np.random.default_rng(offset * 7 + length).integers(0, 256, size, dtype=np.uint8)
+    buf = wxo_q8.DeviceBuffer.from_array(before)
+    wxo_q8._check(wxo_q8.lib().wxo_memset(buf.ptr + offset, 0x15a, length, None))  # value & 0xff = 0x5a
+    wxo_q8.synchronize()
+    got = buf.download(np.uint8, size)
+    want = before.copy()
+    want[offset:offset + length] = 0x5a
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"offset={offset} length={length}: {bad.size} bytes differ, first at {bad[0]}"
+    buf.free()

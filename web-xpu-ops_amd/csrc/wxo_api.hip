@@ -311,6 +311,36 @@ int wxo_memcpy_dtod(void* dst, const void* src, size_t bytes, wxo_stream_t strea
     return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream, "memcpy D2D");
 }
 
+namespace {
+// Sets bytes [0, head) and [head + 16 body, + tail) one by one and the 16-byte
+// aligned body between them with 16-byte stores (head, tail < 16).
+__global__ __launch_bounds__(256) void fill_bytes_kernel(uint8_t* p, uint32_t v4, size_t head, size_t body, size_t tail) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+    uint4* b = reinterpret_cast<uint4*>(p + head);
+    for (size_t i = tid; i < body; i += stride) b[i] = make_uint4(v4, v4, v4, v4);
+    if (tid < head) p[tid] = (uint8_t)v4;
+    if (tid < tail) p[head + 16u * body + tid] = (uint8_t)v4;
+}
+}  // namespace
+
+int wxo_memset(void* ptr, int value, size_t bytes, wxo_stream_t stream) {
+    if (bytes == 0) return ok();
+    if (!ptr) return fail(WXO_ERR_INVALID, "memset: NULL pointer");
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    const uintptr_t a = (uintptr_t)ptr;
+    size_t head = (16u - (a & 15u)) & 15u;
+    if (head > bytes) head = bytes;
+    const size_t body = (bytes - head) / 16u, tail = bytes - head - 16u * body;
+    const uint32_t v = (uint32_t)(value & 0xff) * 0x01010101u;
+    const size_t blocks = (body + 255u) / 256u;
+    const uint32_t grid = (uint32_t)(blocks < 4096u ? (blocks > 0u ? blocks : 1u) : 4096u);
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3(grid), dim3(256), 0, as_hip(stream), static_cast<uint8_t*>(ptr), v, head,
+                       body, tail);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? ok() : hip_fail(e, "fill launch");
+}
+
 int wxo_synchronize(void) {
     hipError_t e = hipDeviceSynchronize();
     return e == hipSuccess ? ok() : hip_fail(e, "hipDeviceSynchronize");

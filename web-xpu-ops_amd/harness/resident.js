@@ -109,7 +109,12 @@ export class ResidentQ8Device {
     if (usage & BufferUsage.MAP_READ) {
       return this.track({ ptr: null, host: new Uint8Array(size), size, usage, kind: "staging" });
     }
-    return this.track({ ptr: this.addon.malloc(size), size, usage, kind: "storage" });
+    // WebGPU hands out zero-filled buffers, and the engine relies on it (an
+    // all-zero attention mask is never uploaded, llm/engine-q8-resident.ts:
+    // 1103-1110, :1424): cleared here, once, before anything else can write it.
+    const ptr = this.addon.malloc(size);
+    this.addon.zero(ptr, size);
+    return this.track({ ptr, size, usage, kind: "storage" });
   }
 
   /** A uniform buffer of max(16, bytes) bytes, held in host memory (read when a dispatch is enqueued). */

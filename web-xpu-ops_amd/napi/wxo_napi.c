@@ -717,6 +717,25 @@ static napi_value js_download(napi_env env, napi_callback_info info) {
     return argv[1];
 }
 
+/* zero(ptr, bytes): the bytes cleared on the null stream, done before it
+ * returns (a new buffer's WebGPU contents; set-up, never inside a batch). */
+static napi_value js_zero(napi_env env, napi_callback_info info) {
+    size_t argc = 2;
+    napi_value argv[2];
+    uint64_t p;
+    if (!get_args(env, info, 2, &argc, argv) || !get_ptr(env, argv[0], &p, "ptr")) return NULL;
+    double d = -1;
+    napi_get_value_double(env, argv[1], &d);
+    if (!(d >= 0) || d != (double)(uint64_t)d) {
+        napi_throw_type_error(env, NULL, "bytes must be a non-negative integer");
+        return NULL;
+    }
+    int st = wxo_memset((void*)(uintptr_t)p, 0, (size_t)d, NULL);
+    if (st == WXO_OK) st = wxo_stream_synchronize(NULL);
+    if (st != WXO_OK) return throw_status(env, st, "zero");
+    return NULL;
+}
+
 static napi_value js_copy(napi_env env, napi_callback_info info) {
     size_t argc = 3;
     napi_value argv[3];
@@ -1099,6 +1118,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"upload", NULL, js_upload, NULL, NULL, NULL, napi_enumerable, NULL},
         {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
         {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"zero", NULL, js_zero, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8MultiDevice", NULL, js_matvec_q8_multi_device, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8ResidualDevice", NULL, js_matvec_q8_residual_device, NULL, NULL, NULL, napi_enumerable, NULL},

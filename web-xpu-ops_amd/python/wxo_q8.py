@@ -54,6 +54,7 @@ SIGNATURES = {
     "wxo_memcpy_htod": ([_P, _P, _SZ, _P], _I),
     "wxo_memcpy_dtoh": ([_P, _P, _SZ, _P], _I),
     "wxo_memcpy_dtod": ([_P, _P, _SZ, _P], _I),
+    "wxo_memset": ([_P, _I, _SZ, _P], _I),
     "wxo_synchronize": ([], _I),
     "wxo_stream_create": ([ctypes.POINTER(_P)], _I),
     "wxo_stream_destroy": ([_P], _I),
