@@ -616,6 +616,19 @@ def run_prefill_suite(stream, steps, warmup, results, check):
                         "TFLOP/s": round(short_flops / (short_us * 1e-6) / 1e12, 1), "variants": variants})
         log(f"suite prefill layer, {Ts} tokens, coalesced: {short_us:.1f} us  "
             f"{short_flops / (short_us * 1e-6) / 1e12:.1f} TFLOP/s")
+    # The same four launches without a workspace (wxo_matmul_q8_multi: no K
+    # split between workgroups), at every prompt length, beside the above.
+    for Ts in (64, 128, 256, T):
+        plain_us = 0.0
+        for act, names in groups:
+            K = by[names[0]][1]
+            projs = [(by[n][2].ptr, by[n][3].ptr, outs[n].ptr, by[n][0]) for n in names]
+            plain_us += time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, Ts, K, stream),
+                                  max(1, steps // 20), max(1, warmup // 20))
+        results.append({"case": f"prefill matmulQ8: one decoder layer, {Ts} tokens, 4 launches without a workspace",
+                        "us": round(plain_us, 3),
+                        "TFLOP/s": round(total_flops * Ts / T / (plain_us * 1e-6) / 1e12, 1)})
+        log(f"suite prefill layer, {Ts} tokens, 4 launches without a workspace: {plain_us:.1f} us")
     for b in outs.values():
         b.free()
     ws.free()
