@@ -538,7 +538,6 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
-// One launch over `count` (1 to 4) projections of the same activations.
 // One launch over `count` (1 to 4) projections of the same activations.  With
 // splits > 0 (a SPLIT instance) the last `splits` tiles of the sequence have
 // their K steps split into `parts` runs, with the workspace `part` holding
