@@ -12,10 +12,13 @@
  *   Int32Array[i]   = v   -> ToInt32(v); NaN -> 0, -0 -> 0     (to_int32 below)
  *   Uint32Array[i]  = v   -> ToUint32(v)
  */
+#define _DEFAULT_SOURCE /* sysconf */
 #include "q8_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
+#include <unistd.h>
 
 /* Math.max / Math.min: NaN if either operand is NaN (ECMAScript 21.3.2.24/25). */
 static double js_max(double a, double b) {
@@ -102,25 +105,86 @@ void q8o_pack_int8_rows(const int8_t* codes, size_t N, size_t K, uint32_t* packe
     }
 }
 
+/* The output rows of the matvec and matmul oracles are independent, so they
+ * are split over threads; every output element is still one f64 sum over k
+ * in ascending order, the same operations as one loop per element, so the
+ * results do not depend on the thread count.  Threads: OMP_NUM_THREADS when
+ * set, else the online CPUs, at most 16; small problems run on the caller's
+ * thread. */
+typedef void (*rows_fn)(size_t r0, size_t r1, void* ctx);
+struct rows_task {
+    rows_fn fn;
+    void* ctx;
+    size_t r0, r1;
+};
+
+static void* rows_thread(void* p) {
+    struct rows_task* t = (struct rows_task*)p;
+    t->fn(t->r0, t->r1, t->ctx);
+    return NULL;
+}
+
+static void parallel_rows(size_t rows, size_t work, rows_fn fn, void* ctx) {
+    long threads = 1;
+    const char* env = getenv("OMP_NUM_THREADS");
+    if (env && atol(env) > 0) threads = atol(env);
+    else threads = sysconf(_SC_NPROCESSORS_ONLN);
+    if (threads > 16) threads = 16;
+    if (threads < 1 || work < ((size_t)1 << 24)) threads = 1;
+    if ((size_t)threads > rows) threads = (long)rows;
+    if (threads <= 1) {
+        fn(0, rows, ctx);
+        return;
+    }
+    pthread_t tid[16];
+    struct rows_task task[16];
+    int created[16] = {0};
+    for (long i = 0; i < threads; ++i)
+        task[i] = (struct rows_task){fn, ctx, rows * (size_t)i / (size_t)threads, rows * (size_t)(i + 1) / (size_t)threads};
+    for (long i = 1; i < threads; ++i) created[i] = pthread_create(&tid[i], NULL, rows_thread, &task[i]) == 0;
+    fn(task[0].r0, task[0].r1, ctx);
+    for (long i = 1; i < threads; ++i) {
+        if (created[i]) pthread_join(tid[i], NULL);
+        else fn(task[i].r0, task[i].r1, ctx);  /* no thread: these rows run here */
+    }
+}
+
 /* ops/matvec/reference.ts:113-115 (unpackI8: byte >= 128 ? byte - 256 : byte). */
 static int unpack_i8(uint32_t byte) { return byte >= 128 ? (int)byte - 256 : (int)byte; }
+
+struct matvec_job {
+    const uint32_t* weight;
+    const float* scale;
+    const float* vector;
+    size_t K;
+    float* output;  /* matvecQ8, or */
+    double* bound;  /* sum_k |s q x| */
+};
 
 /* ops/matvec/reference.ts:117-131.  Sum left to right in f64 over col < K only
  * (pad lanes are never read), then one f64 multiply by the row's scale and
  * one rounding to f32. */
-void q8o_matvec_q8(const uint32_t* weight, const float* scale, const float* vector,
-                   size_t N, size_t K, float* output) {
-    const size_t W = (K + 3) / 4;
-    for (size_t row = 0; row < N; ++row) {
+static void matvec_rows(size_t r0, size_t r1, void* ctx) {
+    const struct matvec_job* j = (const struct matvec_job*)ctx;
+    const size_t K = j->K, W = (K + 3) / 4;
+    for (size_t row = r0; row < r1; ++row) {
         const size_t rowOffset = row * W;
         double sum = 0.0;
         for (size_t col = 0; col < K; ++col) {
-            const uint32_t word = weight[rowOffset + (col >> 2)];
+            const uint32_t word = j->weight[rowOffset + (col >> 2)];
             const uint32_t byte = (word >> ((col & 3) * 8)) & 0xffu;
-            sum += (double)unpack_i8(byte) * (double)vector[col];
+            const double t = (double)unpack_i8(byte) * (double)j->vector[col];
+            sum += j->output ? t : fabs(t);
         }
-        output[row] = (float)(sum * (double)scale[row]);
+        if (j->output) j->output[row] = (float)(sum * (double)j->scale[row]);
+        else j->bound[row] = sum * fabs((double)j->scale[row]);
     }
+}
+
+void q8o_matvec_q8(const uint32_t* weight, const float* scale, const float* vector,
+                   size_t N, size_t K, float* output) {
+    struct matvec_job job = {weight, scale, vector, K, output, NULL};
+    parallel_rows(N, N * K, matvec_rows, &job);
 }
 
 /* M independent matvecQ8 calls: vectors [M, K], output [M, N]. */
@@ -135,16 +199,8 @@ void q8o_matvec_q8_batched(const uint32_t* weight, const float* scale, const flo
  * |y - y_ref| <= 1e-5 * bound + 1e-7. */
 void q8o_matvec_q8_absterm(const uint32_t* weight, const float* scale, const float* vector,
                            size_t N, size_t K, double* bound) {
-    const size_t W = (K + 3) / 4;
-    for (size_t row = 0; row < N; ++row) {
-        double sum = 0.0;
-        for (size_t col = 0; col < K; ++col) {
-            const uint32_t word = weight[row * W + (col >> 2)];
-            const uint32_t byte = (word >> ((col & 3) * 8)) & 0xffu;
-            sum += fabs((double)unpack_i8(byte) * (double)vector[col]);
-        }
-        bound[row] = sum * fabs((double)scale[row]);
-    }
+    struct matvec_job job = {weight, scale, vector, K, NULL, bound};
+    parallel_rows(N, N * K, matvec_rows, &job);
 }
 
 /* ops/matvec/reference.ts:235-243 (matvecQ8Residual): projected = matvecQ8 row
@@ -184,6 +240,60 @@ static float dequant_term(uint32_t word, size_t lane, float s) {
     return (float)((double)unpack_i8(byte) * (double)s);
 }
 
+/* b[row * K + k]: the dequantized terms of weight row `row`, in k order. */
+static float* dequant_rows(const uint32_t* weight, const float* scale, size_t M, size_t K) {
+    const size_t W = (K + 3) / 4;
+    float* b = (float*)malloc((K * M != 0 ? K * M : 1) * sizeof(float));
+    for (size_t row = 0; row < M; ++row)
+        for (size_t k = 0; k < K; ++k) b[row * K + k] = dequant_term(weight[row * W + (k >> 2)], k & 3, scale[row]);
+    return b;
+}
+
+struct matmul_job {
+    const float* a;
+    const float* b;
+    size_t N, M, K;
+    float* output;  /* the matmul, or */
+    double* bound;  /* sum_k |a * b| */
+};
+
+/* Columns c0 .. c0 + NC - 1 of one output row: NC independent sums, each
+ * over k in ascending order.  ABS sums |a * b| instead (the error bound). */
+#define MATMUL_COLUMNS(NAME, NC, ABS)                                                     \
+    static void NAME(const float* ar, const float* b, size_t c0, size_t nc, size_t K,     \
+                     double* out) {                                                       \
+        double sum[NC];                                                                   \
+        for (size_t c = 0; c < (NC); ++c) sum[c] = 0.0;                                   \
+        for (size_t k = 0; k < K; ++k) {                                                  \
+            const double x = (double)ar[k];                                               \
+            for (size_t c = 0; c < (NC); ++c) {                                           \
+                const double t = x * (double)b[(c0 + (c < nc ? c : 0)) * K + k];          \
+                sum[c] += (ABS) ? fabs(t) : t;                                            \
+            }                                                                             \
+        }                                                                                 \
+        for (size_t c = 0; c < nc; ++c) out[c] = sum[c];                                  \
+    }
+MATMUL_COLUMNS(columns8, 8, 0)
+MATMUL_COLUMNS(columns8_abs, 8, 1)
+
+static void matmul_rows(size_t r0, size_t r1, void* ctx) {
+    const struct matmul_job* j = (const struct matmul_job*)ctx;
+    const size_t M = j->M, K = j->K;
+    double s[8];
+    for (size_t row = r0; row < r1; ++row) {
+        for (size_t c0 = 0; c0 < M; c0 += 8) {
+            const size_t nc = M - c0 < 8 ? M - c0 : 8;
+            if (j->output) {
+                columns8(j->a + row * K, j->b, c0, nc, K, s);
+                for (size_t c = 0; c < nc; ++c) j->output[row * M + c0 + c] = (float)s[c];
+            } else {
+                columns8_abs(j->a + row * K, j->b, c0, nc, K, s);
+                for (size_t c = 0; c < nc; ++c) j->bound[row * M + c0 + c] = s[c];
+            }
+        }
+    }
+}
+
 /* ops/matmul/reference.ts:124-137 (matmulQ8): b[k * M + row] =
  * Float32Array(unpackI8(byte) * scale[row]) for the weight's M rows, then
  * matmul({a, b, M: N, N: M, K}) (:37-49): for each output element, an f64
@@ -191,18 +301,9 @@ static float dequant_term(uint32_t word, size_t lane, float s) {
  * Float32Array.  output is [N, M]. */
 void q8o_matmul_q8(const float* a, const uint32_t* weight, const float* scale, size_t N, size_t M, size_t K,
                    float* output) {
-    const size_t W = (K + 3) / 4;
-    float* b = (float*)malloc((K * M != 0 ? K * M : 1) * sizeof(float));
-    for (size_t row = 0; row < M; ++row)
-        for (size_t k = 0; k < K; ++k)
-            b[k * M + row] = dequant_term(weight[row * W + (k >> 2)], k & 3, scale[row]);
-    for (size_t row = 0; row < N; ++row) {
-        for (size_t col = 0; col < M; ++col) {
-            double sum = 0.0;
-            for (size_t k = 0; k < K; ++k) sum += (double)a[row * K + k] * (double)b[k * M + col];
-            output[row * M + col] = (float)sum;
-        }
-    }
+    float* b = dequant_rows(weight, scale, M, K);
+    struct matmul_job job = {a, b, N, M, K, output, NULL};
+    parallel_rows(N, (size_t)N * M * K, matmul_rows, &job);
     free(b);
 }
 
@@ -210,18 +311,12 @@ void q8o_matmul_q8(const float* a, const uint32_t* weight, const float* scale, s
  * magnitude the f32 kernel's rounding error is measured against. */
 void q8o_matmul_q8_absterm(const float* a, const uint32_t* weight, const float* scale, size_t N, size_t M,
                            size_t K, double* bound) {
-    const size_t W = (K + 3) / 4;
-    for (size_t n = 0; n < N; ++n)
-        for (size_t m = 0; m < M; ++m) {
-            double sum = 0.0;
-            for (size_t k = 0; k < K; ++k)
-                sum += fabs((double)a[n * K + k] * (double)dequant_term(weight[m * W + (k >> 2)], k & 3, scale[m]));
-            bound[n * M + m] = sum;
-        }
+    float* b = dequant_rows(weight, scale, M, K);
+    struct matmul_job job = {a, b, N, M, K, NULL, bound};
+    parallel_rows(N, (size_t)N * M * K, matmul_rows, &job);
+    free(b);
 }
 
-/* llm/weights-q8.ts:161-177 (dequantizePackedQ8): output[row * K + col] =
- * signed byte col of the row times scale[row], stored to a Float32Array. */
 void q8o_dequantize_packed_q8(const uint32_t* weight, const float* scale, size_t N, size_t K, float* output) {
     const size_t W = (K + 3) / 4;
     for (size_t row = 0; row < N; ++row)
