@@ -8,6 +8,8 @@
     finite) with subnormal elements, so the fast path meets subnormal operands;
   * the batched LM head (cfg5) checked against the oracle on every row;
   * which kernel instance ran (wxo_last_variant), per thread.
+  * rows far longer than the other suites' (K = 65539 and 131075) on every
+    kernel family.
 
 Bars as everywhere: codes, packed words and scales bit-exact;
 matvecQ8 |y - y_ref| <= 1e-5 * sum_k |s q x| + 1e-7 per row.
@@ -20,7 +22,7 @@ import pytest
 import oracle
 import wxo_q8
 import wxo_workloads as wl
-from test_gpu_parity import assert_bits_equal, assert_matvec
+from test_gpu_parity import assert_bits_equal, assert_ffn, assert_matvec, assert_residual, random_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -370,3 +372,73 @@ def test_graph_replays_match_eager_issue():
         g.destroy()
         st.destroy()
 
+
+
+# ---------------------------------------------------------------- long rows
+
+def test_long_rows_single_vector_and_fused_forms():
+    """K = 131075 (128 whole 1 KiB chunks and one word): the single-vector
+    kernel's chunk-slot loop far past the sweeps' 20000, with the fused
+    residual and FFN epilogues on the same rows."""
+    rng = np.random.default_rng(131075)
+    N, K = 37, 131075
+    w = random_weights(rng, N, K, full_range=True)
+    wu = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    su = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    r = rng.standard_normal(N).astype(np.float32)
+    assert_matvec(wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K), w, s, x, N, K)
+    assert_residual(wxo_q8.matvecQ8Residual(weight=w, scale=s, vector=x, residual=r, N=N, K=K), w, s, x, r, N, K)
+    assert_ffn(wxo_q8.matvecQ8Ffn(weightGate=w, scaleGate=s, weightUp=wu, scaleUp=su, vector=x, N=N, K=K),
+               w, s, wu, su, x, N, K)
+
+
+@pytest.mark.parametrize("M", [3, 8, 16])
+def test_long_rows_batched(M):
+    """K = 65539 with several vectors: past every matrix-core kernel's LDS
+    budget for the vectors' parts, so the VALU kernel's chunk loop runs."""
+    rng = np.random.default_rng(65539 + M)
+    N, K = 19, 65539
+    w = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    y = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs.reshape(-1), N=N, K=K, M=M).reshape(M, N)
+    for m in range(M):
+        assert_matvec(y[m], w, s, xs[m], N, K)
+
+
+def test_long_rows_matmul_with_and_without_workspace():
+    """matmulQ8 over K = 65539 (1025 steps of 64 codes, 65 accumulator folds):
+    the plain plan and the workspace's K split, each within the bar."""
+    from test_gpu_prefill import assert_matmul
+    rng = np.random.default_rng(40 * 65539)
+    N, M, K = 40, 300, 65539
+    w = random_weights(rng, M, K, full_range=True)
+    s = rng.uniform(1e-4, 1e-2, M).astype(np.float32)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    ba, bw, bs = (wxo_q8.DeviceBuffer.from_array(v) for v in (a, w, s))
+    ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
+    for workspace, nbytes in ((None, 0), (ws, ws_bytes)):
+        out = wxo_q8.DeviceBuffer(4 * N * M)
+        wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, out, M)], N, K, workspace=workspace, workspace_bytes=nbytes)
+        wxo_q8.synchronize()
+        assert ("wgsplit" in wxo_q8.last_variant()) == (workspace is not None), wxo_q8.last_variant()
+        assert_matmul(out.download(np.float32, N * M), a, w, s, N, M, K)
+
+
+def test_long_rows_quantize_and_pack():
+    """Rows of D = 131075 through the two-pass quantize+pack: codes, scales
+    and packed words bit-exact, the absmax in the row's last element."""
+    rng = np.random.default_rng(7)
+    N, D = 3, 131075
+    x = (rng.standard_normal((N, D)) * 0.05).astype(np.float32)
+    x[0, D - 1] = 2.5
+    want_codes, want_scales = oracle.quantize(x, N, D)
+    codes, scales = wxo_q8.quantize(input=x.reshape(-1), N=N, D=D)
+    assert_bits_equal(codes, want_codes, "codes")
+    assert_bits_equal(scales, want_scales, "scales")
+    packed, scales2 = wxo_q8.quantizePackQ8(input=x.reshape(-1), N=N, K=D)
+    assert_bits_equal(packed, oracle.pack_q8(want_codes, N, D), "packed words")
+    assert_bits_equal(scales2, want_scales, "scales (fused)")
