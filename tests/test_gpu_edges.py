@@ -442,3 +442,22 @@ def test_long_rows_quantize_and_pack():
     packed, scales2 = wxo_q8.quantizePackQ8(input=x.reshape(-1), N=N, K=D)
     assert_bits_equal(packed, oracle.pack_q8(want_codes, N, D), "packed words")
     assert_bits_equal(scales2, want_scales, "scales (fused)")
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_two_million_short_rows(M):
+    """N = 2,000,003 rows of K = 7 (two words, one partial): grids of more than
+    100,000 workgroups, the row tail in the last block."""
+    rng = np.random.default_rng(2_000_003 + M)
+    N, K = 2_000_003, 7
+    w = random_weights(rng, N, K, full_range=True)
+    s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    y = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs.reshape(-1), N=N, K=K, M=M).reshape(M, N)
+    for m in range(M):
+        assert_matvec(y[m], w, s, xs[m], N, K)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    want_codes, want_scales = oracle.quantize(x, N, K)
+    packed, scales = wxo_q8.quantizePackQ8(input=x.reshape(-1), N=N, K=K)
+    assert_bits_equal(packed, oracle.pack_q8(want_codes, N, K), "packed words")
+    assert_bits_equal(scales, want_scales, "scales")
