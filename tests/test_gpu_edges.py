@@ -10,6 +10,7 @@
   * which kernel instance ran (wxo_last_variant), per thread.
   * rows far longer than the other suites' (K = 65539 and 131075) on every
     kernel family.
+  * eight host threads on their own streams at once.
 
 Bars as everywhere: codes, packed words and scales bit-exact;
 matvecQ8 |y - y_ref| <= 1e-5 * sum_k |s q x| + 1e-7 per row.
@@ -461,3 +462,97 @@ def test_two_million_short_rows(M):
     packed, scales = wxo_q8.quantizePackQ8(input=x.reshape(-1), N=N, K=K)
     assert_bits_equal(packed, oracle.pack_q8(want_codes, N, K), "packed words")
     assert_bits_equal(scales, want_scales, "scales")
+
+
+# ---------------------------------------------------------------- threads
+
+def test_threads_on_their_own_streams():
+    """Eight host threads, each on its own stream and buffers, issue the
+    library's kernels at the same time (ctypes drops the GIL for every call):
+    every result within its bar, every repeat bit-equal to the first, and each
+    thread's wxo_last_variant its own kernel's."""
+    jobs = []
+    for t in range(8):
+        rng = np.random.default_rng(900 + t)
+        kind = t % 4
+        if kind == 0:    # single vector, ragged rows
+            N, K, M = 4096, 4099, 1
+        elif kind == 1:  # 8 vectors on the k-split kernel
+            N, K, M = 20000, 1024, 8
+        elif kind == 2:  # prefill GEMM with its own workspace
+            N, K, M = 128, 2048, 1000
+        else:            # quantize + pack
+            N, K, M = 512, 5000, 0
+        job = {"kind": kind, "N": N, "K": K, "M": M, "outs": [], "error": None}
+        if kind == 3:
+            job["x"] = (rng.standard_normal(N * K) * 0.05).astype(np.float32)
+        else:
+            rows = M if kind == 2 else N
+            job["w"] = random_weights(rng, rows, K, full_range=True)
+            job["s"] = rng.uniform(1e-3, 5e-2, rows).astype(np.float32)
+            job["x"] = rng.standard_normal((N if kind == 2 else M) * K).astype(np.float32)
+        jobs.append(job)
+
+    def run(job):
+        try:
+            st = wxo_q8.Stream()
+            kind, N, K, M = job["kind"], job["N"], job["K"], job["M"]
+            bx = wxo_q8.DeviceBuffer.from_array(job["x"])
+            if kind == 3:
+                W = (K + 3) // 4
+                bp, bsc = wxo_q8.DeviceBuffer(4 * N * W), wxo_q8.DeviceBuffer(4 * N)
+            else:
+                bw, bs = wxo_q8.DeviceBuffer.from_array(job["w"]), wxo_q8.DeviceBuffer.from_array(job["s"])
+                by = wxo_q8.DeviceBuffer(4 * N * M)
+            if kind == 2:
+                ws_bytes = wxo_q8.matmul_q8_workspace_bytes()
+                ws = wxo_q8.DeviceBuffer(ws_bytes)
+            for _ in range(10):
+                if kind in (0, 1):
+                    wxo_q8.matvec_q8_device(bw, bs, bx, by, N, K, M, stream=st)
+                elif kind == 2:
+                    wxo_q8.matmul_q8_multi_device(bx, [(bw, bs, by, M)], N, K, stream=st, workspace=ws,
+                                                  workspace_bytes=ws_bytes)
+                else:
+                    wxo_q8.quantize_pack_q8_device(bx, N, K, bp, bsc, stream=st)
+                st.synchronize()
+                if kind == 3:
+                    job["outs"].append((bp.download(np.uint32, N * W), bsc.download(np.float32, N)))
+                else:
+                    job["outs"].append(by.download(np.float32, N * M))
+            job["variant"] = wxo_q8.last_variant()
+            st.destroy()
+        except Exception as e:  # reported by the main thread
+            job["error"] = e
+
+    threads = [threading.Thread(target=run, args=(job,)) for job in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    heads = {0: "matvec_q8_m1 ", 1: "matvec_q8_ksplit ", 2: "matmul_q8 ", 3: "quantize_row_wg "}
+    for job in jobs:
+        assert job["error"] is None, job["error"]
+        kind, N, K, M = job["kind"], job["N"], job["K"], job["M"]
+        assert job["variant"].startswith(heads[kind]), job["variant"]
+        first = job["outs"][0]
+        for again in job["outs"][1:]:
+            if kind == 3:
+                assert_bits_equal(again[0], first[0], "packed words on a repeat")
+                assert_bits_equal(again[1], first[1], "scales on a repeat")
+            else:
+                assert_bits_equal(again, first, "output on a repeat")
+        if kind == 0:
+            assert_matvec(first, job["w"], job["s"], job["x"], N, K)
+        elif kind == 1:
+            y = first.reshape(M, N)
+            xs = job["x"].reshape(M, K)
+            for m in range(M):
+                assert_matvec(y[m], job["w"], job["s"], xs[m], N, K)
+        elif kind == 2:
+            from test_gpu_prefill import assert_matmul
+            assert_matmul(first, job["x"], job["w"], job["s"], N, M, K)
+        else:
+            codes, scales = oracle.quantize(job["x"], N, K)
+            assert_bits_equal(first[0], oracle.pack_q8(codes, N, K), "packed words")
+            assert_bits_equal(first[1], scales, "scales")
