@@ -70,3 +70,53 @@ def test_no_alloc_matches_the_workspace_entry():
             bad = np.flatnonzero(got[:N * M].view(np.uint32) != ref[:N * M].view(np.uint32))
             assert bad.size == 0, f"N={N} M={M}: {bad.size} outputs differ from the workspace entry's, first {bad[0]}"
             check_matmul(got[:N * M], a, w, s, N, M, K, np.unique(np.r_[np.arange(0, N, 7), N - 1]))
+
+
+def test_no_alloc_entry_in_a_captured_graph():
+    """The callers the entry point is for include code under HIP graph
+    capture.  A 64-token projection through it (every tile's K steps in four
+    parts through the array) is captured once and replayed on new
+    activations, with an eager call of another shape through the same array
+    between replays: every replay gives the bits of the workspace entry issued
+    eagerly on the same inputs."""
+    rng = np.random.default_rng(77)
+    ws_bytes = min(wxo_q8.matmul_q8_workspace_bytes(), SCRATCH_BYTES)
+    ws = wxo_q8.DeviceBuffer(ws_bytes)
+
+    def projection(N, M, K):
+        w = oracle.pack_q8(rng.integers(-128, 128, (M, K)).astype(np.int32).reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        return w, s, wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s)
+
+    N, M, K = 64, 2048, 2048
+    w, s, bw, bs = projection(N, M, K)
+    ba, out, ref = wxo_q8.DeviceBuffer(4 * N * K), wxo_q8.DeviceBuffer(4 * N * M), wxo_q8.DeviceBuffer(4 * N * M)
+    N2, M2, K2 = 40, 512, 1030  # the eager call between replays: two parts per tile
+    _, _, bw2, bs2 = projection(N2, M2, K2)
+    ba2 = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(N2 * K2).astype(np.float32))
+    out2 = wxo_q8.DeviceBuffer(4 * N2 * M2)
+    st = wxo_q8.Stream()
+    g = wxo_q8.Graph.capture(st, lambda: wxo_q8.matmul_q8_multi_static_device(ba, [(bw, bs, out, M)], N, K, stream=st))
+    try:
+        for step in range(4):
+            a = rng.standard_normal(N * K).astype(np.float32)
+            ba.upload(a)
+            wxo_q8.synchronize()
+            g.launch(st)
+            st.synchronize()
+            got = out.download(np.float32, N * M)
+            wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, ref, M)], N, K, stream=st, workspace=ws,
+                                          workspace_bytes=ws_bytes)
+            st.synchronize()
+            assert "wgsplit4" in wxo_q8.last_variant(), wxo_q8.last_variant()
+            want = ref.download(np.float32, N * M)
+            bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+            assert bad.size == 0, f"replay {step}: {bad.size} outputs differ from the eager workspace entry's"
+            if step == 0:
+                check_matmul(got, a, w, s, N, M, K, np.arange(0, N, 9))
+            wxo_q8.matmul_q8_multi_static_device(ba2, [(bw2, bs2, out2, M2)], N2, K2, stream=st)
+            st.synchronize()
+            assert "wgsplit2" in wxo_q8.last_variant(), wxo_q8.last_variant()
+    finally:
+        g.destroy()
+        st.destroy()
