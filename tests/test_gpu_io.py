@@ -7,6 +7,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import oracle
 import wxo_q8
 
 pytestmark = pytest.mark.gpu
@@ -93,3 +94,20 @@ def test_memset_any_offset_and_length(offset, length):
     bad = np.flatnonzero(got != want)
     assert bad.size == 0, f"offset={offset} length={length}: {bad.size} bytes differ, first at {bad[0]}"
     buf.free()
+
+
+def test_failed_allocation_leaves_later_calls_working():
+    """An allocation the device cannot hold fails with WXO_ERR_OOM and
+    allocates nothing; the next allocation and launch on the same thread
+    succeed (the failure is not reported a second time)."""
+    with pytest.raises(wxo_q8.WxoError) as e:
+        wxo_q8.DeviceBuffer(1 << 50)
+    assert e.value.status == wxo_q8.WXO_ERR_OOM, e.value
+    rng = np.random.default_rng(5)
+    N, K = 300, 1030
+    w = rng.integers(0, 2 ** 32, N * ((K + 3) // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(1e-3, 1e-2, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K)
+    ok, msg = oracle.check_matvec(y, oracle.matvec_q8(w, s, x, N, K), oracle.absterm(w, s, x, N, K))
+    assert ok, msg

@@ -39,6 +39,9 @@ int ok() {
 }
 
 int hip_fail(hipError_t e, const char* what) {
+    // The error is reported here; consume the runtime's per-thread copy so
+    // that a later launch's hipGetLastError does not report it again.
+    (void)hipGetLastError();
     if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
         return fail(WXO_ERR_OOM, "%s: %s", what, hipGetErrorString(e));
     if (e == hipErrorNoDevice || e == hipErrorInsufficientDriver)
