@@ -596,3 +596,31 @@ def test_gather_bit_exact(rows, D):
     idx = np.concatenate([rng.integers(0, rows, 50), [-1, rows, 2 ** 40, -(2 ** 40), 0, rows - 1, 0]]).astype(np.int64)
     got = wxo_q8.gatherDequantRows((codes, s), idx, D)
     assert_bits_equal(got, oracle.gather_dequant_rows(codes, s, rows, D, idx), f"gather rows={rows} D={D}")
+
+
+@pytest.mark.parametrize("N,Ms,K", [(2048, [4096], 4100), (1024, [4224, 3968], 4096)])
+def test_matmul_tile_pairs(N, Ms, K):
+    """Long rows whose 128-row tiles make two whole rounds of two per CU: one
+    workgroup of 16 waves per two tiles, one per K group (in the second case
+    a pair of tiles straddles the two projections).  Every 37th token
+    against the oracle, nothing past the outputs."""
+    rng = np.random.default_rng(N + sum(Ms) + K)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[3 * K + 5] = np.inf
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    host, bufs = [], []
+    for M in Ms:
+        w = oracle.pack_q8(rng.integers(-128, 128, (M, K)).astype(np.int32).reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        out.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), out, M))
+    wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
+    wxo_q8.synchronize()
+    assert " FB4.pairs " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    rows = np.unique(np.r_[np.arange(0, N, 37), 3, N - 1])
+    for (w, s, M), (_, _, out, _) in zip(host, bufs):
+        got = out.download(np.float32, N * M + 64)
+        assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)

@@ -54,6 +54,10 @@
 // tile-sized workspace blocks, and a second launch adds them in part order
 // and scales them.  The stream order between the two launches is the only
 // synchronisation, so every run gives the same bits.
+//
+// Long rows whose tiles make whole rounds of two per CU run one workgroup of
+// 16 waves per two tiles, each group of 8 waves on a tile of its own (the
+// PAIR instances); the sums are the one-group form's.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -140,8 +144,11 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
 // whose K steps are shared by `parts` workgroups (a short prompt's few tiles,
 // which would leave most CUs idle, or the tiles past the last whole round of
 // a long prompt, which would leave some CUs with one tile more than others).
-// The other instances run every tile whole, with no branch on it.
-template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false>
+// PAIR instances (two K groups) run the first P.whole tiles two per
+// workgroup, one whole tile per group, and the rest one per workgroup with
+// the K steps split between the groups.  The other instances run every tile
+// whole, with no branch on it.
+template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a, MatmulProjections P,
                                                         uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
                                                         uint32_t ntiles) {
@@ -172,9 +179,25 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     // split tiles' parts, so every XCD holds its share of both and the whole
     // tiles are dispatched first.  Workgroups past the end return whole (no
     // barrier is skipped by part of one).
+    static_assert(!PAIR || (KS == 2 && !SPLIT), "pairs are the two K groups of a whole-tile launch");
     const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
     uint32_t tile, xs = 0u, np = (uint32_t)KS;  // np: runs of this tile's K steps
-    if constexpr (!SPLIT) {
+    bool pair = false;                          // this group runs a tile of its own
+    if constexpr (PAIR) {
+        const uint32_t pairs = P.whole / 2u, singles = mtiles * ntiles - P.whole;
+        const uint32_t wpx = (pairs + 7u) / 8u;
+        if (slot < wpx) {
+            const uint32_t i = xcd * wpx + slot;
+            if (i >= pairs) return;
+            tile = 2u * i + __builtin_amdgcn_readfirstlane(threadIdx.x / (64u * NW));
+            np = 1u;
+            pair = true;
+        } else {
+            const uint32_t q = xcd * ((singles + 7u) / 8u) + (slot - wpx);
+            if (q >= singles) return;
+            tile = P.whole + q;
+        }
+    } else if constexpr (!SPLIT) {
         const uint32_t total = mtiles * ntiles;
         const uint32_t lin = xcd * ((total + 7u) / 8u) + slot;
         if (lin >= total) return;
@@ -390,7 +413,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     // past its own steps.
     constexpr bool kOneRun = KS == 1 && !SPLIT;  // every group takes all the steps: no skip
     const uint32_t iters = kOneRun ? steps : (steps + np - 1u) / np;
-    const uint32_t s0 = kOneRun ? 0u : (xs * (uint32_t)KS + kg) * iters;
+    const uint32_t s0 = kOneRun || pair ? 0u : (xs * (uint32_t)KS + kg) * iters;
     const uint32_t gs = kOneRun ? steps : (s0 < steps ? min(iters, steps - s0) : 0u);
     auto convert_checked = [&](int s, int st) {
         const float rsum = convert_store(s, st);
@@ -436,27 +459,31 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     }
 
     if constexpr (KS > 1) {
-        // Group 1's sums through LDS (its stages are done) into group 0's.
+        // Group 1's sums through LDS (its stages are done) into group 0's;
+        // a pair's groups each store their own tile (`pair` is
+        // workgroup-uniform, and always false outside PAIR instances).
         constexpr uint32_t E = (uint32_t)(FB * TB * 4);
-        float* red = reinterpret_cast<float*>(lds);
-        __syncthreads();
-        if (kg == 1u) {
+        static_assert(E * NT * 4u <= 2u * AST + 2u * BST, "the reduction fits in group 0's stages");
+        if (!pair) {
+            float* red = reinterpret_cast<float*>(lds);
+            __syncthreads();
+            if (kg == 1u) {
+#pragma unroll
+                for (int f = 0; f < FB; ++f)
+#pragma unroll
+                    for (int b = 0; b < TB; ++b)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) red[((uint32_t)((f * TB + b) * 4 + v)) * NT + t] = sum[f][b][v];
+            }
+            __syncthreads();
+            if (kg != 0u) return;  // after the last barrier
 #pragma unroll
             for (int f = 0; f < FB; ++f)
 #pragma unroll
                 for (int b = 0; b < TB; ++b)
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) red[((uint32_t)((f * TB + b) * 4 + v)) * NT + t] = sum[f][b][v];
+                    for (int v = 0; v < 4; ++v) sum[f][b][v] += red[((uint32_t)((f * TB + b) * 4 + v)) * NT + t];
         }
-        __syncthreads();
-        if (kg != 0u) return;  // after the last barrier
-#pragma unroll
-        for (int f = 0; f < FB; ++f)
-#pragma unroll
-            for (int b = 0; b < TB; ++b)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) sum[f][b][v] += red[((uint32_t)((f * TB + b) * 4 + v)) * NT + t];
-        static_assert(E * NT * 4u <= 2u * AST + 2u * BST, "the reduction fits in group 0's stages");
     }
 
     // Epilogue: lane (j, g) of block (f, b) holds features m0 + wm + 16 f +
@@ -543,7 +570,7 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
 // their K steps split into `parts` runs, with the workspace `part` holding
 // (parts - 1) x splits blocks of BM x kBN floats, and a second launch sums
 // them.
-template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false>
+template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false, bool PAIR = false>
 hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
                      hipStream_t stream, float* part = nullptr, uint32_t splits = 0, uint32_t parts = 1) {
     constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
@@ -571,8 +598,13 @@ hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, 
     P.parts = parts;
     uint32_t grid = ((tiles + 7u) / 8u) * 8u;
     if constexpr (SPLIT) grid = 8u * ((P.whole + 7u) / 8u + (splits * parts + 7u) / 8u);
+    if constexpr (PAIR) {  // `splits` here: the tiles run in pairs (even)
+        P.whole = splits;
+        P.splits = 0;
+        grid = 8u * ((splits / 2u + 7u) / 8u + (tiles - splits + 7u) / 8u);
+    }
     const size_t lds = (size_t)KS * (2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes);
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT, PAIR>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
                        P, N, K, W, mtiles, ntiles);
     if constexpr (SPLIT) {
         const hipError_t err = hipGetLastError();
@@ -669,6 +701,19 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
         if (workspace && S > 0 && steps >= 8u && S * blk <= workspace_bytes) {
             set_variant(variant, kname, "FB4.balance2", 8, 128, 0, (int)kBN, (uint32_t)(t4 + S));
             return launch_fb<4, 8, 64, 2, 1, true>(a, p, n, N, K, stream, workspace, (uint32_t)S, 2u);
+        }
+        // Long rows whose tiles make two or more whole rounds of two per CU:
+        // one workgroup of 16 waves per two tiles, one per K group, both of
+        // one token tile.  Same process, one-group -> pairs (us): 1024 tiles
+        // at K = 4096 240-245 -> 226-232, at K = 11008 645-647 -> 607-612 and
+        // 334-338 -> 300-302, at K = 5632 299-317 -> 290-323; one round (512
+        // tiles) even, and 5.5 rounds (2816 tiles, K = 4096) 658 -> 686-690,
+        // where two workgroups per CU even out the last half round better;
+        // at K = 2048 no gain.  The same sums in the same order as the
+        // one-group form.
+        if (K >= 4096u && t4 >= 4ull * cus && t4 % (2ull * cus) == 0) {
+            set_variant(variant, kname, "FB4.pairs", 16, 128, 0, (int)kBN, (uint32_t)((t4 / 2u + 7u) / 8u * 8u));
+            return launch_fb<4, 8, 64, 2, 2, false, true>(a, p, n, N, K, stream, nullptr, (uint32_t)t4, 1u);
         }
         set_variant(variant, kname, "FB4", 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
         return launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
