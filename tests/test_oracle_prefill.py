@@ -275,3 +275,34 @@ def test_c_oracle_matches_ecmascript_oracle_prefill_ops():
                  "arrays": {"codes": enc(i8, "i8"), "scale": enc(s, "f32"), "indices": enc(idx, "f64")}})
     assert np.array_equal(dec(js["output"], np.float32).view(np.uint32),
                           oracle.gather_dequant_rows(i8, s, M, K, idx.astype(np.int64)).view(np.uint32))
+
+
+def test_threaded_rows_give_the_same_bits():
+    """The C oracle splits matvec and matmul output rows over threads; each
+    output is one f64 sum in the reference's order, so the bits do not depend
+    on the thread count (OMP_NUM_THREADS is read at each call)."""
+    rng = np.random.default_rng(3)
+    N, M, K = 64, 515, 1031
+    W = (K + 3) // 4
+    w = rng.integers(0, 2 ** 32, M * W, dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(1e-3, 5e-2, M).astype(np.float32)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[17] = np.inf
+    N2 = 20000  # matvec rows: enough work for the threads
+    w2 = rng.integers(0, 2 ** 32, N2 * W, dtype=np.uint64).astype(np.uint32)
+    s2 = rng.uniform(1e-3, 5e-2, N2).astype(np.float32)
+    old = os.environ.get("OMP_NUM_THREADS")
+    runs = []
+    try:
+        for threads in ("1", "3", "7"):
+            os.environ["OMP_NUM_THREADS"] = threads
+            runs.append((oracle.matmul_q8(a, w, s, N, M, K), oracle.matmul_absterm(a, w, s, N, M, K),
+                         oracle.matvec_q8(w2, s2, a[:K], N2, K), oracle.absterm(w2, s2, a[:K], N2, K)))
+    finally:
+        if old is None:
+            os.environ.pop("OMP_NUM_THREADS", None)
+        else:
+            os.environ["OMP_NUM_THREADS"] = old
+    for other in runs[1:]:
+        for x, y in zip(runs[0], other):
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
