@@ -31,6 +31,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import itertools
 import json
 import os
 import re
@@ -77,6 +78,30 @@ def read_traffic():
     return vals.get("hbm_bytes_per_launch")
 
 
+def calibrated_ceiling():
+    """This device's own ceilings, measured now by wxo_roofline (the
+    reference's harness/roofline.ts method: 512 MiB hashed buffers swept once
+    per launch, fastest of several attempts; FMA chains from registers)."""
+    r = wxo_q8.roofline()
+    cal = {"GB/s": round(r["bandwidth"] / 1e9, 1), "fma_TFLOP/s": round(r["compute"] / 1e12, 2),
+           "source": "wxo_roofline: two 512 MiB hash-filled buffers swept alternately with dwordx4 loads, fastest of "
+                     "3 regions of 8 back-to-back sweeps (launch cost included); one-wide f32 FMA chains"}
+    log(f"calibrated ceiling: {cal['GB/s']} GB/s HBM read ({100 * cal['GB/s'] / PEAK_HBM_GBS:.1f}% of 8 TB/s), "
+        f"{cal['fma_TFLOP/s']} TFLOP/s one-wide f32 FMA")
+    return cal
+
+
+def add_calibrated(table, cal):
+    """Every GPU row measured against HBM also as a % of the calibrated read
+    ceiling; the ceiling itself heads the table."""
+    for row in table:
+        if "pct_hbm" in row and "GB/s" in row:
+            row["pct_of_calibrated"] = round(100.0 * row["GB/s"] / cal["GB/s"], 1)
+    table.insert(0, {"case": "calibrated ceiling (wxo_roofline): HBM read stream and f32 FMA", "GB/s": cal["GB/s"],
+                     "pct_hbm": round(100.0 * cal["GB/s"] / PEAK_HBM_GBS, 1), "fma_TFLOP/s": cal["fma_TFLOP/s"],
+                     "source": cal["source"]})
+
+
 def cpu_baseline(packed, scales, x, N, K, budget_s):
     node = shutil.which("node")
     if node is None:
@@ -110,17 +135,30 @@ def cpu_baseline(packed, scales, x, N, K, budget_s):
 LEAD_STEPS = 10
 
 
-def time_loop(stream, launch, steps, warmup):
-    """Mean us per step over `steps` back-to-back steps (timing-only events on the stream)."""
-    for i in range(warmup):
-        launch(i)
+# Every launch of one measured case takes the next index of ONE sequence, from
+# the first set-up call through the last timed call.  A launch that picks its
+# weight copy as index % copies therefore reads each copy exactly `copies`
+# launches after its previous read, i.e. after every other copy has streamed
+# through the caches in between.  Restarting the index at the timed region
+# would re-read the copies the lead calls had just streamed (a few tens of MB
+# back, well inside the 256 MB Infinity Cache).
+
+
+def time_loop(stream, launch, steps, warmup, seq=None, setup=0):
+    """Mean us per step over `steps` back-to-back steps (timing-only events on
+    the stream).  `seq` continues the case's launch index sequence; `setup`
+    untimed launches (one per rotated copy) run before the warm-up, so no copy
+    is first read inside the timed region."""
+    seq = itertools.count() if seq is None else seq
+    for _ in range(setup + warmup):
+        launch(next(seq))
     stream.synchronize()
     e0, e1 = wxo_q8.Event(timer=True), wxo_q8.Event(timer=True)
-    for i in range(LEAD_STEPS):
-        launch(warmup + i)
+    for _ in range(LEAD_STEPS):
+        launch(next(seq))
     e0.record(stream)
-    for i in range(steps):
-        launch(i)
+    for _ in range(steps):
+        launch(next(seq))
     e1.record(stream)
     e1.synchronize()
     return e0.elapsed_ms(e1) * 1e3 / steps
@@ -139,14 +177,16 @@ def _spin(stream, us):
     _check(wxo_q8.lib().wxo_spin(int(us), stream.handle))
 
 
-def time_loop_queued(stream, launch, steps):
+def time_loop_queued(stream, launch, steps, seq=None):
     """GPU-side mean us per step: `steps` launches queued behind a spin kernel
     long enough for the host to issue them all, between timing-only events.
-    Returns None if the host did not finish issuing inside the spin."""
+    Returns None if the host did not finish issuing inside the spin.  `seq`
+    continues the case's launch index sequence."""
+    seq = itertools.count() if seq is None else seq
     stream.synchronize()
     t0 = time.perf_counter()
-    for i in range(5):  # the host's issue time per step, to size the spin
-        launch(i)
+    for _ in range(5):  # the host's issue time per step, to size the spin
+        launch(next(seq))
     per_step_us = (time.perf_counter() - t0) * 1e6 / 5
     stream.synchronize()
     e0, e1 = wxo_q8.Event(timer=True), wxo_q8.Event(timer=True)
@@ -154,8 +194,8 @@ def time_loop_queued(stream, launch, steps):
     _spin(stream, spin_us)
     t0 = time.perf_counter()
     e0.record(stream)
-    for i in range(steps):
-        launch(i)
+    for _ in range(steps):
+        launch(next(seq))
     e1.record(stream)
     host_us = (time.perf_counter() - t0) * 1e6
     e1.synchronize()
@@ -165,10 +205,12 @@ def time_loop_queued(stream, launch, steps):
     return e0.elapsed_ms(e1) * 1e3 / steps
 
 
-def time_both(stream, launch, steps, warmup):
-    """(host-issued us per step, GPU-side queued us per step or None)."""
-    us = time_loop(stream, launch, steps, warmup)
-    return us, time_loop_queued(stream, launch, steps)
+def time_both(stream, launch, steps, warmup, setup=0):
+    """(host-issued us per step, GPU-side queued us per step or None), one
+    launch index sequence across both (`setup`: see time_loop)."""
+    seq = itertools.count()
+    us = time_loop(stream, launch, steps, warmup, seq, setup)
+    return us, time_loop_queued(stream, launch, steps, seq)
 
 
 def _q(usq):
@@ -202,6 +244,40 @@ def prepare_weights(stream, w_f32, N, K, copies):
     return packed, scale
 
 
+def timed_headline(stream, call, copies, warmup, steps, event=None, sync=None):
+    """The headline's timed region: `steps` back-to-back calls between two
+    timing-only events (recording them fences nothing, so no cache write-back
+    or invalidation lands inside the interval), synchronised on both sides.
+    Returns the interval in ms.
+
+    Before it, on one continuing index sequence (call(i) reads copy i % copies):
+    one set-up call per copy, so every copy's pages have been read once before
+    any is timed; `warmup` untimed calls; then LEAD_STEPS untimed calls
+    enqueued just ahead of the first event, so the timed launches queue behind
+    running work and the host's latency to the first launch stays outside the
+    interval.  Every timed call reads the copy read longest ago."""
+    event = event or wxo_q8.Event
+    sync = sync or wxo_q8.synchronize
+    seq = itertools.count()
+    for _ in range(copies):
+        call(next(seq))
+    stream.synchronize()
+    for _ in range(warmup):
+        call(next(seq))
+    stream.synchronize()
+    e0, e1 = event(timer=True), event(timer=True)
+    sync()
+    for _ in range(LEAD_STEPS):
+        call(next(seq))
+    e0.record(stream)
+    for _ in range(steps):
+        call(next(seq))
+    e1.record(stream)
+    e1.synchronize()
+    sync()
+    return e0.elapsed_ms(e1)
+
+
 def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup, queued=False):
     """One matvecQ8 configuration on rotated weights: us per call, algorithmic
     GB/s, the bound (HBM, or the compute rate of the path that runs: one-wide
@@ -216,12 +292,14 @@ def measure_matvec(stream, name, N, K, M, w_f32, x, steps, warmup, queued=False)
     vec = wxo_q8.DeviceBuffer.from_array(x, stream)
     out = wxo_q8.DeviceBuffer(N * M * 4)
     ptrs = [packed.ptr + i * N * W * 4 for i in range(copies)]
-    for i in range(copies):  # every copy read once before timing
-        _check(L.wxo_matvec_q8(ptrs[i], scale.ptr, vec.ptr, out.ptr, N, K, M, sp))
+
     def call(i):
         _check(L.wxo_matvec_q8(ptrs[i % copies], scale.ptr, vec.ptr, out.ptr, N, K, M, sp))
-    us = time_loop(stream, call, steps, warmup)
-    usq = time_loop_queued(stream, call, steps) if queued else None
+    seq = itertools.count()
+    for _ in range(copies):  # every copy read once before timing
+        call(next(seq))
+    us = time_loop(stream, call, steps, warmup, seq)
+    usq = time_loop_queued(stream, call, steps, seq) if queued else None
     variant = wxo_q8.last_variant()
     gbs = nbytes / (us * 1e-6) / 1e9
     flops = 2.0 * N * K * M
@@ -297,7 +375,7 @@ def run_suite(stream, steps, warmup):
             W = (K + 3) // 4
             check(L.wxo_matvec_q8(packed.ptr + li * N * W * 4, scale.ptr, (vf if K == 5632 else vh).ptr, outb.ptr,
                                   N, K, 1, sp))
-    us, usq = time_both(stream, layer_step, max(1, steps // 7), max(1, warmup // 7))
+    us, usq = time_both(stream, layer_step, max(1, steps // 7), max(1, warmup // 7), layers)
     gbs = layer_bytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 decoder layer: 7 matvecQ8 calls", "bytes": layer_bytes, "us": round(us, 3),
                     "GB/s": round(gbs, 1), "pct_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "layers_rotated": layers,
@@ -329,7 +407,7 @@ def run_suite(stream, steps, warmup):
         check(L.wxo_matvec_q8_ffn(wg, sg, wu, su, vh.ptr, hidden.ptr, 5632, 2048, sp))
         w, sc = wp("wDown")
         check(L.wxo_matvec_q8_residual(w, sc, vf.ptr, resid.ptr, resid.ptr, 2048, 5632, sp))
-    us, usq = time_both(stream, fused_step, max(1, steps // 7), max(1, warmup // 7))
+    us, usq = time_both(stream, fused_step, max(1, steps // 7), max(1, warmup // 7), layers)
     gbs = layer_bytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 decoder layer as the resident engine runs it: 3 matvecQ8 + 2 matvecQ8Residual "
                             "+ 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3), "GB/s": round(gbs, 1),
@@ -359,7 +437,8 @@ def run_suite(stream, steps, warmup):
         check(L.wxo_matvec_q8_ffn(wg, sg, wu, su, vh.ptr, hidden.ptr, 5632, 2048, sp))
         w, sc = wp("wDown")
         check(L.wxo_matvec_q8_residual(w, sc, vf.ptr, resid.ptr, resid.ptr, 2048, 5632, sp))
-    us, usq = time_both(stream, coalesced_step, max(1, steps // 7), max(1, warmup // 7))
+    us, usq = time_both(stream, coalesced_step, max(1, steps // 7), max(1, warmup // 7),
+                       layers)
     gbs = layer_bytes / (us * 1e-6) / 1e9
     results.append({"case": "cfg4 decoder layer as the resident batch issues it: wq/wk/wv in one matvecQ8 multi "
                             "launch + 2 matvecQ8Residual + 1 matvecQ8Ffn", "bytes": layer_bytes, "us": round(us, 3),
@@ -445,7 +524,7 @@ def run_suite(stream, steps, warmup):
     dst3 = wxo_q8.DeviceBuffer(N3 * W3 * 4 * copies3)
     us, usq = time_both(stream, lambda i: check(L.wxo_pack_int8_rows(src3.ptr + (i % copies3) * N3 * K3, N3, K3,
                                                                      dst3.ptr + (i % copies3) * N3 * W3 * 4, sp)),
-                        max(1, steps // 4), max(1, warmup // 4))
+                        max(1, steps // 4), max(1, warmup // 4), copies3)
     pbytes = N3 * K3 + N3 * W3 * 4
     gbs = pbytes / (us * 1e-6) / 1e9
     results.append({"case": "packInt8Rows on the GPU, device-resident codes, N=4096 K=4099 (ragged)", "bytes": pbytes,
@@ -707,6 +786,7 @@ def main() -> int:
             if st != 0:
                 raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
         run_prefill_suite(stream, args.steps, args.warmup, table, check)
+        add_calibrated(table, calibrated_ceiling())
         if not args.no_cpu_baseline:
             table.extend(cpu_reference_ops(budget_s=1.0))
         with open(args.prefill_suite, "w") as f:
@@ -742,33 +822,8 @@ def main() -> int:
         if st != 0:
             raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
 
-    # Set-up, outside the warmup and the timed region: one call per rotated
-    # copy, so every copy's pages have been read once before any is timed.
-    for i in range(copies):
-        call(i)
-    stream.synchronize()
-    for i in range(args.warmup):
-        call(i)
-    stream.synchronize()
-
-    # Timed region: K back-to-back calls between two timing-only events
-    # (recording them fences nothing, so no cache write-back or invalidation
-    # lands inside the interval), synchronised on both sides.  LEAD_STEPS
-    # untimed calls are enqueued before the first event, so the timed launches
-    # queue behind running work and the host's latency to the first launch
-    # stays outside the interval.
-    e0, e1 = wxo_q8.Event(timer=True), wxo_q8.Event(timer=True)
-    wxo_q8.synchronize()
-    for i in range(LEAD_STEPS):
-        call(args.warmup + i)
-    e0.record(stream)
-    for i in range(args.steps):
-        call(i)
-    e1.record(stream)
-    e1.synchronize()
-    wxo_q8.synchronize()
+    total_ms = timed_headline(stream, call, copies, args.warmup, args.steps)
     variant = wxo_q8.last_variant()
-    total_ms = e0.elapsed_ms(e1)
     ms_per_step = total_ms / args.steps
     bytes_per_call = wl.matvec_bytes(N, K, M)
     value = bytes_per_call / (ms_per_step * 1e-3) / 1e9
@@ -779,6 +834,8 @@ def main() -> int:
     launch_us = ms_per_step * 1e3
     achieved = bytes_per_call / (launch_us * 1e-6) / 1e9
     log(f"timed region {total_ms:.3f} ms / {args.steps} calls = {launch_us:.3f} us/call ({variant})")
+
+    cal = calibrated_ceiling()
 
     if args.calibrate_copy:
         # Plain device copies of one weight copy into another (rocclr's
@@ -799,6 +856,7 @@ def main() -> int:
 
     if args.suite:
         table = run_suite(stream, args.steps, args.warmup)
+        add_calibrated(table, cal)
         with open(args.suite, "w") as f:
             json.dump(table, f, indent=1)
 
@@ -825,6 +883,8 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": read_traffic(),
             "traffic_source": TRAFFIC_NOTE,
             "launch_us_events": round(launch_us, 3),
+            "calibrated": {"GB/s": cal["GB/s"], "frac": round(achieved / cal["GB/s"], 4),
+                           "fma_TFLOP/s": cal["fma_TFLOP/s"], "source": cal["source"]},
         },
         "cpu_baseline": baseline,
     }

@@ -143,6 +143,18 @@ int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
  * behind it are all queued by the time the GPU reaches them, so events around
  * them time back-to-back execution rather than the host's issue rate. */
 int wxo_spin(uint32_t us, wxo_stream_t stream);
+/* This device's own ceilings, measured now; replaces measureRoofline
+ * (harness/roofline.ts:162-198, the same method).  *bandwidth: the best
+ * sustained read rate from HBM in bytes/s -- two 512 MiB buffers filled with
+ * hashed words, swept once per launch with dwordx4 loads, alternately (each
+ * sweep's data was last read 512 MiB earlier, so none comes from the 256 MB
+ * Infinity Cache), fastest of three timed regions of eight back-to-back sweeps,
+ * each sweep's launch cost included.  *compute: the best sustained one-wide
+ * f32 FMA rate in flop/s (an FMA counts 2).  Either pointer may be NULL to skip
+ * that part, not both.  Synchronous; allocates and frees 1 GiB of device
+ * memory and a stream of its own; takes tens of milliseconds.  A measurement
+ * aid: ops are reported as a fraction of it beside the nominal 8 TB/s. */
+int wxo_roofline(double* bandwidth, double* compute);
 
 /* ---- captured batches ------------------------------------------------------
  * The reference encodes a resident batch's passes into one command encoder

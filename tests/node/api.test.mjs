@@ -11,6 +11,7 @@ import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
 import { runMatVecQ8 } from "../../web-xpu-ops_amd/llm/kernels.js";
 import { createResidentQ8Device } from "../../web-xpu-ops_amd/harness/resident.js";
 import { native, describe } from "../../web-xpu-ops_amd/native/index.js";
+import { roofline, measureRoofline } from "../../web-xpu-ops_amd/harness/roofline.js";
 import * as oracle from "../../oracle/q8_oracle.mjs";
 
 const F = "api.test.mjs";
@@ -24,6 +25,8 @@ test(F, "exports the reference's op names", () => {
   for (const name of ["quantize", "quantizePackQ8"]) assert.strictEqual(typeof quantizeOps[name], "function", name);
   assert.strictEqual(typeof packInt8Rows, "function");
   assert.strictEqual(typeof runMatVecQ8, "function");
+  assert.strictEqual(typeof roofline, "function");
+  assert.strictEqual(typeof measureRoofline, "function");
 });
 
 test(F, "the addon loads and exports its whole surface", () => {
@@ -31,7 +34,7 @@ test(F, "the addon loads and exports its whole surface", () => {
   for (const name of ["abiVersion", "describe", "deviceCount", "init", "synchronize", "matvecQ8", "matvecQ8Ffn",
     "matvecQ8Residual", "quantize", "packQ8", "packInt8Rows", "quantizePackQ8", "malloc", "free", "upload", "download",
     "copy", "matvecQ8Device", "matvecQ8FfnDevice", "matvecQ8ResidualDevice", "quantizeDevice", "packQ8Device",
-    "packInt8RowsDevice", "quantizePackQ8Device"]) {
+    "packInt8RowsDevice", "quantizePackQ8Device", "roofline"]) {
     assert.strictEqual(typeof a[name], "function", name);
   }
   assert.strictEqual(a.abiVersion(), 1);
@@ -335,4 +338,12 @@ gpuTest(F, "ResidentQ8Device: consecutive quantizePackQ8 ops with one K share a 
     assert.strictEqual(dev.stats.launches - launches0, coalesce ? 1 : 3);
     dev.destroy();
   }
+});
+
+gpuTest(F, "roofline(): this device's own ceilings (harness/roofline.ts:162-222), measured once per session", async () => {
+  const r = await roofline();
+  // a read stream cannot beat the 8 TB/s rating; the FMA rate is one-wide f32 (78.6 TFLOP/s at 2.4 GHz)
+  assert.ok(r.bandwidth > 3e12 && r.bandwidth < 8.2e12, `bandwidth ${r.bandwidth}`);
+  assert.ok(r.compute > 2e13 && r.compute < 8.2e13, `compute ${r.compute}`);
+  assert.strictEqual(await roofline(), r, "cached: the same measurement object");
 });

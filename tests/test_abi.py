@@ -71,6 +71,9 @@ def test_validation_happens_before_device_access():
     # the measurement spin refuses more than a second before touching a device
     assert L.wxo_spin(1000001, None) == wxo_q8.WXO_ERR_INVALID
     assert "spin longer than 1 s" in L.wxo_last_error().decode()
+    # the calibrated ceiling needs at least one output
+    assert L.wxo_roofline(None, None) == wxo_q8.WXO_ERR_INVALID
+    assert "roofline" in L.wxo_last_error().decode()
     # graph capture needs a stream of its own
     assert L.wxo_graph_capture_begin(None) == wxo_q8.WXO_ERR_INVALID
     assert "not the null stream" in L.wxo_last_error().decode()

@@ -111,3 +111,18 @@ def test_failed_allocation_leaves_later_calls_working():
     y = wxo_q8.matvecQ8(weight=w, scale=s, vector=x, N=N, K=K)
     ok, msg = oracle.check_matvec(y, oracle.matvec_q8(w, s, x, N, K), oracle.absterm(w, s, x, N, K))
     assert ok, msg
+
+
+def test_roofline_ceilings():
+    """wxo_roofline: the calibrated HBM read ceiling and one-wide f32 FMA rate
+    fall inside what the hardware allows, either part can be asked for alone,
+    and neither part is an error; the matvec at cfg2 does not stream faster
+    than the ceiling (beyond timing noise)."""
+    print("wxo_roofline", flush=True)
+    r = wxo_q8.roofline()
+    assert 3e12 < r["bandwidth"] < 8.2e12, r
+    assert 2e13 < r["compute"] < 8.2e13, r
+    only_bw = wxo_q8.roofline(compute=False)
+    assert only_bw["compute"] is None and 3e12 < only_bw["bandwidth"] < 8.2e12
+    with pytest.raises(wxo_q8.WxoError, match="roofline"):
+        wxo_q8.roofline(bandwidth=False, compute=False)

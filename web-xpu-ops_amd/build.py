@@ -28,7 +28,7 @@ LIB = os.path.join(LIB_DIR, "libwxo_q8.so")
 ADDON = os.path.join(LIB_DIR, "wxo_q8.node")
 INCLUDE = os.path.join(ROOT, "include")
 
-HIP_SOURCES = ["matvec_q8.hip", "quantize_q8.hip", "matmul_q8.hip", "dequant_q8.hip", "wxo_api.hip"]
+HIP_SOURCES = ["matvec_q8.hip", "quantize_q8.hip", "matmul_q8.hip", "dequant_q8.hip", "roofline.hip", "wxo_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

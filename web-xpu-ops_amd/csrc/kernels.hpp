@@ -132,4 +132,9 @@ hipError_t launch_gather_dequant_rows(const int8_t* codes, const float* scale, u
                                       const int64_t* indices, uint32_t count, float* out, const DeviceInfo& dev,
                                       hipStream_t stream);
 
+// roofline.hip: this device's best sustained HBM read bandwidth (bytes/s) and
+// one-wide f32 FMA rate (flop/s), measured now; either output may be null to
+// skip that part.  Allocates (and frees) two 512 MiB buffers on its own stream.
+hipError_t measure_roofline(const DeviceInfo& dev, double* bandwidth, double* compute);
+
 }  // namespace wxo

@@ -467,6 +467,18 @@ int wxo_spin(uint32_t us, wxo_stream_t stream) {
     return e == hipSuccess ? ok() : hip_fail(e, "spin launch");
 }
 
+int wxo_roofline(double* bandwidth, double* compute) {
+    if (!bandwidth && !compute) return fail(WXO_ERR_INVALID, "roofline: give bandwidth, compute or both");
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    double bw = 0.0, fl = 0.0;
+    const hipError_t e = wxo::measure_roofline(*d, bandwidth ? &bw : nullptr, compute ? &fl : nullptr);
+    if (e != hipSuccess) return hip_fail(e, "roofline measurement");
+    if (bandwidth) *bandwidth = bw;
+    if (compute) *compute = fl;
+    return ok();
+}
+
 // ---- ops on device pointers ------------------------------------------------
 
 int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output, uint32_t N,

@@ -205,6 +205,24 @@ static napi_value js_synchronize(napi_env env, napi_callback_info info) {
     return NULL;
 }
 
+/* roofline() -> {bandwidth, compute}: this device's best sustained HBM read
+ * bytes/s and one-wide f32 FMA flop/s, measured now (wxo_roofline); the
+ * reference's measureRoofline(runner) (harness/roofline.ts:162-198) returns
+ * the same two fields. */
+static napi_value js_roofline(napi_env env, napi_callback_info info) {
+    (void)info;
+    double bw = 0.0, fl = 0.0;
+    int st = wxo_roofline(&bw, &fl);
+    if (st != WXO_OK) return throw_status(env, st, "roofline");
+    napi_value r, v;
+    napi_create_object(env, &r);
+    napi_create_double(env, bw, &v);
+    napi_set_named_property(env, r, "bandwidth", v);
+    napi_create_double(env, fl, &v);
+    napi_set_named_property(env, r, "compute", v);
+    return r;
+}
+
 /* ---------------------------------------------------------------- streams and captured batches
  * Device-pointer ops enqueue on g_stream: the null stream, except while a
  * batch is being captured (graphBegin .. graphEnd), when it is the addon's
@@ -1106,6 +1124,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"deviceCount", NULL, js_device_count, NULL, NULL, NULL, napi_enumerable, NULL},
         {"init", NULL, js_init, NULL, NULL, NULL, napi_enumerable, NULL},
         {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"roofline", NULL, js_roofline, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8", NULL, js_matvec_q8, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Residual", NULL, js_matvec_q8_residual, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Ffn", NULL, js_matvec_q8_ffn, NULL, NULL, NULL, napi_enumerable, NULL},

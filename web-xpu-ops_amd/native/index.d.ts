@@ -5,6 +5,8 @@ export interface WxoAddon {
   deviceCount(): number;
   init(): void;
   synchronize(): void;
+  /** Best sustained HBM read bytes/s and one-wide f32 FMA flop/s of this device, measured now. */
+  roofline(): { bandwidth: number; compute: number };
   matvecQ8(weight: Uint32Array, scale: Float32Array, vector: Float32Array, N: number, K: number, M?: number): Float32Array;
   matvecQ8Residual(weight: Uint32Array, scale: Float32Array, vector: Float32Array, residual: Float32Array, N: number, K: number): Float32Array;
   matvecQ8Ffn(weightGate: Uint32Array, scaleGate: Float32Array, weightUp: Uint32Array, scaleUp: Float32Array, vector: Float32Array, N: number, K: number): Float32Array;

@@ -62,6 +62,7 @@ SIGNATURES = {
     "wxo_event_create": ([ctypes.POINTER(_P)], _I),
     "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
     "wxo_spin": ([ctypes.c_uint32, _P], _I),
+    "wxo_roofline": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], _I),
     "wxo_matmul_q8_multi": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
     "wxo_matmul_q8_multi_ws": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _SZ, _P], _I),
     "wxo_matmul_q8_workspace_bytes": ([ctypes.POINTER(_SZ)], _I),
@@ -148,6 +149,15 @@ def device_count() -> int:
 
 def init() -> None:
     _check(lib().wxo_init())
+
+
+def roofline(bandwidth: bool = True, compute: bool = True) -> dict:
+    """This device's own ceilings, measured now (harness/roofline.ts:162-198):
+    {"bandwidth": best sustained HBM read bytes/s, "compute": best sustained
+    one-wide f32 FMA flop/s}; a part not asked for is None."""
+    bw, fl = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    _check(lib().wxo_roofline(ctypes.byref(bw) if bandwidth else None, ctypes.byref(fl) if compute else None))
+    return {"bandwidth": bw.value if bandwidth else None, "compute": fl.value if compute else None}
 
 
 def words_per_row(K: int) -> int:
