@@ -13,6 +13,9 @@ export function gpuTest(file, name, fn) {
   globalThis.__wxoTests.push({ file, name, fn, gpu: true });
 }
 
+/** Thrown by a test that cannot run here; the runner lists it as skipped, with the reason. */
+export class Skip extends Error {}
+
 const golden = join(dirname(fileURLToPath(import.meta.url)), "..", "golden");
 export const kat = JSON.parse(readFileSync(join(golden, "kat.json"), "utf8"));
 

@@ -9,7 +9,8 @@
 // build; device copies stand in for them so the data stays on the device.
 // Every op's output is checked against the ECMAScript oracle on the inputs
 // the op saw (read back from the device).
-import { test, gpuTest, assert, assertMatvecAgrees, assertResidualAgrees, assertFfnAgrees } from "./harness.mjs";
+import { test, gpuTest, assert, assertMatvecAgrees, assertResidualAgrees, assertFfnAgrees, Skip } from "./harness.mjs";
+import { existsSync, readFileSync } from "fs";
 import { Q8, Q8_FFN, Q8_RESIDUAL, MATMUL_Q8, RMSNORM_LIKE, kernel } from "./wgsl_interfaces.mjs";
 import { createResidentQ8Device, createResidentDevice, runnerFromResident, params, UnsupportedPipelineError } from "../../web-xpu-ops_amd/harness/resident.js";
 import { recognise, parseBindings } from "../../web-xpu-ops_amd/harness/wgsl-interface.js";
@@ -26,6 +27,21 @@ test(F, "pipelineFor's WGSL recognition: the four interfaces, by binding declara
   assert.strictEqual(recognise(Q8_RESIDUAL).op, "matvecQ8Residual");
   assert.strictEqual(recognise(MATMUL_Q8).op, "matmulQ8");
   assert.deepStrictEqual(parseBindings(Q8).map((b) => b.name), ["weight", "scale", "vector", "output", "params"]);
+});
+
+// The reference's own kernel sources, read where that tree is mounted (the
+// build container); nothing of them is kept under tests/.
+const REFERENCE = "/root/reference";
+
+test(F, "pipelineFor's WGSL recognition on the reference's own WGSL files (llm/engine-q8-resident.ts:1059-1078)", () => {
+  if (!existsSync(REFERENCE)) throw new Skip(`the reference tree ${REFERENCE} is not mounted on this machine`);
+  const src = (rel) => readFileSync(`${REFERENCE}/${rel}`, "utf8");
+  assert.strictEqual(recognise(src("ops/matvec/wgsl/q8.wgsl")).op, "matvecQ8");
+  assert.strictEqual(recognise(src("ops/matvec/wgsl/q8_ffn.wgsl")).op, "matvecQ8Ffn");
+  assert.strictEqual(recognise(src("ops/matvec/wgsl/q8_residual.wgsl")).op, "matvecQ8Residual");
+  assert.strictEqual(recognise(src("ops/matmul/wgsl/q8.wgsl")).op, "matmulQ8");
+  // the engine's other kernels are refused with the named error
+  assert.throws(() => recognise(src("ops/rmsnorm/wgsl/kernel.wgsl")), (e) => e instanceof UnsupportedPipelineError);
 });
 
 test(F, "pipelineFor's WGSL recognition refuses other kernels and near misses with a named error", () => {

@@ -7,6 +7,7 @@ import { pathToFileURL } from "url";
 import { dirname, join } from "path";
 import { fileURLToPath } from "url";
 import { readdirSync } from "fs";
+import { Skip } from "./harness.mjs";
 
 const mode = process.argv[2] || "cpu";
 const here = dirname(fileURLToPath(import.meta.url));
@@ -31,6 +32,11 @@ for (const t of registry) {
     passed += 1;
     console.log(`PASS ${t.file} > ${t.name}`);
   } catch (e) {
+    if (e instanceof Skip) {
+      skipped += 1;
+      console.log(`SKIP ${t.file} > ${t.name} (${e.message})`);
+      continue;
+    }
     failed += 1;
     console.log(`FAIL ${t.file} > ${t.name}\n  ${e && e.stack ? e.stack.split("\n").slice(0, 4).join("\n  ") : e}`);
   }

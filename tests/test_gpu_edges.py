@@ -156,8 +156,11 @@ def test_quantize_fast_path_meets_subnormal_elements(D):
     assert_bits_equal(s2, want_scales, f"fused scales D={D}")
 
 
-@pytest.mark.parametrize("M", [4, 8, 16])
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
 def test_batched_lm_head_every_row(M):
+    """cfg5 (N=151936, K=1024) at every M the configuration names, every row
+    against the oracle; M = 1 is the single-vector kernel's own instance
+    (9,496 blocks of 16 rows, one chunk per wave)."""
     c = wl.make_config("cfg5", M=M)
     N, K = c["N"], c["K"]
     codes, scales = oracle.quantize(c["w"], N, K)
@@ -166,6 +169,8 @@ def test_batched_lm_head_every_row(M):
     print(f"cfg5 M={M}: every row", flush=True)
     ys = wxo_q8.matvecQ8Batched(weight=w, scale=scales, vectors=xs, N=N, K=K, M=M)
     print(f"  {wxo_q8.last_variant()}", flush=True)
+    if M == 1:
+        assert wxo_q8.last_variant().startswith("matvec_q8_m1 "), wxo_q8.last_variant()
     for m in range(M):
         assert_matvec(ys[m], w, scales, xs[m], N, K)
 

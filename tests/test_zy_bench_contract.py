@@ -71,13 +71,12 @@ def test_json_line_contract():
 @pytest.mark.gpu
 def test_short_and_long_runs_agree():
     """The driver's short run (20 steps after 5 warmups) and a 2000-step run
-    measure the same per-call time: no first touches, no host launch latency
-    and no event fences inside the timed region.  Each bench process places
-    its buffers anew, which moves a run by up to about 1 %, and boxes differ
-    in how a 0.2 ms burst and a 17 ms stretch of streaming compare (one box
-    ran the short runs at 8.43 us and the long ones at 8.66 us, another
-    within 0.2 %), so short and long runs alternate, three of each, and
-    their medians must agree within 3 %."""
+    measure the same per-call time: no first touches, no host launch latency,
+    no event fences and no re-read of a recently streamed weight copy inside
+    the timed region (one launch index runs from the set-up through the
+    timed calls).  Each bench process places its buffers anew, which moves a
+    run by a few tenths of a percent, so short and long runs alternate, three
+    of each, and their medians must agree within 1 %."""
     runs = {20: [], 2000: []}
     for _ in range(3):
         for steps, warmup in ((20, 5), (2000, 200)):
@@ -87,4 +86,4 @@ def test_short_and_long_runs_agree():
             runs[steps].append(json.loads(p.stdout.strip().splitlines()[-1])["ms_per_step"])
             print(f"  ms_per_step {runs[steps][-1]}", flush=True)
     res = {k: sorted(v)[1] for k, v in runs.items()}
-    assert abs(res[20] - res[2000]) <= 0.03 * res[2000], runs
+    assert abs(res[20] - res[2000]) <= 0.01 * res[2000], runs

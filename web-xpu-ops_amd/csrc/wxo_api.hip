@@ -91,6 +91,10 @@ int current_device(const wxo::DeviceInfo** out) {
         void* p = nullptr;
         g_scratch_err[ordinal] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         g_scratch[ordinal] = g_scratch_err[ordinal] == hipSuccess ? p : nullptr;
+        // A failed probe is reported by wxo_matmul_q8_multi_static alone (from
+        // g_scratch_err); clear the runtime's last error so the next launch's
+        // hipGetLastError does not report it against an unrelated op.
+        if (g_scratch_err[ordinal] != hipSuccess) (void)hipGetLastError();
         d.ordinal = ordinal;
     }
     *out = &d;

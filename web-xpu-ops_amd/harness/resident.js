@@ -287,12 +287,17 @@ export class ResidentQ8Device {
       this.graph = null;
       const before = this.stats.launches;
       a.graphBegin();
-      let handle = null;
       try {
         this.enqueue(calls, coalesce, null, null);
-      } finally {
-        handle = a.graphEnd();
+      } catch (err) {
+        // Close the capture and free whatever it instantiated; the error to
+        // report is the one the batch raised, not one from closing it.
+        try {
+          a.graphDestroy(a.graphEnd());
+        } catch (_) { /* the capture was already invalid: nothing was instantiated */ }
+        throw err;
       }
+      const handle = a.graphEnd();
       this.graph = { handle, key, launches: this.stats.launches - before };
       this.stats.graphsCaptured += 1;
     } else {

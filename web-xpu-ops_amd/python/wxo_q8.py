@@ -238,9 +238,13 @@ class Graph:
         p = ctypes.c_void_p(0)
         try:
             record()
-        finally:
-            st = lib().wxo_graph_capture_end(stream.handle, ctypes.byref(p))
-        _check(st)
+        except BaseException:
+            # Close the capture and free whatever it instantiated; the error
+            # raised by `record` is the one reported.
+            if lib().wxo_graph_capture_end(stream.handle, ctypes.byref(p)) == WXO_OK and p.value:
+                lib().wxo_graph_destroy(p)
+            raise
+        _check(lib().wxo_graph_capture_end(stream.handle, ctypes.byref(p)))
         return Graph(p.value)
 
     def launch(self, stream: "Stream") -> None:
