@@ -121,7 +121,9 @@ def test_roofline_ceilings():
     print("wxo_roofline", flush=True)
     r = wxo_q8.roofline()
     assert 3e12 < r["bandwidth"] < 8.2e12, r
-    assert 2e13 < r["compute"] < 8.2e13, r
+    # one-wide v_fma_f32 (packed FP32 is disabled in this build) under MI355X's
+    # published 157.3 TFLOP/s FP32 vector peak
+    assert 2e13 < r["compute"] < 1.6e14, r
     only_bw = wxo_q8.roofline(compute=False)
     assert only_bw["compute"] is None and 3e12 < only_bw["bandwidth"] < 8.2e12
     with pytest.raises(wxo_q8.WxoError, match="roofline"):

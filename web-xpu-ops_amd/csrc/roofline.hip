@@ -24,7 +24,7 @@
 //    part of what any kernel pays).
 //  * The FMA chains: 8 independent chains per lane, 8 waves per SIMD, no
 //    memory.  This build disables packed f32 instructions, so the figure is the
-//    one-wide FMA rate (half MI355X's packed peak).
+//    rate of one-wide v_fma_f32.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
