@@ -624,3 +624,35 @@ def test_matmul_tile_pairs(N, Ms, K):
         got = out.download(np.float32, N * M + 64)
         assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
         assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)
+
+
+def test_matmul_tile_pairs_ragged_tokens_match_one_group():
+    """Tile pairs with a partial last token tile (N = 2040: 31 whole 64-token
+    tiles and one of 56): every 29th token against the oracle, nothing past
+    the output, and the bits of both halves of the tokens equal to runs of
+    those halves alone, whose 512 tiles take the one-group FB4 form (the same
+    sums in the same order; token tile boundaries line up at token 1024)."""
+    N, M, K = 2040, 4096, 4096
+    rng = np.random.default_rng(2040)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    w = oracle.pack_q8(rng.integers(-128, 128, (M, K)).astype(np.int32).reshape(-1), M, K)
+    s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    bw, bs = wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s)
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+    out.upload(np.full(N * M + 64, 7.5, np.float32))
+    wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, out, M)], N, K)
+    wxo_q8.synchronize()
+    assert " FB4.pairs " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    got = out.download(np.float32, N * M + 64)
+    assert np.all(got[N * M:] == np.float32(7.5)), "written past the output"
+    assert_matmul(got[:N * M], a, w, s, N, M, K, rows=np.unique(np.r_[np.arange(0, N, 29), N - 1]))
+    for t0, t1 in ((0, 1024), (1024, N)):
+        n = t1 - t0
+        bh = wxo_q8.DeviceBuffer.from_array(a[t0 * K:t1 * K])
+        oh = wxo_q8.DeviceBuffer(4 * n * M)
+        wxo_q8.matmul_q8_multi_device(bh, [(bw, bs, oh, M)], n, K)
+        wxo_q8.synchronize()
+        variant = wxo_q8.last_variant()
+        assert " FB4 " in variant and "pairs" not in variant, variant
+        assert_bits_equal(oh.download(np.float32, n * M), got[t0 * M:t1 * M], f"tokens {t0}..{t1}: pairs vs one group")
