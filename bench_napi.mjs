@@ -4,6 +4,7 @@
 //   - one resident matvecQ8 per batch at N=11008, K=4096 (one launch, one
 //     stream synchronisation per call), weights rotated over 12 device copies
 //     so HBM, not the 256 MB last-level cache, serves them;
+//   - the same batches issued without awaiting each one (in flight together);
 //   - the same with the 44 KB output read back each call;
 //   - the host convenience call matvecQ8({weight, scale, vector, N, K})
 //     (ops/matvec/reference.ts:117), which copies the 45 MB weight in over
@@ -71,6 +72,18 @@ async function main() {
   let us = await timeLoop(calls, (i) => dev.batch([op(i)]));
   results.push({ case: "N-API end to end: resident matvecQ8, one launch + one synchronisation per call, N=11008 K=4096",
                  us: +us.toFixed(3), "GB/s": +(bytes / us / 1e3).toFixed(1) });
+  // the same batches issued without awaiting each: the host enqueues call
+  // i + 1 while the GPU runs call i, and one await covers them all
+  {
+    for (let i = 0; i < 50; i += 1) await dev.batch([op(i)]);
+    const t0 = nowUs();
+    const pending = [];
+    for (let i = 0; i < calls; i += 1) pending.push(dev.batch([op(i)]));
+    await Promise.all(pending);
+    us = (nowUs() - t0) / calls;
+  }
+  results.push({ case: "N-API end to end: resident matvecQ8, batches in flight together (not awaited one by one), N=11008 K=4096",
+                 us: +us.toFixed(3), "GB/s": +(bytes / us / 1e3).toFixed(1) });
   us = await timeLoop(calls, (i) => dev.batch([op(i)], readback));
   results.push({ case: "N-API end to end: resident matvecQ8 + 44 KB readback per call, N=11008 K=4096",
                  us: +us.toFixed(3), "GB/s": +(bytes / us / 1e3).toFixed(1) });
@@ -112,14 +125,16 @@ async function main() {
   const layerBytes = 4 * (H * (H / 4) * 4) + 2 * (F * (H / 4) * 4) + H * (F / 4) * 4;
   // op by op (every launch issued each step), then as the device runs a
   // repeating step list by default: captured once, one graph launch per step
-  for (const graphs of [false, true]) {
+  for (const [graphs, wait] of [[false, "async"], [true, "async"], [true, "block"]]) {
     dev.graphs = graphs;
+    dev.wait = wait;
     const g0 = dev.stats.graphLaunches;
     us = await timeLoop(steps, () => dev.batch(ops));
     const replayed = dev.stats.graphLaunches - g0;
     results.push({ case: `N-API end to end: one decode step, ${L} layers of cfg4 shapes as one resident batch ` +
                          `(${ops.length} ops, ${launches} launches, one synchronisation), ` +
-                         (graphs ? "replayed as one captured graph" : "launched op by op"),
+                         (graphs ? "replayed as one captured graph" : "launched op by op") +
+                         (wait === "block" ? ", waiting on the JS thread" : ""),
                    us: +us.toFixed(1), us_per_layer: +(us / L).toFixed(2),
                    "GB/s": +(L * layerBytes / us / 1e3).toFixed(1), graph_launches: replayed });
   }

@@ -121,6 +121,20 @@ int wxo_memcpy_dtoh(void* dst, const void* src, size_t bytes, wxo_stream_t strea
  * resident device clears every new storage buffer with this. */
 int wxo_memset(void* ptr, int value, size_t bytes, wxo_stream_t stream);
 int wxo_memcpy_dtod(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
+/* wxo_memcpy_htod / wxo_memcpy_dtoh return once the copy is done (their stream
+ * synchronised).  wxo_memcpy_dtoh_async only enqueues the copy on `stream`,
+ * after the work already there: with `dst` from wxo_host_malloc the host
+ * thread does not wait, and the bytes are in `dst` once an event recorded
+ * after it on `stream` has completed.  This is the resident batch's readback
+ * (harness/resident.ts:321-345: copyBufferToBuffer into the caller's MAP_READ
+ * staging buffer inside the batch's one submit, then mapAsync). */
+int wxo_memcpy_dtoh_async(void* dst, const void* src, size_t bytes, wxo_stream_t stream);
+/* Page-locked host memory, the counterpart of a WebGPU MAP_READ | COPY_DST
+ * staging buffer (harness/resident.ts:41-48): device-to-host copies into it
+ * run asynchronously on their stream.  bytes = 0 gives NULL.  Freeing NULL is
+ * a no-op. */
+int wxo_host_malloc(void** ptr, size_t bytes);
+int wxo_host_free(void* ptr);
 int wxo_synchronize(void);
 int wxo_stream_create(wxo_stream_t* stream);
 int wxo_stream_destroy(wxo_stream_t stream);

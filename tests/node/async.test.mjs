@@ -1,0 +1,147 @@
+// The resident batch as an asynchronous submit: the wait for the GPU runs off
+// the JS thread (the reference's batch awaits queue.onSubmittedWorkDone and
+// mapAsync, harness/resident.ts:321-345), batches called while others are in
+// flight run after them in call order, and each reads back its own values
+// through page-locked staging memory.
+import { gpuTest, assert, assertBitsEqual } from "./harness.mjs";
+import { createResidentQ8Device, BufferUsage } from "../../web-xpu-ops_amd/harness/resident.js";
+import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
+
+const F = "async.test.mjs";
+
+function rng(seed) {
+  let s = seed >>> 0;
+  return () => {
+    s = (Math.imul(s, 1664525) + 1013904223) >>> 0;
+    return s / 4294967296;
+  };
+}
+
+function vec(n, seed) {
+  const r = rng(seed);
+  return Float32Array.from({ length: n }, () => Math.fround(2 * r() - 1));
+}
+
+function nowMs() {
+  const [s, ns] = process.hrtime();
+  return s * 1e3 + ns / 1e6;
+}
+
+function storage(device, data) {
+  const b = device.createStorageBuffer(data.byteLength);
+  device.upload(b, 0, data);
+  return b;
+}
+
+gpuTest(F, "batch(): returns before the GPU is done and the event loop runs while it waits", async () => {
+  const device = await createResidentQ8Device();
+  const n = 4096;
+  const src = storage(device, vec(n, 1));
+  const dst = device.createStorageBuffer(n * 4);
+  const staging = device.createStorageBuffer(n * 4, BufferUsage.MAP_READ | BufferUsage.COPY_DST);
+  device.addon.spin(40000);  // 40 ms of GPU work ahead of the batch
+  const t0 = nowMs();
+  const pending = device.batch([{ kind: "copy", src, srcOffset: 0, dst, dstOffset: 0, size: n * 4 }],
+    [{ staging, source: dst, sourceOffset: 0, length: n, type: "f32" }]);
+  const issued = nowMs() - t0;
+  let ticks = 0;
+  const timer = setInterval(() => { ticks += 1; }, 2);
+  const [got] = await pending;
+  clearInterval(timer);
+  const total = nowMs() - t0;
+  assert.ok(issued < 20, `batch() took ${issued.toFixed(1)} ms to return its promise`);
+  assert.ok(total >= 30, `the batch settled after ${total.toFixed(1)} ms, before the 40 ms of work ahead of it`);
+  assert.ok(ticks >= 3, `the event loop ran ${ticks} timer ticks while the batch waited`);
+  assertBitsEqual(got, vec(n, 1), "copied values");
+  device.destroy();
+});
+
+gpuTest(F, "batches in flight run in call order, each reads back its own values; a staging buffer still being read into is refused", async () => {
+  const device = await createResidentQ8Device();
+  const n = 1000;
+  const a = storage(device, vec(n, 11)), b = storage(device, vec(n, 12));
+  const y = device.createStorageBuffer(n * 4);
+  const sa = device.createStorageBuffer(n * 4, BufferUsage.MAP_READ | BufferUsage.COPY_DST);
+  const sb = device.createStorageBuffer(n * 4, BufferUsage.MAP_READ | BufferUsage.COPY_DST);
+  const copy = (src) => ({ kind: "copy", src, srcOffset: 0, dst: y, dstOffset: 0, size: n * 4 });
+  const read = (staging) => ({ staging, source: y, sourceOffset: 0, length: n, type: "f32" });
+  device.addon.spin(20000);
+  const p1 = device.batch([copy(a)], [read(sa)]);
+  const p2 = device.batch([copy(b)], [read(sb)]);
+  const p3 = device.batch([], [read(undefined)]);  // pooled staging
+  await assert.rejects(device.batch([], [read(sa)]), /pending map/);
+  const [[r1], [r2], [r3]] = await Promise.all([p1, p2, p3]);
+  assertBitsEqual(r1, vec(n, 11), "first batch");
+  assertBitsEqual(r2, vec(n, 12), "second batch");
+  assertBitsEqual(r3, vec(n, 12), "readback-only batch");
+  const [again] = await device.batch([], [read(sa)]);  // free again once its batch settled
+  assertBitsEqual(again, vec(n, 12), "staging reused");
+  device.destroy();
+});
+
+gpuTest(F, "replayed graphs in flight back to back: the same bits as batches awaited one by one", async () => {
+  // Each step adds two projections of x into the residual stream in place,
+  // so every step's readback differs from the last; a readback that ran
+  // before its step's graph would show the previous step's values.
+  const N = 2048, K = 2048, steps = 6;
+  const r = rng(5);
+  const codes = Int8Array.from({ length: N * K }, () => Math.floor(r() * 256) - 128);
+  const scale = Float32Array.from({ length: N }, () => Math.fround(0.001 * (0.5 + r())));
+  const packed = packInt8Rows(codes, N, K);
+  const run = async (pipelined) => {
+    const device = await createResidentQ8Device();
+    const w = storage(device, packed), s = storage(device, scale), x = storage(device, vec(K, 6));
+    const h = storage(device, vec(N, 7));
+    const ops = [
+      { kind: "matvecQ8Residual", weight: w, scale: s, vector: x, residual: h, output: h, N, K },
+      { kind: "matvecQ8Residual", weight: w, scale: s, vector: x, residual: h, output: h, N, K },
+    ];
+    const rb = [{ source: h, sourceOffset: 0, length: N, type: "f32" }];
+    let out;
+    if (pipelined) {
+      const first = [await device.batch(ops, rb)];   // op by op
+      device.addon.spin(20000);
+      const rest = [];
+      for (let k = 1; k < steps; k += 1) rest.push(device.batch(ops, rb));  // captured once, then replayed, none awaited
+      out = first.concat(await Promise.all(rest));
+    } else {
+      out = [];
+      for (let k = 0; k < steps; k += 1) out.push(await device.batch(ops, rb));
+    }
+    const stats = { ...device.stats };
+    device.destroy();
+    return { out: out.map((o) => o[0]), stats };
+  };
+  const serial = await run(false);
+  const piped = await run(true);
+  assert.strictEqual(piped.stats.graphsCaptured, 1);
+  assert.strictEqual(piped.stats.graphLaunches, steps - 1);
+  for (let k = 0; k < steps; k += 1) {
+    assertBitsEqual(piped.out[k], serial.out[k], `step ${k}`);
+    if (k > 0) assert.notDeepStrictEqual(Array.from(serial.out[k]), Array.from(serial.out[k - 1]), `step ${k} changed the stream`);
+  }
+});
+
+gpuTest(F, "wait: \"block\" waits on the JS thread (the promise is settled on return) with the same results", async () => {
+  const n = 2048;
+  const out = [];
+  for (const wait of ["async", "block"]) {
+    const device = await createResidentQ8Device({ wait });
+    const src = storage(device, vec(n, 21));
+    const dst = device.createStorageBuffer(n * 4);
+    device.addon.spin(20000);
+    const t0 = nowMs();
+    let settled = false;
+    const p = device.batch([{ kind: "copy", src, srcOffset: 0, dst, dstOffset: 0, size: n * 4 }],
+      [{ source: dst, sourceOffset: 0, length: n, type: "f32" }]).then((r) => { settled = true; return r; });
+    const issued = nowMs() - t0;
+    await null;  // one microtask turn: a settled promise's reaction has run
+    await null;
+    if (wait === "block") assert.ok(issued >= 15 && settled, `block: returned after ${issued.toFixed(1)} ms, settled ${settled}`);
+    else assert.ok(issued < 15 && !settled, `async: returned after ${issued.toFixed(1)} ms, settled ${settled}`);
+    out.push((await p)[0]);
+    device.destroy();
+  }
+  assertBitsEqual(out[1], out[0], "block vs async");
+  assertBitsEqual(out[0], vec(n, 21), "values");
+});

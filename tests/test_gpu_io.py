@@ -78,6 +78,44 @@ def test_read_waits_for_the_stream():
     stream.destroy()
 
 
+def test_async_read_into_page_locked_memory():
+    """wxo_memcpy_dtoh_async into wxo_host_malloc memory returns while the
+    work ahead of it on its stream still runs, and the bytes are there once an
+    event recorded after it completes; a later write on the stream does not
+    reach the bytes already read."""
+    import time
+    wxo_q8.init()
+    L = wxo_q8.lib()
+    n = 1 << 16
+    src = np.arange(n, dtype=np.uint32) * np.uint32(2654435761)
+    dev = wxo_q8.DeviceBuffer.from_array(src)
+    host = ctypes.c_void_p(0)
+    assert L.wxo_host_malloc(ctypes.byref(host), n * 4) == 0 and host.value
+    pinned = np.ctypeslib.as_array((ctypes.c_uint32 * n).from_address(host.value))
+    pinned[:] = 0
+    stream = wxo_q8.Stream()
+    done = wxo_q8.Event()
+    try:
+        assert L.wxo_spin(30000, stream.handle) == 0  # 30 ms of work ahead of the copy
+        t0 = time.perf_counter()
+        assert L.wxo_memcpy_dtoh_async(host.value, dev.ptr, n * 4, stream.handle) == 0
+        issued = time.perf_counter() - t0
+        assert L.wxo_memset(dev.ptr, 0, n * 4, stream.handle) == 0  # after the copy, in stream order
+        done.record(stream)
+        done.synchronize()
+        assert issued < 0.02, f"the async copy held the host {issued * 1e3:.1f} ms"
+        np.testing.assert_array_equal(pinned, src)
+        assert np.all(dev.download(np.uint32, n) == 0)
+        assert L.wxo_host_free(None) == 0
+        assert L.wxo_memcpy_dtoh_async(None, dev.ptr, 4, stream.handle) == wxo_q8.WXO_ERR_INVALID
+    finally:
+        wxo_q8.synchronize()
+        done.destroy()
+        stream.destroy()
+        assert L.wxo_host_free(host.value) == 0
+        dev.free()
+
+
 @pytest.mark.parametrize("offset", [0, 1, 3, 16, 17])
 @pytest.mark.parametrize("length", [0, 1, 15, 16, 17, 1000, 65536 + 5])
 def test_memset_any_offset_and_length(offset, length):

@@ -317,6 +317,32 @@ int wxo_memcpy_dtoh(void* dst, const void* src, size_t bytes, wxo_stream_t strea
 int wxo_memcpy_dtod(void* dst, const void* src, size_t bytes, wxo_stream_t stream) {
     return copy(dst, src, bytes, hipMemcpyDeviceToDevice, stream, "memcpy D2D");
 }
+int wxo_memcpy_dtoh_async(void* dst, const void* src, size_t bytes, wxo_stream_t stream) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(WXO_ERR_INVALID, "memcpy D2H async: NULL pointer");
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_hip(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "memcpy D2H async");
+}
+
+int wxo_host_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(WXO_ERR_INVALID, "ptr is NULL");
+    *ptr = nullptr;
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    if (bytes == 0) return ok();
+    hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        return hip_fail(e, "hipHostMalloc");
+    }
+    return ok();
+}
+
+int wxo_host_free(void* ptr) {
+    if (!ptr) return ok();
+    hipError_t e = hipHostFree(ptr);
+    return e == hipSuccess ? ok() : hip_fail(e, "hipHostFree");
+}
 
 namespace {
 // Sets bytes [0, head) and [head + 16 body, + tail) one by one and the 16-byte

@@ -1,7 +1,7 @@
 // Declarations of harness/resident.js: the reference's ResidentDevice
 // (harness/resident.ts:28-145) for the ops this build runs, plus native op kinds.
 export interface ResidentBuffer {
-  /** Device address (storage buffers) or null (uniform and MAP_READ staging buffers, held in host memory). */
+  /** Device address (storage buffers) or null (uniform buffers in host memory, MAP_READ staging buffers in page-locked host memory). */
   readonly ptr: bigint | null;
   readonly size: number;
   readonly usage: number;
@@ -33,7 +33,7 @@ export type ResidentOp =
   | { kind: "matmulQ8"; a: ResidentBuffer; weight: ResidentBuffer; scale: ResidentBuffer; output: ResidentBuffer; N: number; M: number; K: number }
   | { kind: "dequantTranspose"; weight: ResidentBuffer; scale: ResidentBuffer; outFeatures: number; inFeatures: number; output: ResidentBuffer }
   | { kind: "gatherDequantRows"; codes: ResidentBuffer; scale: ResidentBuffer; rows: number; D: number; indices: ResidentBuffer; count: number; output: ResidentBuffer };
-/** harness/resident.ts:41-48; `staging` is accepted and not needed. */
+/** harness/resident.ts:41-48; the values land in `staging` (a MAP_READ buffer of this device) when given, else in pooled page-locked memory. */
 export interface ResidentReadback {
   staging?: ResidentBuffer;
   source: ResidentBuffer;
@@ -56,6 +56,12 @@ export interface ResidentQ8Options {
   coalesce?: boolean;
   /** Capture a batch that repeats its predecessor as a HIP graph and replay it (default true). */
   graphs?: boolean;
+  /**
+   * Where a batch waits for the GPU: "async" (default) off the JS thread, so
+   * the event loop runs and later batches can be enqueued meanwhile; "block"
+   * on the JS thread, ~8-10 us less per awaited batch.
+   */
+  wait?: "async" | "block";
 }
 export declare const BufferUsage: {
   readonly MAP_READ: number; readonly MAP_WRITE: number; readonly COPY_SRC: number; readonly COPY_DST: number;
@@ -68,13 +74,22 @@ export declare class ResidentQ8Device {
     graphsCaptured: number; graphLaunches: number };
   /** Whether repeating batches are captured and replayed (the `graphs` option). */
   graphs: boolean;
+  /** Where a batch waits for the GPU (the `wait` option). */
+  wait: "async" | "block";
   readonly timestampsSupported: boolean;
   createStorageBuffer(bytes: number, usage?: number): ResidentBuffer;
   createUniformBuffer(bytes: number): ResidentBuffer;
   upload(buffer: ResidentBuffer, offset: number, data: ArrayBufferView): void;
   pipelineFor(code: string, entry?: string): Promise<ResidentPipeline>;
   bindGroup(pipeline: ResidentPipeline, buffers: ResidentBuffer[]): Promise<ResidentBindGroup>;
+  /**
+   * Enqueues the ops and the readback copies at once and settles when the GPU
+   * has run them, waiting off the JS thread; batches called while others are
+   * in flight run after them, in call order.
+   */
   batch(ops: ResidentOp[], readback?: ResidentReadback[], profile?: BatchProfile): Promise<(Float32Array | Int32Array | Uint32Array)[]>;
+  /** Settles once every batch in flight has. */
+  idle(): Promise<void>;
   destroy(): void;
 }
 export declare function createResidentQ8Device(options?: ResidentQ8Options): Promise<ResidentQ8Device | null>;

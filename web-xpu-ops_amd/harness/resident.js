@@ -32,11 +32,16 @@
 // loader and the prefill side use.
 //
 // Buffers: storage buffers are HBM allocations owned by the device and freed
-// by destroy(); uniform buffers and MAP_READ staging buffers live in host
-// memory (the kernels take their sizes as arguments, and readback needs no
-// staging copy), and still count in stats.buffersCreated.  Ops are enqueued in
-// order on the device's stream; batch() synchronises once and reads back only
-// `readback`, so nothing is allocated in a decode loop's steady state.
+// by destroy(); uniform buffers live in host memory (the kernels take their
+// values as arguments when a dispatch is enqueued) and MAP_READ staging
+// buffers in page-locked host memory; all count in stats.buffersCreated.  Ops
+// are enqueued in order on the device's stream.  batch() enqueues its ops and
+// then the copies of `readback` into staging memory, and returns a Promise
+// that settles when the GPU has run them: the wait happens off the JS thread
+// (the reference's onSubmittedWorkDone + mapAsync, harness/resident.ts:
+// 321-345), so the caller's event loop keeps running and the next batch may
+// be enqueued behind this one before it finishes.  Batches run in the order
+// they were called.  Nothing is allocated in a decode loop's steady state.
 //
 // Consecutive single-vector matvecQ8 ops (dispatch or native) on the same
 // vector and K run as one launch when no op of the run reads what another
@@ -85,6 +90,12 @@ export class ResidentQ8Device {
     this.workspace = this.addon.malloc(this.workspaceBytes);
     this.coalesce = options.coalesce !== false;
     this.graphs = options.graphs !== false;
+    // "async": a batch's wait runs off the JS thread; "block": on it (the
+    // lowest latency per awaited batch, the event loop held meanwhile)
+    if (options.wait !== undefined && options.wait !== "async" && options.wait !== "block") {
+      throw new TypeError(`wait must be "async" or "block", got ${options.wait}`);
+    }
+    this.wait = options.wait || "async";
     this.stats = { buffersCreated: 0, pipelinesCreated: 0, submits: 0, launches: 0, graphsCaptured: 0,
       graphLaunches: 0 };
     this.graph = null;        // the last captured batch: { handle, key, launches }
@@ -96,18 +107,21 @@ export class ResidentQ8Device {
     this.pipelineSet = new WeakSet();
     this.groupSet = new WeakSet();
     this.events = [];
+    this.inflight = new Set();  // completion promises of batches still running
+    this.stagingPool = new Map();  // byte size -> free page-locked buffers for readbacks without staging
   }
 
   /**
    * A buffer of max(4, bytes) bytes.  With the default usage (or any usage
    * without MAP_READ) an HBM allocation `{ ptr: bigint, size }`; a MAP_READ
-   * staging buffer (harness/resident.ts:41-48) is host memory, since readback
-   * copies straight to a fresh typed array.
+   * staging buffer (harness/resident.ts:41-48) is page-locked host memory,
+   * which a batch's readback copies into without blocking the host.
    */
   createStorageBuffer(bytes, usage = DEFAULT_USAGE) {
     const size = Math.max(4, bytes);
     if (usage & BufferUsage.MAP_READ) {
-      return this.track({ ptr: null, host: new Uint8Array(size), size, usage, kind: "staging" });
+      return this.track({ ptr: null, host: new Uint8Array(this.addon.hostAlloc(size)), size, usage, kind: "staging",
+        busy: false });
     }
     // WebGPU hands out zero-filled buffers, and the engine relies on it (an
     // all-zero attention mask is never uploaded, llm/engine-q8-resident.ts:
@@ -126,8 +140,8 @@ export class ResidentQ8Device {
 
   /**
    * Registers a new buffer and gives it GPUBuffer's destroy(): the memory is
-   * released at once (a batch has synchronised before it returns, so no
-   * enqueued work still reads it), later calls are no-ops, and any later use
+   * released at once (after the batches in flight, which may read it, have
+   * run), later calls are no-ops, and any later use
    * of the buffer (upload, a bind group that holds it, an op, a readback)
    * throws.  The engine destroys its transient per-prefill buffers this way
    * (llm/engine-q8-resident.ts:1693), as runnerFromResident does its
@@ -136,6 +150,7 @@ export class ResidentQ8Device {
   track(buffer) {
     buffer.destroy = () => {
       if (!this.buffers.delete(buffer)) return;
+      if (buffer.ptr !== null && this.inflight.size > 0) this.addon.synchronize();  // a batch in flight may read it
       if (buffer.ptr !== null) this.addon.free(buffer.ptr);
       buffer.ptr = null;
       buffer.host = null;
@@ -214,31 +229,59 @@ export class ResidentQ8Device {
   }
 
   /**
-   * Enqueues every op in order, synchronises once, then reads back only
-   * `readback` ({ staging?, source, sourceOffset, length, type }; a staging
-   * buffer, when given, is not needed and not touched).  Every op is checked
-   * before the first is enqueued.  `profile` ({ labels?, sink }) as
-   * harness/resident.ts:75-96: sink.submitToDoneMs (enqueue end to
-   * completion), sink.readbackMs, and with labels sink.gpuEntries
-   * [{ label, seconds }] for each labelled non-copy op, from HIP events
-   * around its launch.
+   * Enqueues every op in order, then the copies of `readback` ({ staging?,
+   * source, sourceOffset, length, type }) into page-locked staging memory
+   * (the caller's MAP_READ staging buffer when given, sized for length * 4
+   * bytes, else a pooled one), and resolves to fresh typed arrays of the read
+   * values once the GPU has run all of it.  Every op is checked before the
+   * first is enqueued.  The wait runs off the JS thread; a batch called while
+   * another is in flight is enqueued behind it at once, except that a batch
+   * that captures a graph, or carries profile labels, first waits for the
+   * batches in flight.  A staging buffer that an unfinished batch is reading
+   * back into is refused, as WebGPU refuses a buffer with a pending map.
+   * `profile` ({ labels?, sink }) as harness/resident.ts:75-96:
+   * sink.submitToDoneMs (enqueue end to completion, the device-to-host copies
+   * included), sink.readbackMs (the copies out of staging), and with labels
+   * sink.gpuEntries [{ label, seconds }] for each labelled non-copy op, from
+   * HIP events around its launch.
    */
   async batch(ops, readback = [], profile = undefined) {
     const calls = ops.map((op, i) => this.resolve(op, i));
     const reads = readback.map((r) => checkReadback(r, this.buffers));
     const labels = profile && profile.labels ? profile.labels : null;
     const coalesce = this.coalesce && !labels;
+    const graphed = this.graphs && !labels && calls.length > 1;
+    if ((labels || (graphed && this.wouldCapture(calls, coalesce))) && this.inflight.size > 0) await this.idle();
+    const targets = this.stagingTargets(reads);
     const a = this.addon;
     const timed = [];
-    if (!(this.graphs && !labels && calls.length > 1 && this.replay(calls, coalesce))) {
-      this.enqueue(calls, coalesce, labels, timed);
+    let done;
+    try {
+      if (!(graphed && this.replay(calls, coalesce))) this.enqueue(calls, coalesce, labels, timed);
+      reads.forEach((r, k) => a.downloadAsync(r.source.ptr + BigInt(r.sourceOffset), targets[k].view));
+      if (this.wait === "block") {
+        a.synchronize();
+        done = Promise.resolve();
+      } else {
+        done = a.whenDone();
+      }
+    } catch (err) {
+      this.releaseStaging(targets);
+      throw err;
     }
-    const t0 = profile ? performanceNow() : 0;
-    a.synchronize();
     this.stats.submits += 1;
-    if (profile) profile.sink.submitToDoneMs = performanceNow() - t0;
-    const t1 = profile ? performanceNow() : 0;
-    const results = reads.map((r) => a.download(r.source.ptr + BigInt(r.sourceOffset), new TYPED[r.type](r.length)));
+    const t0 = profile ? performanceNow() : 0;
+    this.inflight.add(done);
+    let results, t1 = 0;
+    try {
+      await done;
+      if (profile) profile.sink.submitToDoneMs = performanceNow() - t0;
+      t1 = profile ? performanceNow() : 0;
+      results = reads.map((r, k) => new TYPED[r.type](targets[k].view.slice(0, r.length * 4).buffer));
+    } finally {
+      this.inflight.delete(done);
+      this.releaseStaging(targets);
+    }
     if (profile) {
       profile.sink.readbackMs = performanceNow() - t1;
       if (labels) {
@@ -251,6 +294,52 @@ export class ResidentQ8Device {
       }
     }
     return results;
+  }
+
+  /** Settles once every batch in flight has (their failures are theirs to report). */
+  async idle() {
+    while (this.inflight.size > 0) await Promise.allSettled([...this.inflight]);
+  }
+
+  /**
+   * Where each readback lands: { view, staging?, pooled? }, `view` a
+   * Uint8Array over page-locked memory.  Taken before anything is enqueued;
+   * released when the batch settles.
+   */
+  stagingTargets(reads) {
+    const targets = [];
+    try {
+      for (const r of reads) {
+        const bytes = r.length * 4;
+        const st = r.staging;
+        if (st !== undefined && st !== null && this.buffers.has(st) && st.kind === "staging") {
+          if (st.size < bytes) throw new RangeError(`readback staging buffer holds ${st.size} B, ${bytes} needed`);
+          if (st.busy) throw new Error("readback staging buffer is in use by a batch that has not finished (a pending map)");
+          st.busy = true;
+          targets.push({ view: st.host.subarray(0, bytes), staging: st });
+        } else {
+          const free = this.stagingPool.get(bytes);
+          const view = free && free.length ? free.pop() : new Uint8Array(this.addon.hostAlloc(bytes));
+          targets.push({ view, pooled: true });
+        }
+      }
+    } catch (err) {
+      this.releaseStaging(targets);
+      throw err;
+    }
+    return targets;
+  }
+
+  releaseStaging(targets) {
+    for (const t of targets) {
+      if (t.staging) {
+        t.staging.busy = false;
+      } else if (t.pooled) {
+        const list = this.stagingPool.get(t.view.byteLength) || [];
+        list.push(t.view);
+        this.stagingPool.set(t.view.byteLength, list);
+      }
+    }
   }
 
   /** Enqueues every call (coalesced runs as one launch), with events around labelled ones. */
@@ -269,6 +358,13 @@ export class ResidentQ8Device {
         timed.push({ label, events });
       }
     }
+  }
+
+  /** Whether replay(calls) would capture a new graph (calls that repeat the previous batch's but not the graph's). */
+  wouldCapture(calls, coalesce) {
+    const key = callKey(calls, coalesce);
+    const g = this.graph;
+    return (g === null || !sameKey(g.key, key)) && this.lastKey !== null && sameKey(this.lastKey, key);
   }
 
   /**
@@ -310,6 +406,7 @@ export class ResidentQ8Device {
 
   /** Frees every buffer and event this device created. */
   destroy() {
+    if (this.inflight.size > 0) this.addon.synchronize();  // nothing in flight reads what is freed below
     if (this.workspace !== null) {
       this.addon.free(this.workspace);
       this.workspace = null;

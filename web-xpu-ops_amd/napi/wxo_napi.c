@@ -32,6 +32,10 @@
  *   lastVariant() -> string (wxo_last_variant: the kernel instance of the last op)
  *   eventCreate() -> bigint, eventRecord(ev), eventElapsedMs(start, stop), eventDestroy(ev)
  *   graphBegin(), graphEnd() -> bigint, graphLaunch(graph), graphDestroy(graph)
+ *   hostAlloc(bytes) -> ArrayBuffer (page-locked: a MAP_READ staging buffer),
+ *   downloadAsync(ptr, typedArray) (enqueued, the host does not wait),
+ *   whenDone() -> Promise<void> (settles when everything enqueued before it
+ *   has run, waited for off the JS thread), spin(us)
  * Device functions are stream-ordered on the null stream (on the capture
  * stream while a capture is open); synchronize() (or any download) waits for
  * them.
@@ -228,7 +232,7 @@ static napi_value js_roofline(napi_env env, napi_callback_info info) {
  * batch is being captured (graphBegin .. graphEnd), when it is the addon's
  * capture stream.  graphBegin() starts recording; graphEnd() -> bigint closes
  * the capture and instantiates it (wxo_graph_capture_end); graphLaunch(g)
- * replays it on the capture stream; graphDestroy(g) frees it.  synchronize()
+ * replays it on the null stream; graphDestroy(g) frees it.  synchronize()
  * waits for every stream.  upload/download stay synchronous on the null
  * stream. */
 static wxo_stream_t g_stream = NULL;
@@ -263,6 +267,10 @@ static napi_value js_graph_end(napi_env env, napi_callback_info info) {
     return r;
 }
 
+/* The replay runs on the null stream, in order with every other op and
+ * readback the addon enqueues there (the capture itself needs a stream of its
+ * own; the graph does not), so callers need not synchronise between
+ * batches. */
 static napi_value js_graph_launch(napi_env env, napi_callback_info info) {
     size_t argc = 1;
     napi_value argv[1];
@@ -272,7 +280,7 @@ static napi_value js_graph_launch(napi_env env, napi_callback_info info) {
         napi_throw_error(env, "WXO_NAPI", "graphLaunch: a capture is open");
         return NULL;
     }
-    int st = wxo_graph_launch((wxo_graph_t)(uintptr_t)g, g_capture);
+    int st = wxo_graph_launch((wxo_graph_t)(uintptr_t)g, NULL);
     if (st != WXO_OK) return throw_status(env, st, "graphLaunch");
     return NULL;
 }
@@ -284,6 +292,138 @@ static napi_value js_graph_destroy(napi_env env, napi_callback_info info) {
     if (!get_args(env, info, 1, &argc, argv) || !get_ptr(env, argv[0], &g, "graph")) return NULL;
     int st = wxo_graph_destroy((wxo_graph_t)(uintptr_t)g);
     if (st != WXO_OK) return throw_status(env, st, "graphDestroy");
+    return NULL;
+}
+
+/* ---------------------------------------------------------------- asynchronous completion
+ * hostAlloc(bytes) -> ArrayBuffer over page-locked host memory (freed when the
+ * buffer is collected): what a WebGPU MAP_READ | COPY_DST staging buffer is
+ * (harness/resident.ts:41-48).  downloadAsync(ptr, typedArray) enqueues the
+ * copy of typedArray.byteLength bytes at ptr into it after the work already
+ * enqueued; the bytes are there once a later whenDone() has settled.
+ * whenDone() -> Promise<void>: records an event on the ops stream and waits
+ * for it on a libuv worker thread, so the JS thread keeps running meanwhile
+ * (the reference's queue.onSubmittedWorkDone() / mapAsync,
+ * harness/resident.ts:321-345).  It rejects with the library's error text if
+ * the wait fails.  spin(us): wxo_spin on the ops stream (a test aid that keeps
+ * the GPU busy for `us` microseconds). */
+
+static int typed_bytes(napi_env env, napi_value v, void** data, size_t* bytes);
+
+static void host_finalize(napi_env env, void* data, void* hint) {
+    (void)env;
+    (void)hint;
+    (void)wxo_host_free(data);
+}
+
+static napi_value js_host_alloc(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint32_t bytes;
+    if (!get_args(env, info, 1, &argc, argv) || !get_u32(env, argv[0], &bytes, "bytes")) return NULL;
+    void* p = NULL;
+    int st = wxo_host_malloc(&p, bytes > 0 ? bytes : 1);
+    if (st != WXO_OK) return throw_status(env, st, "hostAlloc");
+    napi_value ab;
+    if (napi_create_external_arraybuffer(env, p, bytes, host_finalize, NULL, &ab) != napi_ok) {
+        (void)wxo_host_free(p);
+        napi_throw_error(env, "WXO_NAPI", "hostAlloc: cannot wrap the page-locked buffer");
+        return NULL;
+    }
+    return ab;
+}
+
+static napi_value js_download_async(napi_env env, napi_callback_info info) {
+    size_t argc = 2;
+    napi_value argv[2];
+    uint64_t p;
+    void* data;
+    size_t bytes;
+    if (!get_args(env, info, 2, &argc, argv) || !get_ptr(env, argv[0], &p, "ptr") ||
+        !typed_bytes(env, argv[1], &data, &bytes))
+        return NULL;
+    if (g_stream != NULL) {
+        napi_throw_error(env, "WXO_NAPI", "downloadAsync: a capture is open");
+        return NULL;
+    }
+    int st = wxo_memcpy_dtoh_async(data, (const void*)(uintptr_t)p, bytes, NULL);
+    if (st != WXO_OK) return throw_status(env, st, "downloadAsync");
+    return NULL;
+}
+
+typedef struct {
+    napi_async_work work;
+    napi_deferred deferred;
+    wxo_event_t event;
+    int status;
+    char message[512];
+} DoneWait;
+
+static void done_execute(napi_env env, void* data) {
+    (void)env;
+    DoneWait* w = (DoneWait*)data;
+    w->status = wxo_event_synchronize(w->event);
+    if (w->status != WXO_OK) snprintf(w->message, sizeof w->message, "whenDone failed (wxo status %d): %s", w->status, wxo_last_error());
+}
+
+static void done_complete(napi_env env, napi_status status, void* data) {
+    DoneWait* w = (DoneWait*)data;
+    (void)wxo_event_destroy(w->event);
+    if (status == napi_ok && w->status == WXO_OK) {
+        napi_value undef;
+        napi_get_undefined(env, &undef);
+        napi_resolve_deferred(env, w->deferred, undef);
+    } else {
+        napi_value text, err, code;
+        napi_create_string_utf8(env, w->status != WXO_OK ? w->message : "whenDone: the wait was cancelled",
+                                NAPI_AUTO_LENGTH, &text);
+        napi_create_error(env, NULL, text, &err);
+        napi_create_int32(env, w->status, &code);
+        napi_set_named_property(env, err, "status", code);
+        napi_reject_deferred(env, w->deferred, err);
+    }
+    napi_delete_async_work(env, w->work);
+    free(w);
+}
+
+static napi_value js_when_done(napi_env env, napi_callback_info info) {
+    (void)info;
+    if (g_stream != NULL) {
+        napi_throw_error(env, "WXO_NAPI", "whenDone: a capture is open");
+        return NULL;
+    }
+    DoneWait* w = (DoneWait*)calloc(1, sizeof *w);
+    if (w == NULL) {
+        napi_throw_error(env, "WXO_NAPI", "whenDone: out of host memory");
+        return NULL;
+    }
+    int st = wxo_event_create(&w->event);
+    if (st == WXO_OK) st = wxo_event_record(w->event, NULL);
+    if (st != WXO_OK) {
+        (void)wxo_event_destroy(w->event);
+        free(w);
+        return throw_status(env, st, "whenDone");
+    }
+    napi_value promise, name;
+    napi_create_string_utf8(env, "wxo.whenDone", NAPI_AUTO_LENGTH, &name);
+    if (napi_create_promise(env, &w->deferred, &promise) != napi_ok ||
+        napi_create_async_work(env, NULL, name, done_execute, done_complete, w, &w->work) != napi_ok ||
+        napi_queue_async_work(env, w->work) != napi_ok) {
+        (void)wxo_event_destroy(w->event);
+        free(w);
+        napi_throw_error(env, "WXO_NAPI", "whenDone: cannot queue the wait");
+        return NULL;
+    }
+    return promise;
+}
+
+static napi_value js_spin(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint32_t us;
+    if (!get_args(env, info, 1, &argc, argv) || !get_u32(env, argv[0], &us, "us")) return NULL;
+    int st = wxo_spin(us, g_stream);
+    if (st != WXO_OK) return throw_status(env, st, "spin");
     return NULL;
 }
 
@@ -1136,6 +1276,10 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"free", NULL, js_free, NULL, NULL, NULL, napi_enumerable, NULL},
         {"upload", NULL, js_upload, NULL, NULL, NULL, napi_enumerable, NULL},
         {"download", NULL, js_download, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"downloadAsync", NULL, js_download_async, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"hostAlloc", NULL, js_host_alloc, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"whenDone", NULL, js_when_done, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"spin", NULL, js_spin, NULL, NULL, NULL, napi_enumerable, NULL},
         {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
         {"zero", NULL, js_zero, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},

@@ -18,6 +18,14 @@ export interface WxoAddon {
   free(ptr: bigint): void;
   upload(ptr: bigint, data: ArrayBufferView): void;
   download<T extends ArrayBufferView>(ptr: bigint, into: T): T;
+  /** Page-locked host memory (a MAP_READ staging buffer's storage). */
+  hostAlloc(bytes: number): ArrayBuffer;
+  /** Enqueues a device-to-host copy into `into` behind the work already enqueued; the host does not wait. */
+  downloadAsync(ptr: bigint, into: ArrayBufferView): void;
+  /** Settles when everything enqueued before the call has run; the wait runs off the JS thread. */
+  whenDone(): Promise<void>;
+  /** Keeps the GPU busy for `us` microseconds on the ops stream (a test aid). */
+  spin(us: number): void;
   copy(dst: bigint, src: bigint, bytes: number): void;
   matvecQ8Device(weight: bigint, scale: bigint, vector: bigint, output: bigint, N: number, K: number, M?: number): void;
   matvecQ8MultiDevice(projections: [bigint, bigint, bigint, number][], vector: bigint, K: number): void;

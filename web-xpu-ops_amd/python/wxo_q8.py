@@ -53,6 +53,9 @@ SIGNATURES = {
     "wxo_free": ([_P], _I),
     "wxo_memcpy_htod": ([_P, _P, _SZ, _P], _I),
     "wxo_memcpy_dtoh": ([_P, _P, _SZ, _P], _I),
+    "wxo_memcpy_dtoh_async": ([_P, _P, _SZ, _P], _I),
+    "wxo_host_malloc": ([ctypes.POINTER(_P), _SZ], _I),
+    "wxo_host_free": ([_P], _I),
     "wxo_memcpy_dtod": ([_P, _P, _SZ, _P], _I),
     "wxo_memset": ([_P, _I, _SZ, _P], _I),
     "wxo_synchronize": ([], _I),
