@@ -145,3 +145,40 @@ gpuTest(F, "wait: \"block\" waits on the JS thread (the promise is settled on re
   assertBitsEqual(out[1], out[0], "block vs async");
   assertBitsEqual(out[0], vec(n, 21), "values");
 });
+
+gpuTest(F, "a batch that waits to capture a graph holds back the batches called after it (call order kept)", async () => {
+  const N = 1024, K = 1024;
+  const r = rng(31);
+  const codes = Int8Array.from({ length: N * K }, () => Math.floor(r() * 256) - 128);
+  const scale = Float32Array.from({ length: N }, () => Math.fround(0.001 * (0.5 + r())));
+  const packed = packInt8Rows(codes, N, K);
+  const run = async (awaitEach) => {
+    const device = await createResidentQ8Device();
+    const w = storage(device, packed), s = storage(device, scale), x = storage(device, vec(K, 32));
+    const h = storage(device, vec(N, 33)), c = storage(device, vec(N, 34));
+    const twice = [
+      { kind: "matvecQ8Residual", weight: w, scale: s, vector: x, residual: h, output: h, N, K },
+      { kind: "matvecQ8Residual", weight: w, scale: s, vector: x, residual: h, output: h, N, K },
+    ];
+    const reset = [{ kind: "copy", src: c, srcOffset: 0, dst: h, dstOffset: 0, size: N * 4 }];
+    const rb = [{ source: h, sourceOffset: 0, length: N, type: "f32" }];
+    const lists = [twice, twice, reset, twice];  // the second captures a graph, the fourth replays it
+    let out;
+    if (awaitEach) {
+      out = [];
+      for (const l of lists) out.push(await device.batch(l, rb));
+    } else {
+      device.addon.spin(20000);
+      out = await Promise.all(lists.map((l) => device.batch(l, rb)));
+    }
+    const stats = { ...device.stats };
+    device.destroy();
+    return { out: out.map((o) => o[0]), stats };
+  };
+  const serial = await run(true);
+  const piped = await run(false);
+  assert.strictEqual(piped.stats.graphsCaptured, 1);
+  assert.strictEqual(piped.stats.graphLaunches, 2);
+  assertBitsEqual(serial.out[2], vec(N, 34), "the reset batch's readback");
+  for (let k = 0; k < 4; k += 1) assertBitsEqual(piped.out[k], serial.out[k], `batch ${k}`);
+});

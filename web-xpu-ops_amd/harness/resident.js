@@ -108,6 +108,7 @@ export class ResidentQ8Device {
     this.groupSet = new WeakSet();
     this.events = [];
     this.inflight = new Set();  // completion promises of batches still running
+    this.pendingIssue = null;   // settles when a batch waiting to issue has issued
     this.stagingPool = new Map();  // byte size -> free page-locked buffers for readbacks without staging
   }
 
@@ -246,12 +247,27 @@ export class ResidentQ8Device {
    * HIP events around its launch.
    */
   async batch(ops, readback = [], profile = undefined) {
-    const calls = ops.map((op, i) => this.resolve(op, i));
-    const reads = readback.map((r) => checkReadback(r, this.buffers));
+    // Batches issue in call order: while one waits for the batches in flight
+    // (below), the ones called after it wait for it to issue.
+    while (this.pendingIssue) await this.pendingIssue;
+    let calls = ops.map((op, i) => this.resolve(op, i));
+    let reads = readback.map((r) => checkReadback(r, this.buffers));
     const labels = profile && profile.labels ? profile.labels : null;
     const coalesce = this.coalesce && !labels;
     const graphed = this.graphs && !labels && calls.length > 1;
-    if ((labels || (graphed && this.wouldCapture(calls, coalesce))) && this.inflight.size > 0) await this.idle();
+    if ((labels || (graphed && this.wouldCapture(calls, coalesce))) && this.inflight.size > 0) {
+      let release;
+      this.pendingIssue = new Promise((r) => { release = r; });
+      try {
+        await this.idle();
+        // checked again: a buffer may have been destroyed meanwhile
+        calls = ops.map((op, i) => this.resolve(op, i));
+        reads = readback.map((r) => checkReadback(r, this.buffers));
+      } finally {
+        this.pendingIssue = null;
+        release();
+      }
+    }
     const targets = this.stagingTargets(reads);
     const a = this.addon;
     const timed = [];
