@@ -697,6 +697,30 @@ def run_prefill_suite(stream, steps, warmup, results, check):
                         "TFLOP/s": round(short_flops / (short_us * 1e-6) / 1e12, 1), "variants": variants})
         log(f"suite prefill layer, {Ts} tokens, coalesced: {short_us:.1f} us  "
             f"{short_flops / (short_us * 1e-6) / 1e12:.1f} TFLOP/s")
+    # A long prompt: the same four launches over 2048 tokens, where the
+    # 256-row tiles fill the CUs in whole rounds (or 5.5 of them for gate/up).
+    TL = 4 * T
+    a_hl = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(TL * 2048, dtype=np.float32), stream)
+    a_fl = wxo_q8.DeviceBuffer.from_array(rng.standard_normal(TL * 5632, dtype=np.float32), stream)
+    outs_l = {name: wxo_q8.DeviceBuffer(TL * N * 4) for name, N, _, _, _ in prepared}
+    long_us = 0.0
+    variants = []
+    for act, names in ((a_hl, ("wq", "wk", "wv")), (a_hl, ("wo",)), (a_hl, ("wGate", "wUp")), (a_fl, ("wDown",))):
+        K = by[names[0]][1]
+        projs = [(by[n][2].ptr, by[n][3].ptr, outs_l[n].ptr, by[n][0]) for n in names]
+        long_us += time_loop(stream, lambda i: wxo_q8.matmul_q8_multi_device(act, projs, TL, K, stream, ws, ws_bytes),
+                             max(1, steps // 40), max(1, warmup // 40))
+        variants.append(wxo_q8.last_variant())
+    long_flops = total_flops * TL / T
+    results.append({"case": f"prefill matmulQ8: one decoder layer, {TL} tokens, as the resident batch issues it "
+                            f"(4 launches)", "us": round(long_us, 3),
+                    "TFLOP/s": round(long_flops / (long_us * 1e-6) / 1e12, 1),
+                    "pct_of_bound": round(100 * 3.0 * long_flops / (PEAK_BF16_MFMA_TFLOPS * 1e12) * 1e6 / long_us, 1),
+                    "variants": variants})
+    log(f"suite prefill layer, {TL} tokens, coalesced: {long_us:.1f} us  {long_flops / (long_us * 1e-6) / 1e12:.1f} "
+        f"TFLOP/s")
+    for b in list(outs_l.values()) + [a_hl, a_fl]:
+        b.free()
     # The same four launches without a workspace (wxo_matmul_q8_multi: no K
     # split between workgroups), at every prompt length, beside the above.
     for Ts in (64, 128, 256, T):

@@ -598,7 +598,7 @@ def test_gather_bit_exact(rows, D):
     assert_bits_equal(got, oracle.gather_dequant_rows(codes, s, rows, D, idx), f"gather rows={rows} D={D}")
 
 
-@pytest.mark.parametrize("N,Ms,K", [(2048, [4096], 4100), (1024, [4224, 3968], 4096)])
+@pytest.mark.parametrize("N,Ms,K", [(2048, [2176, 1920], 4100), (1024, [4224, 3968], 4096)])
 def test_matmul_tile_pairs(N, Ms, K):
     """Long rows whose 128-row tiles make two whole rounds of two per CU: one
     workgroup of 16 waves per two tiles, one per K group (in the second case
@@ -628,31 +628,101 @@ def test_matmul_tile_pairs(N, Ms, K):
 
 def test_matmul_tile_pairs_ragged_tokens_match_one_group():
     """Tile pairs with a partial last token tile (N = 2040: 31 whole 64-token
-    tiles and one of 56): every 29th token against the oracle, nothing past
-    the output, and the bits of both halves of the tokens equal to runs of
-    those halves alone, whose 512 tiles take the one-group FB4 form (the same
-    sums in the same order; token tile boundaries line up at token 1024)."""
-    N, M, K = 2040, 4096, 4096
+    tiles and one of 56) over two projections (2176 and 1920 rows: 17 + 15
+    tiles of 128 rows, 1024 tiles in all, whose 256-row tiles would not make
+    whole rounds): every 29th token against the oracle, nothing past the
+    outputs, and the bits of both halves of the tokens equal to runs of those
+    halves alone, whose 512 tiles take the one-group FB4 form (the same sums
+    in the same order; token tile boundaries line up at token 1024)."""
+    N, K = 2040, 4096
+    Ms = [2176, 1920]
     rng = np.random.default_rng(2040)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    host, dev, outs = [], [], []
+    for M in Ms:
+        w = oracle.pack_q8(rng.integers(-128, 128, (M, K)).astype(np.int32).reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        o = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        o.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        dev.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s)))
+        outs.append(o)
+    wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, o, M) for (bw, bs), o, M in zip(dev, outs, Ms)], N, K)
+    wxo_q8.synchronize()
+    assert " FB4.pairs " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    got = []
+    for (w, s, M), o in zip(host, outs):
+        g = o.download(np.float32, N * M + 64)
+        assert np.all(g[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        assert_matmul(g[:N * M], a, w, s, N, M, K, rows=np.unique(np.r_[np.arange(0, N, 29), N - 1]))
+        got.append(g)
+    for t0, t1 in ((0, 1024), (1024, N)):
+        n = t1 - t0
+        bh = wxo_q8.DeviceBuffer.from_array(a[t0 * K:t1 * K])
+        ohs = [wxo_q8.DeviceBuffer(4 * n * M) for M in Ms]
+        wxo_q8.matmul_q8_multi_device(bh, [(bw, bs, oh, M) for (bw, bs), oh, M in zip(dev, ohs, Ms)], n, K)
+        wxo_q8.synchronize()
+        variant = wxo_q8.last_variant()
+        assert " FB4 " in variant and "pairs" not in variant, variant
+        for oh, g, M in zip(ohs, got, Ms):
+            assert_bits_equal(oh.download(np.float32, n * M), g[t0 * M:t1 * M], f"M={M} tokens {t0}..{t1}: pairs vs one group")
+
+
+def test_matmul_256_row_tiles_match_the_one_group_form():
+    """Launches whose 256-row tiles make whole rounds of the CUs take them (8
+    waves, 4 over the rows): 2048 tokens x 2048 x 2048 is 256 such tiles.  The
+    bits of its first 1536 tokens equal a launch of those tokens alone, whose
+    384 tiles of 128 rows take the one-group form; every 41st token against the
+    oracle."""
+    N, M, K = 2048, 2048, 2048
+    rng = np.random.default_rng(256)
     a = rng.standard_normal(N * K).astype(np.float32)
     w = oracle.pack_q8(rng.integers(-128, 128, (M, K)).astype(np.int32).reshape(-1), M, K)
     s = rng.uniform(0.001, 0.05, M).astype(np.float32)
     bw, bs = wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s)
-    ba = wxo_q8.DeviceBuffer.from_array(a)
-    out = wxo_q8.DeviceBuffer(4 * (N * M + 64))
-    out.upload(np.full(N * M + 64, 7.5, np.float32))
-    wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, out, M)], N, K)
+    out = wxo_q8.DeviceBuffer(4 * N * M)
+    wxo_q8.matmul_q8_multi_device(wxo_q8.DeviceBuffer.from_array(a), [(bw, bs, out, M)], N, K)
     wxo_q8.synchronize()
-    assert " FB4.pairs " in wxo_q8.last_variant(), wxo_q8.last_variant()
-    got = out.download(np.float32, N * M + 64)
-    assert np.all(got[N * M:] == np.float32(7.5)), "written past the output"
-    assert_matmul(got[:N * M], a, w, s, N, M, K, rows=np.unique(np.r_[np.arange(0, N, 29), N - 1]))
-    for t0, t1 in ((0, 1024), (1024, N)):
-        n = t1 - t0
-        bh = wxo_q8.DeviceBuffer.from_array(a[t0 * K:t1 * K])
-        oh = wxo_q8.DeviceBuffer(4 * n * M)
-        wxo_q8.matmul_q8_multi_device(bh, [(bw, bs, oh, M)], n, K)
-        wxo_q8.synchronize()
-        variant = wxo_q8.last_variant()
-        assert " FB4 " in variant and "pairs" not in variant, variant
-        assert_bits_equal(oh.download(np.float32, n * M), got[t0 * M:t1 * M], f"tokens {t0}..{t1}: pairs vs one group")
+    assert " FB8 " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    got = out.download(np.float32, N * M)
+    assert_matmul(got, a, w, s, N, M, K, rows=np.unique(np.r_[np.arange(0, N, 41), N - 1]))
+    n = 1536
+    half = wxo_q8.DeviceBuffer(4 * n * M)
+    wxo_q8.matmul_q8_multi_device(wxo_q8.DeviceBuffer.from_array(a[:n * K]), [(bw, bs, half, M)], n, K)
+    wxo_q8.synchronize()
+    variant = wxo_q8.last_variant()
+    assert " FB4 " in variant, variant
+    assert_bits_equal(got[:n * M], half.download(np.float32, n * M), "256-row tiles vs the one-group 128-row form")
+
+
+def test_matmul_256_row_tiles_ragged():
+    """256-row tiles with partial row tiles (two projections of 728 and 200
+    rows: 3 + 1 row tiles, 216 and 200 rows in the last), a partial last token
+    tile (4066 tokens) and a ragged K (2061): 64 token tiles x 4 row tiles =
+    256 tiles,
+    Inf and NaN among the activations; sentinels after the outputs untouched,
+    every 37th token against the oracle."""
+    N, K = 4066, 2061
+    Ms = [728, 200]
+    rng = np.random.default_rng(984)
+    a = rng.standard_normal(N * K).astype(np.float32)
+    a[5 * K + 7] = np.inf
+    a[9 * K + 100] = np.nan
+    ba = wxo_q8.DeviceBuffer.from_array(a)
+    host, bufs = [], []
+    for M in Ms:
+        w = oracle.pack_q8(rng.integers(-128, 128, (M, K)).astype(np.int32).reshape(-1), M, K)
+        s = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        o = wxo_q8.DeviceBuffer(4 * (N * M + 64))
+        o.upload(np.full(N * M + 64, 7.5, np.float32))
+        host.append((w, s, M))
+        bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), o, M))
+    wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
+    wxo_q8.synchronize()
+    assert " FB8 " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    rows = np.unique(np.r_[np.arange(0, N, 37), 5, 9, N - 1])
+    for (w, s, M), (_, _, o, _) in zip(host, bufs):
+        got = o.download(np.float32, N * M + 64)
+        assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
+        assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)

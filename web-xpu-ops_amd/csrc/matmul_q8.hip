@@ -57,7 +57,10 @@
 //
 // Long rows whose tiles make whole rounds of two per CU run one workgroup of
 // 16 waves per two tiles, each group of 8 waves on a tile of its own (the
-// PAIR instances); the sums are the one-group form's.
+// PAIR instances); the sums are the one-group form's.  Large launches whose
+// 256-row tiles fill the CUs in whole rounds run those tiles with 4 of the 8
+// waves over the rows (WR = 4), each wave on 64 rows x 32 tokens; again the
+// one-group form's sums.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -148,7 +151,7 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
 // workgroup, one whole tile per group, and the rest one per workgroup with
 // the K steps split between the groups.  The other instances run every tile
 // whole, with no branch on it.
-template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false, bool PAIR = false>
+template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false, bool PAIR = false, int WR = 2>
 __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a, MatmulProjections P,
                                                         uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
                                                         uint32_t ntiles) {
@@ -164,7 +167,9 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     constexpr int AL = (int)((ACH + NT - 1u) / NT);   // A loads per thread per step
     constexpr uint32_t FPT = kBK / NW;                // activations per thread per step
     constexpr int BL = (int)(FPT / 4u);               // B loads (dwordx4) per thread per step
-    constexpr int TB = (int)(4u / (NW / 2u));         // 16-token blocks per wave (2 or 1)
+    constexpr int TB = (int)(4u * WR / NW);            // 16-token blocks per wave (2 or 1)
+    constexpr int FW = (int)(BM / (16u * WR));         // 16-row blocks per wave
+    static_assert((WR == 2 && (NW == 4 || NW == 8)) || (WR == 4 && NW == 8), "2 or 4 waves over the rows");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(BK == 64 || BK == 128, "64- or 128-code steps");
     static_assert(PD == 2 || PD == 4, "2 or 4 register sets of loads in flight");
@@ -233,8 +238,8 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     const uint32_t t = KS == 1 ? threadIdx.x : threadIdx.x % NT;
     const uint32_t lane = t & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t wm = (wv & 1u) * (BM / 2u);            // wave's first weight row in the tile
-    const uint32_t wn = (wv >> 1) * (16u * (uint32_t)TB);  // wave's first token in the tile
+    const uint32_t wm = (wv % (uint32_t)WR) * (BM / (uint32_t)WR);  // wave's first weight row in the tile
+    const uint32_t wn = (wv / (uint32_t)WR) * (16u * (uint32_t)TB);  // wave's first token in the tile
     const uint32_t j = lane & 15u, g = lane >> 4;
 
     const uint32_t mrows = min(BM, M - m0);
@@ -359,9 +364,9 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
         store_b(st, hp, mp, lp);
     };
 
-    f32x4 acc[FB][TB], sum[FB][TB];
+    f32x4 acc[FW][TB], sum[FW][TB];
 #pragma unroll
-    for (int f = 0; f < FB; ++f)
+    for (int f = 0; f < FW; ++f)
 #pragma unroll
         for (int b = 0; b < TB; ++b) {
             acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -375,9 +380,9 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
 #pragma unroll
         for (int ss = 0; ss < BK / 32; ++ss) {
             const uint32_t piece = 4u * (uint32_t)ss + g;
-            bf16x8 af[FB], bf[TB][3];
+            bf16x8 af[FW], bf[TB][3];
 #pragma unroll
-            for (int f = 0; f < FB; ++f) {
+            for (int f = 0; f < FW; ++f) {
                 const uint32_t r = wm + 16u * (uint32_t)f + j;
                 af[f] = *reinterpret_cast<const bf16x8*>(as + r * kRowBytes + ((piece ^ (r & 7u)) * 16u));
             }
@@ -392,7 +397,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
 #pragma unroll
             for (int p = 0; p < 3; ++p)
 #pragma unroll
-                for (int f = 0; f < FB; ++f)
+                for (int f = 0; f < FW; ++f)
 #pragma unroll
                     for (int b = 0; b < TB; ++b)
                         acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[f], bf[b][p], acc[f][b], 0, 0, 0);
@@ -450,7 +455,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
         for (int q = 0; q < PD - 1; ++q)
             if (i + (uint32_t)q < gend) iter(q, i + (uint32_t)q);
 #pragma unroll
-        for (int f = 0; f < FB; ++f)
+        for (int f = 0; f < FW; ++f)
 #pragma unroll
             for (int b = 0; b < TB; ++b) {
                 sum[f][b] += acc[f][b];
@@ -462,14 +467,14 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
         // Group 1's sums through LDS (its stages are done) into group 0's;
         // a pair's groups each store their own tile (`pair` is
         // workgroup-uniform, and always false outside PAIR instances).
-        constexpr uint32_t E = (uint32_t)(FB * TB * 4);
+        constexpr uint32_t E = (uint32_t)(FW * TB * 4);
         static_assert(E * NT * 4u <= 2u * AST + 2u * BST, "the reduction fits in group 0's stages");
         if (!pair) {
             float* red = reinterpret_cast<float*>(lds);
             __syncthreads();
             if (kg == 1u) {
 #pragma unroll
-                for (int f = 0; f < FB; ++f)
+                for (int f = 0; f < FW; ++f)
 #pragma unroll
                     for (int b = 0; b < TB; ++b)
 #pragma unroll
@@ -478,7 +483,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
             __syncthreads();
             if (kg != 0u) return;  // after the last barrier
 #pragma unroll
-            for (int f = 0; f < FB; ++f)
+            for (int f = 0; f < FW; ++f)
 #pragma unroll
                 for (int b = 0; b < TB; ++b)
 #pragma unroll
@@ -494,7 +499,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     float* const blk = SPLIT && xs > 0u
         ? P.part + ((size_t)(xs - 1u) * P.splits + (tile - P.whole)) * (size_t)(BM * kBN) : nullptr;
 #pragma unroll
-    for (int f = 0; f < FB; ++f) {
+    for (int f = 0; f < FW; ++f) {
         const uint32_t fm = wm + 16u * (uint32_t)f + 4u * g;  // within the tile
         const u32x4v sv = split ? u32x4v{0x3f800000u, 0x3f800000u, 0x3f800000u, 0x3f800000u}  // 1.0f
                                 : __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
@@ -570,7 +575,7 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
 // their K steps split into `parts` runs, with the workspace `part` holding
 // (parts - 1) x splits blocks of BM x kBN floats, and a second launch sums
 // them.
-template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false, bool PAIR = false>
+template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false, bool PAIR = false, int WR = 2>
 hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
                      hipStream_t stream, float* part = nullptr, uint32_t splits = 0, uint32_t parts = 1) {
     constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
@@ -604,7 +609,7 @@ hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, 
         grid = 8u * ((splits / 2u + 7u) / 8u + (tiles - splits + 7u) / 8u);
     }
     const size_t lds = (size_t)KS * (2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes);
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT, PAIR>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT, PAIR, WR>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
                        P, N, K, W, mtiles, ntiles);
     if constexpr (SPLIT) {
         const hipError_t err = hipGetLastError();
@@ -671,14 +676,29 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
     // their tiles together.
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const uint64_t ntiles = (N + kBN - 1u) / kBN;
-    uint64_t t4 = 0, t2 = 0, t1 = 0;
+    uint64_t t8 = 0, t4 = 0, t2 = 0, t1 = 0;
     for (uint32_t i = 0; i < n; ++i) {
+        t8 += (uint64_t)((p[i].M + 255u) / 256u) * ntiles;
         t4 += (uint64_t)((p[i].M + 127u) / 128u) * ntiles;
         t2 += (uint64_t)((p[i].M + 63u) / 64u) * ntiles;
         t1 += (uint64_t)((p[i].M + 31u) / 32u) * ntiles;
     }
     const uint32_t steps = (uint32_t)(((uint64_t)K + 63u) / 64u);
     const char* kname = n > 1 ? "matmul_q8.multi" : "matmul_q8";
+    // 256-row tiles of 8 waves, 4 over the rows and 2 over the tokens (a wave
+    // holds 64 rows x 32 tokens: ~30 % fewer LDS bytes per matrix op than the
+    // 128-row tiles' 64 x 16), one workgroup per CU, when those tiles make
+    // whole rounds of the CUs or at least 2.75 of them.  The sums and their
+    // order are the one-group 128-row form's, so are the bits.  Same process,
+    // us, FB4 (or FB4.pairs) -> FB8: 1024 x 4096 x 4096 129 -> 113, 2048 x
+    // 2048 x 2048 64 -> 59, 2048 x 4096 x 4096 258 -> 232, 2048 x 4096 x
+    // 11008 670 -> 613, 4096 x 4096 x 4096 495 -> 458, 1024 x 11264 x 2048
+    // (2.75 rounds) 196 -> 185; with 1.1-1.5 rounds (288-384 tiles) they lose
+    // 10-15 %, with less than one round more.
+    if (t8 >= cus && (t8 % cus == 0 || 4u * t8 >= 11u * (uint64_t)cus)) {
+        set_variant(variant, kname, "FB8", 8, 256, 0, (int)kBN, (uint32_t)((t8 + 7u) / 8u * 8u));
+        return launch_fb<8, 8, 64, 2, 1, false, false, 4>(a, p, n, N, K, stream);
+    }
     if (t4 >= cus) {
         if (t4 == cus) {
             set_variant(variant, kname, "FB4.ksplit2", 16, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
