@@ -10,11 +10,14 @@
   * which kernel instance ran (wxo_last_variant), per thread.
   * rows far longer than the other suites' (K = 65539 and 131075) on every
     kernel family.
+  * the batched k-split kernel at its store wave's limit (1023 tiles of 16
+    rows per workgroup) and one row past it.
   * eight host threads on their own streams at once.
 
 Bars as everywhere: codes, packed words and scales bit-exact;
 matvecQ8 |y - y_ref| <= 1e-5 * sum_k |s q x| + 1e-7 per row.
 """
+import re
 import threading
 
 import numpy as np
@@ -238,9 +241,10 @@ def test_variant_names_the_instance_that_ran(cfg, M):
             assert int(kv["waves"]) == (W + 255) // 256  # one wave per 1 KiB chunk of a row
             assert form == ("xreg.masked" if tail else "xreg")
     else:
-        # cfg5 (K = 1024): the k-split kernel, 128 codes per wave, 16 vectors per tile
+        # cfg5 (K = 1024): the k-split kernel, 128 codes per wave, 16 vectors per
+        # tile, 8 streaming waves and the store wave
         assert head == "matvec_q8_ksplit" and form == "x16"
-        assert int(kv["vectors"]) == M and grid[1] == 1 and int(kv["slots"]) == 1 and int(kv["waves"]) == 8
+        assert int(kv["vectors"]) == M and grid[1] == 1 and int(kv["slots"]) == 1 and int(kv["waves"]) == 9
     # describe() carries the same variant
     assert f'last="{v}"' in wxo_q8.describe()
     # thread-local: another thread's calls do not change this thread's variant
@@ -467,6 +471,39 @@ def test_two_million_short_rows(M):
     packed, scales = wxo_q8.quantizePackQ8(input=x.reshape(-1), N=N, K=K)
     assert_bits_equal(packed, oracle.pack_q8(want_codes, N, K), "packed words")
     assert_bits_equal(scales, want_scales, "scales")
+
+
+@pytest.mark.parametrize("M", [5, 16])
+def test_ksplit_store_wave_limit(M):
+    """The batched k-split kernel's store wave (K <= 1024) keeps its
+    workgroup's scales in LDS, up to 1023 tiles of 16 rows per workgroup; one
+    more row runs the eight-wave form.  Rows are independent and both forms
+    add the same partials in the same order, so the shared rows are
+    bit-equal; rows at both ends and a random sample are checked against the
+    oracle.  The weight is one random 4096-row block repeated (3.4 GB)."""
+    cus = int(re.search(r" cus=(\d+)", wxo_q8.describe()).group(1))
+    K, W = 800, 200
+    N1 = 1023 * 16 * cus
+    N2 = N1 + 20
+    rng = np.random.default_rng(N1 + M)
+    w = np.tile(random_weights(rng, 4096, K, full_range=True).reshape(4096, W), ((N2 + 4095) // 4096, 1))[:N2]
+    w = np.ascontiguousarray(w).reshape(-1)
+    s = rng.uniform(1e-3, 1e-1, N2).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    y1 = wxo_q8.matvecQ8Batched(weight=w[: N1 * W], scale=s[:N1], vectors=xs.reshape(-1), N=N1, K=K, M=M)
+    v1 = wxo_q8.last_variant()
+    y2 = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs.reshape(-1), N=N2, K=K, M=M)
+    v2 = wxo_q8.last_variant()
+    print(v1, v2, flush=True)
+    assert parse_variant(v1)[0] == parse_variant(v2)[0] == "matvec_q8_ksplit"
+    assert int(parse_variant(v1)[2]["waves"]) == 9 and int(parse_variant(v2)[2]["waves"]) == 8
+    y1 = y1.reshape(M, N1)
+    y2 = y2.reshape(M, N2)
+    assert_bits_equal(y2[:, :N1], y1, "store-wave form against the eight-wave form")
+    rows = np.unique(np.concatenate([np.arange(64), np.arange(N1 - 64, N2), rng.integers(0, N2, 512)]))
+    ws = w.reshape(N2, W)[rows].reshape(-1)
+    for m in range(M):
+        assert_matvec(y2[m][rows], ws, s[rows], xs[m], len(rows), K)
 
 
 # ---------------------------------------------------------------- threads

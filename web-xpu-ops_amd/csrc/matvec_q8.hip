@@ -905,6 +905,16 @@ __global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
 // The partial sums of a tile are written after the next pair's matrix work is
 // issued, so the write does not hold the next pair's loads back.
 //
+// STW adds a ninth wave that only sums, scales and stores: after each
+// group's barrier it reads the group's partials and writes y, with the
+// workgroup's scales read into LDS once at the start.  Its y stores then
+// count on its own vmcnt, not on the streaming waves', whose stage waits
+// would otherwise also wait for every store issued before them (gfx9 counts
+// loads and stores together, in order).  Same sums in the same order.  Same
+// process at LM head N = 151936, K = 1024, us, eight waves -> nine: 16
+// vectors 36.2-37.7 -> 33.1-33.2, 8 vectors 30.8-33.0 -> 29.9-30.4, 5
+// vectors 29.7-30.6 -> 28.7-28.9, 4 vectors 28.7-29.6 -> 27.6-28.2.
+//
 // PACK sets how the x parts fill a B operand's 16 columns:
 //   1: 16 vectors, one part each: h, m, l in three operands (3 matrix ops per
 //      32-code block)
@@ -938,8 +948,8 @@ constexpr int ks_gcd(int a, int b) { return b == 0 ? a : ks_gcd(b, a % b); }
 template <int PACK>
 constexpr uint32_t ks_vectors() { return PACK == 1 ? 16u : PACK == 2 ? 8u : 5u; }
 
-template <int SW, int PACK>
-__global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
+template <int SW, int PACK, bool STW = false>
+__global__ __launch_bounds__(STW ? 576 : 512) void matvec_q8_ksplit_kernel(
     const uint32_t* __restrict__ weight, const float* __restrict__ scale, const float* __restrict__ x,
     float* __restrict__ y, uint32_t N, uint32_t K, uint32_t W, uint32_t M) {
     extern __shared__ __attribute__((aligned(16))) uint8_t ks_lds[];
@@ -972,6 +982,56 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
     // same barriers.
     const uint32_t total = ((ngroups * (uint32_t)GP + PER - 1) / PER) * PER;
 
+    if constexpr (STW) {
+        if (wv == kKsWaves) {
+            // The store wave: after each group's barrier it sums the group's
+            // tiles (their 8 partials in wave order), scales and stores them,
+            // while the streaming waves go on.  Its y stores count on its own
+            // vmcnt, so the streaming waves' stage waits never include a
+            // store.  The workgroup's scales come into LDS once, before the
+            // first barrier, so no global load sits between two barriers.
+            // It passes the same barriers as the streaming waves.
+            float* scl = reinterpret_cast<float*>(ks_lds + kKsWaves * (uint32_t)D * TBY + 2u * (uint32_t)G * kKsWaves * 1024u);
+            const uint32_t r0 = b0 * 16u, nr = min(b1 * 16u, N) - r0;
+            const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + r0, nr * 4u);
+            for (uint32_t o = 0; o < nr; o += 256u) {
+                const u32x4v v4 = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)((o + 4u * lane) * 4u), 0, 0);
+                if (o + 4u * lane < nr) *reinterpret_cast<u32x4v*>(scl + o + 4u * lane) = v4;
+            }
+            for (uint32_t grp = 0; grp < ngroups; ++grp) {
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // scales in LDS (first pass), partials read (later ones)
+                __builtin_amdgcn_s_barrier();
+#pragma unroll
+                for (int t = 0; t < G; ++t) {
+                    const uint32_t tile = b0 + grp * (uint32_t)G + (uint32_t)t;
+                    const float* rp = red + ((((grp & 1u) * G + (uint32_t)t) * kKsWaves) * 64u + lane) * 4u;
+                    f32x4 part[kKsWaves];
+#pragma unroll
+                    for (int w = 0; w < (int)kKsWaves; ++w)
+                        part[w] = *reinterpret_cast<const f32x4*>(rp + (uint32_t)w * 256u);
+                    const uint32_t rl = (tile - b0) * 16u + 4u * g;  // row within the workgroup's range
+                    const f32x4 sc = *reinterpret_cast<const f32x4*>(scl + (tile < b1 ? rl : 0u));
+                    f32x4 sum = part[0];
+#pragma unroll
+                    for (int w = 1; w < (int)kKsWaves; ++w) sum += part[w];
+                    if (tile < b1 && col_ok && sel == 0u) {
+                        const uint32_t row = tile * 16u + 4u * g;
+                        float* yo = y + (size_t)(m0 + vj) * N + row;
+                        if (row + 3u < N) {
+                            *reinterpret_cast<f32x4_a4*>(yo) = sum * sc;
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+                                if (row + (uint32_t)q < N) yo[q] = sum[q] * sc[q];
+                        }
+                    }
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            return;
+        }
+    }
+
     // DMA instruction ii of a pair: lane -> row 8 ii + lane / 8, stored at
     // position lane % 8, which holds piece (lane % 8) ^ (row % 8)
     int voff[2];
@@ -997,7 +1057,7 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 wrs, (__attribute__((address_space(3))) void*)(sb + (uint32_t)ii * 1024u), 16, voff[ii], (int)c0, 0,
                 kCachePolicyNT);
-        if (s == SW - 1u) {
+        if (!STW && s == SW - 1u) {
             const bool mine = b0 + ti < b1 && (ti & 7u) == wv;  // this wave sums and stores the tile
             const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + (size_t)(mine ? b0 + ti : 0u) * 16u,
                                                          mine ? min(16u, N - (b0 + ti) * 16u) * 4u : 0u);
@@ -1140,7 +1200,7 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
     // it (y stores issued in between only make the wait longer)
     auto after = [](int par) {
         int n = 0;
-        for (int r = 1; r < D; ++r) n += 2 + (((par + r) % SW) == SW - 1 ? 1 : 0);
+        for (int r = 1; r < D; ++r) n += 2 + (!STW && ((par + r) % SW) == SW - 1 ? 1 : 0);
         return n;
     };
     constexpr int kA0 = after(0), kA1 = SW > 1 ? after(1) : after(0);
@@ -1174,7 +1234,7 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
             __builtin_amdgcn_sched_barrier(0);
             if ((q % GP) != 0 && ((q - 1) % SW) == SW - 1) red_write((i + (uint32_t)q - 1u) / SW, pacc);
             finish(i + (uint32_t)q, q % SW, ((q + 1) % GP) != 0, sbuf[q % D]);
-            if (q % GP == 0 && pending != ~0u) {
+            if (!STW && q % GP == 0 && pending != ~0u) {
                 // the previous group's sums, behind this pair's matrix work
                 // (its partials sit in the half of the double buffer that the
                 // next barrier protects)
@@ -1192,7 +1252,7 @@ __global__ __launch_bounds__(512) void matvec_q8_ksplit_kernel(
             }
         }
     }
-    if (pending != ~0u) reduce(pending);
+    if (!STW && pending != ~0u) reduce(pending);
     __builtin_amdgcn_s_waitcnt(0);  // no fetch into LDS outlives the workgroup
 }
 
@@ -1380,18 +1440,21 @@ hipError_t launch_mv(const MatvecArgs& a, hipStream_t stream, Variant* variant) 
     return hipSuccess;
 }
 
-// One workgroup per CU (the LDS stages and partial sums take 128 KiB), each
+// One workgroup per CU (the LDS stages and partial sums take 96 KiB), each
 // with a contiguous range of 16-row tiles; vector groups of ks_vectors<PACK>()
-// on grid y.
-template <int SW, int PACK>
+// on grid y.  STW adds the store wave (K <= 1024 only: with two steps per
+// wave the x parts need more registers than nine waves per workgroup leave).
+template <int SW, int PACK, bool STW = false>
 hipError_t launch_ksplit(const MatvecArgs& a, const DeviceInfo& dev, hipStream_t stream, Variant* variant) {
     constexpr uint32_t VPB = ks_vectors<PACK>();
     const uint32_t ntiles = (a.N + 15u) / 16u;
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const dim3 grid(ntiles < cus ? ntiles : cus, (a.M + VPB - 1u) / VPB);
-    hipLaunchKernelGGL((matvec_q8_ksplit_kernel<SW, PACK>), grid, dim3(64 * kKsWaves), (size_t)kKsLdsBytes, stream,
+    const size_t lds = kKsLdsBytes + (STW ? (size_t)((ntiles + grid.x - 1u) / grid.x + 1u) * 16u * 4u : 0u);
+    hipLaunchKernelGGL((matvec_q8_ksplit_kernel<SW, PACK, STW>), grid, dim3(64 * (kKsWaves + (STW ? 1u : 0u))), lds,
+                       stream,
                        a.weight, a.scale, a.vector, a.output, a.N, a.K, a.W, a.M);
-    set_variant(variant, "matvec_q8_ksplit", PACK == 1 ? "x16" : PACK == 2 ? "x8" : "x5", (int)kKsWaves, 16, SW,
+    set_variant(variant, "matvec_q8_ksplit", PACK == 1 ? "x16" : PACK == 2 ? "x8" : "x5", (int)kKsWaves + (STW ? 1 : 0), 16, SW,
                 (int)(a.M < VPB ? a.M : VPB), grid.x, grid.y);
     return hipGetLastError();
 }
@@ -1469,6 +1532,16 @@ hipError_t launch_matvec_q8(const MatvecArgs& a, const DeviceInfo& dev, hipStrea
     if (a.K > 768u && a.K <= 2048u && (a.M + 15u) / 16u <= 65535u &&
         (a.N >= kMfmaMinRows ? (a.M >= 5u || (a.M == 4u && a.N >= 32768u)) : ksplit_small())) {
         if (a.K <= 1024u) {
+            // The store wave holds its workgroup's scales in LDS beside the
+            // 96 KiB of stages and partials: up to 1023 tiles per workgroup
+            // (4.19M rows on 256 CUs); past that, the eight-wave form.
+            const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+            const uint32_t ntiles = (a.N + 15u) / 16u, gx = ntiles < cus ? ntiles : cus;
+            if (kKsLdsBytes + (uint64_t)((ntiles + gx - 1u) / gx + 1u) * 64u <= kMfmaLdsBytes) {
+                if (a.M <= 5u) return launch_ksplit<1, 3, true>(a, dev, stream, variant);
+                if (a.M <= 8u) return launch_ksplit<1, 2, true>(a, dev, stream, variant);
+                return launch_ksplit<1, 1, true>(a, dev, stream, variant);
+            }
             if (a.M <= 5u) return launch_ksplit<1, 3>(a, dev, stream, variant);
             if (a.M <= 8u) return launch_ksplit<1, 2>(a, dev, stream, variant);
             return launch_ksplit<1, 1>(a, dev, stream, variant);
