@@ -8,7 +8,9 @@
 //   - the same with the 44 KB output read back each call;
 //   - the host convenience call matvecQ8({weight, scale, vector, N, K})
 //     (ops/matvec/reference.ts:117), which copies the 45 MB weight in over
-//     PCIe every call (the PCIe-inclusive rate);
+//     PCIe every call (the PCIe-inclusive rate), and the same call through
+//     runMatVecQ8 (llm/kernels.ts:195), which does it on a worker thread: the
+//     JS thread's share of one call, and calls awaited one by one;
 //   - one decode step of 22 layers shaped like BASELINE cfg4 (hidden 2048,
 //     FFN 5632) as the resident engine issues it (llm/engine-q8-resident.ts:
 //     1843-1869): per layer wq/wk/wv on one vector, matvecQ8Residual for wo,
@@ -18,6 +20,7 @@
 //   node bench_napi.mjs [calls]
 import { createResidentQ8Device } from "./web-xpu-ops_amd/harness/resident.js";
 import { matvecQ8 } from "./web-xpu-ops_amd/ops/matvec/index.js";
+import { runMatVecQ8 } from "./web-xpu-ops_amd/llm/kernels.js";
 
 const N = 11008, K = 4096, W = Math.ceil(K / 4), COPIES = 12;
 
@@ -92,6 +95,20 @@ async function main() {
   us = await timeLoop(hostCalls, () => matvecQ8({ weight: words, scale, vector, N, K }));
   results.push({ case: "N-API end to end: host convenience matvecQ8 (weight copied in over PCIe each call), N=11008 K=4096",
                  us: +us.toFixed(1), "GB/s (PCIe-inclusive)": +(bytes / us / 1e3).toFixed(2) });
+  us = await timeLoop(hostCalls, () => runMatVecQ8(null, { weight: words, scale, vector, M: N, K }));
+  results.push({ case: "N-API end to end: runMatVecQ8 (the same call on a worker thread), awaited one by one, N=11008 K=4096",
+                 us: +us.toFixed(1), "GB/s (PCIe-inclusive)": +(bytes / us / 1e3).toFixed(2) });
+  {
+    let held = 0;
+    for (let i = 0; i < hostCalls; i += 1) {
+      const t0 = nowUs();
+      const p = runMatVecQ8(null, { weight: words, scale, vector, M: N, K });
+      held += nowUs() - t0;
+      await p;
+    }
+    results.push({ case: "N-API end to end: runMatVecQ8, the JS thread's share of one call (until its promise returns), N=11008 K=4096",
+                   us: +(held / hostCalls).toFixed(1) });
+  }
 
   // One decode step, 22 layers of BASELINE cfg4's shapes.
   const L = 22, H = 2048, F = 5632;

@@ -34,14 +34,14 @@ test(F, "the addon loads and exports its whole surface", () => {
   for (const name of ["abiVersion", "describe", "deviceCount", "init", "synchronize", "matvecQ8", "matvecQ8Ffn",
     "matvecQ8Residual", "quantize", "packQ8", "packInt8Rows", "quantizePackQ8", "malloc", "free", "upload", "download",
     "copy", "matvecQ8Device", "matvecQ8FfnDevice", "matvecQ8ResidualDevice", "quantizeDevice", "packQ8Device",
-    "packInt8RowsDevice", "quantizePackQ8Device", "roofline"]) {
+    "packInt8RowsDevice", "quantizePackQ8Device", "roofline", "matvecQ8Async", "whenDone", "hostAlloc", "downloadAsync"]) {
     assert.strictEqual(typeof a[name], "function", name);
   }
   assert.strictEqual(a.abiVersion(), 1);
   assert.ok(describe().startsWith("wxo_q8 abi=1"));
 });
 
-test(F, "argument types and lengths are checked before the device is touched", () => {
+test(F, "argument types and lengths are checked before the device is touched", async () => {
   const w = new Uint32Array(2), s = new Float32Array(2), x = new Float32Array(4);
   assert.throws(() => matvec.matvecQ8({ weight: new Int32Array(2), scale: s, vector: x, N: 2, K: 4 }), TypeError);
   assert.throws(() => matvec.matvecQ8({ weight: w, scale: new Float64Array(2), vector: x, N: 2, K: 4 }), TypeError);
@@ -52,13 +52,18 @@ test(F, "argument types and lengths are checked before the device is touched", (
   assert.throws(() => quantizeOps.quantize({ input: new Float32Array(5), N: 2, D: 3 }), RangeError);
   assert.throws(() => matvec.packQ8({ codes: new Uint8Array(4), N: 1, K: 4 }), TypeError);
   assert.throws(() => packInt8Rows(new Int32Array(4), 1, 4), TypeError);
+  // the asynchronous form rejects with the same errors
+  await assert.rejects(runMatVecQ8(null, { weight: new Uint32Array(1), scale: s, vector: x, M: 2, K: 4 }), RangeError);
+  await assert.rejects(runMatVecQ8(null, { weight: w, scale: new Float64Array(2), vector: x, M: 2, K: 4 }), TypeError);
 });
 
-test(F, "without a gfx950 GPU every op fails loudly (no CPU fallback)", () => {
+test(F, "without a gfx950 GPU every op fails loudly (no CPU fallback)", async () => {
   if (native().deviceCount() > 0) return;  // covered by the GPU suite there
   assert.throws(() => matvec.matvecQ8({ weight: new Uint32Array(2), scale: new Float32Array(2), vector: new Float32Array(4), N: 2, K: 4 }),
     (e) => e.status === 2 && /no ROCm|no HIP device|no CPU fallback/.test(e.message));
   assert.throws(() => quantizeOps.quantize({ input: new Float32Array(4), N: 1, D: 4 }), (e) => e.status === 2);
+  await assert.rejects(runMatVecQ8(null, { weight: new Uint32Array(2), scale: new Float32Array(2), vector: new Float32Array(4), M: 2, K: 4 }),
+    (e) => e.status === 2 && /no ROCm|no HIP device|no CPU fallback/.test(e.message));
 });
 
 // ------------------------------------------------------------------ GPU

@@ -2,10 +2,15 @@
 // the JS thread (the reference's batch awaits queue.onSubmittedWorkDone and
 // mapAsync, harness/resident.ts:321-345), batches called while others are in
 // flight run after them in call order, and each reads back its own values
-// through page-locked staging memory.
+// through page-locked staging memory.  The non-resident runMatVecQ8
+// (llm/kernels.ts:195-211, over harness/wgsl.ts:35-36 Runner.run) likewise
+// returns at once and does its work on a worker thread.
 import { gpuTest, assert, assertBitsEqual } from "./harness.mjs";
 import { createResidentQ8Device, BufferUsage } from "../../web-xpu-ops_amd/harness/resident.js";
 import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
+import { runMatVecQ8 } from "../../web-xpu-ops_amd/llm/kernels.js";
+import * as matvec from "../../web-xpu-ops_amd/ops/matvec/index.js";
+import { native } from "../../web-xpu-ops_amd/native/index.js";
 
 const F = "async.test.mjs";
 
@@ -181,4 +186,35 @@ gpuTest(F, "a batch that waits to capture a graph holds back the batches called 
   assert.strictEqual(piped.stats.graphLaunches, 2);
   assertBitsEqual(serial.out[2], vec(N, 34), "the reset batch's readback");
   for (let k = 0; k < 4; k += 1) assertBitsEqual(piped.out[k], serial.out[k], `batch ${k}`);
+});
+
+gpuTest(F, "runMatVecQ8: returns before the work is done, the vector is taken at the call, the same bits as matvecQ8", async () => {
+  const N = 4096, K = 4096;  // the weight crosses PCIe inside the call
+  const r = rng(41);
+  const codes = Int8Array.from({ length: N * K }, () => Math.floor(r() * 255) - 127);
+  const weight = packInt8Rows(codes, N, K);
+  const scale = Float32Array.from({ length: N }, () => Math.fround(0.001 * (0.5 + r())));
+  const x = vec(K, 42);
+  const want = matvec.matvecQ8({ weight, scale, vector: x, N, K });
+  const vector = Float32Array.from(x);
+  const addon = native();
+  addon.init();
+  addon.spin(40000);  // 40 ms of GPU work ahead of the call's copies
+  const t0 = nowMs();
+  const pending = runMatVecQ8(null, { weight, scale, vector, M: N, K });
+  const issued = nowMs() - t0;
+  vector.fill(0);  // after the call: must not change its result
+  let ticks = 0;
+  const timer = setInterval(() => { ticks += 1; }, 2);
+  const got = await pending;
+  clearInterval(timer);
+  const total = nowMs() - t0;
+  assert.ok(issued < 20, `runMatVecQ8 took ${issued.toFixed(1)} ms to return its promise`);
+  assert.ok(total >= 30, `it settled after ${total.toFixed(1)} ms, before the 40 ms of work ahead of it`);
+  assert.ok(ticks >= 3, `the event loop ran ${ticks} timer ticks while the call waited`);
+  assertBitsEqual(got, want, "runMatVecQ8 against matvecQ8");
+  // several in flight at once, each with its own vector
+  const xs = [1, 2, 3, 4].map((k) => vec(K, 50 + k));
+  const outs = await Promise.all(xs.map((v) => runMatVecQ8(null, { weight, scale, vector: v, M: N, K })));
+  xs.forEach((v, k) => assertBitsEqual(outs[k], matvec.matvecQ8({ weight, scale, vector: v, N, K }), `call ${k} in flight`));
 });

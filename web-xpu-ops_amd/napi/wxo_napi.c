@@ -12,6 +12,9 @@
  * and lengths before touching the device, and return fresh typed arrays:
  *   matvecQ8(weight: Uint32Array, scale: Float32Array, vector: Float32Array,
  *            N, K, M = 1) -> Float32Array [M*N]
+ *   matvecQ8Async(weight, scale, vector, N, K, M = 1) -> Promise<Float32Array [M*N]>
+ *            (the same call on a libuv worker thread; scale and vector are
+ *            copied when it is made, the weight is read while it is pending)
  *   quantize(input: Float32Array, N, D) -> { output: Int32Array, scales: Float32Array }
  *   packQ8(codes: Int32Array, N, K) -> Uint32Array
  *   packInt8Rows(codes: Int8Array, N, K) -> Uint32Array
@@ -518,6 +521,130 @@ static napi_value js_matvec_q8(napi_env env, napi_callback_info info) {
     int st = wxo_matvec_q8_host(w, s, x, y, N, K, M);
     if (st != WXO_OK) return throw_status(env, st, "matvecQ8");
     return out;
+}
+
+/* matvecQ8Async(weight u32, scale f32, vector f32, N, K, M = 1) -> Promise<Float32Array[M*N]>
+ *
+ * The reference's non-resident dispatch returns a promise and waits for the
+ * GPU without holding the JS thread (harness/wgsl.ts:35-36 Runner.run, used by
+ * llm/kernels.ts:195-211 runMatVecQ8).  Here the whole host call (device
+ * buffers, the copies in, the kernel, the copy out) runs on a libuv worker
+ * thread.  Arguments are checked on the calling thread (a bad one throws
+ * there).  As WebGPU's queue.writeBuffer does, the call takes its inputs when
+ * it is made: scale and vector are copied then (they are small and an engine
+ * reuses its activation buffers); the weight, megabytes of static model data,
+ * is held by reference and read on the worker, so it must not change while
+ * the promise is pending.  The result array is handed over only on success;
+ * a failed call rejects with the library's error text and `status`. */
+typedef struct {
+    napi_async_work work;
+    napi_deferred deferred;
+    napi_ref weight_ref, out_ref;
+    const void* weight;
+    float *scale, *vector;
+    void* out;
+    uint32_t N, K, M;
+    int status;
+    char message[512];
+} HostMatvec;
+
+static void host_matvec_execute(napi_env env, void* data) {
+    (void)env;
+    HostMatvec* h = (HostMatvec*)data;
+    h->status = wxo_matvec_q8_host((const uint32_t*)h->weight, h->scale, h->vector, (float*)h->out, h->N, h->K, h->M);
+    if (h->status != WXO_OK)
+        snprintf(h->message, sizeof h->message, "matvecQ8Async failed (wxo status %d): %s", h->status, wxo_last_error());
+}
+
+static void host_matvec_free(napi_env env, HostMatvec* h) {
+    if (h->weight_ref != NULL) napi_delete_reference(env, h->weight_ref);
+    if (h->out_ref != NULL) napi_delete_reference(env, h->out_ref);
+    free(h->scale);
+    free(h->vector);
+    free(h);
+}
+
+static void host_matvec_complete(napi_env env, napi_status status, void* data) {
+    HostMatvec* h = (HostMatvec*)data;
+    napi_value out;
+    if (status == napi_ok && h->status == WXO_OK && napi_get_reference_value(env, h->out_ref, &out) == napi_ok) {
+        napi_resolve_deferred(env, h->deferred, out);
+    } else {
+        napi_value text, err, code;
+        napi_create_string_utf8(env, h->status != WXO_OK ? h->message : "matvecQ8Async: the call was cancelled",
+                                NAPI_AUTO_LENGTH, &text);
+        napi_create_error(env, NULL, text, &err);
+        napi_create_int32(env, h->status != WXO_OK ? h->status : WXO_ERR_DEVICE, &code);
+        napi_set_named_property(env, err, "status", code);
+        napi_reject_deferred(env, h->deferred, err);
+    }
+    napi_delete_async_work(env, h->work);
+    host_matvec_free(env, h);
+}
+
+static napi_value js_matvec_q8_async(napi_env env, napi_callback_info info) {
+    size_t argc = 6;
+    napi_value argv[6];
+    if (!get_args(env, info, 5, &argc, argv)) return NULL;
+    void *w, *s, *x;
+    size_t lw, ls, lx;
+    uint32_t N, K, M = 1;
+    if (!get_typed(env, argv[0], napi_uint32_array, &w, &lw, "weight") ||
+        !get_typed(env, argv[1], napi_float32_array, &s, &ls, "scale") ||
+        !get_typed(env, argv[2], napi_float32_array, &x, &lx, "vector") || !get_u32(env, argv[3], &N, "N") ||
+        !get_u32(env, argv[4], &K, "K"))
+        return NULL;
+    if (argc > 5) {
+        napi_valuetype t;
+        napi_typeof(env, argv[5], &t);
+        if (t != napi_undefined && !get_u32(env, argv[5], &M, "M")) return NULL;
+    }
+    if (M == 0) {
+        range_error(env, "M must be >= 1");
+        return NULL;
+    }
+    if (!need_len(env, lw, (uint64_t)N * words_per_row(K), "weight") || !need_len(env, ls, N, "scale") ||
+        !need_len(env, lx, (uint64_t)M * K, "vector"))
+        return NULL;
+    HostMatvec* h = (HostMatvec*)calloc(1, sizeof *h);
+    if (h == NULL) {
+        napi_throw_error(env, "WXO_NAPI", "matvecQ8Async: out of host memory");
+        return NULL;
+    }
+    h->weight = w;
+    h->N = N;
+    h->K = K;
+    h->M = M;
+    const size_t sb = (size_t)N * 4, xb = (size_t)M * K * 4;
+    h->scale = (float*)malloc(sb > 0 ? sb : 1);
+    h->vector = (float*)malloc(xb > 0 ? xb : 1);
+    napi_value out = NULL, promise, name;
+    if (h->scale != NULL && h->vector != NULL) out = new_typed(env, napi_float32_array, 4, (size_t)M * N, &h->out);
+    if (out == NULL) {
+        host_matvec_free(env, h);
+        bool pending = false;
+        napi_is_exception_pending(env, &pending);
+        if (!pending) napi_throw_error(env, "WXO_NAPI", "matvecQ8Async: out of host memory");
+        return NULL;
+    }
+    if (sb > 0) memcpy(h->scale, s, sb);
+    if (xb > 0) memcpy(h->vector, x, xb);
+    napi_create_string_utf8(env, "wxo.matvecQ8Async", NAPI_AUTO_LENGTH, &name);
+    if (napi_create_reference(env, argv[0], 1, &h->weight_ref) != napi_ok ||
+        napi_create_reference(env, out, 1, &h->out_ref) != napi_ok ||
+        napi_create_promise(env, &h->deferred, &promise) != napi_ok ||
+        napi_create_async_work(env, NULL, name, host_matvec_execute, host_matvec_complete, h, &h->work) != napi_ok) {
+        host_matvec_free(env, h);
+        napi_throw_error(env, "WXO_NAPI", "matvecQ8Async: cannot queue the call");
+        return NULL;
+    }
+    if (napi_queue_async_work(env, h->work) != napi_ok) {
+        napi_delete_async_work(env, h->work);
+        host_matvec_free(env, h);
+        napi_throw_error(env, "WXO_NAPI", "matvecQ8Async: cannot queue the call");
+        return NULL;
+    }
+    return promise;
 }
 
 /* matvecQ8Residual(weight u32, scale f32, vector f32, residual f32, N, K) -> Float32Array[N] */
@@ -1266,6 +1393,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
         {"roofline", NULL, js_roofline, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8", NULL, js_matvec_q8, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecQ8Async", NULL, js_matvec_q8_async, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Residual", NULL, js_matvec_q8_residual, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Ffn", NULL, js_matvec_q8_ffn, NULL, NULL, NULL, napi_enumerable, NULL},
         {"quantize", NULL, js_quantize, NULL, NULL, NULL, napi_enumerable, NULL},

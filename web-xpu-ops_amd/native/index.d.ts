@@ -8,6 +8,8 @@ export interface WxoAddon {
   /** Best sustained HBM read bytes/s and one-wide f32 FMA flop/s of this device, measured now. */
   roofline(): { bandwidth: number; compute: number };
   matvecQ8(weight: Uint32Array, scale: Float32Array, vector: Float32Array, N: number, K: number, M?: number): Float32Array;
+  /** The same call on a libuv worker thread: scale and vector are copied when it is made; the weight is read while the promise is pending. */
+  matvecQ8Async(weight: Uint32Array, scale: Float32Array, vector: Float32Array, N: number, K: number, M?: number): Promise<Float32Array>;
   matvecQ8Residual(weight: Uint32Array, scale: Float32Array, vector: Float32Array, residual: Float32Array, N: number, K: number): Float32Array;
   matvecQ8Ffn(weightGate: Uint32Array, scaleGate: Float32Array, weightUp: Uint32Array, scaleUp: Float32Array, vector: Float32Array, N: number, K: number): Float32Array;
   quantize(input: Float32Array, N: number, D: number): { output: Int32Array; scales: Float32Array };
