@@ -335,7 +335,7 @@ def run_case(stream, spec, steps, warmup):
     return measure_matvec(stream, f"{name} matvecQ8 M={M}", c["N"], c["K"], M, c["w"], c["x"], steps, warmup)
 
 
-def run_suite(stream, steps, warmup):
+def run_suite(stream, steps, warmup, napi=True):
     """Every BASELINE configuration on one GPU: us/step, algorithmic GB/s and
     the fraction of the bound that applies (HBM, or the compute rate of the
     path that runs when that is lower: one-wide FP32 FMA for one vector, bf16
@@ -544,7 +544,8 @@ def run_suite(stream, steps, warmup):
         del c5
 
     run_prefill_suite(stream, steps, warmup, results, check)
-    results.extend(napi_end_to_end())
+    if napi:
+        results.extend(napi_end_to_end())
     results.extend(cpu_reference_ops(budget_s=1.0))
     return results
 
@@ -788,6 +789,9 @@ def main() -> int:
     ap.add_argument("--case", metavar="CFG[:M]", default=None,
                     help="measure one BASELINE configuration alone (e.g. cfg5:16) and print its line (diagnostics, "
                          "profiling)")
+    ap.add_argument("--no-napi", action="store_true",
+                    help="leave the Node-API end-to-end rows out of --suite (kernel traces: the tracer would follow "
+                         "the node child too)")
     ap.add_argument("--calibrate-copy", type=int, default=0,
                     help="after timing, run this many device copies of the packed weight (counter calibration)")
     args = ap.parse_args()
@@ -881,7 +885,7 @@ def main() -> int:
         baseline = cpu_baseline(packed_host, scales_host, c["x"], N, K, args.cpu_budget)
 
     if args.suite:
-        table = run_suite(stream, args.steps, args.warmup)
+        table = run_suite(stream, args.steps, args.warmup, napi=not args.no_napi)
         add_calibrated(table, cal)
         with open(args.suite, "w") as f:
             json.dump(table, f, indent=1)
