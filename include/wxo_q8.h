@@ -157,6 +157,17 @@ int wxo_event_elapsed_ms(float* ms, wxo_event_t start, wxo_event_t stop);
  * behind it are all queued by the time the GPU reaches them, so events around
  * them time back-to-back execution rather than the host's issue rate. */
 int wxo_spin(uint32_t us, wxo_stream_t stream);
+/* Holds `stream` until wxo_gate_release(*gate) or until `max_us` microseconds
+ * of the GPU's 100 MHz clock have passed (max_us <= 1,000,000, else
+ * WXO_ERR_INVALID), whichever comes first: a one-wave kernel polls a flag in
+ * page-locked, coherent host memory.  A measurement aid with no counterpart in
+ * the reference, whose timestamps sit inside one submit
+ * (harness/resident.ts:75-96): work enqueued behind a held gate runs back to
+ * back once it opens, so events around that work time the GPU, not the host's
+ * issue rate.  Gates are numbered in order; releasing one also opens every
+ * gate held before it. */
+int wxo_gate_hold(uint32_t max_us, wxo_stream_t stream, uint32_t* gate);
+int wxo_gate_release(uint32_t gate);
 /* This device's own ceilings, measured now; replaces measureRoofline
  * (harness/roofline.ts:162-198, the same method).  *bandwidth: the best
  * sustained read rate from HBM in bytes/s -- two 512 MiB buffers filled with

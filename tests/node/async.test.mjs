@@ -218,3 +218,29 @@ gpuTest(F, "runMatVecQ8: returns before the work is done, the vector is taken at
   const outs = await Promise.all(xs.map((v) => runMatVecQ8(null, { weight, scale, vector: v, M: N, K })));
   xs.forEach((v, k) => assertBitsEqual(outs[k], matvec.matvecQ8({ weight, scale, vector: v, N, K }), `call ${k} in flight`));
 });
+
+gpuTest(F, "BatchProfile times (harness/timing.test.ts:56-120): positive, more for more work, inside the batch's wall time", async () => {
+  // A labelled batch is held on the GPU until all of it is enqueued, so a
+  // short op's interval is its GPU time, not the host's issue time.
+  const device = await createResidentQ8Device();
+  const K = 4096, W = K / 4;
+  const mk = (N) => ({ weight: device.createStorageBuffer(N * W * 4), scale: device.createStorageBuffer(N * 4),
+    output: device.createStorageBuffer(N * 4), N });
+  const small = mk(2048), big = mk(65536);  // 8 MB and 268 MB of weights
+  const x = device.createStorageBuffer(K * 4);
+  const op = (p) => ({ kind: "matvecQ8", weight: p.weight, scale: p.scale, vector: x, output: p.output, N: p.N, K });
+  for (let rep = 0; rep < 3; rep += 1) {
+    const sink = { submitToDoneMs: null, readbackMs: null, gpuEntries: [] };
+    const t0 = nowMs();
+    await device.batch([op(small), op(big)], [], { labels: ["small", "big"], sink });
+    const wallMs = nowMs() - t0;
+    const [s, b] = sink.gpuEntries;
+    assert.deepStrictEqual(sink.gpuEntries.map((e) => e.label), ["small", "big"]);
+    assert.ok(s.seconds > 0 && b.seconds > 0, `positive: ${s.seconds} ${b.seconds}`);
+    assert.ok(b.seconds > 4 * s.seconds, `32x the bytes: ${b.seconds} s against ${s.seconds} s`);
+    assert.ok((s.seconds + b.seconds) * 1e3 < wallMs, `GPU ${(s.seconds + b.seconds) * 1e3} ms within the wall ${wallMs} ms`);
+    // a physically possible rate (harness/roofline.test.ts's < 20 TB/s)
+    assert.ok(65536 * W * 4 / b.seconds < 20e12, `big: ${65536 * W * 4 / b.seconds / 1e12} TB/s`);
+  }
+  device.destroy();
+});

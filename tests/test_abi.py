@@ -71,6 +71,10 @@ def test_validation_happens_before_device_access():
     # the measurement spin refuses more than a second before touching a device
     assert L.wxo_spin(1000001, None) == wxo_q8.WXO_ERR_INVALID
     assert "spin longer than 1 s" in L.wxo_last_error().decode()
+    g = ctypes.c_uint32(0)
+    assert L.wxo_gate_hold(1000001, None, ctypes.byref(g)) == wxo_q8.WXO_ERR_INVALID
+    assert "gate held longer than 1 s" in L.wxo_last_error().decode()
+    assert L.wxo_gate_release(0) == wxo_q8.WXO_ERR_INVALID
     # the calibrated ceiling needs at least one output
     assert L.wxo_roofline(None, None) == wxo_q8.WXO_ERR_INVALID
     assert "roofline" in L.wxo_last_error().decode()

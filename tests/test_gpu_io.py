@@ -116,6 +116,61 @@ def test_async_read_into_page_locked_memory():
         dev.free()
 
 
+def test_gate_holds_the_stream_until_released():
+    """wxo_gate_hold: work enqueued behind a held gate waits for the host's
+    release (the host sleeps 30 ms before it); releasing a later gate opens
+    an earlier one too; a gate nobody releases opens by itself after its time
+    limit, and gates still work afterwards."""
+    import time
+    wxo_q8.init()
+    L = wxo_q8.lib()
+    n = 4096
+    buf = wxo_q8.DeviceBuffer.from_array(np.arange(n, dtype=np.uint32))
+    stream = wxo_q8.Stream()
+    ev = [wxo_q8.Event(timer=True) for _ in range(3)]
+    g1, g2 = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    try:
+        ev[0].record(stream)
+        assert L.wxo_gate_hold(500000, stream.handle, ctypes.byref(g1)) == 0
+        assert L.wxo_memset(buf.ptr, 0x11, n * 4, stream.handle) == 0
+        assert L.wxo_gate_hold(500000, stream.handle, ctypes.byref(g2)) == 0
+        assert g2.value == g1.value + 1
+        assert L.wxo_memset(buf.ptr, 0x22, n * 4, stream.handle) == 0
+        ev[1].record(stream)
+        time.sleep(0.03)
+        assert L.wxo_gate_release(g2.value) == 0  # opens g1 as well
+        ev[1].synchronize()
+        held = ev[0].elapsed_ms(ev[1])
+        assert 25.0 < held < 400.0, f"the stream ran {held:.1f} ms after it was held"
+        assert np.all(buf.download(np.uint32, n) == 0x22222222)
+        assert L.wxo_gate_release(g1.value) == 0  # a late release of an opened gate is harmless
+        # nobody releases: the gate opens after its 5 ms
+        ev[0].record(stream)
+        assert L.wxo_gate_hold(5000, stream.handle, ctypes.byref(g1)) == 0
+        ev[2].record(stream)
+        ev[2].synchronize()
+        alone = ev[0].elapsed_ms(ev[2])
+        assert 4.0 < alone < 200.0, f"an unreleased 5 ms gate held the stream {alone:.2f} ms"
+        # and later gates still hold and release
+        ev[0].record(stream)
+        assert L.wxo_gate_hold(500000, stream.handle, ctypes.byref(g2)) == 0
+        ev[1].record(stream)
+        time.sleep(0.01)
+        assert L.wxo_gate_release(g2.value) == 0
+        ev[1].synchronize()
+        assert 8.0 < ev[0].elapsed_ms(ev[1]) < 400.0
+        # numbers never handed out are refused
+        assert L.wxo_gate_release(0) == wxo_q8.WXO_ERR_INVALID
+        assert L.wxo_gate_release(g2.value + 1) == wxo_q8.WXO_ERR_INVALID
+        assert L.wxo_gate_hold(1000, stream.handle, None) == wxo_q8.WXO_ERR_INVALID
+    finally:
+        wxo_q8.synchronize()
+        for e in ev:
+            e.destroy()
+        stream.destroy()
+        buf.free()
+
+
 @pytest.mark.parametrize("offset", [0, 1, 3, 16, 17])
 @pytest.mark.parametrize("length", [0, 1, 15, 16, 17, 1000, 65536 + 5])
 def test_memset_any_offset_and_length(offset, length):

@@ -448,6 +448,27 @@ __global__ __launch_bounds__(64) void spin_kernel(uint64_t ticks) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
 }
+
+// Waits until the host has released gate `gen` (the flag has reached it; the
+// difference taken as signed, so the count may wrap) or `ticks` of the 100 MHz
+// counter have passed.  The flag lives in coherent page-locked host memory and
+// is read with system-scope loads (they bypass the GPU's caches), so each poll
+// sees the host's latest store.  Relaxed: nothing after the wait depends on
+// the flag's ordering (stream order carries the work behind the gate), and an
+// acquire would invalidate the caches on every poll.
+__global__ __launch_bounds__(64) void gate_kernel(const uint32_t* flag, uint32_t gen, uint64_t ticks) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while ((int32_t)(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) - gen) < 0 &&
+           __builtin_amdgcn_s_memrealtime() - t0 < ticks)
+        __builtin_amdgcn_s_sleep(2);
+}
+
+// One flag per process: hold hands out the next number, release raises the
+// flag to it (never lowers it).
+std::mutex g_gate_mu;
+uint32_t* g_gate_host = nullptr;   // the flag, as the host writes it
+uint32_t* g_gate_dev = nullptr;    // the same flag, as kernels read it
+uint32_t g_gate_next = 0;
 }  // namespace
 
 int wxo_graph_capture_begin(wxo_stream_t stream) {
@@ -495,6 +516,45 @@ int wxo_spin(uint32_t us, wxo_stream_t stream) {
     hipLaunchKernelGGL(spin_kernel, dim3(1), dim3(64), 0, as_hip(stream), (uint64_t)us * 100u);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? ok() : hip_fail(e, "spin launch");
+}
+
+int wxo_gate_hold(uint32_t max_us, wxo_stream_t stream, uint32_t* gate) {
+    if (!gate) return fail(WXO_ERR_INVALID, "gate is NULL");
+    if (max_us > 1000000u) return fail(WXO_ERR_INVALID, "gate held longer than 1 s");
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    std::lock_guard<std::mutex> lock(g_gate_mu);
+    if (!g_gate_host) {
+        void* h = nullptr;
+        hipError_t e = hipHostMalloc(&h, 64, hipHostMallocCoherent | hipHostMallocMapped | hipHostMallocPortable);
+        if (e != hipSuccess) return hip_fail(e, "hipHostMalloc (gate flag)");
+        void* dp = nullptr;
+        e = hipHostGetDevicePointer(&dp, h, 0);
+        if (e != hipSuccess) {
+            (void)hipHostFree(h);
+            return hip_fail(e, "hipHostGetDevicePointer (gate flag)");
+        }
+        g_gate_host = static_cast<uint32_t*>(h);
+        g_gate_dev = static_cast<uint32_t*>(dp);
+        __atomic_store_n(g_gate_host, 0u, __ATOMIC_RELEASE);
+    }
+    const uint32_t gen = g_gate_next + 1u;
+    hipLaunchKernelGGL(gate_kernel, dim3(1), dim3(64), 0, as_hip(stream), (const uint32_t*)g_gate_dev, gen,
+                       (uint64_t)max_us * 100u);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "gate launch");
+    g_gate_next = gen;
+    *gate = gen;
+    return ok();
+}
+
+int wxo_gate_release(uint32_t gate) {
+    std::lock_guard<std::mutex> lock(g_gate_mu);
+    if (!g_gate_host || (int32_t)(gate - g_gate_next) > 0 || gate == 0u)
+        return fail(WXO_ERR_INVALID, "gate %u was never held", gate);
+    const uint32_t cur = __atomic_load_n(g_gate_host, __ATOMIC_ACQUIRE);
+    if ((int32_t)(gate - cur) > 0) __atomic_store_n(g_gate_host, gate, __ATOMIC_RELEASE);
+    return ok();
 }
 
 int wxo_roofline(double* bandwidth, double* compute) {

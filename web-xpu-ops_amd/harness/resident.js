@@ -70,6 +70,9 @@ import { recognise, UnsupportedPipelineError, params } from "./wgsl-interface.js
 export { UnsupportedPipelineError, params };
 
 const TYPED = { f32: Float32Array, i32: Int32Array, u32: Uint32Array };
+// How long a profiled batch's gate may hold the GPU if the host has not
+// enqueued the batch by then (it opens at once when the host has).
+const GATE_MAX_US = 200000;
 
 /** WebGPU's GPUBufferUsage bit values (the spec's), for callers without a WebGPU global. */
 export const BufferUsage = Object.freeze({
@@ -244,7 +247,9 @@ export class ResidentQ8Device {
    * sink.submitToDoneMs (enqueue end to completion, the device-to-host copies
    * included), sink.readbackMs (the copies out of staging), and with labels
    * sink.gpuEntries [{ label, seconds }] for each labelled non-copy op, from
-   * HIP events around its launch.
+   * HIP events around its launch.  A labelled batch is held on the GPU until
+   * it is all enqueued (wxo_gate_hold), so those intervals are the ops' GPU
+   * time back to back, not the host's issue rate.
    */
   async batch(ops, readback = [], profile = undefined) {
     // Batches issue in call order: while one waits for the batches in flight
@@ -275,7 +280,15 @@ export class ResidentQ8Device {
     const timed = [];
     let done;
     try {
-      if (!(graphed && this.replay(calls, coalesce, key))) this.enqueue(calls, coalesce, labels, timed);
+      // A labelled batch runs behind a gate that opens once all of it is
+      // enqueued, so its ops run back to back and each op's interval is GPU
+      // time, as timestamps inside one submit are (not the host's issue rate).
+      const gate = labels ? a.gateHold(GATE_MAX_US) : 0;
+      try {
+        if (!(graphed && this.replay(calls, coalesce, key))) this.enqueue(calls, coalesce, labels, timed);
+      } finally {
+        if (labels) a.gateRelease(gate);
+      }
       reads.forEach((r, k) => a.downloadAsync(r.source.ptr + BigInt(r.sourceOffset), targets[k].view));
       if (this.wait === "block") {
         a.synchronize();

@@ -38,7 +38,9 @@
  *   hostAlloc(bytes) -> ArrayBuffer (page-locked: a MAP_READ staging buffer),
  *   downloadAsync(ptr, typedArray) (enqueued, the host does not wait),
  *   whenDone() -> Promise<void> (settles when everything enqueued before it
- *   has run, waited for off the JS thread), spin(us)
+ *   has run, waited for off the JS thread), spin(us),
+ *   gateHold(maxUs) -> number, gateRelease(number) (the stream held until the
+ *   host has enqueued what follows: a profiled batch's timings)
  * Device functions are stream-ordered on the null stream (on the capture
  * stream while a capture is open); synchronize() (or any download) waits for
  * them.
@@ -427,6 +429,34 @@ static napi_value js_spin(napi_env env, napi_callback_info info) {
     if (!get_args(env, info, 1, &argc, argv) || !get_u32(env, argv[0], &us, "us")) return NULL;
     int st = wxo_spin(us, g_stream);
     if (st != WXO_OK) return throw_status(env, st, "spin");
+    return NULL;
+}
+
+/* gateHold(maxUs) -> number: holds the ops stream until gateRelease(number)
+ * or maxUs of GPU time (wxo_gate_hold); gateRelease(number). */
+static napi_value js_gate_hold(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint32_t us, gate = 0;
+    if (!get_args(env, info, 1, &argc, argv) || !get_u32(env, argv[0], &us, "maxUs")) return NULL;
+    if (g_stream != NULL) {
+        napi_throw_error(env, "WXO_NAPI", "gateHold: a capture is open");
+        return NULL;
+    }
+    int st = wxo_gate_hold(us, NULL, &gate);
+    if (st != WXO_OK) return throw_status(env, st, "gateHold");
+    napi_value r;
+    napi_create_uint32(env, gate, &r);
+    return r;
+}
+
+static napi_value js_gate_release(napi_env env, napi_callback_info info) {
+    size_t argc = 1;
+    napi_value argv[1];
+    uint32_t gate;
+    if (!get_args(env, info, 1, &argc, argv) || !get_u32(env, argv[0], &gate, "gate")) return NULL;
+    int st = wxo_gate_release(gate);
+    if (st != WXO_OK) return throw_status(env, st, "gateRelease");
     return NULL;
 }
 
@@ -1408,6 +1438,8 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"hostAlloc", NULL, js_host_alloc, NULL, NULL, NULL, napi_enumerable, NULL},
         {"whenDone", NULL, js_when_done, NULL, NULL, NULL, napi_enumerable, NULL},
         {"spin", NULL, js_spin, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"gateHold", NULL, js_gate_hold, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"gateRelease", NULL, js_gate_release, NULL, NULL, NULL, napi_enumerable, NULL},
         {"copy", NULL, js_copy, NULL, NULL, NULL, napi_enumerable, NULL},
         {"zero", NULL, js_zero, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Device", NULL, js_matvec_q8_device, NULL, NULL, NULL, napi_enumerable, NULL},

@@ -28,6 +28,10 @@ export interface WxoAddon {
   whenDone(): Promise<void>;
   /** Keeps the GPU busy for `us` microseconds on the ops stream (a test aid). */
   spin(us: number): void;
+  /** Holds the ops stream until gateRelease(gate) or `maxUs` of GPU time (<= 1e6), whichever comes first. */
+  gateHold(maxUs: number): number;
+  /** Opens `gate` and every gate held before it. */
+  gateRelease(gate: number): void;
   copy(dst: bigint, src: bigint, bytes: number): void;
   matvecQ8Device(weight: bigint, scale: bigint, vector: bigint, output: bigint, N: number, K: number, M?: number): void;
   matvecQ8MultiDevice(projections: [bigint, bigint, bigint, number][], vector: bigint, K: number): void;

@@ -65,6 +65,8 @@ SIGNATURES = {
     "wxo_event_create": ([ctypes.POINTER(_P)], _I),
     "wxo_event_create_timer": ([ctypes.POINTER(_P)], _I),
     "wxo_spin": ([ctypes.c_uint32, _P], _I),
+    "wxo_gate_hold": ([ctypes.c_uint32, _P, ctypes.POINTER(ctypes.c_uint32)], _I),
+    "wxo_gate_release": ([ctypes.c_uint32], _I),
     "wxo_roofline": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], _I),
     "wxo_matmul_q8_multi": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
     "wxo_matmul_q8_multi_ws": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _SZ, _P], _I),
