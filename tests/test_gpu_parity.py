@@ -312,6 +312,8 @@ def test_batched_same_sign_long_k(M, K):
     (8191, 1900, 24, "matvec_q8_ksplit"), (2048, 2048, 32, "matvec_q8_ksplit"), (2047, 1500, 32, "matvec_q8_ksplit"),
     (8192, 1024, 5, "matvec_q8_ksplit"), (5632, 1000, 8, "matvec_q8_ksplit"), (4096, 1024, 16, "matvec_q8_ksplit"),
     (4100, 800, 12, "matvec_q8_ksplit"),
+    # fewer tiles than CUs (one per workgroup, its barrier group half empty), ragged rows
+    (1000, 900, 32, "matvec_q8_ksplit"), (33, 1024, 48, "matvec_q8_ksplit"), (17, 1000, 35, "matvec_q8_ksplit"),
     (4096, 2048, 16, "matvec_q8_mv"), (11008, 2048, 4, "matvec_q8_mv"), (2048, 2048, 16, "matvec_q8_mv"),
     (4096, 2048, 32, "matvec_q8_mv"), (4096, 1024, 24, "matvec_q8_mv"), (5632, 768, 16, "matvec_q8_mv"),
 ])
