@@ -923,13 +923,15 @@ __global__ __launch_bounds__(64 * NWV) void matvec_q8_mfma_dma_kernel(
 //   3: up to 5 vectors: h | m | l in one operand (1 op)
 // A column's parts are summed as h + (m + l), the order PACK 1 uses too.
 //
-// Measured on MI355X (same-process, rotating weight copies), against the
-// matrix-core kernels above: LM head N = 151936, K = 1024: 16 vectors
-// 38-39 us (45-47), 8 vectors 34-35 (41), 5 vectors 32-33 (41); K = 2048:
-// 16 vectors 71 us (240); N = 32768, K = 2048, 16 vectors 18.5-20 us (58).
-// Of the 16-vector time at K = 1024: the weight stream alone (loads, no
-// matrix work) 29.8 us; the shader clock runs at 1.8-2.1 GHz while the
-// matrix cores work against 2.3-2.4 GHz for the loads alone.
+// Measured on MI355X (rotating weight copies), against the matrix-core
+// kernels above: LM head N = 151936, K = 1024: 16 vectors 33-34 us (45-47),
+// 8 vectors 30-31 (41), 5 vectors 29-30 (41); N = 32768, K = 2048, 16
+// vectors 17.7-18 us (58).  Of the 16-vector time at K = 1024: a
+// workgroup's weight stream alone (loads, no matrix work) takes 25.5 us; the
+// shader clock runs at 1.8-2.1 GHz while the matrix cores work against
+// 2.3-2.4 GHz for the loads alone, and leaving out the codes' conversion and
+// a third of the matrix ops (timing bounds) saves only 2-3 us.  Deeper
+// stages (5-7) or four tiles per barrier measured no faster.
 constexpr int kKsGroup = 2;   // tiles per barrier
 constexpr int kKsStages = 4;  // LDS stages per wave (3 pairs in flight)
 constexpr uint32_t kKsWaves = 8;
