@@ -244,3 +244,28 @@ gpuTest(F, "BatchProfile times (harness/timing.test.ts:56-120): positive, more f
   }
   device.destroy();
 });
+
+gpuTest(F, "matvecQ8Async with several vectors equals the synchronous call; the gate is refused inside a capture", async () => {
+  const addon = native();
+  addon.init();
+  const N = 3000, K = 1500, M = 6;
+  const r = rng(61);
+  const codes = Int8Array.from({ length: N * K }, () => Math.floor(r() * 256) - 128);
+  const weight = packInt8Rows(codes, N, K);
+  const scale = Float32Array.from({ length: N }, () => Math.fround(0.001 * (0.5 + r())));
+  const xs = vec(M * K, 62);
+  const want = addon.matvecQ8(weight, scale, xs, N, K, M);
+  const got = await addon.matvecQ8Async(weight, scale, xs, N, K, M);
+  assertBitsEqual(got, want, "M = 6");
+  assert.throws(() => addon.matvecQ8Async(weight, scale, xs.subarray(1), N, K, M), RangeError);  // checked at the call
+  addon.graphBegin();
+  try {
+    addon.spin(1);  // something to capture
+    assert.throws(() => addon.gateHold(1000), /capture is open/);
+  } finally {
+    addon.graphDestroy(addon.graphEnd());
+  }
+  const g = addon.gateHold(100000);
+  addon.gateRelease(g);
+  addon.synchronize();
+});
