@@ -12,6 +12,7 @@
     kernel family.
   * the batched k-split kernel at its store wave's limit (1023 tiles of 16
     rows per workgroup) and one row past it.
+  * a weight past 4 GiB (64-bit row addressing), one and five vectors.
   * eight host threads on their own streams at once.
 
 Bars as everywhere: codes, packed words and scales bit-exact;
@@ -504,6 +505,33 @@ def test_ksplit_store_wave_limit(M):
     ws = w.reshape(N2, W)[rows].reshape(-1)
     for m in range(M):
         assert_matvec(y2[m][rows], ws, s[rows], xs[m], len(rows), K)
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_weight_past_4_gib(M):
+    """A 4.6 GB weight (4.5M rows of K = 1024): every kernel addresses its
+    block of rows from a 64-bit base, so rows past the first 4 GiB read
+    their own words.  The last rows' outputs are bit-equal to a call on those
+    rows alone; rows at both ends and a random sample are checked against the
+    oracle.  The weight is one random 4096-row block repeated."""
+    K, W = 1024, 256
+    N = 4_500_000
+    rng = np.random.default_rng(4500 + M)
+    w = np.tile(random_weights(rng, 4096, K, full_range=True).reshape(4096, W), ((N + 4095) // 4096, 1))[:N]
+    w = np.ascontiguousarray(w).reshape(-1)
+    s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    xs = rng.standard_normal((M, K)).astype(np.float32)
+    y = wxo_q8.matvecQ8Batched(weight=w, scale=s, vectors=xs.reshape(-1), N=N, K=K, M=M).reshape(M, N)
+    print(wxo_q8.last_variant(), flush=True)
+    tail = 100
+    yt = wxo_q8.matvecQ8Batched(weight=w[(N - tail) * W:], scale=s[N - tail:], vectors=xs.reshape(-1), N=tail, K=K,
+                                M=M).reshape(M, tail)
+    if M == 1:  # the same kernel on both calls: the same bits
+        assert_bits_equal(y[:, N - tail:], yt, "rows past 4 GiB against a call on them alone")
+    rows = np.unique(np.concatenate([np.arange(64), np.arange(N - tail, N), rng.integers(0, N, 512)]))
+    ws = w.reshape(N, W)[rows].reshape(-1)
+    for m in range(M):
+        assert_matvec(y[m][rows], ws, s[rows], xs[m], len(rows), K)
 
 
 # ---------------------------------------------------------------- threads
