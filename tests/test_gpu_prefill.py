@@ -726,3 +726,22 @@ def test_matmul_256_row_tiles_ragged():
         got = o.download(np.float32, N * M + 64)
         assert np.all(got[N * M:] == np.float32(7.5)), f"M={M}: written past the output"
         assert_matmul(got[:N * M], a, w, s, N, M, K, rows=rows)
+
+
+def test_matmul_weight_past_4_gib():
+    """64 tokens against a 4.6 GB packed weight (4.5M rows of K = 1024):
+    the tiles address their weight rows and output columns from 64-bit bases,
+    so columns past the first 4 GiB of weight are their own rows' sums.
+    Sampled weight rows (output columns) at both ends and at random against
+    the oracle; the weight is one random 4096-row block repeated."""
+    T, M, K, W = 64, 4_500_000, 1024, 256
+    rng = np.random.default_rng(64)
+    block = rng.integers(0, 2 ** 32, 4096 * W, dtype=np.uint64).astype(np.uint32).reshape(4096, W)
+    w = np.ascontiguousarray(np.tile(block, ((M + 4095) // 4096, 1))[:M]).reshape(-1)
+    s = rng.uniform(1e-3, 1e-1, M).astype(np.float32)
+    a = rng.standard_normal((T, K)).astype(np.float32)
+    y = np.asarray(wxo_q8.matmulQ8(a=a, weight=w, scale=s, N=T, M=M, K=K)).reshape(T, M)
+    print(wxo_q8.last_variant(), flush=True)
+    cols = np.unique(np.concatenate([np.arange(64), np.arange(M - 100, M), rng.integers(0, M, 256)]))
+    wsub = w.reshape(M, W)[cols].reshape(-1)
+    assert_matmul(np.ascontiguousarray(y[:, cols]), a, wsub, s[cols], T, len(cols), K)
