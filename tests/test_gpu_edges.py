@@ -12,7 +12,8 @@
     kernel family.
   * the batched k-split kernel at its store wave's limit (1023 tiles of 16
     rows per workgroup) and one row past it.
-  * a weight past 4 GiB (64-bit row addressing), one and five vectors.
+  * a weight past 4 GiB (64-bit row addressing), one and five vectors;
+    packInt8Rows and quantize+pack with inputs and outputs past 4 GiB.
   * eight host threads on their own streams at once.
 
 Bars as everywhere: codes, packed words and scales bit-exact;
@@ -532,6 +533,35 @@ def test_weight_past_4_gib(M):
     ws = w.reshape(N, W)[rows].reshape(-1)
     for m in range(M):
         assert_matvec(y[m][rows], ws, s[rows], xs[m], len(rows), K)
+
+
+def test_pack_and_quantize_past_4_gib():
+    """packInt8Rows with 4.5 GB of codes in and out (1.1M rows of K = 4099:
+    the streaming kernel's 64-bit output offsets, rows ending mid-word), and
+    quantize+pack of a 4.5 GB f32 matrix (1.1M rows of K = 1024).  Rows at
+    both ends and a random sample checked bit for bit against the oracle; the
+    inputs are one random 4096-row block repeated."""
+    rng = np.random.default_rng(1100)
+    N, K = 1_100_000, 4099
+    W = (K + 3) // 4
+    block = rng.integers(-128, 128, (4096, K)).astype(np.int8)
+    codes = np.ascontiguousarray(np.tile(block, ((N + 4095) // 4096, 1))[:N]).reshape(-1)
+    assert N * W * 4 > 1 << 32
+    packed = wxo_q8.packInt8Rows(codes, N, K).reshape(N, W)
+    rows = np.unique(np.concatenate([np.arange(32), np.arange(N - 64, N), rng.integers(0, N, 256)]))
+    sub = codes.reshape(N, K)[rows].reshape(-1)
+    assert_bits_equal(packed[rows].reshape(-1), oracle.pack_int8_rows(sub, len(rows), K), "packInt8Rows past 4 GiB")
+    del codes, packed
+    N, K = 1_100_000, 1024
+    fblock = (rng.standard_normal((4096, K)) * 0.02).astype(np.float32)
+    x = np.ascontiguousarray(np.tile(fblock, ((N + 4095) // 4096, 1))[:N]).reshape(-1)
+    assert N * K * 4 > 1 << 32
+    pk, sc = wxo_q8.quantizePackQ8(input=x, N=N, K=K)
+    rows = np.unique(np.concatenate([np.arange(32), np.arange(N - 64, N), rng.integers(0, N, 256)]))
+    want_codes, want_scales = oracle.quantize(x.reshape(N, K)[rows], len(rows), K)
+    assert_bits_equal(pk.reshape(N, K // 4)[rows].reshape(-1), oracle.pack_q8(want_codes, len(rows), K),
+                      "quantize+pack past 4 GiB")
+    assert_bits_equal(sc[rows], want_scales, "scales past 4 GiB")
 
 
 # ---------------------------------------------------------------- threads
