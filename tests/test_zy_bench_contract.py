@@ -76,7 +76,11 @@ def test_short_and_long_runs_agree():
     the timed region (one launch index runs from the set-up through the
     timed calls).  Each bench process places its buffers anew, which moves a
     run by up to about 1 %, so short and long runs alternate, seven of each,
-    and their medians must agree within 1 %."""
+    and their medians must agree within 2 %.  A cache re-read of weight copies
+    would show as more than that; what remains is the box: sustained 17 ms
+    streams ran 0.5 % slower than 0.17 ms bursts on one MI355X and 1.5 % on
+    another (medians 8.69 against 8.56 us), so a 1 % bar fails by the box.
+    The rotation itself is pinned exactly on the CPU (test_bench_rotation)."""
     runs = {20: [], 2000: []}
     for _ in range(7):
         for steps, warmup in ((20, 5), (2000, 200)):
@@ -86,4 +90,4 @@ def test_short_and_long_runs_agree():
             runs[steps].append(json.loads(p.stdout.strip().splitlines()[-1])["ms_per_step"])
             print(f"  ms_per_step {runs[steps][-1]}", flush=True)
     res = {k: sorted(v)[3] for k, v in runs.items()}
-    assert abs(res[20] - res[2000]) <= 0.01 * res[2000], runs
+    assert abs(res[20] - res[2000]) <= 0.02 * res[2000], runs

@@ -44,8 +44,13 @@
 // features of one token: one 16-byte store into out[token, :].
 //
 // Workgroups are numbered so that the 8 XCDs (which take workgroups
-// round-robin) each hold a contiguous run of tiles that share activation
-// tiles in that XCD's L2.
+// round-robin) each hold a contiguous run of the tile sequence, and the
+// sequence walks groups of 4 weight-row tiles, each group through all its
+// token tiles (tile_coords).  So an XCD's L2 holds about an eighth of the
+// weight, reused by every token tile, and its resident workgroups share 4
+// weight tiles and a few activation tiles.  A token-major sequence (each XCD
+// one token tile and every weight row) streamed the whole weight through
+// every XCD's L2: 512-token layer 215 -> 182 us, 2048 tokens 629 -> 570.
 //
 // With a caller's workspace, a launch may also split some tiles' K steps
 // between 2 or 4 workgroups (a short prompt's tiles, which would leave most
@@ -97,6 +102,23 @@ struct MatmulProjections {
 };
 
 
+
+// Tile `tile` of the launch's sequence -> weight-row tile mt, token tile nt.
+// The sequence takes kTileGroup row tiles at a time (fewer in the last
+// group) and walks all token tiles of the group, its row tiles innermost:
+// consecutive workgroups share activation tiles, and a group's weight tiles
+// stay in one XCD's L2 while all token tiles use them.  Same-process sweep of
+// the group size (1, 2, 4, 8, 16, all): 512-token layer 182 / 181 / 182 / 187
+// / 199 / 215 us, 2048 tokens 574 / 573 / 570 / 572 / 581 / 629.
+constexpr uint32_t kTileGroup = 4;
+__device__ __forceinline__ void tile_coords(uint32_t tile, uint32_t mtiles, uint32_t ntiles, uint32_t& mt,
+                                            uint32_t& nt) {
+    const uint32_t gi = tile / (kTileGroup * ntiles), first = gi * kTileGroup;
+    const uint32_t gs = min(kTileGroup, mtiles - first);
+    const uint32_t r = tile - gi * (kTileGroup * ntiles);
+    nt = r / gs;
+    mt = first + (r - nt * gs);
+}
 
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
     // upper halves of two f32 bit patterns, a in the low half
@@ -179,7 +201,7 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     // XCD-aware tile order: workgroup i runs on XCD i % 8; give each XCD a
-    // contiguous run of the (token-major) tile sequence.  A split launch
+    // contiguous run of the tile sequence (tile_coords).  A split launch
     // gives each XCD a run of the whole tiles first and then a run of the
     // split tiles' parts, so every XCD holds its share of both and the whole
     // tiles are dispatched first.  Workgroups past the end return whole (no
@@ -222,7 +244,8 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
             np = (uint32_t)KS * P.parts;
         }
     }
-    const uint32_t nt = tile / mtiles, mt = tile - nt * mtiles;
+    uint32_t mt, nt;
+    tile_coords(tile, mtiles, ntiles, mt, nt);
     // the projection that owns weight-row tile mt (wave-uniform)
     const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
     const uint32_t* __restrict__ weight = P.weight[pj];
@@ -533,7 +556,8 @@ __global__ __launch_bounds__(256) void split_sum_kernel(MatmulProjections P, uin
     constexpr uint32_t G = BM / 4u;  // 4-row groups per token
     static_assert(kBN * G == 256u * (BM / 16u), "one group per thread");
     const uint32_t st = blockIdx.x, tile = P.whole + st;
-    const uint32_t nt = tile / mtiles, mt = tile - nt * mtiles;
+    uint32_t mt, nt;
+    tile_coords(tile, mtiles, (N + kBN - 1u) / kBN, mt, nt);
     const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
     const uint32_t M = P.M[pj];
     const uint32_t m0 = (mt - P.mt0[pj]) * BM, n0 = nt * kBN;
@@ -723,8 +747,9 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
             return launch_fb<4, 8, 64, 2, 1, true>(a, p, n, N, K, stream, workspace, (uint32_t)S, 2u);
         }
         // Long rows whose tiles make two or more whole rounds of two per CU:
-        // one workgroup of 16 waves per two tiles, one per K group, both of
-        // one token tile.  Same process, one-group -> pairs (us): 1024 tiles
+        // one workgroup of 16 waves per two consecutive tiles of the sequence,
+        // one per K group.  Same process, one-group -> pairs (us, measured
+        // with a token-major tile sequence): 1024 tiles
         // at K = 4096 240-245 -> 226-232, at K = 11008 645-647 -> 607-612 and
         // 334-338 -> 300-302, at K = 5632 299-317 -> 290-323; one round (512
         // tiles) even, and 5.5 rounds (2816 tiles, K = 4096) 658 -> 686-690,
