@@ -335,20 +335,25 @@ def test_matmul_workspace_split(N, Ms, K, form):
 
 
 BALANCE_CASES = [
-    # (N, Ms, K): between cus and 2 x cus 128-row tiles
-    (512, [2048, 2048, 2048], 2048),  # a 512-token prompt's q, k, v: 384 tiles, 128 of them split
-    (256, [5632, 5632], 2048),        # a 256-token prompt's gate, up: 352 tiles, 160 split
-    (700, [2048, 1500], 1030),        # ragged tokens, rows and K: 308 tiles, 204 split
+    # (N, Ms, K, form with a workspace, form without): between cus and 2 x cus
+    # 128-row tiles
+    (512, [2048, 2048, 2048], 2048, "D256.PD2", "D256.PD2"),  # 512-token q, k, v: 192 256-row tiles
+    (256, [5632, 5632], 2048, "D256.PD2", "D256.PD2"),        # 256-token gate, up: 176 256-row tiles
+    (500, [3000, 2800], 1030, "D256.PD2", "D256.PD2"),        # ragged tokens, rows and K: 184 256-row tiles
+    (700, [2048, 1500], 1030, "FB4.balance2", "D128"),        # 154 256-row tiles: 308 128-row tiles, 204 split
 ]
 
 
-@pytest.mark.parametrize("N,Ms,K", BALANCE_CASES)
-def test_matmul_workspace_balance(N, Ms, K):
+@pytest.mark.parametrize("N,Ms,K,form_ws,form_plain", BALANCE_CASES)
+def test_matmul_workspace_balance(N, Ms, K, form_ws, form_plain):
     """Prompts whose 128-row tiles fill one round of two workgroups per CU
-    unevenly: with a workspace the last tiles split their K steps in two, so
-    every CU holds the same work.  Outputs within the matmulQ8 bar of the oracle (every 5th
-    token, both split and whole tiles among them), Inf and NaN activations
-    included; the same bits on every run; nothing written past the outputs."""
+    unevenly.  Where 256-row tiles fill two thirds of the CUs or more they run
+    on the direct kernel, workspace or not; otherwise with a workspace the
+    last 128-row tiles split their K steps in two, so every CU holds the same
+    work, and without one the direct kernel runs the 128-row tiles.  Outputs
+    within the matmulQ8 bar of the oracle (every 5th token, split and whole
+    tiles among them), Inf and NaN activations included; the same bits on
+    every run; nothing written past the outputs."""
     rng = np.random.default_rng(N + K + sum(Ms))
     a = rng.standard_normal(N * K).astype(np.float32)
     a[(N - 1) * K + 2] = np.inf   # the last token row is a split tile's
@@ -369,7 +374,7 @@ def test_matmul_workspace_balance(N, Ms, K):
     for _ in range(2):
         wxo_q8.matmul_q8_multi_device(ba, bufs, N, K, workspace=ws, workspace_bytes=ws_bytes)
         wxo_q8.synchronize()
-        assert wxo_q8.last_variant().split()[1] == "FB4.balance2", wxo_q8.last_variant()
+        assert wxo_q8.last_variant().split()[1] == form_ws, wxo_q8.last_variant()
         runs.append([b[2].download(np.float32, N * b[3] + 64) for b in bufs])
     rows = np.unique(np.concatenate([np.arange(0, N, 5), [3, N - 1]]))
     for (w, s, M), got, again in zip(host, runs[0], runs[1]):
@@ -381,7 +386,7 @@ def test_matmul_workspace_balance(N, Ms, K):
         out.upload(np.zeros(out.nbytes // 4, np.float32))
     wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
     wxo_q8.synchronize()
-    assert wxo_q8.last_variant().split()[1] == "FB4", wxo_q8.last_variant()
+    assert wxo_q8.last_variant().split()[1] == form_plain, wxo_q8.last_variant()
     for (w, s, M), b in zip(host, bufs):
         assert_matmul(b[2].download(np.float32, N * M), a, w, s, N, M, K, rows=rows)
 
@@ -504,7 +509,7 @@ def test_matmul_workspace_leaves_several_rounds_unsplit():
     wxo_q8.matmul_q8_multi_device(ba, [(bw, bs, outs[0], M), (bw, bs, outs[1], M)], N, K, workspace=ws,
                                   workspace_bytes=ws_bytes)
     wxo_q8.synchronize()
-    assert wxo_q8.last_variant().split()[1] == "FB4", wxo_q8.last_variant()
+    assert wxo_q8.last_variant().split()[1] == "D128", wxo_q8.last_variant()
     assert_bits_equal(outs[1].download(np.float32, N * M), outs[0].download(np.float32, N * M), "same weight")
 
 
@@ -632,8 +637,9 @@ def test_matmul_tile_pairs_ragged_tokens_match_one_group():
     tiles of 128 rows, 1024 tiles in all, whose 256-row tiles would not make
     whole rounds): every 29th token against the oracle, nothing past the
     outputs, and the bits of both halves of the tokens equal to runs of those
-    halves alone, whose 512 tiles take the one-group FB4 form (the same sums
-    in the same order; token tile boundaries line up at token 1024)."""
+    halves alone, whose 512 tiles take the one-group form on the direct
+    kernel (D128: the same sums in the same order; token tile boundaries line
+    up at token 1024)."""
     N, K = 2040, 4096
     Ms = [2176, 1920]
     rng = np.random.default_rng(2040)
@@ -664,17 +670,18 @@ def test_matmul_tile_pairs_ragged_tokens_match_one_group():
         wxo_q8.matmul_q8_multi_device(bh, [(bw, bs, oh, M) for (bw, bs), oh, M in zip(dev, ohs, Ms)], n, K)
         wxo_q8.synchronize()
         variant = wxo_q8.last_variant()
-        assert " FB4 " in variant and "pairs" not in variant, variant
+        assert " D128 " in variant, variant
         for oh, g, M in zip(ohs, got, Ms):
             assert_bits_equal(oh.download(np.float32, n * M), g[t0 * M:t1 * M], f"M={M} tokens {t0}..{t1}: pairs vs one group")
 
 
 def test_matmul_256_row_tiles_match_the_one_group_form():
-    """Launches whose 256-row tiles make whole rounds of the CUs take them (8
-    waves, 4 over the rows): 2048 tokens x 2048 x 2048 is 256 such tiles.  The
-    bits of its first 1536 tokens equal a launch of those tokens alone, whose
-    384 tiles of 128 rows take the one-group form; every 41st token against the
-    oracle."""
+    """Launches whose 256-row tiles make whole rounds of the CUs take them on
+    the direct kernel (8 waves of 32 rows): 2048 tokens x 2048 x 2048 is 256
+    such tiles.  The bits of its first 1280 tokens equal a launch of those
+    tokens alone, whose 320 tiles of 128 rows (160 of 256 rows: under two
+    thirds of the CUs) take the 128-row direct form; every 41st token against
+    the oracle."""
     N, M, K = 2048, 2048, 2048
     rng = np.random.default_rng(256)
     a = rng.standard_normal(N * K).astype(np.float32)
@@ -684,15 +691,15 @@ def test_matmul_256_row_tiles_match_the_one_group_form():
     out = wxo_q8.DeviceBuffer(4 * N * M)
     wxo_q8.matmul_q8_multi_device(wxo_q8.DeviceBuffer.from_array(a), [(bw, bs, out, M)], N, K)
     wxo_q8.synchronize()
-    assert " FB8 " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    assert " D256 " in wxo_q8.last_variant(), wxo_q8.last_variant()
     got = out.download(np.float32, N * M)
     assert_matmul(got, a, w, s, N, M, K, rows=np.unique(np.r_[np.arange(0, N, 41), N - 1]))
-    n = 1536
+    n = 1280
     half = wxo_q8.DeviceBuffer(4 * n * M)
     wxo_q8.matmul_q8_multi_device(wxo_q8.DeviceBuffer.from_array(a[:n * K]), [(bw, bs, half, M)], n, K)
     wxo_q8.synchronize()
     variant = wxo_q8.last_variant()
-    assert " FB4 " in variant, variant
+    assert " D128 " in variant, variant
     assert_bits_equal(got[:n * M], half.download(np.float32, n * M), "256-row tiles vs the one-group 128-row form")
 
 
@@ -720,7 +727,7 @@ def test_matmul_256_row_tiles_ragged():
         bufs.append((wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s), o, M))
     wxo_q8.matmul_q8_multi_device(ba, bufs, N, K)
     wxo_q8.synchronize()
-    assert " FB8 " in wxo_q8.last_variant(), wxo_q8.last_variant()
+    assert " D256 " in wxo_q8.last_variant(), wxo_q8.last_variant()
     rows = np.unique(np.r_[np.arange(0, N, 37), 5, 9, N - 1])
     for (w, s, M), (_, _, o, _) in zip(host, bufs):
         got = o.download(np.float32, N * M + 64)

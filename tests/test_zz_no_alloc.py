@@ -35,10 +35,10 @@ def test_no_alloc_matches_the_workspace_entry():
     rng = np.random.default_rng(2024)
     ws_bytes = min(wxo_q8.matmul_q8_workspace_bytes(), SCRATCH_BYTES)
     ws = wxo_q8.DeviceBuffer(ws_bytes)
-    # a 512-token q, k, v (128 of its 384 tiles split in two: 4 MiB of the
-    # array), then a 64-token projection (every tile in four parts), then a
-    # smaller one over two projections (two parts)
-    for N, Ms, K, form in [(512, [2048, 2048, 2048], 2048, "balance2"), (64, [2048], 2048, "wgsplit4"),
+    # 700 tokens over two projections (204 of their 308 tiles split in two:
+    # 6.4 MiB of the array), then a 64-token projection (every tile in four
+    # parts), then a smaller one over two projections (two parts)
+    for N, Ms, K, form in [(700, [2048, 1500], 1030, "balance2"), (64, [2048], 2048, "wgsplit4"),
                            (40, [512, 256], 1030, "wgsplit2")]:
         a = rng.standard_normal(N * K).astype(np.float32)
         a[1] = np.inf

@@ -62,10 +62,16 @@
 //
 // Long rows whose tiles make whole rounds of two per CU run one workgroup of
 // 16 waves per two tiles, each group of 8 waves on a tile of its own (the
-// PAIR instances); the sums are the one-group form's.  Large launches whose
-// 256-row tiles fill the CUs in whole rounds run those tiles with 4 of the 8
-// waves over the rows (WR = 4), each wave on 64 rows x 32 tokens; again the
-// one-group form's sums.
+// PAIR instances); the sums are the one-group form's.
+//
+// Launches with enough tiles for one workgroup per CU and no K split run
+// matmul_q8_direct_kernel instead: every wave of 8 owns 16 FW weight rows and
+// all 64 tokens of the tile, and loads its rows' codes straight into VGPRs
+// (two dwordx2 per 16-row block and step, in the operand's k order), so only
+// the activation parts pass through LDS.  That removes the codes' LDS writes
+// (gfx950 writes LDS at ~75 B/clk per CU against ~200 for reads) and converts
+// each code once per wave, at the matrix work.  Same sums in the same order
+// as the one-group form, so the same bits; 2-7 % faster than it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -78,6 +84,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kBN = 64;            // tokens per workgroup
 constexpr uint32_t kFoldCodes = 1024;   // fold the accumulator every 1024 codes
@@ -142,6 +149,22 @@ __device__ __forceinline__ void codes16_to_bf16(u32x4v w, u32x4v& lo, u32x4v& hi
     hi = u32x4v{r[4], r[5], r[6], r[7]};
 }
 
+// 8 codes (2 packed words) -> 8 bf16.
+__device__ __forceinline__ bf16x8 codes8_to_bf16(u32x2v w) {
+    const uint32_t ws[2] = {w.x, w.y};
+    uint32_t r[4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const float c0 = (float)(int8_t)(ws[q]);
+        const float c1 = (float)(int8_t)(ws[q] >> 8);
+        const float c2 = (float)(int8_t)(ws[q] >> 16);
+        const float c3 = (float)((int32_t)ws[q] >> 24);
+        r[2 * q] = hi_pair(__float_as_uint(c0), __float_as_uint(c1));
+        r[2 * q + 1] = hi_pair(__float_as_uint(c2), __float_as_uint(c3));
+    }
+    return __builtin_bit_cast(bf16x8, u32x4v{r[0], r[1], r[2], r[3]});
+}
+
 // Splits activations into bf16 parts h + m + l (bit patterns in the upper
 // halves).  Finite values split exactly by truncation: h keeps the top 8
 // significant bits, r = a - h is exact, m keeps r's top 8, l = r - m is exact
@@ -173,7 +196,7 @@ __device__ __forceinline__ void split3_any(uint32_t bits, uint32_t& h, uint32_t&
 // workgroup, one whole tile per group, and the rest one per workgroup with
 // the K steps split between the groups.  The other instances run every tile
 // whole, with no branch on it.
-template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false, bool PAIR = false, int WR = 2>
+template <int FB, int NW, int BK, int PD, int KS, bool SPLIT = false, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __restrict__ a, MatmulProjections P,
                                                         uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
                                                         uint32_t ntiles) {
@@ -189,9 +212,9 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     constexpr int AL = (int)((ACH + NT - 1u) / NT);   // A loads per thread per step
     constexpr uint32_t FPT = kBK / NW;                // activations per thread per step
     constexpr int BL = (int)(FPT / 4u);               // B loads (dwordx4) per thread per step
+    constexpr uint32_t WR = 2u;                        // waves over the rows
     constexpr int TB = (int)(4u * WR / NW);            // 16-token blocks per wave (2 or 1)
     constexpr int FW = (int)(BM / (16u * WR));         // 16-row blocks per wave
-    static_assert((WR == 2 && (NW == 4 || NW == 8)) || (WR == 4 && NW == 8), "2 or 4 waves over the rows");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(BK == 64 || BK == 128, "64- or 128-code steps");
     static_assert(PD == 2 || PD == 4, "2 or 4 register sets of loads in flight");
@@ -261,8 +284,8 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     const uint32_t t = KS == 1 ? threadIdx.x : threadIdx.x % NT;
     const uint32_t lane = t & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t wm = (wv % (uint32_t)WR) * (BM / (uint32_t)WR);  // wave's first weight row in the tile
-    const uint32_t wn = (wv / (uint32_t)WR) * (16u * (uint32_t)TB);  // wave's first token in the tile
+    const uint32_t wm = (wv % WR) * (BM / WR);                  // wave's first weight row in the tile
+    const uint32_t wn = (wv / WR) * (16u * (uint32_t)TB);       // wave's first token in the tile
     const uint32_t j = lane & 15u, g = lane >> 4;
 
     const uint32_t mrows = min(BM, M - m0);
@@ -547,6 +570,249 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
     }
 }
 
+// The one-group GEMM with each wave's weight codes loaded straight into
+// registers.  A workgroup of 8 waves owns BM = 128 FW weight rows x 64 tokens;
+// wave w owns rows 16 FW w .. +16 FW - 1 and every token of the tile, so
+// nothing it converts is shared and no code passes through LDS.  Per 64-code
+// step, lane (j, g) of 16-row block f loads codes 8g .. 8g+7 and 32+8g ..
+// 32+8g+7 of row 16 f + j (the operand's k order for the step's two 32-code
+// halves) PD steps ahead; the activations go through the same double-buffered,
+// XOR-swizzled LDS stage as matmul_q8_kernel, split into three parts once per
+// workgroup.  Matrix ops, their order and the fold points are the one-group
+// form's, so the bits are too.
+template <int FW, int PD>
+__global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __restrict__ a, MatmulProjections P,
+                                                               uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
+                                                               uint32_t ntiles) {
+    constexpr uint32_t NW = 8u, TB = 4u;
+    constexpr uint32_t BM = 16u * FW * NW;
+    constexpr uint32_t kRowBytes = 128u;              // one LDS row: 64 codes of bf16
+    constexpr uint32_t BST = 3u * kBN * kRowBytes;    // one stage: three parts of 64 tokens
+    constexpr uint32_t NT = 64u * NW;
+    constexpr uint32_t FPT = kBN * 64u / NT;          // activations per thread per step
+    constexpr int BL = (int)(FPT / 4u);
+    constexpr uint32_t TPT = NT / kBN;                // threads per token
+    constexpr uint32_t kFoldSteps = kFoldCodes / 64u;
+    static_assert(TB * 16u == kBN, "a wave covers the tile's tokens");
+    static_assert(FPT % 8u == 0u, "whole 16-byte pieces per part");
+    static_assert(kFoldSteps % (uint32_t)PD == 0u, "a fold group starts on register set 0 and stage 0");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t total = mtiles * ntiles;
+    const uint32_t lin = xcd * ((total + 7u) / 8u) + slot;
+    if (lin >= total) return;
+    uint32_t mt, nt;
+    tile_coords(lin, mtiles, ntiles, mt, nt);
+    const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
+    const uint32_t* __restrict__ weight = P.weight[pj];
+    const float* __restrict__ scale = P.scale[pj];
+    float* __restrict__ out = P.out[pj];
+    const uint32_t M = P.M[pj];
+    const uint32_t m0 = (mt - P.mt0[pj]) * BM, n0 = nt * kBN;
+
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t wm = wv * (16u * FW);
+    const uint32_t j = lane & 15u, g = lane >> 4;
+    const uint32_t mrows = min(BM, M - m0), ntok = min(kBN, N - n0);
+    const uint32_t rowbytes = W * 4u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(weight + (size_t)m0 * W, mrows * rowbytes);
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(a + (size_t)n0 * K, ntok * K * 4u);
+    const uint32_t btok = t / TPT, bc = t % TPT;
+    const int boff = (int)((btok * K + bc * FPT) * 4u);
+
+    // PD register sets each of codes (set i % PD: step i, loaded PD steps
+    // before its matrix work) and activations (loaded PD steps before their
+    // conversion, one step ahead of the matrix work).
+    u32x2v ga[PD][FW][2];
+    u32x4v gb[PD][BL];
+    auto issue_a = [&](int b, uint32_t k0) {
+#pragma unroll
+        for (int f = 0; f < FW; ++f)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                ga[b][f][h] = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(
+                    wrs, (int)((wm + 16u * (uint32_t)f + j) * rowbytes + 8u * g + 32u * (uint32_t)h), (int)k0, 0));
+    };
+    auto issue_b = [&](int b, uint32_t k0) {
+#pragma unroll
+        for (int q = 0; q < BL; ++q)
+            gb[b][q] = __builtin_amdgcn_raw_buffer_load_b128(ars, boff + 16 * q, (int)(k0 * 4u), 0);
+    };
+    // activations at k >= K of step k0 belong to the next token: zero
+    auto mask_b = [&](int s, uint32_t k0) {
+        const uint32_t kb = k0 + bc * FPT;
+#pragma unroll
+        for (int q = 0; q < BL; ++q) {
+            if (kb + 4u * (uint32_t)q >= K) gb[s][q].x = 0u;
+            if (kb + 4u * (uint32_t)q + 1u >= K) gb[s][q].y = 0u;
+            if (kb + 4u * (uint32_t)q + 2u >= K) gb[s][q].z = 0u;
+            if (kb + 4u * (uint32_t)q + 3u >= K) gb[s][q].w = 0u;
+        }
+    };
+    auto store_b = [&](int st, const uint32_t (&hp)[FPT / 2], const uint32_t (&mp)[FPT / 2],
+                       const uint32_t (&lp)[FPT / 2]) {
+        uint8_t* row = lds + (uint32_t)st * BST + btok * kRowBytes;
+#pragma unroll
+        for (uint32_t q = 0; q < FPT / 8u; ++q) {
+            const uint32_t pc = ((bc * (FPT / 8u) + q) ^ (btok & 7u)) * 16u;
+            *reinterpret_cast<u32x4v*>(row + pc) = u32x4v{hp[4 * q], hp[4 * q + 1], hp[4 * q + 2], hp[4 * q + 3]};
+            *reinterpret_cast<u32x4v*>(row + kBN * kRowBytes + pc) =
+                u32x4v{mp[4 * q], mp[4 * q + 1], mp[4 * q + 2], mp[4 * q + 3]};
+            *reinterpret_cast<u32x4v*>(row + 2u * kBN * kRowBytes + pc) =
+                u32x4v{lp[4 * q], lp[4 * q + 1], lp[4 * q + 2], lp[4 * q + 3]};
+        }
+    };
+    // The three parts of register set s into stage st; a wave holding an Inf
+    // or NaN (r = a - h is NaN exactly then) redoes its part with the split
+    // that handles every value.
+    auto convert_b = [&](int s, int st) {
+        uint32_t v[FPT];
+#pragma unroll
+        for (int q = 0; q < BL; ++q) {
+            v[4 * q] = gb[s][q].x;
+            v[4 * q + 1] = gb[s][q].y;
+            v[4 * q + 2] = gb[s][q].z;
+            v[4 * q + 3] = gb[s][q].w;
+        }
+        uint32_t hp[FPT / 2], mp[FPT / 2], lp[FPT / 2];
+        float rsum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < (int)FPT; e += 2) {
+            uint32_t h0, m0_, l0, h1, m1, l1;
+            float r0, r1;
+            split3_fast(v[e], h0, m0_, l0, r0);
+            split3_fast(v[e + 1], h1, m1, l1, r1);
+            rsum += r0 + r1;
+            hp[e / 2] = hi_pair(h0, h1);
+            mp[e / 2] = hi_pair(m0_, m1);
+            lp[e / 2] = hi_pair(l0, l1);
+        }
+        store_b(st, hp, mp, lp);
+        if (__builtin_amdgcn_ballot_w64(__builtin_isnan(rsum)) != 0) {  // wave-uniform
+#pragma unroll
+            for (int e = 0; e < (int)FPT; e += 2) {
+                uint32_t h0, m0_, l0, h1, m1, l1;
+                split3_any(v[e], h0, m0_, l0);
+                split3_any(v[e + 1], h1, m1, l1);
+                hp[e / 2] = hi_pair(h0, h1);
+                mp[e / 2] = hi_pair(m0_, m1);
+                lp[e / 2] = hi_pair(l0, l1);
+            }
+            store_b(st, hp, mp, lp);
+        }
+    };
+
+    f32x4 acc[FW][TB], sum[FW][TB];
+#pragma unroll
+    for (int f = 0; f < FW; ++f)
+#pragma unroll
+        for (uint32_t b = 0; b < TB; ++b) {
+            acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            sum[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+    // Matrix work of one step: activation parts from stage st, codes from
+    // register set q, two 32-code halves.
+    auto compute = [&](int st, int q) {
+        const uint8_t* bs = lds + (uint32_t)st * BST;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t piece = 4u * (uint32_t)h + g;
+            bf16x8 af[FW], bf[TB][3];
+#pragma unroll
+            for (uint32_t b = 0; b < TB; ++b) {
+                const uint32_t tk = 16u * b + j;
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    bf[b][p] = *reinterpret_cast<const bf16x8*>(bs + ((uint32_t)p * kBN + tk) * kRowBytes +
+                                                                ((piece ^ (tk & 7u)) * 16u));
+            }
+#pragma unroll
+            for (int f = 0; f < FW; ++f) af[f] = codes8_to_bf16(ga[q][f][h]);
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int f = 0; f < FW; ++f)
+#pragma unroll
+                    for (uint32_t b = 0; b < TB; ++b)
+                        acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[f], bf[b][p], acc[f][b], 0, 0, 0);
+        }
+    };
+
+    // One barrier per step: iteration i runs step i's matrix work (stage
+    // i & 1, code set i % PD), refills that code set with step i + PD,
+    // converts step i + 1's activations into the other stage and refills
+    // their set with step i + 1 + PD.  Loads past K fall outside the buffer
+    // resources and return 0.
+    const uint32_t steps = (K + 63u) / 64u;
+    const bool ragged = (K % 64u) != 0u;
+#pragma unroll
+    for (int q = 0; q < PD; ++q) {
+        issue_a(q, 64u * (uint32_t)q);
+        issue_b(q, 64u * (uint32_t)q);
+    }
+    if (ragged && steps == 1u) mask_b(0, 0u);
+    convert_b(0, 0);
+    issue_b(0, 64u * (uint32_t)PD);
+    __syncthreads();
+    auto iter = [&](int q, uint32_t i) {
+        const int nx = (q + 1) % PD;
+        if (ragged && i + 2u == steps) mask_b(nx, (i + 1u) * 64u);  // uniform
+        compute(q & 1, q);
+        issue_a(q, (i + (uint32_t)PD) * 64u);
+        convert_b(nx, (q + 1) & 1);
+        issue_b(nx, (i + 1u + (uint32_t)PD) * 64u);
+        __syncthreads();
+    };
+    for (uint32_t g0 = 0; g0 < steps; g0 += kFoldSteps) {
+        const uint32_t gend = min(g0 + kFoldSteps, steps);
+        uint32_t i = g0;
+        for (; i + (uint32_t)PD <= gend; i += (uint32_t)PD) {
+#pragma unroll
+            for (int q = 0; q < PD; ++q) iter(q, i + (uint32_t)q);
+        }
+#pragma unroll
+        for (int q = 0; q < PD - 1; ++q)
+            if (i + (uint32_t)q < gend) iter(q, i + (uint32_t)q);
+#pragma unroll
+        for (int f = 0; f < FW; ++f)
+#pragma unroll
+            for (uint32_t b = 0; b < TB; ++b) {
+                sum[f][b] += acc[f][b];
+                acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+    }
+
+    // lane (j, g) of block (f, b): rows m0 + wm + 16 f + 4 g .. +3 of token
+    // n0 + 16 b + j
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + m0, mrows * 4u);
+#pragma unroll
+    for (int f = 0; f < FW; ++f) {
+        const uint32_t fm = wm + 16u * (uint32_t)f + 4u * g;
+        const u32x4v sv = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
+#pragma unroll
+        for (uint32_t b = 0; b < TB; ++b) {
+            const uint32_t tok = 16u * b + j;
+            if (tok >= ntok) continue;
+            f32x4 y;
+            y[0] = sum[f][b][0] * __uint_as_float(sv.x);
+            y[1] = sum[f][b][1] * __uint_as_float(sv.y);
+            y[2] = sum[f][b][2] * __uint_as_float(sv.z);
+            y[3] = sum[f][b][3] * __uint_as_float(sv.w);
+            float* o = out + (size_t)(n0 + tok) * M + m0 + fm;
+            if (fm + 3u < mrows) {
+                *reinterpret_cast<f32x4_a4*>(o) = f32x4_a4{y[0], y[1], y[2], y[3]};
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (fm + (uint32_t)q < mrows) o[q] = y[q];
+            }
+        }
+    }
+}
+
 // out = (part 0 + part 1 + ... + part parts-1) * scale, in part order, for
 // every output of the split tiles of a split launch.  Grid x: split tile;
 // grid y: BM / 16 slices of it; a thread takes 4 consecutive rows of one
@@ -594,18 +860,9 @@ __global__ void fill_zero_kernel(float* __restrict__ y, size_t n) {
         y[i] = 0.0f;
 }
 
-// One launch over `count` (1 to 4) projections of the same activations.  With
-// splits > 0 (a SPLIT instance) the last `splits` tiles of the sequence have
-// their K steps split into `parts` runs, with the workspace `part` holding
-// (parts - 1) x splits blocks of BM x kBN floats, and a second launch sums
-// them.
-template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false, bool PAIR = false, int WR = 2>
-hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
-                     hipStream_t stream, float* part = nullptr, uint32_t splits = 0, uint32_t parts = 1) {
-    constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
-    constexpr uint32_t BM = 32u * FB;
-    const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
-    MatmulProjections P = {};
+// The launch's projection table for BM-row tiles; returns the row tiles of
+// all projections together.
+uint32_t fill_projections(const MatmulProjection* p, uint32_t count, uint32_t BM, MatmulProjections& P) {
     uint32_t mtiles = 0;
     for (uint32_t i = 0; i < kMaxMatmulProjections; ++i) {
         if (i < count) {
@@ -619,6 +876,38 @@ hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, 
             P.mt0[i] = 0xffffffffu;
         }
     }
+    return mtiles;
+}
+
+// One launch of matmul_q8_direct_kernel (128 FW-row tiles, PD register sets)
+// over `count` projections of the same activations.
+template <int FW, int PD>
+hipError_t launch_direct(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
+                         hipStream_t stream) {
+    const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
+    MatmulProjections P = {};
+    const uint32_t mtiles = fill_projections(p, count, 128u * FW, P);
+    const uint32_t ntiles = (N + kBN - 1u) / kBN;
+    const uint32_t grid = ((mtiles * ntiles + 7u) / 8u) * 8u;
+    const size_t lds = 2u * 3u * kBN * 128u;
+    hipLaunchKernelGGL((matmul_q8_direct_kernel<FW, PD>), dim3(grid), dim3(512), lds, stream, a, P, N, K, W, mtiles,
+                       ntiles);
+    return hipGetLastError();
+}
+
+// One launch over `count` (1 to 4) projections of the same activations.  With
+// splits > 0 (a SPLIT instance) the last `splits` tiles of the sequence have
+// their K steps split into `parts` runs, with the workspace `part` holding
+// (parts - 1) x splits blocks of BM x kBN floats, and a second launch sums
+// them.
+template <int FB, int NW, int BK, int PD, int KS = 1, bool SPLIT = false, bool PAIR = false>
+hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
+                     hipStream_t stream, float* part = nullptr, uint32_t splits = 0, uint32_t parts = 1) {
+    constexpr uint32_t kRowBytes = (uint32_t)BK * 2u;
+    constexpr uint32_t BM = 32u * FB;
+    const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
+    MatmulProjections P = {};
+    const uint32_t mtiles = fill_projections(p, count, BM, P);
     const uint32_t ntiles = (N + kBN - 1u) / kBN;
     const uint32_t tiles = mtiles * ntiles;
     P.part = part;
@@ -633,7 +922,7 @@ hipError_t launch_fb(const float* a, const MatmulProjection* p, uint32_t count, 
         grid = 8u * ((splits / 2u + 7u) / 8u + (tiles - splits + 7u) / 8u);
     }
     const size_t lds = (size_t)KS * (2u * BM * kRowBytes + 2u * 3u * kBN * kRowBytes);
-    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT, PAIR, WR>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
+    hipLaunchKernelGGL((matmul_q8_kernel<FB, NW, BK, PD, KS, SPLIT, PAIR>), dim3(grid), dim3(64 * NW * KS), lds, stream, a,
                        P, N, K, W, mtiles, ntiles);
     if constexpr (SPLIT) {
         const hipError_t err = hipGetLastError();
@@ -709,19 +998,19 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
     }
     const uint32_t steps = (uint32_t)(((uint64_t)K + 63u) / 64u);
     const char* kname = n > 1 ? "matmul_q8.multi" : "matmul_q8";
-    // 256-row tiles of 8 waves, 4 over the rows and 2 over the tokens (a wave
-    // holds 64 rows x 32 tokens: ~30 % fewer LDS bytes per matrix op than the
-    // 128-row tiles' 64 x 16), one workgroup per CU, when those tiles make
-    // whole rounds of the CUs or at least 2.75 of them.  The sums and their
-    // order are the one-group 128-row form's, so are the bits.  Same process,
-    // us, FB4 (or FB4.pairs) -> FB8: 1024 x 4096 x 4096 129 -> 113, 2048 x
-    // 2048 x 2048 64 -> 59, 2048 x 4096 x 4096 258 -> 232, 2048 x 4096 x
-    // 11008 670 -> 613, 4096 x 4096 x 4096 495 -> 458, 1024 x 11264 x 2048
-    // (2.75 rounds) 196 -> 185; with 1.1-1.5 rounds (288-384 tiles) they lose
-    // 10-15 %, with less than one round more.
+    // 256-row tiles on the direct kernel (8 waves of 32 rows x 64 tokens, codes
+    // straight into registers, four sets in flight), one workgroup per CU,
+    // when those tiles make whole rounds of the CUs or at least 2.75 of them.
+    // The sums and their order are the one-group 128-row form's, so are the
+    // bits.  Same process, us, against 256-row tiles through LDS (4 of 8 waves
+    // over the rows, 64 x 32 each), which had replaced the 128-row one-group
+    // form (1024 x 4096 x 4096 129 -> 113): 1024 x 4096 x 4096 108 -> 98,
+    // 2048 x 2048 x 2048 60 -> 56, 2048 x 6144 x 2048 164 -> 155, 2048 x
+    // 11264 x 2048 304 -> 289, 2048 x 2048 x 5632 145 -> 134, 2048 x 4096 x
+    // 11008 502 -> 475, 4096 x 4096 x 4096 391 -> 363.
     if (t8 >= cus && (t8 % cus == 0 || 4u * t8 >= 11u * (uint64_t)cus)) {
-        set_variant(variant, kname, "FB8", 8, 256, 0, (int)kBN, (uint32_t)((t8 + 7u) / 8u * 8u));
-        return launch_fb<8, 8, 64, 2, 1, false, false, 4>(a, p, n, N, K, stream);
+        set_variant(variant, kname, "D256", 8, 256, 0, (int)kBN, (uint32_t)((t8 + 7u) / 8u * 8u));
+        return launch_direct<2, 4>(a, p, n, N, K, stream);
     }
     if (t4 >= cus) {
         if (t4 == cus) {
@@ -742,6 +1031,17 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
         const uint64_t slots = 2ull * cus;
         const uint64_t S = t4 < slots ? slots - t4 : 0u;
         const size_t blk = (size_t)128u * kBN * 4u;
+        // Where the 256-row tiles fill at least two thirds of the CUs, the
+        // direct kernel on those tiles (one workgroup per CU, two register
+        // sets) beats both the split and the uneven round, with or without a
+        // workspace.  Same process, us, split -> 256-row direct: 512 tokens q,
+        // k, v (192 tiles) 51.9 -> 48.7; 256 tokens gate and up (176) 53.9 ->
+        // 49.9.  With fewer (96 at 256 tokens q, k, v) it loses to the 128-row
+        // forms (31.6 -> 45.0).
+        if (S > 0 && 3u * t8 >= 2u * (uint64_t)cus) {
+            set_variant(variant, kname, "D256.PD2", 8, 256, 0, (int)kBN, (uint32_t)((t8 + 7u) / 8u * 8u));
+            return launch_direct<2, 2>(a, p, n, N, K, stream);
+        }
         if (workspace && S > 0 && steps >= 8u && S * blk <= workspace_bytes) {
             set_variant(variant, kname, "FB4.balance2", 8, 128, 0, (int)kBN, (uint32_t)(t4 + S));
             return launch_fb<4, 8, 64, 2, 1, true>(a, p, n, N, K, stream, workspace, (uint32_t)S, 2u);
@@ -760,8 +1060,12 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
             set_variant(variant, kname, "FB4.pairs", 16, 128, 0, (int)kBN, (uint32_t)((t4 / 2u + 7u) / 8u * 8u));
             return launch_fb<4, 8, 64, 2, 2, false, true>(a, p, n, N, K, stream, nullptr, (uint32_t)t4, 1u);
         }
-        set_variant(variant, kname, "FB4", 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
-        return launch_fb<4, 8, 64, 2, 1>(a, p, n, N, K, stream);
+        // Otherwise the 128-row tiles on the direct kernel, two workgroups per
+        // CU.  Same process, us, against the one-group form through LDS: 768
+        // tokens q, k, v 86.1 -> 82.9, 1024 tokens 94.8 -> 92.4, 512 x 11008 x
+        // 4096 166.6 -> 161.7.
+        set_variant(variant, kname, "D128", 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
+        return launch_direct<1, 2>(a, p, n, N, K, stream);
     }
     // 128-row tiles that fill most of the CUs, one per CU with two K groups,
     // beat smaller tiles that fill them all: a 128-row tile moves ~19 bytes
