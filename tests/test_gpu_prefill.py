@@ -560,6 +560,27 @@ def test_dequantize_packed_bit_exact(N, K):
     assert_bits_equal(got, want, f"dequantizePackedQ8 N={N} K={K}")
 
 
+@pytest.mark.parametrize("N,K", [(1, 1), (2, 2), (3, 3), (5, 1), (7, 2), (9, 5), (11, 6), (13, 7), (31, 1027),
+                                 (4096, 4099)])
+def test_dequantize_packed_ragged_sentinels(N, K):
+    """Rows that end mid-word (K % 4 != 0): a thread writes four consecutive
+    outputs, which cross one row end or, for K < 4, several, and the last
+    thread writes the 1-3 outputs left.  Bit-exact against the oracle on
+    device buffers with sentinels after the output, none overwritten."""
+    rng = np.random.default_rng(N * 31 + K)
+    W = (K + 3) // 4
+    w = rng.integers(0, 2 ** 32, N * W, dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(-1, 1, N).astype(np.float32)
+    bw, bs = wxo_q8.DeviceBuffer.from_array(w), wxo_q8.DeviceBuffer.from_array(s)
+    out = wxo_q8.DeviceBuffer(4 * (N * K + 64))
+    out.upload(np.full(N * K + 64, 7.5, np.float32))
+    wxo_q8.dequantize_packed_q8_device(bw, bs, N, K, out)
+    wxo_q8.synchronize()
+    got = out.download(np.float32, N * K + 64)
+    assert np.all(got[N * K:] == np.float32(7.5)), "written past the output"
+    assert_bits_equal(got[:N * K], oracle.dequantize_packed_q8(w, s, N, K), f"dequantizePackedQ8 N={N} K={K}")
+
+
 def test_dequantize_packed_kats():
     c = kat()["dequantize_packed_q8"][1]
     w = oracle.pack_int8_rows(np.array(c["codes"], np.int8), c["N"], c["K"])
