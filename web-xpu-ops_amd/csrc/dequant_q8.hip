@@ -32,14 +32,13 @@ __device__ __forceinline__ float dq(uint32_t word, int lane, float s) {
 
 // out [N, K], K % 4 == 0: one packed word per thread per pass, consecutive
 // threads on consecutive words; the output is the words' flat image, 16 bytes
-// per word, so a wave stores 1 KiB contiguous.
+// per word, so a wave stores 1 KiB contiguous.  IDX: 32-bit below 2^32 words.
+template <typename IDX>
 __global__ __launch_bounds__(256) void dequantize_packed_kernel(const uint32_t* __restrict__ weight,
                                                                 const float* __restrict__ scale,
-                                                                float* __restrict__ out, uint32_t N, uint32_t W) {
-    const uint64_t total = (uint64_t)N * W;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t row = (uint32_t)(i / W);
+                                                                float* __restrict__ out, uint32_t W, IDX total) {
+    for (IDX i = (IDX)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (IDX)gridDim.x * blockDim.x) {
+        const IDX row = i / W;
         const uint32_t word = weight[i];
         const float s = scale[row];
         f32x4_a4 f;
@@ -47,7 +46,7 @@ __global__ __launch_bounds__(256) void dequantize_packed_kernel(const uint32_t* 
         f.y = dq(word, 1, s);
         f.z = dq(word, 2, s);
         f.w = dq(word, 3, s);
-        *reinterpret_cast<f32x4_a4*>(out + 4u * i) = f;
+        *reinterpret_cast<f32x4_a4*>(out + 4u * (size_t)i) = f;
     }
 }
 
@@ -218,8 +217,13 @@ hipError_t launch_dequantize_packed(const uint32_t* weight, const float* scale, 
     const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
     if ((K & 3u) == 0u) {
         const uint64_t items = (uint64_t)N * W;
-        hipLaunchKernelGGL(dequantize_packed_kernel, dim3(grid_cap(items, 256, dev)), dim3(256), 0, stream, weight,
-                           scale, out, N, W);
+        const dim3 grid(grid_cap(items, 256, dev));
+        if (items < 0xff000000ull)
+            hipLaunchKernelGGL(dequantize_packed_kernel<uint32_t>, grid, dim3(256), 0, stream, weight, scale, out, W,
+                               (uint32_t)items);
+        else
+            hipLaunchKernelGGL(dequantize_packed_kernel<uint64_t>, grid, dim3(256), 0, stream, weight, scale, out, W,
+                               items);
     } else {
         const uint64_t total = (uint64_t)N * K;
         const dim3 grid(grid_cap((total + 3u) / 4u, 256, dev));
