@@ -986,7 +986,8 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
     // steps move less through LDS and twice the CUs work (64 tokens, 2048 x
     // 2048: 18.5 -> 16.2 us; 2048 x 5632: 44.7 -> 38.3 us; the same sums in
     // the same order, so the same bits).  Projections in one launch count
-    // their tiles together.
+    // their tiles together.  Launches whose tiles take one K group and no
+    // split run on matmul_q8_direct_kernel (D256, D256.PD2, D128 below).
     const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
     const uint64_t ntiles = (N + kBN - 1u) / kBN;
     uint64_t t8 = 0, t4 = 0, t2 = 0, t1 = 0;
