@@ -299,7 +299,7 @@ int wxo_matmul_q8_workspace_bytes(size_t* bytes);
  * caller passes: no counterpart in the reference.  For callers that cannot
  * allocate device memory at all (code under HIP graph capture, serving loops
  * or harnesses that forbid hipMalloc): it allocates nothing and calls no
- * allocating routine.  The workspace is an 8 MiB array in the library's code
+ * allocating routine.  The workspace is a 16 MiB array in the library's code
  * object (each GPU holds its own from the library's load until the process
  * ends); a split that would need more runs with fewer parts, so no size is
  * refused for it.  The array keeps the last call's contents and needs no

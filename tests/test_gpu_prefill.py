@@ -391,30 +391,37 @@ def test_matmul_workspace_balance(N, Ms, K, form_ws, form_plain):
         assert_matmul(b[2].download(np.float32, N * M), a, w, s, N, M, K, rows=rows)
 
 
+MIB = 1 << 20
 FB4_CASES = [
-    # (N, Ms, K, workspace, form): 128-row tiles with two K groups, one per CU
+    # (N, Ms, K, workspace bytes (True: the full size), form): tiles that fill
+    # the CUs once, with two K groups or split between workgroups
     (128, [5632, 5632], 2048, False, "FB4.ksplit2"),          # 176 tiles: most of the CUs
     (256, [2048, 2048, 2048], 2048, True, "FB4.ksplit2"),     # 192 tiles, with a workspace too
-    (512, [2048], 4096, True, "FB4.ksplit2.wgsplit2"),         # 128 tiles x 2 parts
-    (512, [2048], 2048, True, "FB2.PD4.ksplit2"),              # too few steps per part: 64-row tiles
-    (256, [2048], 5632, True, "FB4.ksplit2.wgsplit4"),         # 64 tiles x 4 parts
-    (500, [1900], 3000, True, "FB4.ksplit2.wgsplit2"),         # ragged tokens, rows and K: 120 tiles x 2
+    (512, [2048], 4096, True, "D256.split4"),                  # 64 256-row tiles x 4 parts
+    (512, [2048], 2048, True, "FB2.PD4.ksplit2"),              # too few steps for 4 parts: 64-row tiles
+    (256, [2048], 5632, True, "D256.split8"),                  # 32 256-row tiles x 8 parts
+    (500, [1900], 3000, True, "D256.split4"),                  # ragged tokens, rows and K: 64 tiles x 4
+    (512, [2048], 4096, 4 * MIB, "FB4.ksplit2.wgsplit2"),      # no room for 4 parts of 256 rows: 128 x 2
+    (256, [2048], 5632, 12 * MIB, "FB4.ksplit2.wgsplit4"),     # no room for 8 parts: 64 tiles x 4
+    (500, [1900], 3000, 4 * MIB, "FB4.ksplit2.wgsplit2"),      # ragged: 120 tiles x 2
 ]
 
 
 @pytest.mark.parametrize("N,Ms,K,use_ws,form", FB4_CASES)
 def test_matmul_128_row_tiles(N, Ms, K, use_ws, form):
-    """128-row tiles filling most of the CUs, or all of them with their K
-    steps split between workgroups through the workspace: within the matmulQ8
-    bar of the oracle (every 3rd token), Inf and NaN activations included, the
-    same bits on a second run, nothing written past the outputs."""
+    """Tiles filling most of the CUs once (128 rows, two K groups), or all of
+    them with their K steps split between workgroups through the workspace:
+    256-row direct tiles in 4 or 8 parts, or, with less workspace, the 128-row
+    two-group tiles in 2 or 4.  Within the matmulQ8 bar of the oracle (every
+    3rd token), Inf and NaN activations included, the same bits on a second
+    run, nothing written past the outputs."""
     rng = np.random.default_rng(N * 3 + K + len(Ms))
     a = rng.standard_normal(N * K).astype(np.float32)
     a[(N - 1) * K + 5] = np.inf
     a[6 * K + 1] = np.nan
     ba = wxo_q8.DeviceBuffer.from_array(a)
-    ws_bytes = wxo_q8.matmul_q8_workspace_bytes() if use_ws else 0
-    ws = wxo_q8.DeviceBuffer(ws_bytes) if use_ws else None
+    ws_bytes = (wxo_q8.matmul_q8_workspace_bytes() if use_ws is True else use_ws) if use_ws else 0
+    ws = wxo_q8.DeviceBuffer(wxo_q8.matmul_q8_workspace_bytes()) if use_ws else None
     host, bufs = [], []
     for M in Ms:
         codes = rng.integers(-128, 128, (M, K)).astype(np.int32)

@@ -13,7 +13,7 @@ import wxo_q8
 
 pytestmark = pytest.mark.gpu
 
-SCRATCH_BYTES = 256 * 32768  # the library's array: 32 KiB per CU of a 256-CU device
+SCRATCH_BYTES = 256 * 65536  # the library's array: 64 KiB per CU of a 256-CU device
 
 
 @pytest.fixture(scope="module", autouse=True)

@@ -118,7 +118,9 @@ struct MatmulProjection {
     float* output;
     uint32_t M;
 };
-constexpr size_t kMatmulWorkspaceBytesPerCu = 32768;  // one 128 x 64-output half per CU
+// Room for every split the dispatch takes: up to 7/8 of a round of 256 x 64
+// f32 tiles per CU (a short prompt's 256-row tiles in 4 or 8 parts).
+constexpr size_t kMatmulWorkspaceBytesPerCu = 65536;
 hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projections, uint32_t count, uint32_t N,
                                   uint32_t K, const DeviceInfo& dev, hipStream_t stream, Variant* variant,
                                   float* workspace = nullptr, size_t workspace_bytes = 0);

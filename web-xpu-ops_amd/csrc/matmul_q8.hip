@@ -579,8 +579,12 @@ __global__ __launch_bounds__(64 * NW * KS) void matmul_q8_kernel(const float* __
 // halves) PD steps ahead; the activations go through the same double-buffered,
 // XOR-swizzled LDS stage as matmul_q8_kernel, split into three parts once per
 // workgroup.  Matrix ops, their order and the fold points are the one-group
-// form's, so the bits are too.
-template <int FW, int PD>
+// form's, so the bits are too.  SPLIT instances split every tile's K steps
+// into P.parts runs, one workgroup each (P.whole = 0): part 0 stores its
+// unscaled sums into the output, part j >= 1 into workspace block
+// (j - 1) * P.splits + tile, and split_sum_kernel adds them in part order and
+// scales them.
+template <int FW, int PD, bool SPLIT = false>
 __global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __restrict__ a, MatmulProjections P,
                                                                uint32_t N, uint32_t K, uint32_t W, uint32_t mtiles,
                                                                uint32_t ntiles) {
@@ -598,12 +602,16 @@ __global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __re
     static_assert(kFoldSteps % (uint32_t)PD == 0u, "a fold group starts on register set 0 and stage 0");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
+    // XCD-aware order as matmul_q8_kernel: each XCD a contiguous run of the
+    // sequence (of tiles, or of split tiles' parts, a tile's parts adjacent)
     const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    const uint32_t total = mtiles * ntiles;
-    const uint32_t lin = xcd * ((total + 7u) / 8u) + slot;
-    if (lin >= total) return;
+    const uint32_t parts = SPLIT ? P.parts : 1u;
+    const uint32_t units = mtiles * ntiles * parts;
+    const uint32_t lin = xcd * ((units + 7u) / 8u) + slot;
+    if (lin >= units) return;
+    const uint32_t tile = lin / parts, xs = lin - tile * parts;
     uint32_t mt, nt;
-    tile_coords(lin, mtiles, ntiles, mt, nt);
+    tile_coords(tile, mtiles, ntiles, mt, nt);
     const uint32_t pj = (mt >= P.mt0[1] ? 1u : 0u) + (mt >= P.mt0[2] ? 1u : 0u) + (mt >= P.mt0[3] ? 1u : 0u);
     const uint32_t* __restrict__ weight = P.weight[pj];
     const float* __restrict__ scale = P.scale[pj];
@@ -746,28 +754,33 @@ __global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __re
     // converts step i + 1's activations into the other stage and refills
     // their set with step i + 1 + PD.  Loads past K fall outside the buffer
     // resources and return 0.
+    // This workgroup's steps: [s0, s0 + gs) (all of them unless SPLIT).
+    // Loads past the run read the next part's steps or past K (0), unused.
     const uint32_t steps = (K + 63u) / 64u;
     const bool ragged = (K % 64u) != 0u;
+    const uint32_t iters = (steps + parts - 1u) / parts;
+    const uint32_t s0 = xs * iters;
+    const uint32_t gs = s0 < steps ? min(iters, steps - s0) : 0u;
 #pragma unroll
     for (int q = 0; q < PD; ++q) {
-        issue_a(q, 64u * (uint32_t)q);
-        issue_b(q, 64u * (uint32_t)q);
+        issue_a(q, 64u * (s0 + (uint32_t)q));
+        issue_b(q, 64u * (s0 + (uint32_t)q));
     }
-    if (ragged && steps == 1u) mask_b(0, 0u);
+    if (ragged && s0 + 1u == steps) mask_b(0, 64u * s0);
     convert_b(0, 0);
-    issue_b(0, 64u * (uint32_t)PD);
+    issue_b(0, 64u * (s0 + (uint32_t)PD));
     __syncthreads();
     auto iter = [&](int q, uint32_t i) {
         const int nx = (q + 1) % PD;
-        if (ragged && i + 2u == steps) mask_b(nx, (i + 1u) * 64u);  // uniform
+        if (ragged && s0 + i + 2u == steps) mask_b(nx, (s0 + i + 1u) * 64u);  // uniform
         compute(q & 1, q);
-        issue_a(q, (i + (uint32_t)PD) * 64u);
+        issue_a(q, (s0 + i + (uint32_t)PD) * 64u);
         convert_b(nx, (q + 1) & 1);
-        issue_b(nx, (i + 1u + (uint32_t)PD) * 64u);
+        issue_b(nx, (s0 + i + 1u + (uint32_t)PD) * 64u);
         __syncthreads();
     };
-    for (uint32_t g0 = 0; g0 < steps; g0 += kFoldSteps) {
-        const uint32_t gend = min(g0 + kFoldSteps, steps);
+    for (uint32_t g0 = 0; g0 < gs; g0 += kFoldSteps) {
+        const uint32_t gend = min(g0 + kFoldSteps, gs);
         uint32_t i = g0;
         for (; i + (uint32_t)PD <= gend; i += (uint32_t)PD) {
 #pragma unroll
@@ -786,12 +799,15 @@ __global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __re
     }
 
     // lane (j, g) of block (f, b): rows m0 + wm + 16 f + 4 g .. +3 of token
-    // n0 + 16 b + j
-    const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + m0, mrows * 4u);
+    // n0 + 16 b + j.  A split tile's parts store unscaled sums: part 0 into
+    // the output, part xs into its workspace block ([token][row] in the tile).
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(scale + m0, SPLIT ? 0u : mrows * 4u);
+    float* const blk = SPLIT && xs > 0u ? P.part + ((size_t)(xs - 1u) * P.splits + tile) * (size_t)(BM * kBN) : nullptr;
 #pragma unroll
     for (int f = 0; f < FW; ++f) {
         const uint32_t fm = wm + 16u * (uint32_t)f + 4u * g;
-        const u32x4v sv = __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
+        const u32x4v sv = SPLIT ? u32x4v{0x3f800000u, 0x3f800000u, 0x3f800000u, 0x3f800000u}  // 1.0f
+                                : __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(fm * 4u), 0, 0);
 #pragma unroll
         for (uint32_t b = 0; b < TB; ++b) {
             const uint32_t tok = 16u * b + j;
@@ -801,7 +817,7 @@ __global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __re
             y[1] = sum[f][b][1] * __uint_as_float(sv.y);
             y[2] = sum[f][b][2] * __uint_as_float(sv.z);
             y[3] = sum[f][b][3] * __uint_as_float(sv.w);
-            float* o = out + (size_t)(n0 + tok) * M + m0 + fm;
+            float* o = blk ? blk + tok * BM + fm : out + (size_t)(n0 + tok) * M + m0 + fm;
             if (fm + 3u < mrows) {
                 *reinterpret_cast<f32x4_a4*>(o) = f32x4_a4{y[0], y[1], y[2], y[3]};
             } else {
@@ -813,8 +829,8 @@ __global__ __launch_bounds__(512) void matmul_q8_direct_kernel(const float* __re
     }
 }
 
-// out = (part 0 + part 1 + ... + part parts-1) * scale, in part order, for
-// every output of the split tiles of a split launch.  Grid x: split tile;
+// out = (part 0 + part 1 + ... + part parts-1) * scale, in part order (up to
+// 8 parts), for every output of the split tiles of a split launch.  Grid x: split tile;
 // grid y: BM / 16 slices of it; a thread takes 4 consecutive rows of one
 // token (one 16-byte group of every part), all its loads in flight at once.
 template <uint32_t BM>
@@ -838,12 +854,12 @@ __global__ __launch_bounds__(256) void split_sum_kernel(MatmulProjections P, uin
     if (r + 3u < mrows) {
         f32x4 v = *reinterpret_cast<const f32x4_a4*>(y);
         const f32x4 s4 = *reinterpret_cast<const f32x4_a4*>(sc);
-        f32x4 q[3];
+        f32x4 q[7];
 #pragma unroll
-        for (uint32_t j = 1; j < 4u; ++j)
+        for (uint32_t j = 1; j < 8u; ++j)
             if (j < parts) q[j - 1u] = *reinterpret_cast<const f32x4*>(P.part + (size_t)(j - 1u) * P.splits * blk + off);
 #pragma unroll
-        for (uint32_t j = 1; j < 4u; ++j)
+        for (uint32_t j = 1; j < 8u; ++j)
             if (j < parts) v += q[j - 1u];
         *reinterpret_cast<f32x4_a4*>(y) = v * s4;
     } else {
@@ -881,17 +897,31 @@ uint32_t fill_projections(const MatmulProjection* p, uint32_t count, uint32_t BM
 
 // One launch of matmul_q8_direct_kernel (128 FW-row tiles, PD register sets)
 // over `count` projections of the same activations.
-template <int FW, int PD>
+// With parts > 1 (a SPLIT instance) every tile's K steps split into `parts`
+// runs, the workspace `part` holding (parts - 1) x tiles blocks of 128 FW x
+// kBN floats, and split_sum_kernel sums them in a second launch.
+template <int FW, int PD, bool SPLIT = false>
 hipError_t launch_direct(const float* a, const MatmulProjection* p, uint32_t count, uint32_t N, uint32_t K,
-                         hipStream_t stream) {
+                         hipStream_t stream, float* part = nullptr, uint32_t parts = 1) {
+    constexpr uint32_t BM = 128u * FW;
     const uint32_t W = (uint32_t)(((uint64_t)K + 3) / 4);
     MatmulProjections P = {};
-    const uint32_t mtiles = fill_projections(p, count, 128u * FW, P);
+    const uint32_t mtiles = fill_projections(p, count, BM, P);
     const uint32_t ntiles = (N + kBN - 1u) / kBN;
-    const uint32_t grid = ((mtiles * ntiles + 7u) / 8u) * 8u;
+    const uint32_t tiles = mtiles * ntiles;
+    P.part = part;
+    P.whole = 0;
+    P.splits = SPLIT ? tiles : 0u;
+    P.parts = SPLIT ? parts : 1u;
+    const uint32_t grid = ((tiles * P.parts + 7u) / 8u) * 8u;
     const size_t lds = 2u * 3u * kBN * 128u;
-    hipLaunchKernelGGL((matmul_q8_direct_kernel<FW, PD>), dim3(grid), dim3(512), lds, stream, a, P, N, K, W, mtiles,
-                       ntiles);
+    hipLaunchKernelGGL((matmul_q8_direct_kernel<FW, PD, SPLIT>), dim3(grid), dim3(512), lds, stream, a, P, N, K, W,
+                       mtiles, ntiles);
+    if constexpr (SPLIT) {
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        hipLaunchKernelGGL(split_sum_kernel<BM>, dim3(tiles, BM / 16u), dim3(256), 0, stream, P, N, mtiles);
+    }
     return hipGetLastError();
 }
 
@@ -1067,6 +1097,23 @@ hipError_t launch_matmul_q8_multi(const float* a, const MatmulProjection* projec
         // 4096 166.6 -> 161.7.
         set_variant(variant, kname, "D128", 8, 128, 0, (int)kBN, (uint32_t)((t4 + 7u) / 8u * 8u));
         return launch_direct<1, 2>(a, p, n, N, K, stream);
+    }
+    // With a workspace, 256-row tiles on the direct kernel with every tile's
+    // K steps split into 4 or 8 parts, one workgroup each, when that fills
+    // more than 7/8 of the CUs with at least 11 steps per part (the parts
+    // meet in split_sum_kernel).  Same box, us, against the two-K-group forms
+    // the dispatch took before: 512 tokens down 50.0 -> 47.1 (4 parts of 22
+    // steps), 256 tokens down 31.6 -> 30.2 (8 parts of 11); with 8 or 4 steps
+    // per part the split's second launch costs more than it saves (o, K =
+    // 2048: 24.6 -> 26.2 at 512 tokens, 19.6 -> 20.6 at 256).
+    for (uint32_t xs : {4u, 8u}) {
+        const size_t blk = (size_t)256u * kBN * 4u;
+        if (workspace && t8 * xs <= cus && 8u * t8 * xs > 7u * cus && steps >= 11u * xs &&
+            (xs - 1u) * t8 * blk <= workspace_bytes) {
+            set_variant(variant, kname, xs == 4u ? "D256.split4" : "D256.split8", 8, 256, 0, (int)kBN,
+                        (uint32_t)(t8 * xs));
+            return launch_direct<2, 2, true>(a, p, n, N, K, stream, workspace, xs);
+        }
     }
     // 128-row tiles that fill most of the CUs, one per CU with two K groups,
     // beat smaller tiles that fill them all: a 128-row tile moves ~19 bytes
