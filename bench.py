@@ -104,6 +104,31 @@ def add_calibrated(table, cal):
                      "source": cal["source"]})
 
 
+def calibrated_matrix_ceiling():
+    """The bf16 matrix cores' sustained rate on every CU with operands of
+    matmulQ8's kinds, measured now by wxo_roofline_matrix (the clock sags under
+    matrix work, so the nominal peak is not what real operands get)."""
+    tf = wxo_q8.roofline_matrix() / 1e12
+    cal = {"TFLOP/s": round(tf, 1),
+           "source": "wxo_roofline_matrix: v_mfma_f32_16x16x32_bf16 on every CU, two waves per SIMD, int8 codes x "
+                     "bf16 parts of random sign/mantissa/exponent, fastest of 3 ~1 ms launches"}
+    log(f"calibrated matrix ceiling: {cal['TFLOP/s']} TFLOP/s bf16 ({100 * tf / PEAK_BF16_MFMA_TFLOPS:.1f}% of "
+        f"{PEAK_BF16_MFMA_TFLOPS:.0f})")
+    return cal
+
+
+def add_calibrated_matrix(table, calm):
+    """Every matmulQ8 row also as a % of the calibrated matrix-core rate (its
+    matrix work is 3x its useful flops: the exact three-part split); the
+    ceiling itself heads the table."""
+    for row in table:
+        if row.get("case", "").startswith("prefill matmulQ8") and "TFLOP/s" in row:
+            row["pct_of_calibrated_matrix"] = round(100.0 * 3.0 * row["TFLOP/s"] / calm["TFLOP/s"], 1)
+    table.insert(0, {"case": "calibrated ceiling (wxo_roofline_matrix): bf16 matrix cores on matmulQ8-like operands",
+                     "TFLOP/s": calm["TFLOP/s"],
+                     "pct_of_peak": round(100.0 * calm["TFLOP/s"] / PEAK_BF16_MFMA_TFLOPS, 1), "source": calm["source"]})
+
+
 def cpu_baseline(packed, scales, x, N, K, budget_s):
     node = shutil.which("node")
     if node is None:
@@ -816,6 +841,7 @@ def main() -> int:
             if st != 0:
                 raise wxo_q8.WxoError(st, wxo_q8.lib().wxo_last_error().decode())
         run_prefill_suite(stream, args.steps, args.warmup, table, check)
+        add_calibrated_matrix(table, calibrated_matrix_ceiling())
         add_calibrated(table, calibrated_ceiling())
         if not args.no_cpu_baseline:
             table.extend(cpu_reference_ops(budget_s=1.0))

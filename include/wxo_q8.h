@@ -180,6 +180,16 @@ int wxo_gate_release(uint32_t gate);
  * memory and a stream of its own; takes tens of milliseconds.  A measurement
  * aid: ops are reported as a fraction of it beside the nominal 8 TB/s. */
 int wxo_roofline(double* bandwidth, double* compute);
+/* The best sustained rate of the bf16 matrix cores (v_mfma_f32_16x16x32_bf16)
+ * in flop/s, on every CU with two waves per SIMD (as matmulQ8 runs them), over
+ * operands of matmulQ8's own kinds (int8 codes against bf16 parts of random
+ * sign, mantissa and exponent).  No counterpart in the reference, whose
+ * roofline measures HBM and f32 FMA only; a measurement aid like
+ * wxo_roofline: the clock sags under matrix work by how much the operands'
+ * bits toggle, so the nominal 2.5 PFLOP/s is not what real operands get.
+ * Synchronous; allocates and frees 1 MiB of device memory and a stream of its
+ * own; takes a few milliseconds. */
+int wxo_roofline_matrix(double* flops);
 
 /* ---- captured batches ------------------------------------------------------
  * The reference encodes a resident batch's passes into one command encoder

@@ -78,6 +78,8 @@ def test_validation_happens_before_device_access():
     # the calibrated ceiling needs at least one output
     assert L.wxo_roofline(None, None) == wxo_q8.WXO_ERR_INVALID
     assert "roofline" in L.wxo_last_error().decode()
+    assert L.wxo_roofline_matrix(None) == wxo_q8.WXO_ERR_INVALID
+    assert "roofline_matrix" in L.wxo_last_error().decode()
     # graph capture needs a stream of its own
     assert L.wxo_graph_capture_begin(None) == wxo_q8.WXO_ERR_INVALID
     assert "not the null stream" in L.wxo_last_error().decode()

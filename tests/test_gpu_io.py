@@ -221,3 +221,15 @@ def test_roofline_ceilings():
     assert only_bw["compute"] is None and 3e12 < only_bw["bandwidth"] < 8.2e12
     with pytest.raises(wxo_q8.WxoError, match="roofline"):
         wxo_q8.roofline(bandwidth=False, compute=False)
+
+
+def test_roofline_matrix_ceiling():
+    """wxo_roofline_matrix: the sustained bf16 matrix-core rate with
+    matmulQ8-like operands is positive and under MI355X's published dense
+    2.5 PFLOP/s (with margin for timing), and a second measurement agrees
+    with the first within a quarter."""
+    print("wxo_roofline_matrix", flush=True)
+    a = wxo_q8.roofline_matrix()
+    assert 5e14 < a < 2.6e15, a
+    b = wxo_q8.roofline_matrix()
+    assert 0.75 < b / a < 1.33, (a, b)

@@ -138,5 +138,8 @@ hipError_t launch_gather_dequant_rows(const int8_t* codes, const float* scale, u
 // one-wide f32 FMA rate (flop/s), measured now; either output may be null to
 // skip that part.  Allocates (and frees) two 512 MiB buffers on its own stream.
 hipError_t measure_roofline(const DeviceInfo& dev, double* bandwidth, double* compute);
+// The sustained bf16 matrix-core rate (flop/s) on every CU, two waves per SIMD,
+// operands like the prefill GEMM's.
+hipError_t measure_matrix_ceiling(const DeviceInfo& dev, double* flops);
 
 }  // namespace wxo

@@ -25,6 +25,15 @@
 //  * The FMA chains: 8 independent chains per lane, 8 waves per SIMD, no
 //    memory.  This build disables packed f32 instructions, so the figure is the
 //    rate of one-wide v_fma_f32.
+//
+// The matrix cores (measure_matrix_ceiling; the reference measures no matrix
+// rate): v_mfma_f32_16x16x32_bf16 on every CU, one workgroup of 8 waves per
+// CU (two per SIMD, as the prefill GEMM runs), 8 independent accumulators per
+// wave over operands loaded once.  The clock sags under matrix work by how
+// much the operands' bits toggle, so the operands are the GEMM's own kinds:
+// A holds int8 codes in bf16, B bf16 values of random sign and mantissa with
+// exponents over 2^-8 .. 2^1 (an activation's split parts).  Each launch runs
+// ~1 ms; the fastest of three after a warm-up counts.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -87,6 +96,56 @@ __global__ __launch_bounds__(256) void fma_chain_kernel(float seed, uint32_t ite
 #pragma unroll
     for (int j = 0; j < kFmaChains; ++j) s += c[j];
     if (s == seed - 999.0f) sink[threadIdx.x] = s;
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kMatrixVectors = 65536;  // 16-byte operand vectors, 1 MiB
+constexpr int kMatrixA = 2, kMatrixB = 4;   // a wave's operands: 8 accumulators
+
+// Operand vector v (4 words, 8 bf16): even v codes, odd v activation parts.
+__global__ __launch_bounds__(256) void fill_matrix_operands_kernel(uint32_t* __restrict__ ops, uint32_t seed) {
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < 4u * kMatrixVectors; i += gridDim.x * 256u) {
+        const uint32_t h = fmix32(i * 0x9e3779b9u + seed);
+        uint32_t lo, hi;
+        if (((i >> 2) & 1u) == 0u) {
+            lo = __float_as_uint((float)(int8_t)h) >> 16;  // exact in bf16
+            hi = __float_as_uint((float)(int8_t)(h >> 8)) >> 16;
+        } else {
+            lo = ((h & 1u) << 15) | ((119u + ((h >> 1) & 0xffu) % 10u) << 7) | ((h >> 9) & 0x7fu);
+            hi = (((h >> 16) & 1u) << 15) | ((119u + ((h >> 17) & 0xffu) % 10u) << 7) | ((h >> 25) & 0x7fu);
+        }
+        ops[i] = lo | (hi << 16);
+    }
+}
+
+__global__ __launch_bounds__(512) void matrix_rate_kernel(const uint32_t* __restrict__ ops, uint32_t iterations,
+                                                          float* sink) {
+    const uint32_t t = blockIdx.x * 512u + threadIdx.x;
+    const uint4* v = reinterpret_cast<const uint4*>(ops);
+    bf16x8 a[kMatrixA], b[kMatrixB];
+#pragma unroll
+    for (int i = 0; i < kMatrixA; ++i) a[i] = __builtin_bit_cast(bf16x8, v[(2u * (t * 4u + (uint32_t)i)) % kMatrixVectors]);
+#pragma unroll
+    for (int j = 0; j < kMatrixB; ++j)
+        b[j] = __builtin_bit_cast(bf16x8, v[(2u * (t * 4u + (uint32_t)j) + 1u) % kMatrixVectors]);
+    f32x4 c[kMatrixA][kMatrixB];
+#pragma unroll
+    for (int i = 0; i < kMatrixA; ++i)
+#pragma unroll
+        for (int j = 0; j < kMatrixB; ++j) c[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t it = 0; it < iterations; ++it) {
+#pragma unroll
+        for (int i = 0; i < kMatrixA; ++i)
+#pragma unroll
+            for (int j = 0; j < kMatrixB; ++j) c[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], c[i][j], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMatrixA; ++i)
+#pragma unroll
+        for (int j = 0; j < kMatrixB; ++j) s += c[i][j][0] + c[i][j][1] + c[i][j][2] + c[i][j][3];
+    if (s == 1234.5f) sink[threadIdx.x] = s;  // keeps the work; the sums never reach it
 }
 
 __global__ __launch_bounds__(64) void roofline_spin_kernel(uint64_t ticks) {
@@ -194,6 +253,37 @@ hipError_t measure_roofline(const DeviceInfo& dev, double* bandwidth, double* co
         }
         *compute = (double)groups * 256.0 * iterations * kFmaChains * 2.0 / best;
     }
+    return hipStreamSynchronize(s.stream);
+}
+
+hipError_t measure_matrix_ceiling(const DeviceInfo& dev, double* flops) {
+    Scope s;
+    RF_TRY(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+    RF_TRY(hipEventCreateWithFlags(&s.e0, hipEventDisableSystemFence));
+    RF_TRY(hipEventCreateWithFlags(&s.e1, hipEventDisableSystemFence));
+    RF_TRY(hipMalloc(&s.sink, 512 * sizeof(uint32_t)));
+    RF_TRY(hipMalloc(&s.buf[0], (size_t)kMatrixVectors * 16u));
+    hipLaunchKernelGGL(fill_matrix_operands_kernel, dim3(1024), dim3(256), 0, s.stream,
+                       static_cast<uint32_t*>(s.buf[0]), 0x51ed270bu);
+    RF_TRY(hipGetLastError());
+    const uint32_t cus = (uint32_t)(dev.cu_count > 0 ? dev.cu_count : 256);
+    const uint32_t iterations = 6000;  // ~1 ms a launch at the sagged clock
+    double best = 1e30;
+    for (int r = 0; r < 1 + kRegions; ++r) {
+        RF_TRY(hipStreamSynchronize(s.stream));
+        RF_TRY(hipEventRecord(s.e0, s.stream));
+        hipLaunchKernelGGL(matrix_rate_kernel, dim3(cus), dim3(512), 0, s.stream,
+                           static_cast<const uint32_t*>(s.buf[0]), iterations, reinterpret_cast<float*>(s.sink));
+        RF_TRY(hipGetLastError());
+        RF_TRY(hipEventRecord(s.e1, s.stream));
+        RF_TRY(hipEventSynchronize(s.e1));
+        float ms = 0.0f;
+        RF_TRY(hipEventElapsedTime(&ms, s.e0, s.e1));
+        if (r > 0 && ms > 0.0f && ms * 1e-3 < best) best = ms * 1e-3;  // r = 0 is the warm-up
+    }
+    // 8 waves per workgroup, kMatrixA x kMatrixB ops per wave and iteration,
+    // 16 x 16 x 32 x 2 flops per op
+    *flops = (double)cus * 8.0 * iterations * (kMatrixA * kMatrixB) * 16384.0 / best;
     return hipStreamSynchronize(s.stream);
 }
 

@@ -569,6 +569,18 @@ int wxo_roofline(double* bandwidth, double* compute) {
     return ok();
 }
 
+int wxo_roofline_matrix(double* flops) {
+    if (!flops) return fail(WXO_ERR_INVALID, "roofline_matrix: flops is NULL");
+    *flops = 0.0;
+    const wxo::DeviceInfo* d = nullptr;
+    WXO_TRY(current_device(&d));
+    double fl = 0.0;
+    const hipError_t e = wxo::measure_matrix_ceiling(*d, &fl);
+    if (e != hipSuccess) return hip_fail(e, "roofline_matrix measurement");
+    *flops = fl;
+    return ok();
+}
+
 // ---- ops on device pointers ------------------------------------------------
 
 int wxo_matvec_q8(const uint32_t* weight, const float* scale, const float* vector, float* output, uint32_t N,

@@ -68,6 +68,7 @@ SIGNATURES = {
     "wxo_gate_hold": ([ctypes.c_uint32, _P, ctypes.POINTER(ctypes.c_uint32)], _I),
     "wxo_gate_release": ([ctypes.c_uint32], _I),
     "wxo_roofline": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)], _I),
+    "wxo_roofline_matrix": ([ctypes.POINTER(ctypes.c_double)], _I),
     "wxo_matmul_q8_multi": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P], _I),
     "wxo_matmul_q8_multi_ws": ([_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _SZ, _P], _I),
     "wxo_matmul_q8_workspace_bytes": ([ctypes.POINTER(_SZ)], _I),
@@ -163,6 +164,14 @@ def roofline(bandwidth: bool = True, compute: bool = True) -> dict:
     bw, fl = ctypes.c_double(0.0), ctypes.c_double(0.0)
     _check(lib().wxo_roofline(ctypes.byref(bw) if bandwidth else None, ctypes.byref(fl) if compute else None))
     return {"bandwidth": bw.value if bandwidth else None, "compute": fl.value if compute else None}
+
+
+def roofline_matrix() -> float:
+    """The sustained bf16 matrix-core rate in flop/s with matmulQ8-like
+    operands, measured now (wxo_roofline_matrix)."""
+    fl = ctypes.c_double(0.0)
+    _check(lib().wxo_roofline_matrix(ctypes.byref(fl)))
+    return fl.value
 
 
 def words_per_row(K: int) -> int:
