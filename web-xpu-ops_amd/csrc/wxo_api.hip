@@ -55,7 +55,7 @@ std::mutex g_dev_mu;
 char g_describe[1024] = {0};
 
 // The workspace of wxo_matmul_q8_multi_static: the largest split workspace
-// wxo_matmul_q8_multi_ws ever uses on a 256-CU device (32 KiB per CU).  Each
+// wxo_matmul_q8_multi_ws ever uses on a 256-CU device (64 KiB per CU, 16 MiB).  Each
 // GPU holds its own copy from the code object's load until the process ends.
 // Host code never passes the array's name to a kernel or a copy (on the host
 // it is only a stand-in for the symbol): it uses g_scratch[device], the
