@@ -53,7 +53,7 @@
 // every XCD's L2: 512-token layer 215 -> 182 us, 2048 tokens 629 -> 570.
 //
 // With a caller's workspace, a launch may also split some tiles' K steps
-// between 2 or 4 workgroups (a short prompt's tiles, which would leave most
+// between 2, 4 or 8 workgroups (a short prompt's tiles, which would leave most
 // CUs idle; the last tiles of a round that would load the CUs unevenly):
 // part 0 stores its unscaled sums into the output, the other parts into
 // tile-sized workspace blocks, and a second launch adds them in part order
@@ -64,8 +64,8 @@
 // 16 waves per two tiles, each group of 8 waves on a tile of its own (the
 // PAIR instances); the sums are the one-group form's.
 //
-// Launches with enough tiles for one workgroup per CU and no K split run
-// matmul_q8_direct_kernel instead: every wave of 8 owns 16 FW weight rows and
+// Launches with enough tiles for one workgroup per CU, and short prompts'
+// 256-row tiles split 4 or 8 ways, run matmul_q8_direct_kernel instead: every wave of 8 owns 16 FW weight rows and
 // all 64 tokens of the tile, and loads its rows' codes straight into VGPRs
 // (two dwordx2 per 16-row block and step, in the operand's k order), so only
 // the activation parts pass through LDS.  That removes the codes' LDS writes
