@@ -141,3 +141,18 @@ def test_a_restarted_index_is_caught(bench):
     timed = list(range(steps))
     with pytest.raises(AssertionError, match="last read"):
         check_rotation(before, timed, copies)
+
+
+def test_prefill_rows_against_the_calibrated_matrix_rate(bench):
+    """Every matmulQ8 row of the prefill suite gets its share of the calibrated
+    matrix-core rate at three matrix flops per useful one; other rows are left
+    alone, and the ceiling itself heads the table."""
+    table = [{"case": "prefill matmulQ8 wq: tokens=512 M=2048 K=2048", "us": 25.0, "TFLOP/s": 170.0},
+             {"case": "prefill matmulQ8: one decoder layer, 512 tokens", "us": 200.0, "TFLOP/s": 250.0},
+             {"case": "dequantizePackedQ8 N=5632 K=2048", "us": 9.5, "GB/s": 6000.0}]
+    bench.add_calibrated_matrix(table, {"TFLOP/s": 1750.0, "source": "test"})
+    assert table[0]["case"].startswith("calibrated ceiling (wxo_roofline_matrix)")
+    assert table[0]["TFLOP/s"] == 1750.0 and table[0]["pct_of_peak"] == 70.0
+    assert table[1]["pct_of_calibrated_matrix"] == round(100 * 3 * 170.0 / 1750.0, 1)
+    assert table[2]["pct_of_calibrated_matrix"] == round(100 * 3 * 250.0 / 1750.0, 1)
+    assert "pct_of_calibrated_matrix" not in table[3]
