@@ -11,7 +11,7 @@ import { packInt8Rows } from "../../web-xpu-ops_amd/llm/weights-q8.js";
 import { runMatVecQ8 } from "../../web-xpu-ops_amd/llm/kernels.js";
 import { createResidentQ8Device } from "../../web-xpu-ops_amd/harness/resident.js";
 import { native, describe } from "../../web-xpu-ops_amd/native/index.js";
-import { roofline, measureRoofline } from "../../web-xpu-ops_amd/harness/roofline.js";
+import { roofline, measureRoofline, measureMatrixRoofline } from "../../web-xpu-ops_amd/harness/roofline.js";
 import * as oracle from "../../oracle/q8_oracle.mjs";
 
 const F = "api.test.mjs";
@@ -27,6 +27,7 @@ test(F, "exports the reference's op names", () => {
   assert.strictEqual(typeof runMatVecQ8, "function");
   assert.strictEqual(typeof roofline, "function");
   assert.strictEqual(typeof measureRoofline, "function");
+  assert.strictEqual(typeof measureMatrixRoofline, "function");
 });
 
 test(F, "the addon loads and exports its whole surface", () => {
@@ -34,7 +35,8 @@ test(F, "the addon loads and exports its whole surface", () => {
   for (const name of ["abiVersion", "describe", "deviceCount", "init", "synchronize", "matvecQ8", "matvecQ8Ffn",
     "matvecQ8Residual", "quantize", "packQ8", "packInt8Rows", "quantizePackQ8", "malloc", "free", "upload", "download",
     "copy", "matvecQ8Device", "matvecQ8FfnDevice", "matvecQ8ResidualDevice", "quantizeDevice", "packQ8Device",
-    "packInt8RowsDevice", "quantizePackQ8Device", "roofline", "matvecQ8Async", "whenDone", "hostAlloc", "downloadAsync"]) {
+    "packInt8RowsDevice", "quantizePackQ8Device", "roofline", "rooflineMatrix", "matvecQ8Async", "whenDone", "hostAlloc",
+    "downloadAsync"]) {
     assert.strictEqual(typeof a[name], "function", name);
   }
   assert.strictEqual(a.abiVersion(), 1);
@@ -351,4 +353,7 @@ gpuTest(F, "roofline(): this device's own ceilings (harness/roofline.ts:162-222)
   assert.ok(r.bandwidth > 3e12 && r.bandwidth < 8.2e12, `bandwidth ${r.bandwidth}`);
   assert.ok(r.compute > 2e13 && r.compute < 1.6e14, `compute ${r.compute}`);
   assert.strictEqual(await roofline(), r, "cached: the same measurement object");
+  // the matrix cores on matmulQ8-like operands: under the published 2.5 PFLOP/s dense bf16
+  const m = await measureMatrixRoofline();
+  assert.ok(m > 5e14 && m < 2.6e15, `matrix ${m}`);
 });

@@ -7,3 +7,5 @@ export interface Roofline {
 }
 export declare function measureRoofline(runner?: unknown): Promise<Roofline>;
 export declare function roofline(runner?: unknown): Promise<Roofline>;
+/** The bf16 matrix cores' sustained flop/s on matmulQ8-like operands, measured now (no counterpart in the reference). */
+export declare function measureMatrixRoofline(): Promise<number>;

@@ -14,6 +14,16 @@ export async function measureRoofline(_runner) {
   return native().roofline();
 }
 
+/** The bf16 matrix cores' sustained rate in flop/s on every CU, with operands
+ * of matmulQ8's kinds (int8 codes against bf16 parts of random bits): the
+ * clock sags under matrix work, so real operands do not get the nominal
+ * 2.5 PFLOP/s.  No counterpart in the reference, whose roofline measures HBM
+ * and FMA only; matmulQ8 (three matrix flops per useful one) is reported
+ * against it. */
+export async function measureMatrixRoofline() {
+  return native().rooflineMatrix();
+}
+
 const CACHE = Symbol.for("web-xpu-ops-mi355x.roofline");
 
 /** The ceiling for this session, measured once and kept on globalThis (as the

@@ -232,6 +232,19 @@ static napi_value js_roofline(napi_env env, napi_callback_info info) {
     return r;
 }
 
+/* rooflineMatrix() -> number: the bf16 matrix cores' sustained rate in flop/s
+ * on every CU with operands of matmulQ8's kinds (wxo_roofline_matrix); no
+ * counterpart in the reference, whose roofline measures HBM and FMA only. */
+static napi_value js_roofline_matrix(napi_env env, napi_callback_info info) {
+    (void)info;
+    double fl = 0.0;
+    int st = wxo_roofline_matrix(&fl);
+    if (st != WXO_OK) return throw_status(env, st, "rooflineMatrix");
+    napi_value v;
+    napi_create_double(env, fl, &v);
+    return v;
+}
+
 /* ---------------------------------------------------------------- streams and captured batches
  * Device-pointer ops enqueue on g_stream: the null stream, except while a
  * batch is being captured (graphBegin .. graphEnd), when it is the addon's
@@ -1422,6 +1435,7 @@ static napi_value init_module(napi_env env, napi_value exports) {
         {"init", NULL, js_init, NULL, NULL, NULL, napi_enumerable, NULL},
         {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
         {"roofline", NULL, js_roofline, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"rooflineMatrix", NULL, js_roofline_matrix, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8", NULL, js_matvec_q8, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Async", NULL, js_matvec_q8_async, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecQ8Residual", NULL, js_matvec_q8_residual, NULL, NULL, NULL, napi_enumerable, NULL},
